@@ -1,0 +1,230 @@
+"""Float reference of the ternary decoder (test infrastructure only, see oracle/__init__.py).
+
+The arithmetic is model/fastref.py's (HybridRef: fp32 activations, weights dequantised as
+(code - 1) * scale and held in fp16, which is exact for ternary; embedding rows from the int16
+BFP table; plain RoPE with float32 angles; NEOX pairs on the first rope_dims of a head). The
+state semantics are model/golden.py:FloatModel's (K/V caches appended post-norm/post-RoPE (K)
+and raw (V), a (K-1)-deep conv window and a per-value-head fp32 recurrent matrix for every
+DeltaNet layer, `pos` advanced per forward), so the reference steps one token at a time like
+the GPU loop does. `kv_fp16=True` rounds cached K/V to fp16 as the GPU cache stores them.
+"""
+
+import numpy as np
+
+from trixium_amd import layout as L
+
+f32 = np.float32
+
+
+class FloatRef:
+    def __init__(self, img, kv_fp16=False):
+        self.img = img
+        h = self.h = img.header
+        self.n_layer, self.n_embd = h["n_layer"], h["n_embd"]
+        self.n_head, self.n_kv, self.hd = h["n_head"], h["n_kv_head"], h["head_dim"]
+        self.nk, self.hk = h["dn_num_k_heads"], h["dn_k_head_dim"]
+        self.nv, self.hv = h["dn_num_v_heads"], h["dn_v_head_dim"]
+        self.K = h["dn_conv_kernel"]
+        self.rope_n = h["rope_dims"] or self.hd
+        self.eps = f32(h["rms_eps"])
+        self.gated = bool(h["attn_gated"])
+        self.vocab = h["vocab"]
+        self.dn = [t == "deltanet" for t in h["layer_types"]]
+        if h["hadamard_block"]:
+            raise NotImplementedError("rotated-basis images are outside this reference")
+        self.kv_fp16 = kv_fp16
+        self.wcache = {}
+        # fastref.py:62-63: theta**(-2i/n) evaluated in float32.
+        self.rope_freq = np.array([f32(f32(h["rope_theta"]) ** f32(-2.0 * i / self.rope_n))
+                                   for i in range(self.rope_n // 2)], dtype=f32)
+        self.norm_attn = [self._f32(L.ROLE_ATTN_NORM, l) for l in range(self.n_layer)]
+        self.norm_ffn = [self._f32(L.ROLE_FFN_NORM, l) for l in range(self.n_layer)]
+        self.norm_q, self.norm_k, self.norm_ssm, self.ssm_a, self.ssm_dt, self.conv_w = {}, {}, {}, {}, {}, {}
+        for l in range(self.n_layer):
+            if self.dn[l]:
+                self.norm_ssm[l] = self._f32(L.ROLE_SSM_NORM, l)
+                self.ssm_a[l] = self._f32(L.ROLE_SSM_A, l)
+                self.ssm_dt[l] = self._f32(L.ROLE_SSM_DT, l)
+                self.conv_w[l] = self._f32(L.ROLE_SSM_CONV, l).reshape(-1, self.K)
+            else:
+                self.norm_q[l] = self._f32(L.ROLE_ATTN_Q_NORM, l)
+                self.norm_k[l] = self._f32(L.ROLE_ATTN_K_NORM, l)
+        self.out_norm = self._f32(L.ROLE_OUT_NORM, 0)
+        self.head_role = L.ROLE_LM_HEAD if img.find(L.ROLE_LM_HEAD, 0) else L.ROLE_TOK_EMB
+        e16 = img.find(L.ROLE_TOK_EMB16, 0)
+        _, self.emb_mant = img.entry_tensor(e16)
+        _, ex = img.entry_tensor(img.find(L.ROLE_TOK_EMB16_EXP, 0))
+        self.emb_exp = np.asarray(ex).reshape(-1)
+        self.reset()
+
+    # Tensors (fastref.py:86-125) -----------------------------------------------------------
+    def _f32(self, role, l):
+        e = self.img.find(role, l, L.KIND_F32)
+        assert e is not None, (role, l)
+        return np.asarray(self.img.entry_tensor(e)[1], dtype=f32).reshape(-1)
+
+    def weight(self, role, l):
+        key = (role, l)
+        if key not in self.wcache:
+            e = self.img.find(role, l)
+            ws = []
+            for t in self.img.ksegs(e):
+                scales, codes = self.img.entry_tensor(t)
+                if t["kind"] == L.KIND_F32:
+                    ws.append(np.asarray(codes, dtype=f32).reshape(t["rows"], t["cols"]))
+                    continue
+                g = 128 if L.is_ternary(t["kind"]) else 32
+                off = f32(1.0) if L.is_ternary(t["kind"]) else f32(0.0)
+                w = (codes.astype(f32).reshape(t["rows"], -1, g) - off) * scales.astype(f32)[:, :, None]
+                ws.append(w.reshape(t["rows"], t["cols"]))
+            self.wcache[key] = np.concatenate(ws, axis=1).astype(np.float16)
+        return self.wcache[key]
+
+    def proj(self, role, l, x):
+        W = self.weight(role, l)
+        return (W.astype(f32) @ np.asarray(x, dtype=f32)).astype(f32)
+
+    # Elementwise ops (fastref.py:143-156) ----------------------------------------------------
+    def rmsnorm(self, x, w):
+        r = f32(1.0) / np.sqrt((x * x).mean(axis=-1, keepdims=True, dtype=f32) + self.eps)
+        return (x * r * w).astype(f32)
+
+    def l2norm(self, x):
+        n = np.maximum(np.sqrt((x * x).sum(axis=-1, keepdims=True, dtype=f32)), self.eps)
+        return (x / n).astype(f32)
+
+    @staticmethod
+    def sigmoid(x):
+        return (f32(1.0) / (f32(1.0) + np.exp(-x))).astype(f32)
+
+    @staticmethod
+    def silu(x):
+        return (x / (f32(1.0) + np.exp(-x))).astype(f32)
+
+    @staticmethod
+    def softplus(x):
+        return np.where(x > 20, x, np.log1p(np.exp(np.minimum(x, 20)))).astype(f32)
+
+    # State (golden.py:304-320) ---------------------------------------------------------------
+    def reset(self):
+        self.pos = 0
+        self.k_cache = {l: [] for l in range(self.n_layer) if not self.dn[l]}
+        self.v_cache = {l: [] for l in range(self.n_layer) if not self.dn[l]}
+        C = 2 * self.nk * self.hk + self.nv * self.hv
+        self.conv_state = {l: np.zeros((self.K - 1, C), f32) for l in range(self.n_layer) if self.dn[l]}
+        self.dn_state = {l: np.zeros((self.nv, self.hv, self.hk), f32) for l in range(self.n_layer) if self.dn[l]}
+
+    def embed(self, tok):
+        return (self.emb_mant[tok].astype(f32) * f32(np.exp2(int(self.emb_exp[tok])))).astype(f32)
+
+    def attention(self, l, hn, pos):
+        hd, nh, nkv = self.hd, self.n_head, self.n_kv
+        qf = self.proj(L.ROLE_ATTN_Q, l, hn)
+        k = self.proj(L.ROLE_ATTN_K, l, hn).reshape(nkv, hd)
+        v = self.proj(L.ROLE_ATTN_V, l, hn).reshape(nkv, hd)
+        if self.gated:
+            qf = qf.reshape(nh, 2 * hd)
+            q, gate = qf[:, :hd], qf[:, hd:]
+        else:
+            q, gate = qf.reshape(nh, hd), None
+        q = self.rmsnorm(q, self.norm_q[l])
+        k = self.rmsnorm(k, self.norm_k[l])
+        ang = (f32(pos) * self.rope_freq).astype(f32)
+        cos, sin = np.cos(ang), np.sin(ang)
+        half = self.rope_n // 2
+
+        def rope(x):
+            x = x.copy()
+            x0, x1 = x[:, :half].copy(), x[:, half:self.rope_n].copy()
+            x[:, :half] = x0 * cos - x1 * sin
+            x[:, half:self.rope_n] = x0 * sin + x1 * cos
+            return x
+
+        q, k = rope(q), rope(k)
+        q = (q * f32(1.0 / np.sqrt(hd))).astype(f32)
+        if self.kv_fp16:
+            k, v = k.astype(np.float16).astype(f32), v.astype(np.float16).astype(f32)
+        self.k_cache[l].append(k)
+        self.v_cache[l].append(v)
+        Kc = np.stack(self.k_cache[l])             # [T, nkv, hd]
+        Vc = np.stack(self.v_cache[l])
+        rep = nh // nkv
+        out = np.empty((nh, hd), f32)
+        for h in range(nh):
+            s = (Kc[:, h // rep] @ q[h]).astype(f32)
+            s = s - s.max()
+            p = np.exp(s)
+            p = (p / p.sum()).astype(f32)
+            out[h] = (p @ Vc[:, h // rep]).astype(f32)
+        if gate is not None:
+            out = (out * self.sigmoid(gate)).astype(f32)
+        return self.proj(L.ROLE_ATTN_OUT, l, out.reshape(-1))
+
+    def deltanet(self, l, hn):
+        """One position of the gated delta rule (fastref.py:182-214, golden.py:400-434)."""
+        nq = self.nk * self.hk
+        qkv = self.proj(L.ROLE_ATTN_QKV, l, hn)
+        z = self.proj(L.ROLE_ATTN_ZGATE, l, hn)
+        beta = self.sigmoid(self.proj(L.ROLE_SSM_BETA, l, hn))
+        alpha = self.proj(L.ROLE_SSM_ALPHA, l, hn)
+        decay = np.exp((self.softplus(alpha + self.ssm_dt[l]) * self.ssm_a[l]).astype(f32))
+        w = self.conv_w[l]
+        win = np.concatenate([self.conv_state[l], qkv[None, :]], axis=0)      # [K, C]
+        conv = sum(win[i] * w[:, i] for i in range(self.K)).astype(f32)
+        self.conv_state[l] = win[1:].copy()
+        conv = self.silu(conv)
+        q = self.l2norm(conv[:nq].reshape(self.nk, self.hk))
+        k = self.l2norm(conv[nq:2 * nq].reshape(self.nk, self.hk))
+        v = conv[2 * nq:].reshape(self.nv, self.hv)
+        kh = np.arange(self.nv) % self.nk
+        M = self.dn_state[l]
+        qt, kt = q[kh], k[kh]
+        M *= decay[:, None, None]
+        delta = (v - np.einsum("hjk,hk->hj", M, kt)) * beta[:, None]
+        M += delta[:, :, None] * kt[:, None, :]
+        o = (np.einsum("hjk,hk->hj", M, qt) * f32(1.0 / np.sqrt(self.hk))).astype(f32)
+        nrm = self.rmsnorm(o, self.norm_ssm[l])
+        gz = nrm * self.silu(z.reshape(self.nv, self.hv))
+        rep = self.nv // self.nk
+        gpos = kh * rep + np.arange(self.nv) // self.nk
+        og = np.empty_like(gz)
+        og[gpos] = gz
+        return self.proj(L.ROLE_SSM_OUT, l, og.reshape(-1).astype(f32))
+
+    def step(self, tok, want_logits=True):
+        """One decode position: residual stream through every layer, then (optionally) the
+        logits over the vocabulary (fastref.py:244-261 per position)."""
+        x = self.embed(tok)
+        for l in range(self.n_layer):
+            hn = self.rmsnorm(x, self.norm_attn[l])
+            y = self.deltanet(l, hn) if self.dn[l] else self.attention(l, hn, self.pos)
+            x = (x + y).astype(f32)
+            hn = self.rmsnorm(x, self.norm_ffn[l])
+            g = self.proj(L.ROLE_FFN_GATE, l, hn)
+            u = self.proj(L.ROLE_FFN_UP, l, hn)
+            x = (x + self.proj(L.ROLE_FFN_DOWN, l, (self.silu(g) * u).astype(f32))).astype(f32)
+        self.pos += 1
+        self.last_hidden = x
+        if not want_logits:
+            return None
+        hn = self.rmsnorm(x, self.out_norm)
+        return self.proj(self.head_role, 0, hn)[:self.vocab]
+
+    def forward(self, tokens):
+        """FloatModel.forward contract (golden.py:436-460): logits of the last position."""
+        logits = None
+        for i, t in enumerate(tokens):
+            logits = self.step(int(t), want_logits=(i == len(tokens) - 1))
+        return logits
+
+    def generate(self, prompt, n_new):
+        """Greedy decode with the firmware loop contract (mirror.py:1036-1044): prefill one token
+        per forward, logits only at the last prompt position, no forward after the last output."""
+        out = []
+        logits = self.forward(prompt)
+        for i in range(n_new):
+            nxt = int(np.argmax(logits))
+            out.append(nxt)
+            if i + 1 < n_new:
+                logits = self.step(nxt)
+        return out

@@ -1,0 +1,151 @@
+"""The CPU oracle pinned before it is trusted: the reference's known-answer tests restated, closed
+forms and brute force on small cases, and the golden fixtures the reference produced."""
+
+import hashlib
+
+import numpy as np
+import pytest
+
+from oracle import bitexact as bx
+from oracle.floatref import FloatRef
+from trixium_amd import bons, configs as C
+
+
+def test_rne_shift_known_answers():
+    # test/model/test_bitexact.py:13-26 of the reference.
+    assert bx.rne_shift(3, 1) == 2 and bx.rne_shift(1, 1) == 0 and bx.rne_shift(5, 1) == 2
+    assert bx.rne_shift(7, 1) == 4 and bx.rne_shift(-1, 1) == 0 and bx.rne_shift(-3, 1) == -2
+    assert bx.rne_shift(-5, 2) == -1 and bx.rne_shift(6, 2) == 2
+    v = np.arange(-1000, 1000)
+    for k in (1, 3, 7):
+        assert np.array_equal(bx.rne_shift(v, k), np.rint(v / 2**k).astype(np.int64))
+
+
+def test_fp16_decompose_exact():
+    rng = np.random.default_rng(5)
+    s = np.concatenate([rng.uniform(-1, 1, 1000).astype(np.float16),
+                        np.array([0.0, 6e-8, -6e-8, 6e-5, 65504.0], np.float16)])
+    m11, e16 = bx.fp16_decompose(s)
+    assert np.array_equal(m11.astype(np.float64) * np.exp2(e16.astype(np.float64)), s.astype(np.float64))
+    assert np.all(np.abs(m11) < 2048)
+
+
+def test_matvec_ternary_accuracy_vs_float64():
+    # test/model/test_bitexact.py:36-56: the only error is the per-group shift truncation.
+    rng = np.random.default_rng(42)
+    M, K = 64, 512
+    scales = rng.uniform(0.01, 0.08, (M, K // 128)).astype(np.float16)
+    codes = rng.integers(0, 3, (M, K), dtype=np.uint8)
+    x8 = rng.integers(-127, 128, K, dtype=np.int8)
+    _, e16 = bx.fp16_decompose(scales)
+    B = bx.choose_scale_bias(e16)
+    R = bx.choose_result_shift(scales, B)
+    res = bx.matvec_ternary(scales, codes, x8, B, R)
+    ref = (((codes.astype(np.float64) - 1) * x8).reshape(M, -1, 128).sum(2) * scales.astype(np.float64)).sum(1)
+    got = res.astype(np.float64) * np.exp2(-B + R)
+    assert np.max(np.abs(got - ref) / np.maximum(np.abs(ref), 1e-3)) < 1e-3
+
+
+def test_matvec_ternary_bounds_hold_adversarial():
+    # test/model/test_bitexact.py:58-70: K = 12288, all +1, x8 = 127, wide scale range.
+    rng = np.random.default_rng(7)
+    M, K = 16, 12288
+    scales = (np.exp2(rng.uniform(-10, 0, (M, K // 128))) * 0.5).astype(np.float16)
+    codes = np.full((M, K), 2, np.uint8)
+    x8 = np.full(K, 127, np.int8)
+    _, e16 = bx.fp16_decompose(scales)
+    B = bx.choose_scale_bias(e16)
+    res = bx.matvec_ternary(scales, codes, x8, B, bx.choose_result_shift(scales, B))
+    assert res.dtype == np.int32
+
+
+def test_matvec_ternary_brute_force_small():
+    """Scalar evaluation of the engine rule on tiny shapes (a wrong shift direction or a
+    dropped group fails here)."""
+    rng = np.random.default_rng(11)
+    for _ in range(20):
+        M, G = 3, 2
+        scales = np.exp2(rng.uniform(-16, 2, (M, G))).astype(np.float16) * rng.choice([-1, 1], (M, G)).astype(np.float16)
+        codes = rng.integers(0, 3, (M, 128 * G), dtype=np.uint8)
+        x8 = rng.integers(-127, 128, 128 * G, dtype=np.int8)
+        B, R = 20, 3
+        got = bx.matvec_ternary(scales, codes, x8, B, R)
+        for m in range(M):
+            acc = 0
+            for g in range(G):
+                gs = sum((int(codes[m, 128 * g + j]) - 1) * int(x8[128 * g + j]) for j in range(128))
+                bits = int(scales[m, g].view(np.uint16))
+                E, frac = (bits >> 10) & 31, bits & 1023
+                m11 = (frac + 1024 if E else frac) * (-1 if bits & 0x8000 else 1)
+                e16 = E - 25 if E else -24
+                p = gs * m11
+                acc += p << (e16 + B) if e16 + B >= 0 else p >> -(e16 + B)
+            assert got[m] == acc >> R
+
+
+def test_matvec_ternary_microbench_fixtures(golden):
+    for (M, K) in C.MICROBENCH_SHAPES:
+        r = np.random.default_rng(M * 7919 + K)
+        u = r.random((M, K))
+        codes = np.where(u < 0.3, 0, np.where(u < 0.7, 1, 2)).astype(np.uint8)
+        scales = r.uniform(0.01, 0.05, (M, K // 128)).astype(np.float16)
+        x8 = r.integers(-127, 128, K, dtype=np.int8)
+        g = golden[f"matvec/{M}x{K}"]
+        _, e16 = bx.fp16_decompose(scales)
+        B = bx.choose_scale_bias(e16)
+        R = bx.choose_result_shift(scales, B)
+        assert (B, R) == (g["B"], g["R"])
+        res = bx.matvec_ternary(scales, codes, x8, B, R)
+        assert hashlib.sha256(res.astype("<i4").tobytes()).hexdigest() == g["sha256"]
+        assert res[:8].tolist() == g["head"]
+
+
+def test_matvec_q8_accuracy():
+    rng = np.random.default_rng(3)
+    M, K = 32, 256
+    scales = rng.uniform(0.005, 0.02, (M, K // 32)).astype(np.float16)
+    q8w = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    x8 = rng.integers(-127, 128, K, dtype=np.int8)
+    _, e16 = bx.fp16_decompose(scales)
+    B = bx.choose_scale_bias(e16)
+    R = bx.choose_result_shift(scales, B, gs_max=bx.GS_MAX_Q8)
+    res = bx.matvec_q8(scales, q8w, x8, B, R)
+    ref = ((q8w.astype(np.float64) * x8).reshape(M, -1, 32).sum(2) * scales.astype(np.float64)).sum(1)
+    got = res.astype(np.float64) * np.exp2(-B + R)
+    assert np.max(np.abs(got - ref) / np.maximum(np.abs(ref), 1e-2)) < 1e-3
+
+
+def test_quantize_f_pow2_closed_form():
+    x = np.array([0.5, -0.25, 1e-3, 0.0, -0.5], np.float32)
+    q, e = bx.quantize_f_pow2(x)
+    assert e == -7  # frexp(0.5) = (0.5, 0)
+    assert q.tolist() == [64, -32, 0, 0, -64]
+    q, e = bx.quantize_f_pow2(np.array([1.0, 0.0078125 * 1.5], np.float32))  # ties away from zero
+    assert e == -6 and q.tolist() == [64, 1]
+    assert bx.quantize_f_pow2(np.zeros(4, np.float32))[1] == 0
+
+
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-hybrid", "tiny-ternemb"])
+def test_floatref_matches_fastref_fixture(tiny_images, golden, golden_arrays, name):
+    """Step-wise oracle vs the reference's teacher-forced HybridRef: greedy tokens identical and
+    logits within 1e-4 relative at the stored positions."""
+    r = FloatRef(bons.BONSReader(tiny_images[(name, True)]))
+    prompt = golden[f"prompt/{name}"]
+    want = golden[f"fastref_tokens/{name}"]
+    assert r.generate(prompt, len(want)) == want
+    pos = golden_arrays[f"fastref_logits_pos/{name}"].tolist()
+    ref = golden_arrays[f"fastref_logits/{name}"]
+    r.reset()
+    for i, t in enumerate(prompt + want):
+        lg = r.step(t, want_logits=i in pos)
+        if lg is not None:
+            j = pos.index(i)
+            assert np.abs(lg - ref[j]).max() <= 1e-4 * np.abs(ref[j]).max()
+
+
+def test_floatref_mirror_loop_contract(tiny_images, golden):
+    """The hybrid mirror (exact) and the oracle agree; 2-bit and trit5 images give one model."""
+    a = FloatRef(bons.BONSReader(tiny_images[("tiny-hybrid", True)]))
+    b = FloatRef(bons.BONSReader(tiny_images[("tiny-hybrid", False)]))
+    p = golden["prompt/tiny-hybrid"]
+    assert a.generate(p, 8) == b.generate(p, 8) == golden["mirror_exact_tokens/tiny-hybrid"]
