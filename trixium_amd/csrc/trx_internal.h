@@ -1,0 +1,114 @@
+// Internal helpers shared by the HIP sources of libtrixium_hip (gfx950 / CDNA4 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/trixium.h"
+
+namespace trx {
+
+// Last error, per host thread. Entry points return TRX_E_* and leave a message here.
+void set_error(const char* fmt, ...);
+const char* get_error();
+
+#define TRX_HIP(call)                                                                   \
+  do {                                                                                  \
+    hipError_t e_ = (call);                                                             \
+    if (e_ != hipSuccess) {                                                             \
+      ::trx::set_error("%s:%d: %s failed: %s", __FILE__, __LINE__, #call,               \
+                       hipGetErrorString(e_));                                          \
+      return TRX_E_HIP;                                                                 \
+    }                                                                                   \
+  } while (0)
+
+#define TRX_CHECK(cond, code, ...)                                                      \
+  do {                                                                                  \
+    if (!(cond)) {                                                                      \
+      ::trx::set_error(__VA_ARGS__);                                                    \
+      return (code);                                                                    \
+    }                                                                                   \
+  } while (0)
+
+// Launch check: a launch error is reported by hipGetLastError right after the launch.
+#define TRX_LAUNCHED()                                                                  \
+  do {                                                                                  \
+    hipError_t e_ = hipGetLastError();                                                  \
+    if (e_ != hipSuccess) {                                                             \
+      ::trx::set_error("%s:%d: kernel launch failed: %s", __FILE__, __LINE__,           \
+                       hipGetErrorString(e_));                                          \
+      return TRX_E_HIP;                                                                 \
+    }                                                                                   \
+  } while (0)
+
+constexpr int kBeat = 32;
+constexpr int kGroup = 128;
+constexpr int kTrit5GroupBytes = 26;
+constexpr uint32_t kRsrcWord3 = 0x00020000u;  // gfx9-family raw buffer resource
+
+// Geometry of a row-packet tensor (rows back to back, one channel).
+struct RowGeom {
+  int K;          // columns
+  int G;          // 128-groups per row
+  int row_bytes;  // bytes per row packet
+  int code_off;   // bytes of fp16 scales before the codes (whole beats)
+};
+
+inline int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+inline RowGeom row_geom(int kind, int K) {
+  RowGeom g;
+  g.K = K;
+  g.G = K / kGroup;
+  g.code_off = kBeat * cdiv(g.G, 16);
+  int code_bytes = (kind == TRX_KIND_TERNARY5) ? kBeat * cdiv(kTrit5GroupBytes * g.G, kBeat)
+                                                : kBeat * g.G;
+  g.row_bytes = g.code_off + code_bytes;
+  return g;
+}
+
+// Device helpers ------------------------------------------------------------------------------
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           (int)kRsrcWord3);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Block-wide sum; `red` is >= 16 floats of shared memory. All threads get the result.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float t = 0.f;
+  for (int i = 0; i < nw; ++i) t += red[i];
+  return t;
+}
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+// Exact fp16 -> (m11, e16): value = m11 * 2^e16.
+__device__ __forceinline__ void fp16_split(uint16_t bits, int& m11, int& e16) {
+  int E = (bits >> 10) & 0x1F, frac = bits & 0x3FF;
+  int mag = E ? (frac | 0x400) : frac;
+  m11 = (bits & 0x8000) ? -mag : mag;
+  e16 = E ? E - 25 : -24;
+}
+
+}  // namespace trx
