@@ -85,6 +85,99 @@ int trx_gemv_ternary_f32(const uint8_t* rows, int kind, int M, int K, const floa
                          const float* norm_w, float eps, float* y, int epilogue,
                          const float* resid, trx_stream_t s);
 
+/* Decoder ----------------------------------------------------------------------------------------
+ * A batch-1 greedy decoder over a BONS model held on the GPU: the GPU counterpart of
+ * model/golden.py:FloatModel (reset/forward/generate, golden.py:304-320,436-470) with the
+ * arithmetic of model/fastref.py:HybridRef (fastref.py:143-273), and of the firmware loop
+ * firmware/infer.c:2001 infer_generate (one position per forward, argmax on the device). */
+
+/* Tensor roles (model/layout.py:95-115). */
+#define TRX_ROLE_TOK_EMB 0
+#define TRX_ROLE_OUT_NORM 1
+#define TRX_ROLE_LM_HEAD 2
+#define TRX_ROLE_ATTN_NORM 3
+#define TRX_ROLE_ATTN_Q 4
+#define TRX_ROLE_ATTN_K 5
+#define TRX_ROLE_ATTN_V 6
+#define TRX_ROLE_ATTN_OUT 7
+#define TRX_ROLE_ATTN_Q_NORM 8
+#define TRX_ROLE_ATTN_K_NORM 9
+#define TRX_ROLE_FFN_NORM 10
+#define TRX_ROLE_FFN_GATE 11
+#define TRX_ROLE_FFN_UP 12
+#define TRX_ROLE_FFN_DOWN 13
+#define TRX_ROLE_TOK_EMB16 15
+#define TRX_ROLE_TOK_EMB16_EXP 16
+#define TRX_ROLE_ATTN_QKV 17
+#define TRX_ROLE_ATTN_ZGATE 18
+#define TRX_ROLE_SSM_OUT 19
+#define TRX_ROLE_SSM_BETA 20
+#define TRX_ROLE_SSM_ALPHA 21
+#define TRX_ROLE_SSM_CONV 22
+#define TRX_ROLE_SSM_A 23
+#define TRX_ROLE_SSM_DT 24
+#define TRX_ROLE_SSM_NORM 25
+
+typedef struct {
+  int n_layer, n_embd, n_head, n_kv_head, head_dim, ffn_dim, vocab, max_ctx;
+  float rms_eps;
+  int rope_dims;               /* rotated dims per head, 0 = head_dim */
+  int attn_gated;              /* q projection carries [q | gate] per head */
+  int dn_num_v_heads, dn_num_k_heads, dn_k_head_dim, dn_v_head_dim, dn_conv_kernel;
+  uint64_t layer_types[2];     /* bit l set: layer l is Gated DeltaNet */
+  int weight_kind;             /* kind of every layer matrix: TRX_KIND_TERNARY5 or _TERNARY */
+  int head_kind;               /* untied LM head: a ternary kind or TRX_KIND_F16 */
+  int head_tied;               /* the LM head is the ternary token embedding */
+  int emb_mode;                /* 0: int16 BFP lookup table; 1: ternary token_embd rows */
+  int emb_kind;                /* kind of token_embd rows (emb_mode 1 or a tied head) */
+  int max_new;                 /* capacity of the generated-token buffer */
+} trx_model_config;
+
+typedef struct trx_model trx_model;
+
+/* rope_freq: rope_dims/2 float32 frequencies theta^(-2i/rope_dims) (fastref.py:62-63). */
+int trx_model_create(const trx_model_config* cfg, const float* rope_freq, trx_model** out);
+int trx_model_destroy(trx_model* m);
+/* Upload one tensor (synchronous). Ternary and Q8: BONS row packets of the model's kind; F32:
+ * float32 values; F16 head: fp16 values; TOK_EMB16: int16 [vocab, n_embd]; TOK_EMB16_EXP: int32
+ * [vocab]. The fused groups (q|k|v, gate|up, qkv|z, beta|alpha) are laid out adjacent. */
+int trx_model_set_tensor(trx_model* m, int role, int layer, const void* data, size_t bytes);
+/* Fill every tensor from the counter-based generator (trixium_amd/synth.py's hash). ranges:
+ * float32 {scale_lo, scale_span, gain_lo, gain_span}. */
+int trx_model_synthesize(trx_model* m, uint32_t seed, const float* ranges);
+/* Clear the position, the argmax slot and the DeltaNet state (golden.py:304-320). */
+int trx_model_reset(trx_model* m);
+/* Feed tokens at the next n positions (after the forwards already enqueued); logits are computed
+ * from absolute position head_from on (-1: the last fed token). */
+int trx_model_set_prompt(trx_model* m, const int32_t* tokens, int n, int head_from);
+/* Enqueue n forwards of one position each (eagerly, or as replays of one captured hipGraph). */
+int trx_model_step(trx_model* m, int n_steps, int use_graph);
+/* Resolve the argmax of the last forward into the output buffer. */
+int trx_model_finalize(trx_model* m);
+int trx_model_sync(trx_model* m);
+/* Greedy decode: n_prompt + n_new - 1 forwards, then the generated ids (FloatModel.generate,
+ * golden.py:462-470, with the firmware's no-final-forward contract, mirror.py:1040-1043). */
+int trx_model_generate(trx_model* m, const int32_t* prompt, int n_prompt, int n_new, int32_t* out,
+                       int use_graph);
+#define TRX_READ_LOGITS 0      /* float32 [vocab] of the last forward that ran the head */
+#define TRX_READ_HIDDEN 1      /* float32 [n_embd]: residual stream after the last layer */
+#define TRX_READ_POSITION 2    /* int32 */
+#define TRX_READ_TOKEN 3       /* int32: the token of the last forward */
+#define TRX_READ_OUT 4         /* int32 [max_new]: generated tokens */
+#define TRX_READ_SLOT 5        /* uint64: packed argmax */
+int trx_model_read(trx_model* m, int what, void* host, size_t bytes);
+#define TRX_INFO_ARENA_BYTES 0
+#define TRX_INFO_DEVICE_BYTES 1
+#define TRX_INFO_STREAM 2
+#define TRX_INFO_WEIGHT_BYTES 3
+int trx_model_info(trx_model* m, int what, int64_t* value);
+/* Device address and size of one resident tensor (for benchmarks and tests). */
+int trx_model_tensor_ptr(trx_model* m, int role, int layer, void** ptr, int64_t* bytes);
+
+/* Tuning: force a GEMV launch variant (0 = automatic; 1..5 fixed rows-per-item/block-size
+ * pairs). Process-wide; for benchmarks and tests. No counterpart in the reference. */
+int trx_gemv_set_variant(int variant);
+
 #ifdef __cplusplus
 }
 #endif

@@ -5,6 +5,8 @@ import ctypes
 import os
 import re
 
+import numpy as np
+
 from trixium_amd import _lib
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -39,3 +41,17 @@ def test_errors_are_reported_without_a_device_call():
     assert b"null" in L.trx_last_error()
     rc = L.trx_gemv_ternary_f32(ctypes.c_void_p(16), 7, 4, 256, None, None, 1e-6, None, 0, None, None)
     assert rc == _lib.TRX_E_INVALID
+
+
+def test_decoder_config_from_images(tiny_images):
+    """The decoder's trx_model_config derived from the fixture images (host logic only)."""
+    from trixium_amd import bons, layout as L
+    from trixium_amd.model import config_from_header, make_config, rope_frequencies
+    img = bons.BONSReader(tiny_images[("tiny-hybrid", True)])
+    mc = config_from_header(img.header)
+    c = make_config(mc, L.KIND_TERNARY5, L.KIND_F16, False, 0, L.KIND_TERNARY5, max_new=8)
+    assert (c.n_layer, c.n_embd, c.vocab, c.max_ctx) == (4, 256, 1024, img.header["max_ctx"])
+    assert c.layer_types[0] == 0b0111 and c.layer_types[1] == 0
+    assert c.attn_gated == 1 and c.rope_dims == 16 and c.dn_num_v_heads == 8
+    f = rope_frequencies(mc.rope_theta, 16)
+    assert f.dtype == np.float32 and f[0] == 1.0 and np.all(np.diff(f) < 0)

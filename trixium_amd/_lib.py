@@ -19,6 +19,22 @@ EPI_STORE, EPI_RESID, EPI_SWIGLU = 0, 1, 2
 _vp, _i, _u64, _f, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_uint64, ctypes.c_float, ctypes.c_size_t
 _ip = ctypes.POINTER(ctypes.c_int)
 _fp = ctypes.POINTER(ctypes.c_float)
+_i64p = ctypes.POINTER(ctypes.c_int64)
+
+
+class ModelConfig(ctypes.Structure):
+    """trx_model_config of include/trixium.h."""
+    _fields_ = [(n, ctypes.c_int) for n in ("n_layer", "n_embd", "n_head", "n_kv_head", "head_dim",
+                                            "ffn_dim", "vocab", "max_ctx")] + [
+        ("rms_eps", ctypes.c_float), ("rope_dims", ctypes.c_int), ("attn_gated", ctypes.c_int)] + [
+        (n, ctypes.c_int) for n in ("dn_num_v_heads", "dn_num_k_heads", "dn_k_head_dim",
+                                    "dn_v_head_dim", "dn_conv_kernel")] + [
+        ("layer_types", ctypes.c_uint64 * 2)] + [
+        (n, ctypes.c_int) for n in ("weight_kind", "head_kind", "head_tied", "emb_mode", "emb_kind",
+                                    "max_new")]
+
+
+_mcp = ctypes.POINTER(ModelConfig)
 
 # name -> argtypes (restype is int unless listed in _RESTYPES)
 SIGNATURES = {
@@ -43,6 +59,20 @@ SIGNATURES = {
     "trx_gemv_ternary_exact": [_vp, _i, _i, _i, _vp, _i, _i, _vp, _vp, _vp],
     "trx_gemv_ternary_groupsums": [_vp, _i, _i, _i, _vp, _vp, _vp],
     "trx_gemv_ternary_f32": [_vp, _i, _i, _i, _vp, _vp, _f, _vp, _i, _vp, _vp],
+    "trx_gemv_set_variant": [_i],
+    "trx_model_create": [_mcp, _fp, ctypes.POINTER(_vp)],
+    "trx_model_destroy": [_vp],
+    "trx_model_set_tensor": [_vp, _i, _i, _vp, _sz],
+    "trx_model_synthesize": [_vp, ctypes.c_uint32, _fp],
+    "trx_model_reset": [_vp],
+    "trx_model_set_prompt": [_vp, _ip, _i, _i],
+    "trx_model_step": [_vp, _i, _i],
+    "trx_model_finalize": [_vp],
+    "trx_model_sync": [_vp],
+    "trx_model_generate": [_vp, _ip, _i, _i, _ip, _i],
+    "trx_model_read": [_vp, _i, _vp, _sz],
+    "trx_model_info": [_vp, _i, _i64p],
+    "trx_model_tensor_ptr": [_vp, _i, _i, ctypes.POINTER(_vp), _i64p],
 }
 _RESTYPES = {"trx_last_error": ctypes.c_char_p}
 

@@ -22,11 +22,12 @@ const char* get_error() { return g_err; }
 
 int gemv_f32(const uint8_t* rows, int kind, int M, int K, const float* x, const float* norm_w,
              float eps, float* y, int epi, const float* resid, int swiglu_F,
-             unsigned long long* amax_slot, hipStream_t s);
+             unsigned long long* amax_slot, hipStream_t s, const int* gate_pos, const int* gate_from);
 int gemv_exact(const uint8_t* rows, int kind, int M, int K, const int8_t* x8, int B, int R,
                int32_t* y, int32_t* status, hipStream_t s);
 int gemv_groupsums(const uint8_t* rows, int kind, int M, int K, const int8_t* x8, int32_t* gs,
                    hipStream_t s);
+int gemv_set_variant(int v);
 
 }  // namespace trx
 
@@ -162,5 +163,7 @@ TRX_API int trx_gemv_ternary_f32(const uint8_t* rows, int kind, int M, int K, co
   TRX_CHECK(epilogue == TRX_EPI_STORE || epilogue == TRX_EPI_RESID || epilogue == TRX_EPI_SWIGLU,
             TRX_E_INVALID, "trx_gemv_ternary_f32: unknown epilogue %d", epilogue);
   return gemv_f32(rows, kind, M, K, x, norm_w, eps, y, epilogue, resid,
-                  epilogue == TRX_EPI_SWIGLU ? M / 2 : 0, nullptr, (hipStream_t)s);
+                  epilogue == TRX_EPI_SWIGLU ? M / 2 : 0, nullptr, (hipStream_t)s, nullptr, nullptr);
 }
+
+TRX_API int trx_gemv_set_variant(int variant) { return gemv_set_variant(variant); }

@@ -8,18 +8,20 @@
 //   exact mode:  x is the caller's int8 vector; y[m] = (sum_g (S*m11) << (e16+B)) >> R  (int32)
 //   group sums:  gs[m,g] = S[m,g]
 //
-// Mapping. A lane owns one 128-group at a time; LPR lanes (power of two dividing G, <= 64)
-// cover LPR groups of R rows, and step through the G/LPR group slots of those rows. The x
-// values of a group are held in 65 registers in a "dot-ready" form built once per block in
-// LDS, and reused across the R rows. No MFMA: the path is a bandwidth-bound GEMV.
+// Mapping. A lane owns one half-group (64 columns: 13 trit5 code bytes, or 16 2-bit code bytes)
+// at a time; LPR lanes (power of two dividing the 2G half-groups, <= 64) cover LPR half-groups of
+// R rows (an "item"), and step through the 2G/LPR slots of those rows. The x values of a
+// half-group are held in 33 registers in a "dot-ready" form built once per block in LDS, and
+// reused across the R rows. The codes of the next item are loaded while the current one is
+// computed. No MFMA: the path is a bandwidth-bound GEMV.
 //
-// Decode. trit5: every code byte b is looked up in an LDS table giving its five base-3 digits
-// as four byte lanes (d0..d3, fed to v_dot4 against the int8 planes of x) plus d4 (fed to
-// v_dot2 against int16 x). 2-bit: every code byte gives its four 2-bit codes as byte lanes.
-// The table is replicated so that the 64 lanes of a wave hit distinct LDS banks; the entry
-// address (b << 8 | lane copy) is formed by one v_perm_b32. Since sum (code-1)x =
-// sum code*x - sum x, codes are used as unsigned digits and the group's sum of x is
-// subtracted once per row.
+// Decode. trit5: every code byte b is looked up in an LDS table giving its base-3 digits d0..d3
+// as byte lanes (fed to v_dot4 against the int8 planes of x) and d4 (two bytes' d4 are paired by
+// one v_perm and fed to v_dot2 against int16 x). 2-bit: every code byte gives its four 2-bit
+// codes as byte lanes. The table is replicated 32x (64x for the 4-byte 2-bit entries) so the
+// lanes of a wave hit distinct LDS banks; the entry address (b << 8 | lane copy) is formed by one
+// v_perm_b32. Since sum (code-1)x = sum code*x - sum x, codes are used as unsigned digits and
+// the half-group's sum of x is subtracted once per row.
 
 #include "trx_internal.h"
 
@@ -27,15 +29,14 @@ namespace trx {
 
 enum { MODE_F32 = 0, MODE_EXACT = 1, MODE_GSUM = 2 };
 
-constexpr int kThreads = 512;
 constexpr int kLutBytes = 65536;    // 256 entries x 256 bytes
-constexpr int kXStride = 68;        // dwords per group in the dot-ready layout (65 used)
-constexpr int kXDwords5 = 65;       // trit5: 26 x (hi, lo) + 13 d4 pairs
-constexpr int kXDwords2 = 64;       // 2-bit: 32 x (hi, lo)
+constexpr int kXStride = 36;        // dwords per half-group in the dot-ready layout
+constexpr int kXDwords5 = 33;       // trit5: 13 x (hi, lo) + 7 d4 pairs
+constexpr int kXDwords2 = 32;       // 2-bit: 16 x (hi, lo)
 
 struct GemvParams {
   const uint8_t* W;
-  uint32_t w_bytes;       // bytes addressable from W (bounds of the buffer loads)
+  uint32_t w_bytes;       // bytes addressable from W (tensor + 32-byte tail)
   int M;                  // physical rows
   int K, G, row_bytes, code_off;
   int LPR, NSLOT;
@@ -53,22 +54,31 @@ struct GemvParams {
   int B, R;
   int32_t* status;
   unsigned long long* amax_slot;  // argmax epilogue: packed (ordered value, ~index)
+  const int* gate_pos;    // when set: the kernel does nothing while *gate_pos < *gate_from
+  const int* gate_from;
 };
 
-__device__ __forceinline__ uint32_t trit5_entry_lo(int b) {
-  uint32_t v = 0;
-  for (int k = 0; k < 4; ++k) { v |= (uint32_t)(b % 3) << (8 * k); b /= 3; }
-  return v;
+// Decode tables, computed at compile time: trit5 byte -> (d0 | d1<<8 | d2<<16 | d3<<24, d4),
+// 2-bit byte -> (c0 | c1<<8 | c2<<16 | c3<<24). Every byte value decodes as
+// digit k = floor(b / 3^k) mod 3 (the numpy decode of the reference, model/bons.py:125-130).
+struct DecodeTables {
+  uint32_t t5lo[256], t5hi[256], c2[256];
+};
+constexpr DecodeTables make_tables() {
+  DecodeTables t{};
+  for (int b = 0; b < 256; ++b) {
+    int v = b;
+    uint32_t lo = 0;
+    for (int k = 0; k < 4; ++k) { lo |= (uint32_t)(v % 3) << (8 * k); v /= 3; }
+    t.t5lo[b] = lo;
+    t.t5hi[b] = (uint32_t)(v % 3);
+    uint32_t c = 0;
+    for (int k = 0; k < 4; ++k) c |= (uint32_t)((b >> (2 * k)) & 3) << (8 * k);
+    t.c2[b] = c;
+  }
+  return t;
 }
-__device__ __forceinline__ uint32_t trit5_entry_hi(int b) {
-  for (int k = 0; k < 4; ++k) b /= 3;
-  return (uint32_t)(b % 3);
-}
-__device__ __forceinline__ uint32_t code2_entry(int b) {
-  uint32_t v = 0;
-  for (int k = 0; k < 4; ++k) v |= (uint32_t)((b >> (2 * k)) & 3) << (8 * k);
-  return v;
-}
+__constant__ const DecodeTables kTables = make_tables();
 
 // Float -> ordered unsigned (monotonic), for the packed argmax.
 __device__ __forceinline__ uint32_t ordered_bits(float f) {
@@ -76,42 +86,100 @@ __device__ __forceinline__ uint32_t ordered_bits(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-template <int FMT, int MODE, int R>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams p) {
+typedef short s2_t __attribute__((ext_vector_type(2)));
+
+template <int FMT, int R>
+struct ItemBuf {
+  uint32_t cd[R][4];
+  uint32_t sc[R];
+};
+
+template <int FMT, int MODE, int R, int NT>
+__global__ __launch_bounds__(NT) void gemv_kernel(GemvParams p) {
+  constexpr int kThreads = NT;
+  constexpr int kWaves = NT / 64;
+  constexpr bool T5 = (FMT == TRX_KIND_TERNARY5);
+  constexpr int NPL = (MODE == MODE_F32) ? 2 : 1;              // int8 planes of x
+  // First column of the second half-group of a group (trit5 bytes 13..25 start at column 65).
+  constexpr int kHalfCol = T5 ? 65 : 64;
   // The decode table is static LDS (its base folds into the ds_read offsets); the x layout and
   // staging buffers are dynamic LDS sized by K.
   __shared__ __align__(16) uint64_t lut64[kLutBytes / 8];
   extern __shared__ __align__(16) uint8_t smem[];
-  uint8_t* lut = (uint8_t*)lut64;
-  uint32_t* xl = (uint32_t*)smem;                              // G * kXStride dwords
-  int16_t* stage = (int16_t*)(xl + p.G * kXStride);            // K int16
+  if (p.gate_pos && *p.gate_pos < *p.gate_from) return;        // uniform over the grid
+  const uint8_t* lut = (const uint8_t*)lut64;
+  uint32_t* xl = (uint32_t*)smem;                              // 2G * kXStride dwords
+  int16_t* stage = (int16_t*)(xl + 2 * p.G * kXStride);        // K int16
   float* gsig = (float*)(stage + p.K);                         // G: sigma_g
-  int32_t* gsum = (int32_t*)(gsig + p.G);                      // G: sum of q over the group
-  float* red = (float*)(gsum + p.G);                           // 16
+  int32_t* usum = (int32_t*)(gsig + p.G);                      // 2G: sum of q over a half-group
+  float* red = (float*)(usum + 2 * p.G);                       // 16
 
   const int tid = threadIdx.x;
-  constexpr bool T5 = (FMT == TRX_KIND_TERNARY5);
-  constexpr int NPL = (MODE == MODE_F32) ? 2 : 1;              // int8 planes of x
+  const int lane = tid & 63, wave = tid >> 6;
+  const int LPR = p.LPR;
+  const int rg = lane / LPR, lg = lane - rg * LPR;
+  const int RG = 64 / LPR;
+  const int first = (blockIdx.x * kWaves + wave) * RG + rg;
+  const int stride = gridDim.x * kWaves * RG;
+  const int NSLOT = p.NSLOT;
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.W, p.w_bytes);
+  // v_perm sources: byte 0 of the address comes from the lane-copy word (selector 0), byte 1
+  // from code byte k of the code word (selector 4 + k), bytes 2..3 are zero (selector 0x0c).
+  const uint32_t lcopy = T5 ? (uint32_t)((lane & 31) << 3) : (uint32_t)(lane << 2);
+  const bool swiglu = (p.epi == TRX_EPI_SWIGLU);
+  // Rows of batch bt: plain, bt*R + r; SwiGLU, gate rows bt*R/2 + r and up rows F + bt*R/2 + r.
+  const int rows_per_batch = swiglu ? R / 2 : R;
+  const uint32_t rb = (uint32_t)p.row_bytes;
+  const uint32_t up_off = swiglu ? (uint32_t)p.swiglu_F * rb : 0u;
 
-  // Decode table: 256 entries at a 256-byte stride, lane copies inside an entry.
-  if (T5) {
-    uint64_t* l64 = (uint64_t*)lut;
-    // Copies 0..15 carry d4 in the low half of the high word (even code bytes), copies
-    // 16..31 in the high half (odd code bytes), matching the d4 pairs of the x layout.
-    for (int i = tid; i < 256 * 32; i += kThreads) {
-      int b = i >> 5;
-      uint32_t hi = trit5_entry_hi(b) << ((i & 16) ? 16 : 0);
-      l64[i] = (uint64_t)trit5_entry_lo(b) | ((uint64_t)hi << 32);
+  auto out_index = [&](int bt, int r) -> int { return bt * rows_per_batch + (swiglu ? (r % (R > 1 ? R / 2 : 1)) : r); };
+  auto row_offset = [&](int bt, int r) -> uint32_t {
+    const int o = out_index(bt, r);
+    if (o >= p.n_out) return p.w_bytes;                          // out of range: loads read 0
+    const uint32_t base = (uint32_t)(bt * rows_per_batch) * rb;
+    if (!swiglu) return base + (uint32_t)r * rb;
+    return (r < R / 2) ? base + (uint32_t)r * rb : base + up_off + (uint32_t)(r - R / 2) * rb;
+  };
+  // Byte offset of half-group u inside a row's code area.
+  auto unit_off = [&](int u) -> uint32_t {
+    return T5 ? (uint32_t)(kTrit5GroupBytes * (u >> 1) + 13 * (u & 1)) : (uint32_t)(16 * u);
+  };
+  auto load_item = [&](ItemBuf<FMT, R>& b, int bt, int sl) {
+    const int u = sl * LPR + lg;
+    const uint32_t uoff = p.code_off + unit_off(u);
+    const uint32_t soff = 2u * (uint32_t)(u >> 1);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint32_t ro = row_offset(bt, r);
+      // trit5: the 16 bytes at the half-group's own (unaligned) offset; the last 3 may be the
+      // next half-group's or the row padding (the tensor has a 32-byte tail).
+      auto a = __builtin_amdgcn_raw_buffer_load_b128(rs, ro + uoff, 0, 0);
+      b.cd[r][0] = a[0]; b.cd[r][1] = a[1]; b.cd[r][2] = a[2]; b.cd[r][3] = a[3];
+      b.sc[r] = __builtin_amdgcn_raw_buffer_load_b16(rs, ro + soff, 0, 0);
     }
-  } else {
-    uint32_t* l32 = (uint32_t*)lut;
-    for (int i = tid; i < 256 * 64; i += kThreads) l32[i] = code2_entry(i >> 6);
+  };
+
+  // The first item's codes do not depend on x: fetch them before the prologue.
+  ItemBuf<FMT, R> bufA, bufB;
+  if (first < p.n_batches) load_item(bufA, first, 0);
+
+  // Decode table replicated into LDS: 4096 chunks of 16 bytes, 16 chunks per entry.
+  {
+    uint4* l = (uint4*)lut64;
+    for (int i = tid; i < kLutBytes / 16; i += kThreads) {
+      int b = i >> 4;
+      uint4 v;
+      if (T5) { v.x = kTables.t5lo[b]; v.y = kTables.t5hi[b]; v.z = v.x; v.w = v.y; }
+      else { v.x = v.y = v.z = v.w = kTables.c2[b]; }
+      l[i] = v;
+    }
   }
 
-  // x -> int16 per group (float mode) or int8 copy (exact modes), staged in LDS.
-  if (MODE == MODE_F32) {
+  // x -> int16 per group (float mode, sigma_g = amax/32767) or the int8 vector itself (exact
+  // modes), staged in LDS, with the sum of the staged values over every half-group.
+  {
     float rinv = 1.0f;
-    if (p.norm_w) {
+    if (MODE == MODE_F32 && p.norm_w) {
       float ss = 0.f;
       for (int c = tid * 4; c < p.K; c += kThreads * 4) {
         float4 v = *(const float4*)(p.x + c);
@@ -120,31 +188,44 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams p) {
       ss = block_sum(ss, red);
       rinv = 1.0f / sqrtf(ss / (float)p.K + p.eps);
     }
-    // 16 threads per group, 8 columns each.
-    for (int c0 = tid * 8; c0 < ((p.K + kThreads * 8 - 1) / (kThreads * 8)) * kThreads * 8; c0 += kThreads * 8) {
-      bool live = c0 < p.K;
-      float v[8];
+    // 16 threads per group, 8 columns each; every thread runs the same number of rounds.
+    const int rounds = (p.K + kThreads * 8 - 1) / (kThreads * 8);
+    for (int rd = 0; rd < rounds; ++rd) {
+      const int c0 = (rd * kThreads + tid) * 8;
+      const bool live = c0 < p.K;
+      int q[8] = {0, 0, 0, 0, 0, 0, 0, 0};
       float am = 0.f;
-      if (live) {
-        float4 a = *(const float4*)(p.x + c0), b = *(const float4*)(p.x + c0 + 4);
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-        if (p.norm_w) {
-          float4 wa = *(const float4*)(p.norm_w + c0), wb = *(const float4*)(p.norm_w + c0 + 4);
-          float w[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+      if (MODE == MODE_F32) {
+        float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (live) {
+          float4 a = *(const float4*)(p.x + c0), b = *(const float4*)(p.x + c0 + 4);
+          v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+          if (p.norm_w) {
+            float4 wa = *(const float4*)(p.norm_w + c0), wb = *(const float4*)(p.norm_w + c0 + 4);
+            float w[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
 #pragma unroll
-          for (int k = 0; k < 8; ++k) v[k] = v[k] * rinv * w[k];
+            for (int k = 0; k < 8; ++k) v[k] = v[k] * rinv * w[k];
+          }
+#pragma unroll
+          for (int k = 0; k < 8; ++k) am = fmaxf(am, fabsf(v[k]));
         }
 #pragma unroll
-        for (int k = 0; k < 8; ++k) am = fmaxf(am, fabsf(v[k]));
+        for (int o = 8; o >= 1; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+        const float inv = am > 0.f ? 32767.0f / am : 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) q[k] = (int)rintf(v[k] * inv);
+      } else if (live) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) q[k] = p.x8[c0 + k];
       }
+      int s0 = 0, s1 = 0;
+      const int lc = c0 & (kGroup - 1);
 #pragma unroll
-      for (int o = 8; o >= 1; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
-      float inv = am > 0.f ? 32767.0f / am : 0.f;
-      int s = 0;
+      for (int k = 0; k < 8; ++k) {
+        if (lc + k < kHalfCol) s0 += q[k];
+        else s1 += q[k];
+      }
       if (live) {
-        int q[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) { q[k] = (int)rintf(v[k] * inv); s += q[k]; }
         uint4 pk;
         pk.x = (uint32_t)(uint16_t)q[0] | ((uint32_t)(uint16_t)q[1] << 16);
         pk.y = (uint32_t)(uint16_t)q[2] | ((uint32_t)(uint16_t)q[3] << 16);
@@ -153,230 +234,251 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams p) {
         *(uint4*)(stage + c0) = pk;
       }
 #pragma unroll
-      for (int o = 8; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+      for (int o = 8; o >= 1; o >>= 1) {
+        s0 += __shfl_xor(s0, o, 64);
+        s1 += __shfl_xor(s1, o, 64);
+      }
       if (live && (tid & 15) == 0) {
         gsig[c0 >> 7] = am / 32767.0f;
-        gsum[c0 >> 7] = s;
+        usum[2 * (c0 >> 7)] = s0;
+        usum[2 * (c0 >> 7) + 1] = s1;
       }
-    }
-  } else {
-    for (int c = tid; c < p.K; c += kThreads) stage[c] = (int16_t)p.x8[c];
-    __syncthreads();
-    for (int g = tid; g < p.G; g += kThreads) {
-      int s = 0;
-      for (int j = 0; j < kGroup; ++j) s += stage[g * kGroup + j];
-      gsum[g] = s;
     }
   }
   __syncthreads();
 
-  // Dot-ready layout of every group.
+  // Dot-ready layout of every half-group u = 2g + h.
   {
     const int per = T5 ? kXDwords5 : kXDwords2;
-    for (int i = tid; i < p.G * per; i += kThreads) {
-      int g = i / per, j = i - g * per;
-      const int16_t* xs = stage + g * kGroup;
+    for (int i = tid; i < 2 * p.G * per; i += kThreads) {
+      const int u = i / per, j = i - u * per;
+      const int16_t* xs = stage + (u >> 1) * kGroup;
+      const int h = u & 1;
       uint32_t v = 0;
-      if (j < (T5 ? 52 : 64)) {
-        int byte = j >> 1, plane = j & 1;
-        int c0 = T5 ? 5 * byte : 4 * byte;
+      if (j < (T5 ? 26 : 32)) {
+        const int byte = (T5 ? 13 : 16) * h + (j >> 1), plane = j & 1;
+        const int c0 = T5 ? 5 * byte : 4 * byte;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          int c = c0 + k;
-          int q = (c < kGroup) ? xs[c] : 0;
-          uint32_t b8 = (NPL == 2) ? (plane == 0 ? (uint32_t)((q >> 8) & 0xFF) : (uint32_t)(q & 0xFF))
-                                   : (plane == 0 ? (uint32_t)(q & 0xFF) : 0u);
+          const int c = c0 + k;
+          const int q = (c < kGroup) ? xs[c] : 0;
+          const uint32_t b8 = (NPL == 2) ? (plane == 0 ? (uint32_t)((q >> 8) & 0xFF) : (uint32_t)(q & 0xFF))
+                                         : (plane == 0 ? (uint32_t)(q & 0xFF) : 0u);
           v |= b8 << (8 * k);
         }
       } else {
-        int pr = j - 52;
-        int ca = 5 * (2 * pr) + 4, cb = 5 * (2 * pr + 1) + 4;
-        int qa = ca < kGroup ? xs[ca] : 0, qb = cb < kGroup ? xs[cb] : 0;
+        // d4 pair: unit bytes 2pr and 2pr+1 (the 13th byte has no partner).
+        const int pr = j - 26;
+        const int ba = 13 * h + 2 * pr, bb = ba + 1;
+        const int ca = 5 * ba + 4, cb = 5 * bb + 4;
+        const int qa = ca < kGroup ? xs[ca] : 0;
+        const int qb = (2 * pr + 1 < 13 && cb < kGroup) ? xs[cb] : 0;
         v = (uint32_t)(uint16_t)qa | ((uint32_t)(uint16_t)qb << 16);
       }
-      xl[g * kXStride + j] = v;
+      xl[u * kXStride + j] = v;
     }
   }
   __syncthreads();
 
-  // Main loop.
-  const int lane = tid & 63, wave = tid >> 6;
-  const int LPR = p.LPR;
-  const int rg = lane / LPR, lg = lane - rg * LPR;
-  const int RG = 64 / LPR;
-  const int slot = (blockIdx.x * (kThreads / 64) + wave) * RG + rg;
-  const int nslots = gridDim.x * (kThreads / 64) * RG;
-  const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.W, p.w_bytes);
-  // v_perm sources: byte 0 of the result comes from the lane-copy word (selector 0), byte 1
-  // from code byte k of the code word (selector 4 + k), bytes 2..3 are zero (selector 0x0c).
-  const uint32_t lc_even = T5 ? (uint32_t)((lane & 15) << 3) : (uint32_t)(lane << 2);
-  const uint32_t lc_odd = T5 ? (uint32_t)(((lane & 15) | 16) << 3) : lc_even;
+  uint32_t xr[T5 ? kXDwords5 : kXDwords2];
+  auto load_x = [&](int sl) {
+    const int u = sl * LPR + lg;
+    const uint4* src = (const uint4*)(xl + u * kXStride);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      uint4 t = src[i];
+      xr[4 * i] = t.x; xr[4 * i + 1] = t.y; xr[4 * i + 2] = t.z; xr[4 * i + 3] = t.w;
+    }
+    if (T5) xr[32] = xl[u * kXStride + 32];
+  };
 
-  for (int bt = slot; bt < p.n_batches; bt += nslots) {
-    int prow[R];
-    bool pok[R];
+  float facc[R];
+  long long iacc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) { facc[r] = 0.f; iacc[r] = 0; }
+
+  auto compute_item = [&](const ItemBuf<FMT, R>& b, int bt, int sl) {
+    const int u = sl * LPR + lg;
+    const float sig = (MODE == MODE_F32) ? gsig[u >> 1] : 0.f;
+    const int usx = usum[u];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      int lr = bt * R + r;
-      if (p.epi == TRX_EPI_SWIGLU) {
-        int half = R / 2;
-        int o = bt * half + (r % half);
-        pok[r] = o < p.n_out;
-        prow[r] = (r < half) ? o : p.swiglu_F + o;
-      } else {
-        pok[r] = lr < p.n_out;
-        prow[r] = lr;
-      }
-    }
-    float facc[R];
-    long long iacc[R];
+      int accH = 0, acc4 = 0;
+      unsigned accL = 0;
+      if (T5) {
+        uint32_t d4prev = 0;
 #pragma unroll
-    for (int r = 0; r < R; ++r) { facc[r] = 0.f; iacc[r] = 0; }
-
-    for (int sl = 0; sl < p.NSLOT; ++sl) {
-      const int g = sl * LPR + lg;
-      // x registers for group g.
-      uint32_t xr[T5 ? kXDwords5 : kXDwords2];
-      {
-        const uint4* src = (const uint4*)(xl + g * kXStride);
+        for (int i = 0; i < 13; ++i) {
+          const uint32_t sel = 0x0c0c0400u | ((uint32_t)(i & 3) << 8);
+          const uint32_t addr = __builtin_amdgcn_perm(b.cd[r][i >> 2], lcopy, sel);
+          const uint64_t e64 = *(const uint64_t*)__builtin_assume_aligned(lut + addr, 8);
+          const uint32_t elo = (uint32_t)e64, ehi = (uint32_t)(e64 >> 32);
+          accH = __builtin_amdgcn_sdot4((int)elo, (int)xr[2 * i], accH, false);
+          if (NPL == 2) accL = __builtin_amdgcn_udot4(elo, xr[2 * i + 1], accL, false);
+          if ((i & 1) || i == 12) {
+            // [d4 of byte i-1, d4 of byte i] (or [d4 of byte 12, 0]) as int16 halves, against
+            // the x pair of the two bytes.
+            const uint32_t pair = (i & 1) ? __builtin_amdgcn_perm(ehi, d4prev, 0x0c040c00u) : ehi;
+            acc4 = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2_t, pair),
+                                          __builtin_bit_cast(s2_t, xr[26 + (i >> 1)]), acc4, false);
+          } else {
+            d4prev = ehi;
+          }
+        }
+      } else {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          uint4 t = src[i];
-          xr[4 * i] = t.x; xr[4 * i + 1] = t.y; xr[4 * i + 2] = t.z; xr[4 * i + 3] = t.w;
+          const uint32_t sel = 0x0c0c0400u | ((uint32_t)(i & 3) << 8);
+          const uint32_t addr = __builtin_amdgcn_perm(b.cd[r][i >> 2], lcopy, sel);
+          const uint32_t e = *(const uint32_t*)__builtin_assume_aligned(lut + addr, 4);
+          accH = __builtin_amdgcn_sdot4((int)e, (int)xr[2 * i], accH, false);
+          if (NPL == 2) accL = __builtin_amdgcn_udot4(e, xr[2 * i + 1], accL, false);
         }
-        if (T5) xr[64] = xl[g * kXStride + 64];
       }
-      const float sig = (MODE == MODE_F32) ? gsig[g] : 0.f;
-      const int gsx = gsum[g];
-      // Codes (and scales) of the R rows for this group.
-      uint32_t cd[R][T5 ? 7 : 8];
-      uint32_t sc[R];
-      const int shift = T5 ? ((kTrit5GroupBytes * g) & 3) : 0;
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        uint32_t rowoff = (uint32_t)prow[r] * (uint32_t)p.row_bytes;
-        if (!pok[r]) rowoff = p.w_bytes;                      // out of range: loads read 0
-        if (T5) {
-          // 28 bytes from the dword-aligned start of the group; the last dword is read as two
-          // halves so that no access of an in-range row crosses the end of the tensor.
-          uint32_t off = rowoff + p.code_off + ((kTrit5GroupBytes * g) & ~3);
-          auto a = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
-          auto b = __builtin_amdgcn_raw_buffer_load_b64(rs, off + 16, 0, 0);
-          uint32_t c0 = __builtin_amdgcn_raw_buffer_load_b16(rs, off + 24, 0, 0);
-          uint32_t c1 = __builtin_amdgcn_raw_buffer_load_b16(rs, off + 26, 0, 0);
-          cd[r][0] = a[0]; cd[r][1] = a[1]; cd[r][2] = a[2]; cd[r][3] = a[3];
-          cd[r][4] = b[0]; cd[r][5] = b[1]; cd[r][6] = c0 | (c1 << 16);
-        } else {
-          uint32_t off = rowoff + p.code_off + 32 * g;
-          auto a = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
-          auto b = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16, 0, 0);
-          cd[r][0] = a[0]; cd[r][1] = a[1]; cd[r][2] = a[2]; cd[r][3] = a[3];
-          cd[r][4] = b[0]; cd[r][5] = b[1]; cd[r][6] = b[2]; cd[r][7] = b[3];
-        }
-        sc[r] = __builtin_amdgcn_raw_buffer_load_b16(rs, rowoff + 2 * g, 0, 0);
-      }
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        int accH = 0, acc4 = 0;
-        unsigned accL = 0;
-        if (T5) {
-          uint32_t d[7];
-#pragma unroll
-          for (int i = 0; i < 6; ++i) d[i] = __builtin_amdgcn_alignbyte(cd[r][i + 1], cd[r][i], shift);
-          d[6] = __builtin_amdgcn_alignbyte(0u, cd[r][6], shift);
-#pragma unroll
-          for (int i = 0; i < 26; ++i) {
-            // Entry address: code byte i into bits 8..15, the lane copy into bits 0..7.
-            const uint32_t sel = 0x0c0c0400u | ((uint32_t)(i & 3) << 8);
-            uint32_t addr = __builtin_amdgcn_perm(d[i >> 2], (i & 1) ? lc_odd : lc_even, sel);
-            const uint64_t e64 = *(const uint64_t*)__builtin_assume_aligned(lut + addr, 8);
-            const uint2 e = make_uint2((uint32_t)e64, (uint32_t)(e64 >> 32));
-            accH = __builtin_amdgcn_sdot4((int)e.x, (int)xr[2 * i], accH, false);
-            if (NPL == 2) accL = __builtin_amdgcn_udot4(e.x, xr[2 * i + 1], accL, false);
-            typedef short s2 __attribute__((ext_vector_type(2)));
-            s2 ea = __builtin_bit_cast(s2, e.y), xa = __builtin_bit_cast(s2, xr[52 + (i >> 1)]);
-            acc4 = __builtin_amdgcn_sdot2(ea, xa, acc4, false);
+      const int S = (NPL == 2) ? (accH << 8) + (int)accL + acc4 - usx : accH + acc4 - usx;
+      if (MODE == MODE_F32) {
+        const float s = __half2float(__ushort_as_half((unsigned short)b.sc[r]));
+        facc[r] = fmaf((float)S * sig, s, facc[r]);
+      } else {
+        // The engine shifts whole-group sums (a right shift floors the sum, not each half): the
+        // partner lane (lg ^ 1) holds the other half of the group.
+        const int Sg = S + __shfl_xor(S, 1, 64);
+        if (MODE == MODE_EXACT) {
+          if (!(u & 1)) {
+            int m11, e16;
+            fp16_split((uint16_t)b.sc[r], m11, e16);
+            const long long prod = (long long)Sg * (long long)m11;
+            const int sh = e16 + p.B;
+            long long c;
+            if (sh >= 0) c = prod << sh;
+            else c = (-sh >= 63) ? (prod < 0 ? -1 : 0) : (prod >> (-sh));
+            iacc[r] += c;
           }
         } else {
-#pragma unroll
-          for (int i = 0; i < 32; ++i) {
-            const uint32_t sel = 0x0c0c0400u | ((uint32_t)(i & 3) << 8);
-            uint32_t addr = __builtin_amdgcn_perm(cd[r][i >> 2], lc_even, sel);
-            uint32_t e = *(const uint32_t*)__builtin_assume_aligned(lut + addr, 4);
-            accH = __builtin_amdgcn_sdot4((int)e, (int)xr[2 * i], accH, false);
-            if (NPL == 2) accL = __builtin_amdgcn_udot4(e, xr[2 * i + 1], accL, false);
-          }
-        }
-        int S;
-        if (NPL == 2) S = (accH << 8) + (int)accL + acc4 - gsx;
-        else S = accH + acc4 - gsx;
-        if (MODE == MODE_F32) {
-          float s = __half2float(__ushort_as_half((unsigned short)sc[r]));
-          facc[r] += (float)S * (s * sig);
-        } else if (MODE == MODE_EXACT) {
-          int m11, e16;
-          fp16_split((uint16_t)sc[r], m11, e16);
-          long long prod = (long long)S * (long long)m11;
-          int sh = e16 + p.B;
-          long long c;
-          if (sh >= 0) c = prod << sh;
-          else c = (-sh >= 63) ? (prod < 0 ? -1 : 0) : (prod >> (-sh));
-          iacc[r] += c;
-        } else {
-          if (pok[r]) p.yi[(size_t)prow[r] * p.G + g] = S;
+          const int o = out_index(bt, r);
+          if (o < p.n_out && !(u & 1)) p.yi[(size_t)o * p.G + (u >> 1)] = Sg;
         }
       }
     }
+  };
 
-    if (MODE == MODE_GSUM) continue;
-    // Reduce over the LPR lanes of the row group.
+  // Cross-lane reduction of the R row sums over the LPR lanes of the row group, by recursive
+  // halving (each step sends half of the remaining values). Afterwards every lane holds the full
+  // sum of row `held`; the lanes whose low bits (below the halving bits) are zero store it.
+  auto finish_batch = [&](int bt) {
+    if (MODE == MODE_GSUM) return;
+    int held = 0;
+    float fv[R];
+    long long iv[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      for (int o = LPR >> 1; o >= 1; o >>= 1) {
-        if (MODE == MODE_F32) facc[r] += __shfl_xor(facc[r], o, 64);
-        else iacc[r] += __shfl_xor(iacc[r], o, 64);
+    for (int r = 0; r < R; ++r) { fv[r] = facc[r]; iv[r] = iacc[r]; }
+    bool writer;
+    const bool halving = (LPR >= R) && !swiglu;
+    if (halving) {
+      int o = LPR >> 1;
+#pragma unroll
+      for (int n = R; n > 1; n >>= 1) {
+        const bool up = (lg & o) != 0;
+#pragma unroll
+        for (int i = 0; i < n / 2; ++i) {
+          if (MODE == MODE_F32) {
+            const float send = up ? fv[i] : fv[i + n / 2];
+            const float keep = up ? fv[i + n / 2] : fv[i];
+            fv[i] = keep + __shfl_xor(send, o, 64);
+          } else {
+            const long long send = up ? iv[i] : iv[i + n / 2];
+            const long long keep = up ? iv[i + n / 2] : iv[i];
+            iv[i] = keep + __shfl_xor(send, o, 64);
+          }
+        }
+        if (up) held += n / 2;
+        o >>= 1;
       }
-    }
-    if (MODE == MODE_EXACT) {
+      for (; o >= 1; o >>= 1) {
+        if (MODE == MODE_F32) fv[0] += __shfl_xor(fv[0], o, 64);
+        else iv[0] += __shfl_xor(iv[0], o, 64);
+      }
+      writer = (lg & ((LPR / R) - 1)) == 0;
+    } else if (!swiglu) {
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        if (lg == (r % LPR) && pok[r]) {
-          long long a = iacc[r];
-          long long res = a >> p.R;
-          int bad = ((a >= (1LL << 47)) || (a <= -(1LL << 47))) ? 1 : 0;
-          bad |= (res >= (1LL << 31) || res <= -(1LL << 31)) ? 2 : 0;
-          if (bad) atomicOr(p.status, bad);
-          p.yi[prow[r]] = (int32_t)res;
+      for (int r = 0; r < R; ++r)
+        for (int o = LPR >> 1; o >= 1; o >>= 1) {
+          if (MODE == MODE_F32) fv[r] += __shfl_xor(fv[r], o, 64);
+          else iv[r] += __shfl_xor(iv[r], o, 64);
+        }
+      writer = false;
+    } else {
+      writer = false;
+    }
+    // One value per writing lane: row `held` (or, for narrow row groups, every row by lane 0).
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      if (swiglu) break;
+      const int r = halving ? held : k;
+      const bool w = halving ? (writer && k == 0) : (lg == 0);
+      if (!w) continue;
+      const float fval = halving ? fv[0] : fv[k];
+      const long long ival = halving ? iv[0] : iv[k];
+      const int o = out_index(bt, r);
+      if (o >= p.n_out) continue;
+      if (MODE == MODE_EXACT) {
+        const long long res = ival >> p.R;
+        int bad = ((ival >= (1LL << 47)) || (ival <= -(1LL << 47))) ? 1 : 0;
+        bad |= (res >= (1LL << 31) || res <= -(1LL << 31)) ? 2 : 0;
+        if (bad) atomicOr(p.status, bad);
+        p.yi[o] = (int32_t)res;
+      } else {
+        float v = fval;
+        if (p.epi == TRX_EPI_RESID) v += p.resid[o];
+        p.y[o] = v;
+        if (p.amax_slot) {
+          const unsigned long long key = ((unsigned long long)ordered_bits(v) << 32) |
+                                         (unsigned long long)(0xFFFFFFFFu - (uint32_t)o);
+          atomicMax(p.amax_slot, key);
         }
       }
-    } else if (p.epi == TRX_EPI_SWIGLU) {
+    }
+    if (MODE == MODE_F32 && swiglu) {
+      // SwiGLU: the gate and up sums of an output sit in different lanes after the halving;
+      // a plain butterfly keeps all R sums in every lane.
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        for (int o = LPR >> 1; o >= 1; o >>= 1) facc[r] += __shfl_xor(facc[r], o, 64);
 #pragma unroll
       for (int r = 0; r < R / 2; ++r) {
-        if (lg == (r % LPR) && pok[r]) p.y[prow[r]] = silu(facc[r]) * facc[r + R / 2];
-      }
-    } else {
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        if (lg == (r % LPR) && pok[r]) {
-          float v = facc[r];
-          if (p.epi == TRX_EPI_RESID) v += p.resid[prow[r]];
-          p.y[prow[r]] = v;
-          if (p.amax_slot) {
-            unsigned long long key = ((unsigned long long)ordered_bits(v) << 32) |
-                                     (unsigned long long)(0xFFFFFFFFu - (uint32_t)prow[r]);
-            atomicMax(p.amax_slot, key);
-          }
-        }
+        const int o = out_index(bt, r);
+        if (lg == (r % LPR) && o < p.n_out) p.y[o] = silu(facc[r]) * facc[r + R / 2];
       }
     }
+#pragma unroll
+    for (int r = 0; r < R; ++r) { facc[r] = 0.f; iacc[r] = 0; }
+  };
+
+  if (NSLOT == 1) load_x(0);
+  int bt = first, sl = 0;
+  // Two items per trip so the double buffer needs no register moves.
+  while (bt < p.n_batches) {
+    int nbt = bt, nsl = sl + 1;
+    if (nsl == NSLOT) { nsl = 0; nbt += stride; }
+    if (nbt < p.n_batches) load_item(bufB, nbt, nsl);
+    if (NSLOT > 1) load_x(sl);
+    compute_item(bufA, bt, sl);
+    if (sl == NSLOT - 1) finish_batch(bt);
+    bt = nbt; sl = nsl;
+    if (bt >= p.n_batches) break;
+    nbt = bt; nsl = sl + 1;
+    if (nsl == NSLOT) { nsl = 0; nbt += stride; }
+    if (nbt < p.n_batches) load_item(bufA, nbt, nsl);
+    if (NSLOT > 1) load_x(sl);
+    compute_item(bufB, bt, sl);
+    if (sl == NSLOT - 1) finish_batch(bt);
+    bt = nbt; sl = nsl;
   }
 }
 
 // Host side ------------------------------------------------------------------------------------
 
-static int lds_bytes(int K, int G) {
-  return G * kXStride * 4 + K * 2 + G * 8 + 64;
-}
+static int lds_bytes(int K, int G) { return 2 * G * kXStride * 4 + K * 2 + G * 4 + 2 * G * 4 + 64; }
 
 static int pick_lpr(int G) {
   int l = 64;
@@ -384,35 +486,64 @@ static int pick_lpr(int G) {
   return l;
 }
 
-template <int FMT, int MODE, int R>
-static int launch(GemvParams& p, int n_blocks, hipStream_t s) {
-  int shm = lds_bytes(p.K, p.G);
-  static bool attr_set = false;
-  if (!attr_set) {
-    TRX_HIP(hipFuncSetAttribute((const void*)gemv_kernel<FMT, MODE, R>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - kLutBytes));
-    attr_set = true;
-  }
-  p.n_batches = (p.epi == TRX_EPI_SWIGLU) ? cdiv(p.n_out, R / 2) : cdiv(p.n_out, R);
-  int per_block = (kThreads / 64) * (64 / p.LPR);
-  int need = cdiv(p.n_batches, per_block);
-  int nb = need < n_blocks ? need : n_blocks;
-  if (nb < 1) nb = 1;
-  hipLaunchKernelGGL((gemv_kernel<FMT, MODE, R>), dim3(nb), dim3(kThreads), shm, s, p);
-  TRX_LAUNCHED();
-  return TRX_OK;
-}
-
 static int g_num_cus = 0;
 static int num_cus() {
   if (!g_num_cus) {
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return 256;
     hipDeviceProp_t prop;
-    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return 256;
+    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess) return 256;
     g_num_cus = prop.multiProcessorCount;
   }
   return g_num_cus;
+}
+
+template <int FMT, int MODE, int R, int NT>
+static int launch_r(GemvParams& p, hipStream_t s) {
+  constexpr int kWaves = NT / 64;
+  static bool attr_set = false;
+  if (!attr_set) {
+    TRX_HIP(hipFuncSetAttribute((const void*)gemv_kernel<FMT, MODE, R, NT>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - kLutBytes));
+    attr_set = true;
+  }
+  p.n_batches = (p.epi == TRX_EPI_SWIGLU) ? cdiv(p.n_out, R / 2) : cdiv(p.n_out, R);
+  const int per_block = kWaves * (64 / p.LPR);
+  const int need = cdiv(p.n_batches, per_block);
+  const int nb = need < num_cus() ? need : num_cus();
+  hipLaunchKernelGGL((gemv_kernel<FMT, MODE, R, NT>), dim3(nb > 0 ? nb : 1), dim3(NT),
+                     lds_bytes(p.K, p.G), s, p);
+  TRX_LAUNCHED();
+  return TRX_OK;
+}
+
+// Variant selection. g_variant (set by trx_gemv_set_variant, for tuning) forces a
+// (rows per item, threads per block) pair; 0 picks automatically: the largest R that still gives
+// every row group of the grid a batch.
+static int g_variant = 0;
+
+template <int FMT, int MODE>
+static int launch(GemvParams& p, hipStream_t s) {
+  const int outs_per_row = (p.epi == TRX_EPI_SWIGLU) ? 2 : 1;
+  switch (g_variant) {
+    case 1: return launch_r<FMT, MODE, 4, 512>(p, s);
+    case 2: return launch_r<FMT, MODE, 2, 1024>(p, s);
+    case 3: if (outs_per_row == 1) return launch_r<FMT, MODE, 1, 1024>(p, s);
+            return launch_r<FMT, MODE, 2, 1024>(p, s);
+    case 4: return launch_r<FMT, MODE, 2, 512>(p, s);
+    case 5: return launch_r<FMT, MODE, 4, 1024>(p, s);
+    default: break;
+  }
+  const long long groups_in_grid = (long long)num_cus() * 16 * (64 / p.LPR);
+  const long long rows = (long long)p.n_out * outs_per_row;
+  if (rows >= 4 * groups_in_grid) return launch_r<FMT, MODE, 4, 1024>(p, s);
+  if (rows >= 2 * groups_in_grid || outs_per_row == 2) return launch_r<FMT, MODE, 2, 1024>(p, s);
+  return launch_r<FMT, MODE, 1, 1024>(p, s);
+}
+
+int gemv_set_variant(int v) {
+  TRX_CHECK(v >= 0 && v <= 5, TRX_E_INVALID, "gemv variant %d", v);
+  g_variant = v;
+  return TRX_OK;
 }
 
 int gemv_check(int kind, int M, int K) {
@@ -436,14 +567,16 @@ static void fill_geom(GemvParams& p, const uint8_t* rows, int kind, int M, int K
   p.G = rg.G;
   p.row_bytes = rg.row_bytes;
   p.code_off = rg.code_off;
-  p.w_bytes = (uint32_t)((unsigned long long)M * rg.row_bytes);
-  p.LPR = pick_lpr(rg.G);
-  p.NSLOT = rg.G / p.LPR;
+  // The last trit5 group of a row may be read 2 bytes past its end: the tensor is followed by a
+  // readable 32-byte tail (trx_malloc and the model arena guarantee it).
+  p.w_bytes = (uint32_t)((unsigned long long)M * rg.row_bytes + 32);
+  p.LPR = pick_lpr(2 * rg.G);
+  p.NSLOT = 2 * rg.G / p.LPR;
 }
 
 int gemv_f32(const uint8_t* rows, int kind, int M, int K, const float* x, const float* norm_w,
              float eps, float* y, int epi, const float* resid, int swiglu_F,
-             unsigned long long* amax_slot, hipStream_t s) {
+             unsigned long long* amax_slot, hipStream_t s, const int* gate_pos, const int* gate_from) {
   int rc = gemv_check(kind, M, K);
   if (rc) return rc;
   TRX_CHECK(x && y, TRX_E_INVALID, "gemv: null x or y");
@@ -459,6 +592,8 @@ int gemv_f32(const uint8_t* rows, int kind, int M, int K, const float* x, const 
   p.epi = epi;
   p.resid = resid;
   p.amax_slot = amax_slot;
+  p.gate_pos = gate_pos;
+  p.gate_from = gate_from;
   if (epi == TRX_EPI_SWIGLU) {
     TRX_CHECK(swiglu_F > 0 && 2 * swiglu_F == M, TRX_E_INVALID, "gemv: SwiGLU needs M == 2F");
     p.swiglu_F = swiglu_F;
@@ -466,9 +601,8 @@ int gemv_f32(const uint8_t* rows, int kind, int M, int K, const float* x, const 
   } else {
     p.n_out = M;
   }
-  int nb = num_cus();
-  if (kind == TRX_KIND_TERNARY5) return launch<TRX_KIND_TERNARY5, MODE_F32, 4>(p, nb, s);
-  return launch<TRX_KIND_TERNARY, MODE_F32, 4>(p, nb, s);
+  if (kind == TRX_KIND_TERNARY5) return launch<TRX_KIND_TERNARY5, MODE_F32>(p, s);
+  return launch<TRX_KIND_TERNARY, MODE_F32>(p, s);
 }
 
 int gemv_exact(const uint8_t* rows, int kind, int M, int K, const int8_t* x8, int B, int R,
@@ -486,9 +620,8 @@ int gemv_exact(const uint8_t* rows, int kind, int M, int K, const int8_t* x8, in
   p.status = status;
   p.epi = TRX_EPI_STORE;
   p.n_out = M;
-  int nb = num_cus();
-  if (kind == TRX_KIND_TERNARY5) return launch<TRX_KIND_TERNARY5, MODE_EXACT, 4>(p, nb, s);
-  return launch<TRX_KIND_TERNARY, MODE_EXACT, 4>(p, nb, s);
+  if (kind == TRX_KIND_TERNARY5) return launch<TRX_KIND_TERNARY5, MODE_EXACT>(p, s);
+  return launch<TRX_KIND_TERNARY, MODE_EXACT>(p, s);
 }
 
 int gemv_groupsums(const uint8_t* rows, int kind, int M, int K, const int8_t* x8, int32_t* gs,
@@ -502,9 +635,8 @@ int gemv_groupsums(const uint8_t* rows, int kind, int M, int K, const int8_t* x8
   p.yi = gs;
   p.epi = TRX_EPI_STORE;
   p.n_out = M;
-  int nb = num_cus();
-  if (kind == TRX_KIND_TERNARY5) return launch<TRX_KIND_TERNARY5, MODE_GSUM, 4>(p, nb, s);
-  return launch<TRX_KIND_TERNARY, MODE_GSUM, 4>(p, nb, s);
+  if (kind == TRX_KIND_TERNARY5) return launch<TRX_KIND_TERNARY5, MODE_GSUM>(p, s);
+  return launch<TRX_KIND_TERNARY, MODE_GSUM>(p, s);
 }
 
 }  // namespace trx

@@ -1,0 +1,586 @@
+// Batch-1 decode runtime: weight arena, KV cache, DeltaNet state, the per-token launch plan and
+// its hipGraph. The state semantics follow model/golden.py:FloatModel (reset/forward/generate):
+// K cached post-norm and post-RoPE, V raw, the conv window and recurrent matrix per DeltaNet
+// layer, one position per forward; the loop contract follows model/mirror.py:1036-1044 (prefill
+// one token per forward, logits only from the last prompt position on, no forward after the last
+// generated token).
+
+#include <stdio.h>
+#include <string.h>
+#include <map>
+#include <vector>
+#include <functional>
+
+#include "trx_internal.h"
+#include "trx_ops.h"
+#include "trx_model.h"
+
+namespace trx {
+
+struct Tensor {
+  size_t off = 0;      // byte offset in the arena
+  size_t bytes = 0;
+  int rows = 0, cols = 0, kind = 0;
+  bool loaded = false;
+};
+
+struct Model {
+  trx_model_config cfg;
+  std::vector<float> rope_freq;
+  hipStream_t stream = nullptr;
+  uint8_t* arena = nullptr;
+  size_t arena_bytes = 0;
+  std::map<std::pair<int, int>, Tensor> tensors;   // (role, layer) -> tensor
+  // fused groups: (layer) -> offset of [Wq|Wk|Wv] / [Wg|Wu] / [Wqkv|Wz]
+  // device state
+  __half *kcache = nullptr, *vcache = nullptr;     // per attention layer slice
+  float *conv_state = nullptr, *dn_state = nullptr;
+  float *x = nullptr, *qkv = nullptr, *attn_out = nullptr, *act = nullptr, *logits = nullptr;
+  float *part_m = nullptr, *part_l = nullptr, *part_o = nullptr;
+  float *dn_io = nullptr, *dn_ba = nullptr, *dn_out = nullptr, *rope_dev = nullptr;
+  int* ctl = nullptr;  // [0] pos, [1] n_fed, [2] cur_tok, [3] head_from, [8..] fed tokens by
+                       // absolute position (max_ctx), then the generated tokens (max_new)
+  int host_pos = -1;   // host mirror of the device position after the enqueued steps
+  unsigned long long* slot = nullptr;
+  int n_attn = 0, n_dn = 0;
+  std::vector<int> attn_index, dn_index;           // per layer: index among attn / dn layers
+  int n_split = 0, chunk = 64;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t graph_exec = nullptr;
+  size_t dev_bytes = 0;
+  std::vector<void*> allocs;
+
+  bool is_dn(int l) const { return (cfg.layer_types[l >> 6] >> (l & 63)) & 1ull; }
+  int* pos() { return ctl; }
+  int* n_prompt() { return ctl + 1; }
+  int* cur_tok() { return ctl + 2; }
+  int* head_from() { return ctl + 3; }
+  int* prompt() { return ctl + 8; }
+  int* out() { return ctl + 8 + cfg.max_ctx; }
+};
+
+static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+static int row_bytes_of(int kind, int cols) {
+  if (kind == TRX_KIND_TERNARY || kind == TRX_KIND_TERNARY5) return row_geom(kind, cols).row_bytes;
+  if (kind == TRX_KIND_Q8) return kBeat * cdiv(cols / 32, 16) + cols;
+  if (kind == TRX_KIND_F16 || kind == TRX_KIND_NORM16) return 2 * cols;
+  return 4 * cols;  // F32
+}
+
+// Arena plan ----------------------------------------------------------------------------------
+
+static void plan_tensor(Model& m, size_t& cur, int role, int layer, int kind, int rows, int cols,
+                        bool pad = true) {
+  Tensor t;
+  t.rows = rows;
+  t.cols = cols;
+  t.kind = kind;
+  t.bytes = (size_t)rows * row_bytes_of(kind, cols);
+  t.off = cur;
+  cur += t.bytes;
+  if (pad) cur = align_up(cur + 64, 256);  // readable tail past every tensor
+  m.tensors[{role, layer}] = t;
+}
+
+static void plan_arena(Model& m, size_t& cur) {
+  const trx_model_config& c = m.cfg;
+  const int E = c.n_embd, hd = c.head_dim, F = c.ffn_dim;
+  const int qrows = c.n_head * hd * (c.attn_gated ? 2 : 1), kvrows = c.n_kv_head * hd;
+  const int wk = c.weight_kind;
+  const int nq = c.dn_num_k_heads * c.dn_k_head_dim, nvh = c.dn_num_v_heads * c.dn_v_head_dim;
+  const int C = 2 * nq + nvh;
+  for (int l = 0; l < c.n_layer; ++l) {
+    plan_tensor(m, cur, TRX_ROLE_ATTN_NORM, l, TRX_KIND_F32, 1, E);
+    if (m.is_dn(l)) {
+      // [Wqkv | Wz] adjacent: one GEMV launch.
+      plan_tensor(m, cur, TRX_ROLE_ATTN_QKV, l, wk, C, E, false);
+      plan_tensor(m, cur, TRX_ROLE_ATTN_ZGATE, l, wk, nvh, E);
+      plan_tensor(m, cur, TRX_ROLE_SSM_BETA, l, TRX_KIND_Q8, c.dn_num_v_heads, E, false);
+      plan_tensor(m, cur, TRX_ROLE_SSM_ALPHA, l, TRX_KIND_Q8, c.dn_num_v_heads, E);
+      plan_tensor(m, cur, TRX_ROLE_SSM_CONV, l, TRX_KIND_F32, C, c.dn_conv_kernel);
+      plan_tensor(m, cur, TRX_ROLE_SSM_A, l, TRX_KIND_F32, 1, c.dn_num_v_heads);
+      plan_tensor(m, cur, TRX_ROLE_SSM_DT, l, TRX_KIND_F32, 1, c.dn_num_v_heads);
+      plan_tensor(m, cur, TRX_ROLE_SSM_NORM, l, TRX_KIND_F32, 1, c.dn_v_head_dim);
+      plan_tensor(m, cur, TRX_ROLE_SSM_OUT, l, wk, E, nvh);
+    } else {
+      // [Wq | Wk | Wv] adjacent: one GEMV launch.
+      plan_tensor(m, cur, TRX_ROLE_ATTN_Q, l, wk, qrows, E, false);
+      plan_tensor(m, cur, TRX_ROLE_ATTN_K, l, wk, kvrows, E, false);
+      plan_tensor(m, cur, TRX_ROLE_ATTN_V, l, wk, kvrows, E);
+      plan_tensor(m, cur, TRX_ROLE_ATTN_Q_NORM, l, TRX_KIND_F32, 1, hd);
+      plan_tensor(m, cur, TRX_ROLE_ATTN_K_NORM, l, TRX_KIND_F32, 1, hd);
+      plan_tensor(m, cur, TRX_ROLE_ATTN_OUT, l, wk, E, c.n_head * hd);
+    }
+    plan_tensor(m, cur, TRX_ROLE_FFN_NORM, l, TRX_KIND_F32, 1, E);
+    plan_tensor(m, cur, TRX_ROLE_FFN_GATE, l, wk, F, E, false);
+    plan_tensor(m, cur, TRX_ROLE_FFN_UP, l, wk, F, E);
+    plan_tensor(m, cur, TRX_ROLE_FFN_DOWN, l, wk, E, F);
+  }
+  plan_tensor(m, cur, TRX_ROLE_OUT_NORM, 0, TRX_KIND_F32, 1, E);
+  if (c.emb_mode == 0) {
+    plan_tensor(m, cur, TRX_ROLE_TOK_EMB16, 0, TRX_KIND_NORM16, c.vocab, E);
+    plan_tensor(m, cur, TRX_ROLE_TOK_EMB16_EXP, 0, TRX_KIND_F32, 1, c.vocab);  // int32 exponents
+  }
+  if (c.emb_mode == 1 || c.head_tied) plan_tensor(m, cur, TRX_ROLE_TOK_EMB, 0, c.emb_kind, c.vocab, E);
+  if (!c.head_tied) plan_tensor(m, cur, TRX_ROLE_LM_HEAD, 0, c.head_kind, c.vocab, E);
+}
+
+static int dalloc(Model& m, void** p, size_t bytes) {
+  hipError_t e = hipMalloc(p, bytes + 256);
+  if (e != hipSuccess) {
+    set_error("device allocation of %zu bytes failed: %s", bytes, hipGetErrorString(e));
+    return e == hipErrorOutOfMemory ? TRX_E_NOMEM : TRX_E_HIP;
+  }
+  m.allocs.push_back(*p);
+  m.dev_bytes += bytes;
+  TRX_HIP(hipMemset(*p, 0, bytes + 256));
+  return TRX_OK;
+}
+
+// Plan of one decode position -----------------------------------------------------------------
+
+static const Tensor& T(Model& m, int role, int layer) { return m.tensors[{role, layer}]; }
+static uint8_t* P(Model& m, int role, int layer) { return m.arena + T(m, role, layer).off; }
+static float* PF(Model& m, int role, int layer) { return (float*)P(m, role, layer); }
+
+// Gated DeltaNet layer: [qkv|z] GEMV and the beta/alpha Q8 GEMV (both with the attention
+// RMSNorm), conv, recurrence with the gated norm, then the out projection with the residual.
+int dn_layer_launch(Model& m, int l, hipStream_t s) {
+  const trx_model_config& c = m.cfg;
+  const int E = c.n_embd;
+  const int nq = c.dn_num_k_heads * c.dn_k_head_dim, nvh = c.dn_num_v_heads * c.dn_v_head_dim;
+  const int C = 2 * nq + nvh;
+  const int di = m.dn_index[l];
+  int rc;
+  float* io = m.dn_io;                  // [C + nvh] projections
+  float* conv_out = m.dn_io + C + nvh;  // [C]
+  if ((rc = gemv_f32(P(m, TRX_ROLE_ATTN_QKV, l), c.weight_kind, C + nvh, E, m.x,
+                     PF(m, TRX_ROLE_ATTN_NORM, l), c.rms_eps, io, TRX_EPI_STORE, nullptr, 0, nullptr, s))) return rc;
+  DenseParams dp = {};
+  dp.W = P(m, TRX_ROLE_SSM_BETA, l);
+  dp.kind = TRX_KIND_Q8;
+  dp.M = 2 * c.dn_num_v_heads;
+  dp.K = E;
+  dp.row_bytes = kBeat * cdiv(E / 32, 16) + E;
+  dp.code_off = kBeat * cdiv(E / 32, 16);
+  dp.x = m.x;
+  dp.norm_w = PF(m, TRX_ROLE_ATTN_NORM, l);
+  dp.eps = c.rms_eps;
+  dp.y = m.dn_ba;
+  if ((rc = launch_dense_gemv(dp, s))) return rc;
+  DnConvParams cp = {};
+  cp.qkv = io;
+  cp.taps = PF(m, TRX_ROLE_SSM_CONV, l);
+  cp.state = m.conv_state + (size_t)di * (c.dn_conv_kernel - 1) * C;
+  cp.out = conv_out;
+  cp.C = C;
+  cp.Kc = c.dn_conv_kernel;
+  cp.nq = nq;
+  cp.hk = c.dn_k_head_dim;
+  cp.eps = c.rms_eps;
+  if ((rc = launch_dn_conv(cp, s))) return rc;
+  DnRecurParams rp = {};
+  rp.conv = conv_out;
+  rp.z = io + C;
+  rp.ba = m.dn_ba;
+  rp.A = PF(m, TRX_ROLE_SSM_A, l);
+  rp.dt = PF(m, TRX_ROLE_SSM_DT, l);
+  rp.norm_w = PF(m, TRX_ROLE_SSM_NORM, l);
+  rp.S = m.dn_state + (size_t)di * nvh * c.dn_k_head_dim;
+  rp.out = m.dn_out;
+  rp.nv = c.dn_num_v_heads;
+  rp.nk = c.dn_num_k_heads;
+  rp.hk = c.dn_k_head_dim;
+  rp.hv = c.dn_v_head_dim;
+  rp.eps = c.rms_eps;
+  if ((rc = launch_dn_recur(rp, s))) return rc;
+  return gemv_f32(P(m, TRX_ROLE_SSM_OUT, l), c.weight_kind, E, nvh, m.dn_out, nullptr, c.rms_eps, m.x,
+                  TRX_EPI_RESID, m.x, 0, nullptr, s);
+}
+
+static int run_step(Model& m, hipStream_t s) {
+  const trx_model_config& c = m.cfg;
+  const int E = c.n_embd, hd = c.head_dim, F = c.ffn_dim;
+  const int qrows = c.n_head * hd * (c.attn_gated ? 2 : 1), kvrows = c.n_kv_head * hd;
+  const int wk = c.weight_kind;
+  int rc;
+  // Embedding of this position's token.
+  EmbedParams ep = {};
+  ep.mode = c.emb_mode == 0 ? EMBED_TABLE : EMBED_TERNARY;
+  ep.n_embd = E;
+  ep.vocab = c.vocab;
+  if (c.emb_mode == 0) {
+    ep.mant = (const int16_t*)P(m, TRX_ROLE_TOK_EMB16, 0);
+    ep.exps = (const int32_t*)P(m, TRX_ROLE_TOK_EMB16_EXP, 0);
+  } else {
+    ep.rows = P(m, TRX_ROLE_TOK_EMB, 0);
+    ep.kind = c.emb_kind;
+    ep.row_bytes = row_bytes_of(c.emb_kind, E);
+    ep.code_off = row_geom(c.emb_kind, E).code_off;
+  }
+  ep.pos = m.pos();
+  ep.n_prompt = m.n_prompt();
+  ep.prompt = m.prompt();
+  ep.slot = m.slot;
+  ep.out = m.out();
+  ep.max_out = c.max_new;
+  ep.cur_tok = m.cur_tok();
+  ep.x = m.x;
+  if ((rc = launch_embed(ep, s))) return rc;
+
+  for (int l = 0; l < c.n_layer; ++l) {
+    if (m.is_dn(l)) {
+      if ((rc = dn_layer_launch(m, l, s))) return rc;
+    } else {
+      // q|k|v with the attention RMSNorm fused in the prologue.
+      if ((rc = gemv_f32(P(m, TRX_ROLE_ATTN_Q, l), wk, qrows + 2 * kvrows, E, m.x,
+                         PF(m, TRX_ROLE_ATTN_NORM, l), c.rms_eps, m.qkv, TRX_EPI_STORE, nullptr, 0,
+                         nullptr, s))) return rc;
+      AttnParams ap = {};
+      ap.qkv = m.qkv;
+      ap.q_norm = PF(m, TRX_ROLE_ATTN_Q_NORM, l);
+      ap.k_norm = PF(m, TRX_ROLE_ATTN_K_NORM, l);
+      ap.rope_freq = m.rope_dev;
+      ap.pos = m.pos();
+      const size_t per = (size_t)c.n_kv_head * c.max_ctx * hd;
+      ap.kcache = m.kcache + (size_t)m.attn_index[l] * per;
+      ap.vcache = m.vcache + (size_t)m.attn_index[l] * per;
+      ap.part_m = m.part_m;
+      ap.part_l = m.part_l;
+      ap.part_o = m.part_o;
+      ap.out = m.attn_out;
+      ap.n_head = c.n_head;
+      ap.n_kv = c.n_kv_head;
+      ap.n_rep = c.n_head / c.n_kv_head;
+      ap.hd = hd;
+      ap.rope_n = c.rope_dims ? c.rope_dims : hd;
+      ap.max_ctx = c.max_ctx;
+      ap.n_split = m.n_split;
+      ap.chunk = m.chunk;
+      ap.gated = c.attn_gated;
+      ap.eps = c.rms_eps;
+      if ((rc = launch_attention(ap, s))) return rc;
+      if ((rc = gemv_f32(P(m, TRX_ROLE_ATTN_OUT, l), wk, E, c.n_head * hd, m.attn_out, nullptr,
+                         c.rms_eps, m.x, TRX_EPI_RESID, m.x, 0, nullptr, s))) return rc;
+    }
+    // SwiGLU FFN: gate|up with the FFN RMSNorm, then down with the residual add.
+    if ((rc = gemv_f32(P(m, TRX_ROLE_FFN_GATE, l), wk, 2 * F, E, m.x, PF(m, TRX_ROLE_FFN_NORM, l),
+                       c.rms_eps, m.act, TRX_EPI_SWIGLU, nullptr, F, nullptr, s))) return rc;
+    if ((rc = gemv_f32(P(m, TRX_ROLE_FFN_DOWN, l), wk, E, F, m.act, nullptr, c.rms_eps, m.x,
+                       TRX_EPI_RESID, m.x, 0, nullptr, s))) return rc;
+  }
+  // LM head with the output RMSNorm and the greedy argmax; skipped (by the kernel, reading the
+  // position) on prefill positions before head_from.
+  const int head_role = c.head_tied ? TRX_ROLE_TOK_EMB : TRX_ROLE_LM_HEAD;
+  const int head_kind = c.head_tied ? c.emb_kind : c.head_kind;
+  if (head_kind == TRX_KIND_F16) {
+    DenseParams dp = {};
+    dp.W = P(m, head_role, 0);
+    dp.kind = TRX_KIND_F16;
+    dp.M = c.vocab;
+    dp.K = E;
+    dp.row_bytes = 2 * E;
+    dp.x = m.x;
+    dp.norm_w = PF(m, TRX_ROLE_OUT_NORM, 0);
+    dp.eps = c.rms_eps;
+    dp.y = m.logits;
+    dp.amax_slot = m.slot;
+    dp.gate_pos = m.pos();
+    dp.gate_from = m.head_from();
+    if ((rc = launch_dense_gemv(dp, s))) return rc;
+  } else {
+    if ((rc = gemv_f32(P(m, head_role, 0), head_kind, c.vocab, E, m.x, PF(m, TRX_ROLE_OUT_NORM, 0),
+                       c.rms_eps, m.logits, TRX_EPI_STORE, nullptr, 0, m.slot, s, m.pos(),
+                       m.head_from()))) return rc;
+  }
+  return TRX_OK;
+}
+
+}  // namespace trx
+
+using namespace trx;
+
+#define TRX_API extern "C" __attribute__((visibility("default")))
+
+struct trx_model {
+  Model m;
+};
+
+TRX_API int trx_model_create(const trx_model_config* cfg, const float* rope_freq, trx_model** out) {
+  TRX_CHECK(cfg && out && rope_freq, TRX_E_INVALID, "trx_model_create: null argument");
+  *out = nullptr;
+  const trx_model_config& c = *cfg;
+  TRX_CHECK(c.n_layer > 0 && c.n_layer <= 128 && c.n_embd % 128 == 0 && c.ffn_dim % 128 == 0 &&
+            c.head_dim > 0 && c.n_head % (c.n_kv_head ? c.n_kv_head : 1) == 0 && c.vocab > 0 &&
+            c.max_ctx > 0 && c.max_new > 0, TRX_E_INVALID,
+            "trx_model_create: unsupported geometry");
+  TRX_CHECK(c.weight_kind == TRX_KIND_TERNARY || c.weight_kind == TRX_KIND_TERNARY5, TRX_E_INVALID,
+            "trx_model_create: weight_kind must be ternary");
+  trx_model* h = new trx_model();
+  Model& m = h->m;
+  m.cfg = c;
+  const int rope_n = c.rope_dims ? c.rope_dims : c.head_dim;
+  m.rope_freq.assign(rope_freq, rope_freq + rope_n / 2);
+  for (int l = 0; l < c.n_layer; ++l) {
+    m.attn_index.push_back(m.is_dn(l) ? -1 : m.n_attn);
+    m.dn_index.push_back(m.is_dn(l) ? m.n_dn : -1);
+    if (m.is_dn(l)) ++m.n_dn; else ++m.n_attn;
+  }
+  size_t cur = 0;
+  plan_arena(m, cur);
+  m.arena_bytes = cur;
+  int rc;
+  auto fail = [&](int code) { trx_model_destroy(h); return code; };
+  if ((rc = dalloc(m, (void**)&m.arena, m.arena_bytes))) return fail(rc);
+  const int hd = c.head_dim;
+  m.n_split = (c.max_ctx + m.chunk - 1) / m.chunk;
+  const size_t kv = (size_t)m.n_attn * c.n_kv_head * c.max_ctx * hd;
+  if (m.n_attn) {
+    if ((rc = dalloc(m, (void**)&m.kcache, kv * 2))) return fail(rc);
+    if ((rc = dalloc(m, (void**)&m.vcache, kv * 2))) return fail(rc);
+  }
+  const int nq = c.dn_num_k_heads * c.dn_k_head_dim, nvh = c.dn_num_v_heads * c.dn_v_head_dim;
+  const int C = 2 * nq + nvh;
+  if (m.n_dn) {
+    if ((rc = dalloc(m, (void**)&m.conv_state, (size_t)m.n_dn * (c.dn_conv_kernel - 1) * C * 4))) return fail(rc);
+    if ((rc = dalloc(m, (void**)&m.dn_state, (size_t)m.n_dn * c.dn_num_v_heads * c.dn_v_head_dim * c.dn_k_head_dim * 4))) return fail(rc);
+    if ((rc = dalloc(m, (void**)&m.dn_io, (size_t)(C + nvh) * 4 * 2))) return fail(rc);
+    if ((rc = dalloc(m, (void**)&m.dn_ba, (size_t)c.dn_num_v_heads * 2 * 4))) return fail(rc);
+    if ((rc = dalloc(m, (void**)&m.dn_out, (size_t)nvh * 4))) return fail(rc);
+  }
+  const int qrows = c.n_head * hd * (c.attn_gated ? 2 : 1);
+  if ((rc = dalloc(m, (void**)&m.x, (size_t)c.n_embd * 4))) return fail(rc);
+  if ((rc = dalloc(m, (void**)&m.qkv, (size_t)(qrows + 2 * c.n_kv_head * hd) * 4))) return fail(rc);
+  if ((rc = dalloc(m, (void**)&m.attn_out, (size_t)c.n_head * hd * 4))) return fail(rc);
+  if ((rc = dalloc(m, (void**)&m.act, (size_t)c.ffn_dim * 4))) return fail(rc);
+  if ((rc = dalloc(m, (void**)&m.logits, (size_t)c.vocab * 4))) return fail(rc);
+  if ((rc = dalloc(m, (void**)&m.part_m, (size_t)c.n_head * m.n_split * 4))) return fail(rc);
+  if ((rc = dalloc(m, (void**)&m.part_l, (size_t)c.n_head * m.n_split * 4))) return fail(rc);
+  if ((rc = dalloc(m, (void**)&m.part_o, (size_t)c.n_head * m.n_split * hd * 4))) return fail(rc);
+  if ((rc = dalloc(m, (void**)&m.rope_dev, (size_t)rope_n * 4))) return fail(rc);
+  if ((rc = dalloc(m, (void**)&m.ctl, (size_t)(8 + c.max_ctx + c.max_new) * 4))) return fail(rc);
+  if ((rc = dalloc(m, (void**)&m.slot, 8))) return fail(rc);
+  TRX_HIP(hipMemcpy(m.rope_dev, m.rope_freq.data(), m.rope_freq.size() * 4, hipMemcpyHostToDevice));
+  {
+    hipError_t e = hipStreamCreateWithFlags(&m.stream, hipStreamNonBlocking);
+    if (e != hipSuccess) { set_error("stream: %s", hipGetErrorString(e)); return fail(TRX_E_HIP); }
+  }
+  *out = h;
+  return trx_model_reset(h);
+}
+
+TRX_API int trx_model_destroy(trx_model* h) {
+  if (!h) return TRX_OK;
+  Model& m = h->m;
+  // Teardown is best effort: errors here have no caller to act on them.
+  if (m.graph_exec) (void)hipGraphExecDestroy(m.graph_exec);
+  if (m.graph) (void)hipGraphDestroy(m.graph);
+  if (m.stream) (void)hipStreamSynchronize(m.stream);
+  for (void* p : m.allocs) (void)hipFree(p);
+  if (m.stream) (void)hipStreamDestroy(m.stream);
+  delete h;
+  return TRX_OK;
+}
+
+TRX_API int trx_model_set_tensor(trx_model* h, int role, int layer, const void* data, size_t bytes) {
+  TRX_CHECK(h && data, TRX_E_INVALID, "trx_model_set_tensor: null argument");
+  Model& m = h->m;
+  auto it = m.tensors.find({role, layer});
+  TRX_CHECK(it != m.tensors.end(), TRX_E_INVALID, "model has no tensor role=%d layer=%d", role, layer);
+  TRX_CHECK(bytes == it->second.bytes, TRX_E_INVALID,
+            "tensor role=%d layer=%d: %zu bytes given, %zu expected (%d x %d, kind %d)", role, layer,
+            bytes, it->second.bytes, it->second.rows, it->second.cols, it->second.kind);
+  TRX_HIP(hipMemcpy(m.arena + it->second.off, data, bytes, hipMemcpyHostToDevice));
+  it->second.loaded = true;
+  return TRX_OK;
+}
+
+TRX_API int trx_model_synthesize(trx_model* h, uint32_t seed, const float* ranges) {
+  // ranges: {scale_lo, scale_span, norm_lo, norm_span} as float32 (computed by the caller the
+  // way the host generator computes them, so both sides round alike).
+  TRX_CHECK(h && ranges, TRX_E_INVALID, "trx_model_synthesize: null argument");
+  Model& m = h->m;
+  int rc;
+  for (auto& kv : m.tensors) {
+    const int role = kv.first.first, layer = kv.first.second;
+    Tensor& t = kv.second;
+    const uint32_t tid = (uint32_t)(layer * 32 + role);
+    if (t.kind == TRX_KIND_TERNARY || t.kind == TRX_KIND_TERNARY5) {
+      SynthParams sp = {};
+      sp.out = m.arena + t.off;
+      sp.kind = t.kind;
+      sp.rows = t.rows;
+      sp.cols = t.cols;
+      sp.row_bytes = row_bytes_of(t.kind, t.cols);
+      sp.code_off = row_geom(t.kind, t.cols).code_off;
+      sp.seed = seed;
+      sp.tensor_id = tid;
+      sp.lo = ranges[0];
+      sp.span = ranges[1];
+      if ((rc = launch_synth_ternary(sp, m.stream))) return rc;
+      t.loaded = true;
+    } else if (t.kind == TRX_KIND_F32 && role != TRX_ROLE_TOK_EMB16_EXP) {
+      float lo = ranges[2], span = ranges[3];
+      int transform = 0;
+      if (role == TRX_ROLE_SSM_CONV) { lo = -0.5f; span = 1.0f; }
+      if (role == TRX_ROLE_SSM_A) { lo = -1.5f; span = 2.0f; transform = 1; }
+      if (role == TRX_ROLE_SSM_DT) { lo = -2.0f; span = 2.5f; }
+      if ((rc = launch_synth_f32((float*)(m.arena + t.off), (long long)t.rows * t.cols, seed, tid, lo,
+                                 span, transform, m.stream))) return rc;
+      t.loaded = true;
+    } else {
+      TRX_CHECK(false, TRX_E_INVALID, "synthesize: tensor role=%d kind=%d has no generator", role, t.kind);
+    }
+  }
+  TRX_HIP(hipStreamSynchronize(m.stream));
+  return TRX_OK;
+}
+
+TRX_API int trx_model_reset(trx_model* h) {
+  TRX_CHECK(h, TRX_E_INVALID, "trx_model_reset: null");
+  Model& m = h->m;
+  const trx_model_config& c = m.cfg;
+  int init[8] = {-1, 0, 0, 0, 0, 0, 0, 0};
+  m.host_pos = -1;
+  TRX_HIP(hipMemcpyAsync(m.ctl, init, sizeof init, hipMemcpyHostToDevice, m.stream));
+  TRX_HIP(hipMemsetAsync(m.slot, 0, 8, m.stream));
+  if (m.n_dn) {
+    const int nq = c.dn_num_k_heads * c.dn_k_head_dim, nvh = c.dn_num_v_heads * c.dn_v_head_dim;
+    TRX_HIP(hipMemsetAsync(m.conv_state, 0, (size_t)m.n_dn * (c.dn_conv_kernel - 1) * (2 * nq + nvh) * 4, m.stream));
+    TRX_HIP(hipMemsetAsync(m.dn_state, 0, (size_t)m.n_dn * nvh * c.dn_k_head_dim * 4, m.stream));
+  }
+  TRX_HIP(hipStreamSynchronize(m.stream));
+  return TRX_OK;
+}
+
+static int check_loaded(Model& m) {
+  for (auto& kv : m.tensors)
+    TRX_CHECK(kv.second.loaded, TRX_E_STATE, "tensor role=%d layer=%d was never set", kv.first.first, kv.first.second);
+  return TRX_OK;
+}
+
+TRX_API int trx_model_set_prompt(trx_model* h, const int32_t* tokens, int n, int head_from) {
+  // Feeds tokens at the next n positions (after the steps already enqueued); logits are produced
+  // from absolute position head_from on (-1: the last fed token).
+  TRX_CHECK(h && tokens && n > 0, TRX_E_INVALID, "trx_model_set_prompt: bad arguments");
+  Model& m = h->m;
+  const int first = m.host_pos + 1;
+  TRX_CHECK(first + n <= m.cfg.max_ctx, TRX_E_STATE, "%d tokens after position %d exceed max_ctx %d", n,
+            m.host_pos, m.cfg.max_ctx);
+  for (int i = 0; i < n; ++i)
+    TRX_CHECK(tokens[i] >= 0 && tokens[i] < m.cfg.vocab, TRX_E_INVALID, "token %d out of range", tokens[i]);
+  const int n_fed = first + n, hf = head_from < 0 ? first + n - 1 : head_from;
+  TRX_HIP(hipMemcpyAsync(m.prompt() + first, tokens, (size_t)n * 4, hipMemcpyHostToDevice, m.stream));
+  TRX_HIP(hipMemcpyAsync(m.ctl + 1, &n_fed, 4, hipMemcpyHostToDevice, m.stream));
+  TRX_HIP(hipMemcpyAsync(m.ctl + 3, &hf, 4, hipMemcpyHostToDevice, m.stream));
+  TRX_HIP(hipStreamSynchronize(m.stream));
+  return TRX_OK;
+}
+
+TRX_API int trx_model_step(trx_model* h, int n_steps, int use_graph) {
+  TRX_CHECK(h && n_steps >= 0, TRX_E_INVALID, "trx_model_step: bad arguments");
+  Model& m = h->m;
+  int rc;
+  if ((rc = check_loaded(m))) return rc;
+  if (use_graph && !m.graph_exec) {
+    TRX_HIP(hipStreamBeginCapture(m.stream, hipStreamCaptureModeThreadLocal));
+    rc = run_step(m, m.stream);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(m.stream, &g);
+    if (rc) { if (g) (void)hipGraphDestroy(g); return rc; }
+    TRX_CHECK(e == hipSuccess, TRX_E_HIP, "graph capture: %s", hipGetErrorString(e));
+    m.graph = g;
+    TRX_HIP(hipGraphInstantiate(&m.graph_exec, m.graph, nullptr, nullptr, 0));
+  }
+  TRX_CHECK(m.host_pos + n_steps < m.cfg.max_ctx, TRX_E_STATE, "%d steps after position %d exceed max_ctx %d",
+            n_steps, m.host_pos, m.cfg.max_ctx);
+  for (int i = 0; i < n_steps; ++i) {
+    ++m.host_pos;
+    if (use_graph) {
+      TRX_HIP(hipGraphLaunch(m.graph_exec, m.stream));
+    } else if ((rc = run_step(m, m.stream))) {
+      return rc;
+    }
+  }
+  return TRX_OK;
+}
+
+TRX_API int trx_model_finalize(trx_model* h) {
+  TRX_CHECK(h, TRX_E_INVALID, "trx_model_finalize: null");
+  Model& m = h->m;
+  return launch_finalize(m.pos(), m.n_prompt(), m.slot, m.out(), m.cfg.max_new, m.stream);
+}
+
+TRX_API int trx_model_sync(trx_model* h) {
+  TRX_CHECK(h, TRX_E_INVALID, "trx_model_sync: null");
+  TRX_HIP(hipStreamSynchronize(h->m.stream));
+  return TRX_OK;
+}
+
+TRX_API int trx_model_generate(trx_model* h, const int32_t* prompt, int n_prompt, int n_new,
+                               int32_t* out, int use_graph) {
+  TRX_CHECK(h && prompt && out && n_prompt > 0 && n_new > 0, TRX_E_INVALID, "trx_model_generate: bad arguments");
+  Model& m = h->m;
+  TRX_CHECK(n_new <= m.cfg.max_new, TRX_E_INVALID, "n_new %d exceeds max_new %d", n_new, m.cfg.max_new);
+  TRX_CHECK(n_prompt <= m.cfg.max_ctx, TRX_E_INVALID, "prompt of %d tokens exceeds max_ctx", n_prompt);
+  TRX_CHECK(n_prompt + n_new - 1 <= m.cfg.max_ctx, TRX_E_STATE, "context of %d positions exceeds max_ctx %d",
+            n_prompt + n_new - 1, m.cfg.max_ctx);
+  int rc;
+  if ((rc = trx_model_reset(h))) return rc;
+  if ((rc = trx_model_set_prompt(h, prompt, n_prompt, -1))) return rc;
+  if ((rc = trx_model_step(h, n_prompt + n_new - 1, use_graph))) return rc;
+  if ((rc = trx_model_finalize(h))) return rc;
+  TRX_HIP(hipMemcpyAsync(out, m.out(), (size_t)n_new * 4, hipMemcpyDeviceToHost, m.stream));
+  TRX_HIP(hipStreamSynchronize(m.stream));
+  return TRX_OK;
+}
+
+TRX_API int trx_model_read(trx_model* h, int what, void* host, size_t bytes) {
+  TRX_CHECK(h && host, TRX_E_INVALID, "trx_model_read: null argument");
+  Model& m = h->m;
+  const trx_model_config& c = m.cfg;
+  const void* src = nullptr;
+  size_t n = 0;
+  switch (what) {
+    case TRX_READ_LOGITS: src = m.logits; n = (size_t)c.vocab * 4; break;
+    case TRX_READ_HIDDEN: src = m.x; n = (size_t)c.n_embd * 4; break;
+    case TRX_READ_POSITION: src = m.pos(); n = 4; break;
+    case TRX_READ_TOKEN: src = m.cur_tok(); n = 4; break;
+    case TRX_READ_OUT: src = m.out(); n = (size_t)c.max_new * 4; break;
+    case TRX_READ_SLOT: src = m.slot; n = 8; break;
+    default: TRX_CHECK(false, TRX_E_INVALID, "trx_model_read: unknown item %d", what);
+  }
+  TRX_CHECK(bytes <= n, TRX_E_INVALID, "trx_model_read: %zu bytes requested, %zu available", bytes, n);
+  TRX_HIP(hipStreamSynchronize(m.stream));
+  TRX_HIP(hipMemcpy(host, src, bytes, hipMemcpyDeviceToHost));
+  return TRX_OK;
+}
+
+TRX_API int trx_model_info(trx_model* h, int what, int64_t* value) {
+  TRX_CHECK(h && value, TRX_E_INVALID, "trx_model_info: null argument");
+  Model& m = h->m;
+  switch (what) {
+    case TRX_INFO_ARENA_BYTES: *value = (int64_t)m.arena_bytes; break;
+    case TRX_INFO_DEVICE_BYTES: *value = (int64_t)m.dev_bytes; break;
+    case TRX_INFO_STREAM: *value = (int64_t)(intptr_t)m.stream; break;
+    case TRX_INFO_WEIGHT_BYTES: {
+      int64_t s = 0;
+      for (auto& kv : m.tensors) s += (int64_t)kv.second.bytes;
+      *value = s;
+      break;
+    }
+    default: TRX_CHECK(false, TRX_E_INVALID, "trx_model_info: unknown item %d", what);
+  }
+  return TRX_OK;
+}
+
+TRX_API int trx_model_tensor_ptr(trx_model* h, int role, int layer, void** ptr, int64_t* bytes) {
+  TRX_CHECK(h && ptr && bytes, TRX_E_INVALID, "trx_model_tensor_ptr: null argument");
+  Model& m = h->m;
+  auto it = m.tensors.find({role, layer});
+  TRX_CHECK(it != m.tensors.end(), TRX_E_INVALID, "model has no tensor role=%d layer=%d", role, layer);
+  *ptr = m.arena + it->second.off;
+  *bytes = (int64_t)it->second.bytes;
+  return TRX_OK;
+}

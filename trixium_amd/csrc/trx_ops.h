@@ -1,0 +1,102 @@
+// Parameter blocks and launchers of the decode-loop kernels (trx_ops.hip, trx_deltanet.hip).
+#pragma once
+
+#include "trx_internal.h"
+
+namespace trx {
+
+enum { EMBED_TABLE = 0, EMBED_TERNARY = 1 };
+
+struct EmbedParams {
+  int mode;
+  int n_embd, vocab;
+  const int16_t* mant;     // table mode: [vocab, n_embd]
+  const int32_t* exps;     // table mode: [vocab]
+  const uint8_t* rows;     // ternary mode: row packets of token_embd
+  int kind, row_bytes, code_off;
+  int* pos;                // device: position of the current token (incremented here)
+  const int* n_prompt;     // device
+  const int* prompt;       // device [n_prompt]
+  unsigned long long* slot;  // argmax of the previous step (cleared here)
+  int* out;                // generated tokens [max_out]
+  int max_out;
+  int* cur_tok;            // the token embedded this step
+  float* x;                // [n_embd]
+};
+
+struct AttnParams {
+  const float* qkv;        // [n_head*(gated?2:1)*hd | n_kv*hd | n_kv*hd]
+  const float* q_norm;
+  const float* k_norm;
+  const float* rope_freq;  // [rope_n/2]
+  const int* pos;
+  __half* kcache;          // [n_kv][max_ctx][hd]
+  __half* vcache;
+  float* part_m;           // [n_head][n_split]
+  float* part_l;
+  float* part_o;           // [n_head][n_split][hd]
+  float* out;              // [n_head*hd]
+  int n_head, n_kv, n_rep, hd, rope_n, max_ctx, n_split, chunk, gated;
+  float eps;
+};
+
+struct DenseParams {
+  const uint8_t* W;
+  int kind;                // TRX_KIND_F16 or TRX_KIND_Q8
+  int M, K, row_bytes, code_off;
+  const float* x;
+  const float* norm_w;
+  float eps;
+  float* y;
+  int sigmoid;
+  unsigned long long* amax_slot;
+  const int* gate_pos;     // when set: nothing while *gate_pos < *gate_from
+  const int* gate_from;
+};
+
+struct SynthParams {
+  uint8_t* out;
+  int kind, rows, cols, row_bytes, code_off;
+  uint32_t seed, tensor_id;
+  float lo, span;
+};
+
+struct DnConvParams {
+  const float* qkv;        // raw projection [C]
+  const float* taps;       // [C][Kc]
+  float* state;            // [Kc-1][C], oldest row first
+  float* out;              // [C]: conv + SiLU, q and k heads L2-normalised
+  int C, Kc, nq, hk;
+  float eps;
+};
+
+struct DnRecurParams {
+  const float* conv;       // [C]: q [nk*hk] | k [nk*hk] | v [nv*hv]
+  const float* z;          // [nv*hv]
+  const float* ba;         // [2*nv]: beta then alpha (raw projections)
+  const float* A;          // [nv]: -exp(A_log)
+  const float* dt;         // [nv]
+  const float* norm_w;     // [hv]
+  float* S;                // [nv][hv][hk] recurrent state of the layer
+  float* out;              // [nv*hv], grouped head order
+  int nv, nk, hk, hv;
+  float eps;
+};
+
+int launch_dn_conv(const DnConvParams& p, hipStream_t s);
+int launch_dn_recur(const DnRecurParams& p, hipStream_t s);
+int launch_embed(const EmbedParams& p, hipStream_t s);
+int launch_finalize(const int* pos, const int* n_prompt, unsigned long long* slot, int* out, int max_out,
+                    hipStream_t s);
+int launch_attention(const AttnParams& p, hipStream_t s);
+int launch_dense_gemv(const DenseParams& p, hipStream_t s);
+int launch_synth_ternary(const SynthParams& p, hipStream_t s);
+int launch_synth_f32(float* out, long long n, uint32_t seed, uint32_t tensor_id, float lo, float span,
+                     int transform, hipStream_t s);
+
+int gemv_f32(const uint8_t* rows, int kind, int M, int K, const float* x, const float* norm_w,
+             float eps, float* y, int epi, const float* resid, int swiglu_F,
+             unsigned long long* amax_slot, hipStream_t s, const int* gate_pos = nullptr,
+             const int* gate_from = nullptr);
+
+}  // namespace trx

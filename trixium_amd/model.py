@@ -1,0 +1,310 @@
+"""Batch-1 greedy decoder on the GPU (host side of the trx_model_* entry points).
+
+`Decoder` holds one BONS model resident in HBM and runs the token loop of the HIP library: one
+position per forward, the argmax on the device, every per-token launch replayed from one captured
+hipGraph. Its methods mirror model/golden.py:FloatModel (reset / forward / generate,
+golden.py:304-320,436-470); the arithmetic is model/fastref.py:HybridRef's (fp32 activations,
+ternary weights, fp16 KV cache on the GPU).
+
+Differences from FloatModel, both from the firmware's loop (model/mirror.py:1036-1044,
+firmware/infer.c:2001): `generate` runs no forward after its last output token, so the position
+afterwards is len(prompt) + n - 1; and the logits are computed only where the caller asks for
+them (the last fed position), not at every prefill position.
+"""
+
+import ctypes
+
+import numpy as np
+
+from . import _lib
+from . import layout as L
+from .configs import ModelConfig
+
+f32 = np.float32
+
+READ_LOGITS, READ_HIDDEN, READ_POSITION, READ_TOKEN, READ_OUT, READ_SLOT = range(6)
+INFO_ARENA_BYTES, INFO_DEVICE_BYTES, INFO_STREAM, INFO_WEIGHT_BYTES = range(4)
+
+# Ranges of the counter-based synthetic weights (the ternary group scales and the RMSNorm gains).
+SYNTH_SCALE = (0.01, 0.05)
+SYNTH_GAIN = (0.8, 1.2)
+
+_LAYER_MATRICES_ATTN = (L.ROLE_ATTN_Q, L.ROLE_ATTN_K, L.ROLE_ATTN_V, L.ROLE_ATTN_OUT)
+_LAYER_MATRICES_DN = (L.ROLE_ATTN_QKV, L.ROLE_ATTN_ZGATE, L.ROLE_SSM_OUT)
+_LAYER_MATRICES_FFN = (L.ROLE_FFN_GATE, L.ROLE_FFN_UP, L.ROLE_FFN_DOWN)
+
+
+def rope_frequencies(theta, rope_n):
+    """theta**(-2i/n) evaluated in float32 (model/fastref.py:62-63)."""
+    return np.array([f32(f32(theta) ** f32(-2.0 * i / rope_n)) for i in range(rope_n // 2)], dtype=f32)
+
+
+def layer_type_bits(layer_types, n_layer):
+    bits = 0
+    for l in range(n_layer):
+        if layer_types and layer_types[l] == "deltanet":
+            bits |= 1 << l
+    return (bits & (2**64 - 1), bits >> 64)
+
+
+def make_config(mc, weight_kind, head_kind, head_tied, emb_mode, emb_kind, max_ctx=None, max_new=256):
+    """trx_model_config from a ModelConfig (or a BONS header turned into one)."""
+    c = _lib.ModelConfig()
+    for name in ("n_layer", "n_embd", "n_head", "n_kv_head", "head_dim", "ffn_dim", "vocab",
+                 "rope_dims", "dn_num_v_heads", "dn_num_k_heads", "dn_k_head_dim", "dn_v_head_dim",
+                 "dn_conv_kernel"):
+        setattr(c, name, int(getattr(mc, name)))
+    c.max_ctx = int(max_ctx or mc.max_ctx)
+    c.rms_eps = float(mc.rms_eps)
+    c.attn_gated = int(bool(mc.attn_gated))
+    lo, hi = layer_type_bits(mc.layer_types, mc.n_layer)
+    c.layer_types[0], c.layer_types[1] = lo, hi
+    c.weight_kind, c.head_kind, c.head_tied = weight_kind, head_kind, int(bool(head_tied))
+    c.emb_mode, c.emb_kind, c.max_new = emb_mode, emb_kind, int(max_new)
+    return c
+
+
+def config_from_header(h, name="bons-image"):
+    if h["hadamard_block"]:
+        raise NotImplementedError("rotated-basis (Hadamard) images are not supported by the GPU decoder")
+    return ModelConfig(name=name, n_layer=h["n_layer"], n_embd=h["n_embd"], n_head=h["n_head"],
+                       n_kv_head=h["n_kv_head"], head_dim=h["head_dim"], ffn_dim=h["ffn_dim"],
+                       vocab=h["vocab"], rope_theta=float(h["rope_theta"]), rms_eps=float(h["rms_eps"]),
+                       max_ctx=h["max_ctx"], layer_types=tuple(h["layer_types"]),
+                       dn_num_v_heads=h["dn_num_v_heads"], dn_num_k_heads=h["dn_num_k_heads"],
+                       dn_k_head_dim=h["dn_k_head_dim"], dn_v_head_dim=h["dn_v_head_dim"],
+                       dn_conv_kernel=h["dn_conv_kernel"], rope_dims=h["rope_dims"],
+                       attn_gated=bool(h["attn_gated"]))
+
+
+class Decoder:
+    """One model resident on the GPU and its decode state."""
+
+    def __init__(self, mc, cfg, use_graph=True):
+        self.mc = mc
+        self.cfg = cfg
+        self.vocab, self.n_embd = cfg.vocab, cfg.n_embd
+        self.use_graph = use_graph
+        rope_n = mc.rope_dims or mc.head_dim
+        self.rope_freq = rope_frequencies(mc.rope_theta, rope_n)
+        h = ctypes.c_void_p()
+        _lib.call("trx_model_create", ctypes.byref(cfg),
+                  self.rope_freq.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), ctypes.byref(h))
+        self._h = h.value
+
+    # Construction ------------------------------------------------------------------------------
+    @classmethod
+    def from_image(cls, img, max_ctx=None, max_new=256, use_graph=True):
+        """Load a BONS image (path or BONSReader) into HBM."""
+        from .bons import BONSReader
+        if isinstance(img, str):
+            img = BONSReader(img)
+        mc = config_from_header(img.header)
+        nl = mc.n_layer
+        kinds = {img.find(r, l)["kind"] for l in range(nl)
+                 for r in ((_LAYER_MATRICES_DN if mc.layer_type(l) == "deltanet" else _LAYER_MATRICES_ATTN)
+                           + _LAYER_MATRICES_FFN)}
+        if len(kinds) != 1 or not L.is_ternary(next(iter(kinds))):
+            raise ValueError(f"layer matrices must share one ternary kind, found {sorted(kinds)}")
+        weight_kind = kinds.pop()
+        head = img.find(L.ROLE_LM_HEAD, 0)
+        emb = img.find(L.ROLE_TOK_EMB, 0)
+        if img.find(L.ROLE_TOK_EMB16, 0) is None:
+            raise ValueError("the image has no int16 embedding table (token_embd.bfp16)")
+        head_tied = head is None
+        if head_tied:
+            if emb is None or not L.is_ternary(emb["kind"]):
+                raise ValueError("a tied LM head needs ternary token_embd rows")
+            head_kind, emb_kind = emb["kind"], emb["kind"]
+        else:
+            head_kind = L.KIND_F16 if head["kind"] == L.KIND_F32 else head["kind"]
+            emb_kind = emb["kind"] if emb is not None and L.is_ternary(emb["kind"]) else weight_kind
+        cfg = make_config(mc, weight_kind, head_kind, head_tied, 0, emb_kind, max_ctx, max_new)
+        d = cls(mc, cfg, use_graph)
+        try:
+            d._load_image(img)
+        except Exception:
+            d.close()
+            raise
+        return d
+
+    @classmethod
+    def synthetic(cls, mc, seed=0, weight_kind=L.KIND_TERNARY5, max_ctx=None, max_new=256,
+                  use_graph=True):
+        """Fill every tensor on the device from the counter-based generator (same values as
+        trixium_amd.synth.hashed_*): ternary token_embd rows (embedded by decoding the row), an
+        untied ternary LM head unless the config ties them."""
+        if mc.n_dn_layers:
+            raise NotImplementedError("synthetic DeltaNet layers (Q8 beta/alpha) have no device generator")
+        cfg = make_config(mc, weight_kind, weight_kind, mc.tie_embeddings, 1, weight_kind, max_ctx, max_new)
+        d = cls(mc, cfg, use_graph)
+        try:
+            ranges = np.array([SYNTH_SCALE[0], SYNTH_SCALE[1] - SYNTH_SCALE[0],
+                               SYNTH_GAIN[0], SYNTH_GAIN[1] - SYNTH_GAIN[0]], dtype=f32)
+            _lib.call("trx_model_synthesize", d._h, seed & 0xFFFFFFFF,
+                      ranges.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+        except Exception:
+            d.close()
+            raise
+        return d
+
+    def set_tensor(self, role, layer, arr):
+        a = np.ascontiguousarray(arr)
+        _lib.call("trx_model_set_tensor", self._h, role, layer, a.ctypes.data, a.nbytes)
+
+    def _rows(self, img, e, kind):
+        """Row packets of an entry in `kind` (the K-segments of a split entry joined)."""
+        from .bons import decode_rows, encode_rows
+        segs = img.ksegs(e)
+        if len(segs) == 1 and e["kind"] == kind:
+            return img.entry_rows(e)
+        sc, vals = [], []
+        for t in segs:
+            s, v = decode_rows(t["kind"], t["cols"], img.entry_rows(t))
+            sc.append(s)
+            vals.append(v)
+        s, v = np.concatenate(sc, axis=1), np.concatenate(vals, axis=1)
+        return encode_rows(kind, v.shape[1], s, v)
+
+    def _f32(self, img, role, layer):
+        e = img.find(role, layer, L.KIND_F32)
+        if e is None:
+            raise ValueError(f"the image has no float32 {L.ROLE_NAMES[role]} for layer {layer}")
+        return np.asarray(img.entry_tensor(e)[1], dtype=f32)
+
+    def _load_image(self, img):
+        mc, cfg = self.mc, self.cfg
+        wk = cfg.weight_kind
+        for l in range(mc.n_layer):
+            self.set_tensor(L.ROLE_ATTN_NORM, l, self._f32(img, L.ROLE_ATTN_NORM, l))
+            self.set_tensor(L.ROLE_FFN_NORM, l, self._f32(img, L.ROLE_FFN_NORM, l))
+            if mc.layer_type(l) == "deltanet":
+                for r in (L.ROLE_SSM_CONV, L.ROLE_SSM_A, L.ROLE_SSM_DT, L.ROLE_SSM_NORM):
+                    self.set_tensor(r, l, self._f32(img, r, l))
+                for r in (L.ROLE_SSM_BETA, L.ROLE_SSM_ALPHA):
+                    self.set_tensor(r, l, self._rows(img, img.find(r, l), L.KIND_Q8))
+                roles = _LAYER_MATRICES_DN
+            else:
+                for r in (L.ROLE_ATTN_Q_NORM, L.ROLE_ATTN_K_NORM):
+                    self.set_tensor(r, l, self._f32(img, r, l))
+                roles = _LAYER_MATRICES_ATTN
+            for r in roles + _LAYER_MATRICES_FFN:
+                self.set_tensor(r, l, self._rows(img, img.find(r, l), wk))
+        self.set_tensor(L.ROLE_OUT_NORM, 0, self._f32(img, L.ROLE_OUT_NORM, 0))
+        _, mant = img.entry_tensor(img.find(L.ROLE_TOK_EMB16, 0))
+        _, ex = img.entry_tensor(img.find(L.ROLE_TOK_EMB16_EXP, 0))
+        self.set_tensor(L.ROLE_TOK_EMB16, 0, np.asarray(mant, dtype=np.int16))
+        self.set_tensor(L.ROLE_TOK_EMB16_EXP, 0, np.asarray(ex).reshape(-1)[:cfg.vocab].astype(np.int32))
+        if cfg.head_tied:
+            self.set_tensor(L.ROLE_TOK_EMB, 0, self._rows(img, img.find(L.ROLE_TOK_EMB, 0), cfg.emb_kind))
+        else:
+            head = img.find(L.ROLE_LM_HEAD, 0)
+            if cfg.head_kind == L.KIND_F16:
+                w = np.asarray(img.entry_tensor(img.find(L.ROLE_LM_HEAD, 0, L.KIND_F32))[1], dtype=f32)
+                self.set_tensor(L.ROLE_LM_HEAD, 0, w.astype(np.float16))
+            else:
+                self.set_tensor(L.ROLE_LM_HEAD, 0, self._rows(img, head, cfg.head_kind))
+
+    # State and decoding ------------------------------------------------------------------------
+    def reset(self):
+        _lib.call("trx_model_reset", self._h)
+
+    def _feed(self, tokens, head_from=-1):
+        t = np.ascontiguousarray(np.asarray(tokens, dtype=np.int32).reshape(-1))
+        if t.size == 0:
+            raise ValueError("no tokens to feed")
+        _lib.call("trx_model_set_prompt", self._h, t.ctypes.data_as(ctypes.POINTER(ctypes.c_int)),
+                  int(t.size), int(head_from))
+        return t.size
+
+    def step(self, n_steps, use_graph=None):
+        """Enqueue n forwards (one position each); returns without waiting."""
+        g = self.use_graph if use_graph is None else use_graph
+        _lib.call("trx_model_step", self._h, int(n_steps), int(bool(g)))
+
+    def forward(self, tokens, use_graph=None):
+        """Feed `tokens` after the current position; logits (vocab,) of the last one
+        (FloatModel.forward, golden.py:436-460)."""
+        n = self._feed(tokens)
+        self.step(n, use_graph)
+        return self.logits()
+
+    def generate(self, tokens, n, use_graph=None):
+        """Greedy continuation of `tokens` after the current position; the n generated ids
+        (FloatModel.generate, golden.py:462-470)."""
+        if n <= 0:
+            return []
+        if n > self.cfg.max_new:
+            raise ValueError(f"{n} tokens requested, the output buffer holds {self.cfg.max_new}")
+        n_fed = self._feed(tokens)
+        self.step(n_fed + n - 1, use_graph)
+        _lib.call("trx_model_finalize", self._h)
+        out = np.empty(self.cfg.max_new, dtype=np.int32)
+        self._read(READ_OUT, out)
+        return [int(v) for v in out[:n]]
+
+    def generate_fresh(self, prompt, n, use_graph=None):
+        """reset + generate through the single C entry point (firmware infer_generate)."""
+        p = np.ascontiguousarray(np.asarray(prompt, dtype=np.int32))
+        out = np.empty(n, dtype=np.int32)
+        g = self.use_graph if use_graph is None else use_graph
+        _lib.call("trx_model_generate", self._h, p.ctypes.data_as(ctypes.POINTER(ctypes.c_int)),
+                  int(p.size), int(n), out.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), int(bool(g)))
+        return [int(v) for v in out]
+
+    def synchronize(self):
+        _lib.call("trx_model_sync", self._h)
+
+    def _read(self, what, arr):
+        _lib.call("trx_model_read", self._h, what, arr.ctypes.data, arr.nbytes)
+        return arr
+
+    def logits(self):
+        return self._read(READ_LOGITS, np.empty(self.vocab, dtype=f32))
+
+    def hidden(self):
+        return self._read(READ_HIDDEN, np.empty(self.n_embd, dtype=f32))
+
+    def position(self):
+        """Position of the last forward (-1 after reset)."""
+        return int(self._read(READ_POSITION, np.empty(1, dtype=np.int32))[0])
+
+    def info(self, what):
+        v = ctypes.c_int64()
+        _lib.call("trx_model_info", self._h, what, ctypes.byref(v))
+        return v.value
+
+    @property
+    def stream(self):
+        return self.info(INFO_STREAM)
+
+    def tensor_ptr(self, role, layer=0):
+        p, n = ctypes.c_void_p(), ctypes.c_int64()
+        _lib.call("trx_model_tensor_ptr", self._h, role, layer, ctypes.byref(p), ctypes.byref(n))
+        return p.value, n.value
+
+    def read_tensor(self, role, layer=0):
+        """Raw bytes of a resident tensor (uint8)."""
+        p, n = self.tensor_ptr(role, layer)
+        out = np.empty(n, dtype=np.uint8)
+        self.synchronize()
+        _lib.call("trx_memcpy_d2h", out.ctypes.data, p, n, None)
+        _lib.call("trx_stream_sync", None)
+        return out
+
+    def close(self):
+        if getattr(self, "_h", None):
+            _lib.lib().trx_model_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()

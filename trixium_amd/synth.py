@@ -6,9 +6,10 @@ P(0) = 0.4 and P(-1) = P(+1) = 0.3, fp16 group scales U(0.01, 0.05), RMSNorm gai
 fp16 embeddings N(0, 0.02).
 
 Large models are never materialised on the host: their weights come from a counter-based hash
-(splitmix64 of (seed, tensor id, element)), which the device generator (csrc/trx_synth.hip)
-evaluates in place in HBM and `hashed_rows` below evaluates for any rows on the host, so a CPU
-check can rebuild exactly the rows it needs.
+(splitmix64 of (seed, tensor id, element)), which the device generator (csrc/trx_ops.hip:
+synth_ternary_kernel, synth_f32_kernel) evaluates in place in HBM and `hashed_codes` /
+`hashed_scales` / `hashed_uniform` below evaluate for any rows on the host, so a CPU check can
+rebuild exactly the rows it needs.
 """
 
 import numpy as np
@@ -103,7 +104,7 @@ def random_prompt(cfg, n=16, seed=0):
     return [int(t) for t in np.random.default_rng(seed).integers(0, cfg.vocab, n)]
 
 
-# Counter-based generator (host side of csrc/trx_synth.hip) ---------------------------------------
+# Counter-based generator (host side of the device generator in csrc/trx_ops.hip) ---------------------------------------
 
 _M64 = np.uint64(0xFFFFFFFFFFFFFFFF)
 
@@ -156,3 +157,50 @@ def hashed_scales(seed, tensor_id, rows, cols):
     G = cols // L.GROUP
     idx = rows[:, None] * G + np.arange(G)[None, :]
     return hashed_uniform(seed, tensor_id, 2, idx, SCALE_LO, SCALE_HI).astype(np.float16)
+
+
+GAIN_LO, GAIN_HI = 0.8, 1.2
+
+
+def tensor_id(role, layer):
+    return layer * 32 + role
+
+
+def hashed_ternary(seed, role, layer, rows, cols, name):
+    tid = tensor_id(role, layer)
+    r = np.arange(rows)
+    return TensorSpec(name, role, layer, L.KIND_TERNARY, rows, cols,
+                      scales=hashed_scales(seed, tid, r, cols), values=hashed_codes(seed, tid, r, cols))
+
+
+def hashed_gain(seed, role, layer, cols, name):
+    v = hashed_uniform(seed, tensor_id(role, layer), 3, np.arange(cols), GAIN_LO, GAIN_HI)
+    return TensorSpec(name, role, layer, L.KIND_F32, 1, cols, values=v.reshape(1, cols),
+                      flags=L.FLAG_REPLICATED)
+
+
+def hashed_model_tensors(cfg, seed=0):
+    """The tensor list of a full-attention model with every value from the counter-based hash,
+    as the device generator fills it: ternary token_embd, untied ternary output.weight unless
+    cfg.tie_embeddings, RMSNorm gains U(0.8, 1.2). For small configs (CPU checks)."""
+    if cfg.n_dn_layers:
+        raise NotImplementedError("hashed DeltaNet tensors are not generated")
+    E = cfg.n_embd
+    t = [hashed_ternary(seed, L.ROLE_TOK_EMB, 0, cfg.vocab, E, "token_embd.weight")]
+    for l in range(cfg.n_layer):
+        p = f"blk.{l}."
+        t.append(hashed_gain(seed, L.ROLE_ATTN_NORM, l, E, p + "attn_norm.weight"))
+        t.append(hashed_ternary(seed, L.ROLE_ATTN_Q, l, cfg.q_dim, E, p + "attn_q.weight"))
+        t.append(hashed_ternary(seed, L.ROLE_ATTN_K, l, cfg.kv_dim, E, p + "attn_k.weight"))
+        t.append(hashed_ternary(seed, L.ROLE_ATTN_V, l, cfg.kv_dim, E, p + "attn_v.weight"))
+        t.append(hashed_gain(seed, L.ROLE_ATTN_Q_NORM, l, cfg.head_dim, p + "attn_q_norm.weight"))
+        t.append(hashed_gain(seed, L.ROLE_ATTN_K_NORM, l, cfg.head_dim, p + "attn_k_norm.weight"))
+        t.append(hashed_ternary(seed, L.ROLE_ATTN_OUT, l, E, cfg.q_dim, p + "attn_output.weight"))
+        t.append(hashed_gain(seed, L.ROLE_FFN_NORM, l, E, p + "ffn_norm.weight"))
+        t.append(hashed_ternary(seed, L.ROLE_FFN_GATE, l, cfg.ffn_dim, E, p + "ffn_gate.weight"))
+        t.append(hashed_ternary(seed, L.ROLE_FFN_UP, l, cfg.ffn_dim, E, p + "ffn_up.weight"))
+        t.append(hashed_ternary(seed, L.ROLE_FFN_DOWN, l, E, cfg.ffn_dim, p + "ffn_down.weight"))
+    t.append(hashed_gain(seed, L.ROLE_OUT_NORM, 0, E, "output_norm.weight"))
+    if not cfg.tie_embeddings:
+        t.append(hashed_ternary(seed, L.ROLE_LM_HEAD, 0, cfg.vocab, E, "output.weight"))
+    return t
