@@ -1,0 +1,211 @@
+#!/usr/bin/env python3
+"""Batch-1 greedy decode throughput of the Qwen3-8B-shape ternary decoder on one MI355X.
+
+Workload (the reference's 8B decode configuration): hidden 4096, 36 layers, 32 q / 8 kv heads of
+128, SwiGLU FFN 12288, vocab 151936, separate ternary LM head, fp16 KV cache to context 4096;
+greedy decode of 256 tokens after a 2048-token random prompt. Weights are synthetic random
+ternary (P(0) = 0.4, P(+-1) = 0.3, fp16 group scales U(0.01, 0.05)), generated in HBM by the
+counter-based generator, stored as 5-trit packed rows (2-bit with --kind 2bit).
+
+A step is one decode token: one forward of the whole model at the next position (embedding, 36
+layers, LM head, on-device argmax), replayed from the captured hipGraph. The prompt is prefilled
+one position per forward before the clock starts, then `--warmup` tokens are decoded untimed and
+`--steps` tokens timed (defaults 16 + 240 = 256 decode tokens at positions 2048..2303).
+
+Besides the JSON contract fields the line carries
+  roofline      the dominant kernel (the fused FFN gate|up GEMV with RMSNorm prologue and SwiGLU
+                epilogue, 24576 x 4096) timed with HIP events on the model's stream, launched
+                over the 36 resident layer matrices in turn (962 MB, more than the 256 MB
+                Infinity Cache), bytes per launch = weight rows + x + norm gains + output;
+  token_roofline  bytes one decode token must read (every ternary weight row, the embedding row,
+                the KV cache at the mean timed position) against the same 8 TB/s;
+  cpu_baseline  the float oracle's decode step (the reference's numpy CPU path restated) on a
+                sample of the same shape: one layer and the LM head at context 2048, scaled to
+                36 layers.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, 8 TB/s
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=240)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--prompt", type=int, default=2048)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--kind", choices=("trit5", "2bit"), default="trit5")
+    ap.add_argument("--kernel-reps", type=int, default=10,
+                    help="passes over the 36 layers when timing the dominant kernel")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="launch every kernel eagerly")
+    return ap.parse_args()
+
+
+def time_dominant_kernel(dec, mc, reps):
+    """Average duration of the gate|up GEMV over the resident layer matrices (HIP events on
+    the model stream)."""
+    import ctypes
+    from trixium_amd import _lib, layout as L
+    E, F = mc.n_embd, mc.ffn_dim
+    x = _lib.DeviceBuffer.from_array(np.random.default_rng(1).standard_normal(E).astype(np.float32))
+    y = _lib.DeviceBuffer(F * 4)
+    s = dec.stream
+    kind = dec.cfg.weight_kind
+    mats = [dec.tensor_ptr(L.ROLE_FFN_GATE, l)[0] for l in range(mc.n_layer)]
+    norms = [dec.tensor_ptr(L.ROLE_FFN_NORM, l)[0] for l in range(mc.n_layer)]
+
+    def launch():
+        for w, g in zip(mats, norms):
+            _lib.call("trx_gemv_ternary_f32", w, kind, 2 * F, E, x.ptr, g, ctypes.c_float(mc.rms_eps),
+                      y.ptr, _lib.EPI_SWIGLU, None, s)
+
+    launch()
+    _lib.call("trx_stream_sync", s)
+    e0, e1 = ctypes.c_void_p(), ctypes.c_void_p()
+    _lib.call("trx_event_create", ctypes.byref(e0))
+    _lib.call("trx_event_create", ctypes.byref(e1))
+    _lib.call("trx_event_record", e0, s)
+    for _ in range(reps):
+        launch()
+    _lib.call("trx_event_record", e1, s)
+    _lib.call("trx_stream_sync", s)
+    ms = ctypes.c_float()
+    _lib.call("trx_event_elapsed_ms", e0, e1, ctypes.byref(ms))
+    _lib.call("trx_event_destroy", e0)
+    _lib.call("trx_event_destroy", e1)
+    n = reps * len(mats)
+    rb = L.row_bytes(E, kind)
+    algo = 2 * F * rb + E * 4 + E * 4 + F * 4
+    return ms.value * 1e3 / n, algo, n
+
+
+def traffic_from_profile(kind):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 counter summary
+    (FETCH_SIZE + WRITE_SIZE, calibrated on a copy kernel), when one exists for this format."""
+    path = os.path.join(ROOT, "profiles", f"gemv_gateup_8b_{kind}_pmc.md")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    return None
+
+
+def cpu_baseline(mc, ctx):
+    """The oracle's decode step on one layer + the LM head of the shape, scaled to all layers."""
+    from oracle.floatref import ShapeSample
+    cores = len(os.sched_getaffinity(0))
+    threads = int(os.environ.get("OMP_NUM_THREADS", cores))
+    s = ShapeSample(mc, 1, ctx, seed=0)
+    s.step(1)                                   # first touch of every buffer
+    t0 = time.perf_counter()
+    s.step(2, want_logits=False)
+    t_layer = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    s.step(3, want_logits=True)
+    t_head = max(time.perf_counter() - t0 - t_layer, 0.0)
+    per_tok = mc.n_layer * t_layer + t_head
+    return {"value": round(1.0 / per_tok, 6), "unit": "tok/s", "cores": min(cores, threads),
+            "kind": "port",
+            "sample": (f"float oracle decode step (numpy, fp16 weight cache) on 1 of {mc.n_layer} "
+                       f"layers + the {mc.vocab}x{mc.n_embd} LM head at context {ctx}: "
+                       f"layer {t_layer:.2f} s, head {t_head:.2f} s, token = {mc.n_layer} x layer + head "
+                       f"= {per_tok:.1f} s")}
+
+
+def main():
+    a = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if a.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: the batch-1 decode loop runs on a single MI355X "
+              f"(asked for {max(a.gpus, world)}); run it with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    from trixium_amd import configs as C, layout as L, _lib
+    from trixium_amd.model import Decoder, INFO_WEIGHT_BYTES
+    mc = C.QWEN3_8B
+    kind = L.KIND_TERNARY5 if a.kind == "trit5" else L.KIND_TERNARY
+    n_dec = a.warmup + a.steps
+    if a.prompt + n_dec > mc.max_ctx:
+        sys.exit(f"prompt {a.prompt} + {n_dec} decode tokens exceed the context {mc.max_ctx}")
+    graph = not a.no_graph
+    dec = Decoder.synthetic(mc, a.seed, weight_kind=kind, max_ctx=mc.max_ctx, max_new=n_dec + 8,
+                            use_graph=graph)
+    prompt = np.random.default_rng(a.seed).integers(0, mc.vocab, a.prompt).astype(np.int32)
+    dec.reset()
+    dec.feed(prompt)
+    dec.step(a.prompt)                           # prefill, one position per forward
+    dec.synchronize()
+    dec.step(a.warmup)
+    dec.synchronize()
+    t0 = time.perf_counter()
+    dec.step(a.steps)
+    dec.synchronize()
+    dt = time.perf_counter() - t0
+    tok_s = a.steps / dt
+    dec.finalize()
+    toks = dec.outputs()[:n_dec]
+    assert np.all((toks >= 0) & (toks < mc.vocab)), "decoded ids out of range"
+
+    # Bytes per decode token: every weight row except the embedding table, which is read one
+    # row per token; the K and V caches up to the mean timed position.
+    wbytes = dec.info(INFO_WEIGHT_BYTES)
+    emb_rows = dec.tensor_ptr(L.ROLE_TOK_EMB, 0)[1]
+    emb_row = L.row_bytes(mc.n_embd, kind)
+    mean_pos = a.prompt + a.warmup + (a.steps - 1) / 2.0
+    kv = 2 * mc.n_layer * mc.n_kv_head * mc.head_dim * 2 * (mean_pos + 1)
+    tok_bytes = wbytes - emb_rows + emb_row + kv
+    roof_tok_s = HBM_PEAK_GBS * 1e9 / tok_bytes
+
+    us, algo, n_launch = time_dominant_kernel(dec, mc, a.kernel_reps)
+    achieved = algo / (us * 1e-6) / 1e9
+    rec = {
+        "metric": "batch-1 decode tok/s (8B shape); ternary matvec HBM GB/s vs ~8 TB/s peak",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(dt * 1e3 / a.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "ternary weights (fp16 group scales), int16 activations, fp32 accumulate, fp16 KV",
+        "data": "synthetic: random ternary weights from a counter-based hash, random prompt",
+        "config": {"workload": "qwen3-8b-shape ternary decoder, batch-1 greedy decode after a "
+                               f"{a.prompt}-token prompt",
+                   "n_layer": mc.n_layer, "n_embd": mc.n_embd, "n_head": mc.n_head,
+                   "n_kv_head": mc.n_kv_head, "head_dim": mc.head_dim, "ffn_dim": mc.ffn_dim,
+                   "vocab": mc.vocab, "max_ctx": mc.max_ctx, "prompt_tokens": a.prompt,
+                   "decode_tokens": n_dec, "weights": a.kind, "hipgraph": graph},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_from_profile(a.kind),
+                     "kernel": f"ternary GEMV gate|up {2 * mc.ffn_dim}x{mc.n_embd} {a.kind}, "
+                               f"RMSNorm + SwiGLU fused",
+                     "us_per_launch": round(us, 3), "bytes_per_launch": algo, "launches": n_launch},
+        "token_roofline": {"bytes_per_token": int(tok_bytes), "tok_s": round(roof_tok_s, 1),
+                           "frac": round(tok_s / roof_tok_s, 4)},
+        "cpu_baseline": None,
+    }
+    dec.close()
+    if not a.no_cpu_baseline:
+        rec["cpu_baseline"] = cpu_baseline(mc, a.prompt)
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -8,6 +8,6 @@ Contents (each function cites the reference file:line it restates):
   bitexact.py   integer engine contract: fp16 split, B/R choice, exact ternary/Q8 matvec,
                 group sums, the power-of-two int8 activation quantizer
   floatref.py   float reference of the decoder (fastref numerics with FloatModel's step and
-                state semantics): dense Qwen3 and the hybrid Gated-DeltaNet/attention model
-  csrc/         a C restatement of the trit5 decode and the exact matvec, for large shapes
+                state semantics): dense Qwen3 and the hybrid Gated-DeltaNet/attention model;
+                ShapeSample, the same step on random weights of a large shape (CPU timing)
 """

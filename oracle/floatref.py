@@ -228,3 +228,63 @@ class FloatRef:
             if i + 1 < n_new:
                 logits = self.step(nxt)
         return out
+
+
+class ShapeSample(FloatRef):
+    """FloatRef's decode step on random weights of a full-attention shape, built without an
+    image (the CPU baseline of a large model is timed on a sample of its layers).
+
+    Weights are ternary-valued fp16 matrices ((code - 1) * scale, scales U(0.01, 0.05)), the
+    embedding table random int16 mantissas, the KV caches filled with `ctx` random positions, so
+    the next step() runs at position `ctx` with the per-token work of the full shape restricted to
+    `n_layer` layers."""
+
+    def __init__(self, mc, n_layer, ctx, seed=0):
+        rng = np.random.default_rng(seed)
+        self.n_layer, self.n_embd = n_layer, mc.n_embd
+        self.n_head, self.n_kv, self.hd = mc.n_head, mc.n_kv_head, mc.head_dim
+        self.rope_n = mc.rope_dims or mc.head_dim
+        self.eps = f32(mc.rms_eps)
+        self.gated = False
+        self.vocab = mc.vocab
+        self.dn = [False] * n_layer
+        self.nk = self.hk = self.nv = self.hv = 0
+        self.K = 1
+        self.kv_fp16 = True
+        self.rope_freq = np.array([f32(f32(mc.rope_theta) ** f32(-2.0 * i / self.rope_n))
+                                   for i in range(self.rope_n // 2)], dtype=f32)
+
+        def tern(rows, cols):
+            # A block of up to 1024 random rows repeated down the matrix: the step's cost does
+            # not depend on the values, and building a 151936-row head stays fast.
+            b = min(rows, 1024)
+            w = rng.integers(-1, 2, size=(b, cols), dtype=np.int8).astype(np.float16)
+            s = rng.uniform(0.01, 0.05, size=(b, cols // 128, 1)).astype(np.float16)
+            blk = (w.reshape(b, -1, 128) * s).reshape(b, cols)
+            return np.tile(blk, (-(-rows // b), 1))[:rows]
+
+        E, q, kv, F = mc.n_embd, mc.n_head * mc.head_dim, mc.n_kv_head * mc.head_dim, mc.ffn_dim
+        self.wcache = {}
+        for l in range(n_layer):
+            for role, r, c in ((L.ROLE_ATTN_Q, q, E), (L.ROLE_ATTN_K, kv, E), (L.ROLE_ATTN_V, kv, E),
+                               (L.ROLE_ATTN_OUT, E, q), (L.ROLE_FFN_GATE, F, E), (L.ROLE_FFN_UP, F, E),
+                               (L.ROLE_FFN_DOWN, E, F)):
+                self.wcache[(role, l)] = tern(r, c)
+        self.head_role = L.ROLE_LM_HEAD
+        self.wcache[(L.ROLE_LM_HEAD, 0)] = tern(mc.vocab, E)
+        gain = lambda n: rng.uniform(0.8, 1.2, n).astype(f32)
+        self.norm_attn = [gain(E) for _ in range(n_layer)]
+        self.norm_ffn = [gain(E) for _ in range(n_layer)]
+        self.norm_q = {l: gain(mc.head_dim) for l in range(n_layer)}
+        self.norm_k = {l: gain(mc.head_dim) for l in range(n_layer)}
+        self.out_norm = gain(E)
+        self.emb_mant = np.tile(rng.integers(-32767, 32768, size=(256, E), dtype=np.int16),
+                                (-(-mc.vocab // 256), 1))[:mc.vocab]
+        self.emb_exp = np.full(mc.vocab, -20, np.int32)
+        self.reset()
+        for l in range(n_layer):
+            kc = rng.standard_normal((ctx, self.n_kv, self.hd)).astype(np.float16).astype(f32)
+            vc = rng.standard_normal((ctx, self.n_kv, self.hd)).astype(np.float16).astype(f32)
+            self.k_cache[l] = list(kc)
+            self.v_cache[l] = list(vc)
+        self.pos = ctx

@@ -30,6 +30,7 @@ namespace trx {
 enum { MODE_F32 = 0, MODE_EXACT = 1, MODE_GSUM = 2 };
 
 constexpr int kLutBytes = 65536;    // 256 entries x 256 bytes
+constexpr int kDynLds = 160 * 1024 - kLutBytes - 512;   // LDS left for the dynamic part
 constexpr int kXStride = 36;        // dwords per half-group in the dot-ready layout
 constexpr int kXDwords5 = 33;       // trit5: 13 x (hi, lo) + 7 d4 pairs
 constexpr int kXDwords2 = 32;       // 2-bit: 16 x (hi, lo)
@@ -294,6 +295,7 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvParams p) {
 
   float facc[R];
   long long iacc[R];
+  unsigned long long best = 0;   // argmax epilogue: this lane's best (ordered value, ~row) key
 #pragma unroll
   for (int r = 0; r < R; ++r) { facc[r] = 0.f; iacc[r] = 0; }
 
@@ -434,7 +436,7 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvParams p) {
         if (p.amax_slot) {
           const unsigned long long key = ((unsigned long long)ordered_bits(v) << 32) |
                                          (unsigned long long)(0xFFFFFFFFu - (uint32_t)o);
-          atomicMax(p.amax_slot, key);
+          best = key > best ? key : best;
         }
       }
     }
@@ -474,6 +476,22 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvParams p) {
     if (sl == NSLOT - 1) finish_batch(bt);
     bt = nbt; sl = nsl;
   }
+  if (MODE == MODE_F32 && p.amax_slot) {
+    // One atomic per block: wave maximum, then the block's over its waves.
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const unsigned long long other = __shfl_xor(best, o, 64);
+      best = other > best ? other : best;
+    }
+    __shared__ unsigned long long wbest[kWaves];
+    if (lane == 0) wbest[wave] = best;
+    __syncthreads();
+    if (tid == 0) {
+      unsigned long long b = wbest[0];
+      for (int w = 1; w < kWaves; ++w) b = wbest[w] > b ? wbest[w] : b;
+      if (b) atomicMax(p.amax_slot, b);
+    }
+  }
 }
 
 // Host side ------------------------------------------------------------------------------------
@@ -503,7 +521,7 @@ static int launch_r(GemvParams& p, hipStream_t s) {
   static bool attr_set = false;
   if (!attr_set) {
     TRX_HIP(hipFuncSetAttribute((const void*)gemv_kernel<FMT, MODE, R, NT>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - kLutBytes));
+                                hipFuncAttributeMaxDynamicSharedMemorySize, kDynLds));
     attr_set = true;
   }
   p.n_batches = (p.epi == TRX_EPI_SWIGLU) ? cdiv(p.n_out, R / 2) : cdiv(p.n_out, R);
@@ -551,7 +569,7 @@ int gemv_check(int kind, int M, int K) {
             "gemv: kind %d is not a ternary kind", kind);
   TRX_CHECK(M > 0 && K > 0 && (K % kGroup) == 0, TRX_E_INVALID,
             "gemv: M=%d K=%d (K must be a positive multiple of 128)", M, K);
-  TRX_CHECK(lds_bytes(K, K / kGroup) <= 160 * 1024 - kLutBytes, TRX_E_INVALID,
+  TRX_CHECK(lds_bytes(K, K / kGroup) <= kDynLds, TRX_E_INVALID,
             "gemv: K=%d exceeds the LDS budget", K);
   RowGeom rg = row_geom(kind, K);
   TRX_CHECK((unsigned long long)M * rg.row_bytes < 0xFFFF0000ull, TRX_E_INVALID,

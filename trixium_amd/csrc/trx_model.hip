@@ -44,7 +44,7 @@ struct Model {
   unsigned long long* slot = nullptr;
   int n_attn = 0, n_dn = 0;
   std::vector<int> attn_index, dn_index;           // per layer: index among attn / dn layers
-  int n_split = 0, chunk = 64;
+  int n_split = 0;
   hipGraph_t graph = nullptr;
   hipGraphExec_t graph_exec = nullptr;
   size_t dev_bytes = 0;
@@ -257,7 +257,6 @@ static int run_step(Model& m, hipStream_t s) {
       ap.rope_n = c.rope_dims ? c.rope_dims : hd;
       ap.max_ctx = c.max_ctx;
       ap.n_split = m.n_split;
-      ap.chunk = m.chunk;
       ap.gated = c.attn_gated;
       ap.eps = c.rms_eps;
       if ((rc = launch_attention(ap, s))) return rc;
@@ -334,7 +333,11 @@ TRX_API int trx_model_create(const trx_model_config* cfg, const float* rope_freq
   auto fail = [&](int code) { trx_model_destroy(h); return code; };
   if ((rc = dalloc(m, (void**)&m.arena, m.arena_bytes))) return fail(rc);
   const int hd = c.head_dim;
-  m.n_split = (c.max_ctx + m.chunk - 1) / m.chunk;
+  m.n_split = attention_splits(c.n_kv_head, c.head_dim, c.max_ctx);
+  if (m.n_split < 0) {
+    set_error("trx_model_create: context %d is too long for the attention kernel", c.max_ctx);
+    return fail(TRX_E_INVALID);
+  }
   const size_t kv = (size_t)m.n_attn * c.n_kv_head * c.max_ctx * hd;
   if (m.n_attn) {
     if ((rc = dalloc(m, (void**)&m.kcache, kv * 2))) return fail(rc);

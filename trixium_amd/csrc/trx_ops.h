@@ -36,7 +36,7 @@ struct AttnParams {
   float* part_l;
   float* part_o;           // [n_head][n_split][hd]
   float* out;              // [n_head*hd]
-  int n_head, n_kv, n_rep, hd, rope_n, max_ctx, n_split, chunk, gated;
+  int n_head, n_kv, n_rep, hd, rope_n, max_ctx, n_split, gated;
   float eps;
 };
 
@@ -89,6 +89,7 @@ int launch_embed(const EmbedParams& p, hipStream_t s);
 int launch_finalize(const int* pos, const int* n_prompt, unsigned long long* slot, int* out, int max_out,
                     hipStream_t s);
 int launch_attention(const AttnParams& p, hipStream_t s);
+int attention_splits(int n_kv, int head_dim, int max_ctx);   // -1: the context is too long
 int launch_dense_gemv(const DenseParams& p, hipStream_t s);
 int launch_synth_ternary(const SynthParams& p, hipStream_t s);
 int launch_synth_f32(float* out, long long n, uint32_t seed, uint32_t tensor_id, float lo, float span,

@@ -25,10 +25,17 @@ __device__ __forceinline__ float bfp_scale(int e) { return ldexpf(1.0f, e); }
 //   ternary mode: the integer BFP rule of the int16 table, evaluated on the row (model/bons.py:
 //   204-236): every group's (code-1)*m11 aligned to the row's smallest exponent (capped at 20),
 //   the live absmax normalised into [2^14, 2^15), truncated to int16.
+constexpr int kMaxEmbedGroups = 128;
+
+__device__ __forceinline__ int wave_min_i(int v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
 __global__ __launch_bounds__(256) void embed_kernel(EmbedParams p) {
   __shared__ int s_tok;
   __shared__ int s_red[8];
-  __shared__ int s_emin, s_k2;
   const int tid = threadIdx.x;
   if (tid == 0) {
     int pos = *p.pos + 1;
@@ -55,56 +62,56 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedParams p) {
     return;
   }
   // Ternary row: scales at the head of the row packet, codes after code_off.
+  __shared__ int s_live[kMaxEmbedGroups];
+  __shared__ long long s_lred[4];
   const uint8_t* row = p.rows + (size_t)tok * p.row_bytes;
   const uint16_t* sc = (const uint16_t*)row;
   const int G = p.n_embd / kGroup;
-  // Pass 1: smallest exponent over the row, live absmax of aligned |m11|.
+  auto code_of = [&](int c) -> int {
+    if (p.kind == TRX_KIND_TERNARY5) {
+      const int g = c >> 7, j = c & 127, byte = j / 5, k = j - 5 * byte;
+      const int b = row[p.code_off + kTrit5GroupBytes * g + byte];
+      const int d = k == 0 ? b : k == 1 ? b / 3 : k == 2 ? b / 9 : k == 3 ? b / 27 : b / 81;
+      return d % 3;
+    }
+    return (row[p.code_off + (c >> 2)] >> (2 * (c & 3))) & 3;
+  };
+  // Smallest scale exponent of the row, and which groups hold a nonzero weight.
   int emin = 1 << 20;
   for (int g = tid; g < G; g += 256) {
     int m11, e16;
     fp16_split(sc[g], m11, e16);
     emin = min(emin, e16);
+    s_live[g] = 0;
   }
-  for (int o = 32; o >= 1; o >>= 1) emin = min(emin, __shfl_xor(emin, o, 64));
+  emin = wave_min_i(emin);
   if ((tid & 63) == 0) s_red[tid >> 6] = emin;
   __syncthreads();
-  if (tid == 0) {
-    int m = s_red[0];
-    for (int i = 1; i < 4; ++i) m = min(m, s_red[i]);
-    s_emin = m;
-  }
+  emin = min(min(s_red[0], s_red[1]), min(s_red[2], s_red[3]));
+  for (int c = tid; c < p.n_embd; c += 256)
+    if (code_of(c) != 1) s_live[c >> 7] = 1;
   __syncthreads();
-  emin = s_emin;
-  // codes of column c
-  auto code_of = [&](int c) -> int {
-    if (p.kind == TRX_KIND_TERNARY5) {
-      const int g = c >> 7, j = c & 127, byte = j / 5, k = j - 5 * byte;
-      int b = row[p.code_off + kTrit5GroupBytes * g + byte];
-      for (int i = 0; i < k; ++i) b /= 3;
-      return b % 3;
-    }
-    return (row[p.code_off + (c >> 2)] >> (2 * (c & 3))) & 3;
-  };
+  // Largest aligned |m11| over the live groups.
   long long amax = 0;
-  for (int g = 0; g < G; ++g) {
-    int live = 0;
-    for (int j = tid; j < kGroup; j += 256) live |= (code_of(g * kGroup + j) != 1);
-    live = __syncthreads_or(live);
-    if (live && tid == 0) {
-      int m11, e16;
-      fp16_split(sc[g], m11, e16);
-      int sh = min(e16 - emin, 20);
-      long long v = (long long)(m11 < 0 ? -m11 : m11) << sh;
-      if (v > amax) amax = v;
-    }
+  for (int g = tid; g < G; g += 256) {
+    if (!s_live[g]) continue;
+    int m11, e16;
+    fp16_split(sc[g], m11, e16);
+    const long long v = (long long)(m11 < 0 ? -m11 : m11) << min(e16 - emin, 20);
+    amax = v > amax ? v : amax;
   }
-  if (tid == 0) {
-    int bl = 0;
-    while (bl < 63 && (amax >> bl) != 0) ++bl;
-    s_k2 = bl - 15;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const long long other = __shfl_xor(amax, o, 64);
+    amax = other > amax ? other : amax;
   }
+  if ((tid & 63) == 0) s_lred[tid >> 6] = amax;
   __syncthreads();
-  const int k2 = s_k2;
+  amax = s_lred[0];
+  for (int i = 1; i < 4; ++i) amax = s_lred[i] > amax ? s_lred[i] : amax;
+  int bl = 0;
+  while (bl < 63 && (amax >> bl) != 0) ++bl;
+  const int k2 = bl - 15;
   const float scale = bfp_scale(emin + k2);
   for (int c = tid; c < p.n_embd; c += 256) {
     int m11, e16;
@@ -127,171 +134,268 @@ __global__ void finalize_kernel(const int* pos, const int* n_prompt, unsigned lo
 
 // Attention -------------------------------------------------------------------------------------
 //
-// One block per (kv head, split of `chunk` positions). q of the n_rep heads sharing the kv head
-// and (in the split holding the current position) the new k are RMS-normalised per head and
-// rotated (NEOX pairs on the first rope_n dims, angle = pos * freq in fp32; model/fastref.py:
-// 216-241); the new k (post-RoPE) and v are appended to the fp16 cache at pos. Each block writes
-// its split's softmax partials (max, sum, unnormalised output) per q head.
+// One kernel per layer. Block (kv head g, split sp) owns the positions [sp*chunk, (sp+1)*chunk)
+// of the T = pos + 1 cached ones (chunk = ceil(T / n_split)), for the REP q heads sharing g
+// (model/fastref.py:216-241):
+//   - the split's K and V rows are loaded into registers first (16-byte loads, HD/8 lanes per
+//     position), so one memory round trip overlaps the rest of the prologue;
+//   - q: RMS-normalised per head, rotated (NEOX pairs on the first rope_n dims, angle =
+//     pos * freq in fp32) and scaled by 1/sqrt(hd); the block holding `pos` does the same for the
+//     new k and appends k (post-RoPE) and v to the fp16 cache;
+//   - scores, softmax over the split, the unnormalised V sum; the split's (max, sum, output) go
+//     to the partials.
+// A second kernel merges the partials of every q head and applies the output gate of gated
+// attention.
 
 constexpr int kAttnThreads = 256;
-constexpr int kMaxHd = 256;
 constexpr int kMaxRep = 8;
+constexpr int kMaxPass = 8;                 // register-held positions per thread
+constexpr int kMaxChunk = 128;
 
-__device__ void head_norm_rope(float* v, const float* w, const float* freq, int hd, int rope_n,
-                               float eps, int pos, float post_scale, float* red, int tid, int nthreads) {
-  // v: one head in LDS (hd floats), normalised and rotated in place by the block.
-  float ss = 0.f;
-  for (int d = tid; d < hd; d += nthreads) ss += v[d] * v[d];
-  ss = wave_sum(ss);
-  __syncthreads();
-  if ((tid & 63) == 0) red[tid >> 6] = ss;
-  __syncthreads();
-  float tot = 0.f;
-  for (int i = 0; i < (nthreads + 63) / 64; ++i) tot += red[i];
-  const float r = 1.0f / sqrtf(tot / (float)hd + eps);
-  float nv[2] = {0.f, 0.f};
-  int nd = 0;
-  for (int d = tid; d < hd; d += nthreads) nv[nd++] = v[d] * r * w[d];
-  __syncthreads();
-  nd = 0;
-  for (int d = tid; d < hd; d += nthreads) v[d] = nv[nd++];
-  __syncthreads();
-  const int half = rope_n / 2;
-  for (int i = tid; i < half; i += nthreads) {
-    const float ang = (float)pos * freq[i];
-    float sn, cs;
-    sincosf(ang, &sn, &cs);
-    const float x0 = v[i], x1 = v[i + half];
-    v[i] = x0 * cs - x1 * sn;
-    v[i + half] = x0 * sn + x1 * cs;
-  }
-  __syncthreads();
-  if (post_scale != 1.0f)
-    for (int d = tid; d < hd; d += nthreads) v[d] *= post_scale;
-  __syncthreads();
+template <int HD>
+__host__ __device__ constexpr int attn_max_chunk() {
+  // positions per pass = threads / (HD/8); at most kMaxPass passes and kMaxChunk positions.
+  return (kMaxPass * (kAttnThreads / (HD / 8))) < kMaxChunk ? kMaxPass * (kAttnThreads / (HD / 8)) : kMaxChunk;
 }
 
-__global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(AttnParams p) {
-  __shared__ float q_s[kMaxRep][kMaxHd];
-  __shared__ float kn_s[kMaxHd];
-  __shared__ float vn_s[kMaxHd];
-  __shared__ float sc_s[kMaxRep][64];
-  __shared__ float red[8];
-  const int tid = threadIdx.x;
-  const int h = blockIdx.x / p.n_split, sp = blockIdx.x - h * p.n_split;
-  const int pos = *p.pos;
-  const int T = pos + 1;
-  const int p0 = sp * p.chunk;
-  if (p0 >= T) return;
-  const int p1 = min(p0 + p.chunk, T);
-  const int hd = p.hd, rep = p.n_rep;
-  const int qstride = p.gated ? 2 * hd : hd;
-  const float qscale = 1.0f / sqrtf((float)hd);
-  // q heads of this group (raw projection rows) -> LDS, normalised and rotated.
-  for (int j = 0; j < rep; ++j) {
-    const float* src = p.qkv + (size_t)(h * rep + j) * qstride;
-    for (int d = tid; d < hd; d += kAttnThreads) q_s[j][d] = src[d];
-    __syncthreads();
-    head_norm_rope(q_s[j], p.q_norm, p.rope_freq, hd, p.rope_n, p.eps, pos, qscale, red, tid, kAttnThreads);
-  }
-  const bool has_new = (pos >= p0 && pos < p1);
-  if (has_new) {
-    const float* ksrc = p.qkv + (size_t)p.n_head * qstride + (size_t)h * hd;
-    const float* vsrc = p.qkv + (size_t)p.n_head * qstride + (size_t)p.n_kv * hd + (size_t)h * hd;
-    for (int d = tid; d < hd; d += kAttnThreads) { kn_s[d] = ksrc[d]; vn_s[d] = vsrc[d]; }
-    __syncthreads();
-    head_norm_rope(kn_s, p.k_norm, p.rope_freq, hd, p.rope_n, p.eps, pos, 1.0f, red, tid, kAttnThreads);
-    if (sp == pos / p.chunk) {
-      __half* kc = p.kcache + ((size_t)h * p.max_ctx + pos) * hd;
-      __half* vc = p.vcache + ((size_t)h * p.max_ctx + pos) * hd;
-      for (int d = tid; d < hd; d += kAttnThreads) { kc[d] = __float2half(kn_s[d]); vc[d] = __float2half(vn_s[d]); }
-    }
-  }
-  // Scores: one position per 64/ (hd/8)... each wave handles positions; lanes split hd.
-  const int n = p1 - p0;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int lpp = hd / 8;                    // lanes per position (8 dims each)
-  const int ppw = 64 / lpp;                  // positions per wave step
-  const int sub = lane / lpp, li = lane - sub * lpp;
-  for (int t0 = wave * ppw; t0 < n; t0 += (kAttnThreads / 64) * ppw) {
-    const int t = t0 + sub;
-    float kv[8];
-    const bool ok = t < n;
-    if (ok) {
-      const int ap = p0 + t;
-      if (has_new && ap == pos) {
-        for (int k = 0; k < 8; ++k) kv[k] = __half2float(__float2half(kn_s[li * 8 + k]));
+__device__ __forceinline__ void h8_to_f(const uint4 raw, float* out) {
+  const __half* hh = (const __half*)&raw;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) out[k] = __half2float(hh[k]);
+}
+
+template <int REP, int HD>
+__global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnParams p) {
+  constexpr int LPP = HD / 8;                          // lanes per position
+  constexpr int PPW = 64 / LPP;                        // positions per wave per pass
+  constexpr int PPP = PPW * (kAttnThreads / 64);       // positions per pass
+  constexpr int NH = REP + 1;                          // q heads + the new k
+  __shared__ float hv[NH + 1][HD];                     // q heads, k, v (normalised / rotated)
+  __shared__ float cs_s[HD / 2], sn_s[HD / 2];
+  __shared__ float sc_s[REP][kMaxChunk];
+  __shared__ float vred[kAttnThreads / 64][REP][HD];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int S = p.n_split;
+  const int g = blockIdx.x / S, sp = blockIdx.x - g * S;
+  const int pos = *p.pos, T = pos + 1;
+  const int chunk = (T + S - 1) / S;
+  const int p0 = sp * chunk, p1 = min(T, p0 + chunk), n = max(0, p1 - p0);
+  const int qstride = p.gated ? 2 * HD : HD;
+  const size_t cache0 = (size_t)g * p.max_ctx * HD;
+  const bool owner = n > 0 && pos >= p0 && pos < p1;
+  const int li = lane % LPP, sub = lane / LPP;
+  const int npass = (n + PPP - 1) / PPP;
+
+  if (n > 0) {
+    // 1. K and V rows of the split into registers (the position being added is not cached yet:
+    //    its row is taken from LDS below).
+    uint4 kr[kMaxPass], vr[kMaxPass];
+#pragma unroll
+    for (int ps = 0; ps < kMaxPass; ++ps) {
+      const int t = ps * PPP + wave * PPW + sub;
+      if (ps < npass && t < n && p0 + t != pos) {
+        const size_t off = cache0 + (size_t)(p0 + t) * HD + li * 8;
+        kr[ps] = *(const uint4*)(p.kcache + off);
+        vr[ps] = *(const uint4*)(p.vcache + off);
       } else {
-        const uint4 raw = *(const uint4*)(p.kcache + ((size_t)h * p.max_ctx + ap) * hd + li * 8);
-        const __half* hh = (const __half*)&raw;
-        for (int k = 0; k < 8; ++k) kv[k] = __half2float(hh[k]);
+        kr[ps] = make_uint4(0, 0, 0, 0);
+        vr[ps] = make_uint4(0, 0, 0, 0);
       }
-    } else {
-      for (int k = 0; k < 8; ++k) kv[k] = 0.f;
     }
-    for (int j = 0; j < rep; ++j) {
-      float s = 0.f;
-      for (int k = 0; k < 8; ++k) s += q_s[j][li * 8 + k] * kv[k];
-      for (int o = lpp >> 1; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
-      if (ok && li == 0) sc_s[j][t] = s;
+    // 2. q heads (and k, v for the owner) into LDS; rotation table.
+    const float* kraw = p.qkv + (size_t)p.n_head * qstride + (size_t)g * HD;
+    for (int i = tid; i < NH * HD; i += kAttnThreads) {
+      const int j = i / HD, d = i - j * HD;
+      if (j < REP) hv[j][d] = p.qkv[(size_t)(g * REP + j) * qstride + d];
+      else if (owner) hv[REP][d] = kraw[d];
+    }
+    if (owner)
+      for (int d = tid; d < HD; d += kAttnThreads) hv[REP + 1][d] = kraw[(size_t)p.n_kv * HD + d];
+    const int half = p.rope_n / 2;
+    for (int i = tid; i < half; i += kAttnThreads) {
+      float sn, cs;
+      sincosf((float)pos * p.rope_freq[i], &sn, &cs);
+      cs_s[i] = cs;
+      sn_s[i] = sn;
+    }
+    __syncthreads();
+    // 3. RMSNorm per head (a wave per head) and RoPE, in place.
+    for (int j = wave; j < NH; j += kAttnThreads / 64) {
+      if (j == REP && !owner) continue;
+      const float* w = (j < REP) ? p.q_norm : p.k_norm;
+      float ss = 0.f;
+      for (int d = lane; d < HD; d += 64) ss += hv[j][d] * hv[j][d];
+      ss = wave_sum(ss);
+      const float r = 1.0f / sqrtf(ss / (float)HD + p.eps);
+      const float post = (j < REP) ? 1.0f / sqrtf((float)HD) : 1.0f;
+      float nv[HD / 64];
+#pragma unroll
+      for (int k = 0; k < HD / 64; ++k) nv[k] = hv[j][lane + 64 * k] * r * w[lane + 64 * k];
+      // Rotation: pair (i, i + half) for i < half; dims past rope_n pass through.
+      float ov[HD / 64];
+#pragma unroll
+      for (int k = 0; k < HD / 64; ++k) ov[k] = nv[k];
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int k = 0; k < HD / 64; ++k) hv[j][lane + 64 * k] = nv[k];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int k = 0; k < HD / 64; ++k) {
+        const int d = lane + 64 * k;
+        if (d < half) ov[k] = nv[k] * cs_s[d] - hv[j][d + half] * sn_s[d];
+        else if (d < 2 * half) ov[k] = hv[j][d - half] * sn_s[d - half] + nv[k] * cs_s[d - half];
+      }
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int k = 0; k < HD / 64; ++k) hv[j][lane + 64 * k] = ov[k] * post;
+    }
+    __syncthreads();
+    if (owner && tid < HD) {
+      const __half kh = __float2half(hv[REP][tid]), vh = __float2half(hv[REP + 1][tid]);
+      p.kcache[cache0 + (size_t)pos * HD + tid] = kh;
+      p.vcache[cache0 + (size_t)pos * HD + tid] = vh;
+      hv[REP][tid] = __half2float(kh);
+      hv[REP + 1][tid] = __half2float(vh);
+    }
+    __syncthreads();
+    // 4. Scores.
+    float qr[REP][8];
+#pragma unroll
+    for (int j = 0; j < REP; ++j)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) qr[j][k] = hv[j][li * 8 + k];
+#pragma unroll
+    for (int ps = 0; ps < kMaxPass; ++ps) {
+      if (ps >= npass) break;
+      const int t = ps * PPP + wave * PPW + sub;
+      float kv[8];
+      if (owner && p0 + t == pos) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) kv[k] = hv[REP][li * 8 + k];
+      } else {
+        h8_to_f(kr[ps], kv);
+      }
+#pragma unroll
+      for (int j = 0; j < REP; ++j) {
+        float sdot = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) sdot += qr[j][k] * kv[k];
+#pragma unroll
+        for (int o = LPP >> 1; o >= 1; o >>= 1) sdot += __shfl_xor(sdot, o, 64);
+        if (t < n && li == 0) sc_s[j][t] = sdot;
+      }
+    }
+    __syncthreads();
+    // 5. Softmax over the split, a wave per head.
+    for (int j = wave; j < REP; j += kAttnThreads / 64) {
+      float m = -INFINITY;
+      for (int t = lane; t < n; t += 64) m = fmaxf(m, sc_s[j][t]);
+      m = wave_max(m);
+      float l = 0.f;
+      for (int t = lane; t < n; t += 64) {
+        const float e = __expf(sc_s[j][t] - m);
+        sc_s[j][t] = e;
+        l += e;
+      }
+      l = wave_sum(l);
+      if (lane == 0) {
+        p.part_m[(size_t)(g * REP + j) * S + sp] = m;
+        p.part_l[(size_t)(g * REP + j) * S + sp] = l;
+      }
+    }
+    __syncthreads();
+    // 6. V: every thread sums its register-held positions, then over the wave's position slots
+    //    (lanes li, li + LPP, ...) and over the waves.
+    float acc[REP][8];
+#pragma unroll
+    for (int j = 0; j < REP; ++j)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) acc[j][k] = 0.f;
+#pragma unroll
+    for (int ps = 0; ps < kMaxPass; ++ps) {
+      if (ps >= npass) break;
+      const int t = ps * PPP + wave * PPW + sub;
+      if (t >= n) continue;
+      float v[8];
+      if (owner && p0 + t == pos) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = hv[REP + 1][li * 8 + k];
+      } else {
+        h8_to_f(vr[ps], v);
+      }
+#pragma unroll
+      for (int j = 0; j < REP; ++j) {
+        const float pj = sc_s[j][t];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) acc[j][k] += pj * v[k];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < REP; ++j)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        float a = acc[j][k];
+#pragma unroll
+        for (int o = LPP; o < 64; o <<= 1) a += __shfl_xor(a, o, 64);
+        acc[j][k] = a;
+      }
+    if (sub == 0) {
+#pragma unroll
+      for (int j = 0; j < REP; ++j)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) vred[wave][j][li * 8 + k] = acc[j][k];
+    }
+    __syncthreads();
+    for (int i = tid; i < REP * HD; i += kAttnThreads) {
+      const int j = i / HD, d = i - j * HD;
+      float o = 0.f;
+#pragma unroll
+      for (int w = 0; w < kAttnThreads / 64; ++w) o += vred[w][j][d];
+      p.part_o[((size_t)(g * REP + j) * S + sp) * HD + d] = o;
+    }
+  } else {
+    // An empty split contributes nothing to the merge.
+    if (tid < REP) {
+      p.part_m[(size_t)(g * REP + tid) * S + sp] = -INFINITY;
+      p.part_l[(size_t)(g * REP + tid) * S + sp] = 0.f;
     }
   }
-  __syncthreads();
-  // Softmax partials per q head (one wave per head while heads remain).
-  for (int j = wave; j < rep; j += kAttnThreads / 64) {
-    float m = -INFINITY;
-    for (int t = lane; t < n; t += 64) m = fmaxf(m, sc_s[j][t]);
-    m = wave_max(m);
-    float l = 0.f;
-    for (int t = lane; t < n; t += 64) {
-      const float e = __expf(sc_s[j][t] - m);
-      sc_s[j][t] = e;
-      l += e;
-    }
-    l = wave_sum(l);
-    if (lane == 0) {
-      const size_t idx = (size_t)(h * rep + j) * p.n_split + sp;
-      p.part_m[idx] = m;
-      p.part_l[idx] = l;
-    }
-  }
-  __syncthreads();
-  // Unnormalised outputs: thread per (head, dim).
-  for (int od = tid; od < rep * hd; od += kAttnThreads) {
-    const int j = od / hd, d = od - j * hd;
-    float acc = 0.f;
-    for (int t = 0; t < n; ++t) {
-      const int ap = p0 + t;
-      float v;
-      if (has_new && ap == pos) v = __half2float(__float2half(vn_s[d]));
-      else v = __half2float(p.vcache[((size_t)h * p.max_ctx + ap) * hd + d]);
-      acc += sc_s[j][t] * v;
-    }
-    p.part_o[((size_t)(h * rep + j) * p.n_split + sp) * hd + d] = acc;
-  }
+
 }
 
-// Combine the split partials of every q head; gated attention multiplies by sigmoid(gate).
-__global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
-  const int qh = blockIdx.x;
+// Merge of the split partials: one block per q head (the kernel boundary orders it after every
+// split's writes).
+__global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
+  __shared__ float wsp[64];
+  const int qh = blockIdx.x, tid = threadIdx.x;
+  const int S = p.n_split, hd = p.hd;
   const int T = *p.pos + 1;
-  const int ns = (T + p.chunk - 1) / p.chunk;
-  const int hd = p.hd;
-  const float* pm = p.part_m + (size_t)qh * p.n_split;
-  const float* pl = p.part_l + (size_t)qh * p.n_split;
-  float M = -INFINITY;
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, pm[s]);
-  float L = 0.f;
-  for (int s = 0; s < ns; ++s) L += pl[s] * __expf(pm[s] - M);
-  const float invL = 1.0f / L;
-  for (int d = threadIdx.x; d < hd; d += 256) {
-    float acc = 0.f;
-    for (int s = 0; s < ns; ++s) acc += p.part_o[((size_t)qh * p.n_split + s) * hd + d] * __expf(pm[s] - M);
-    float o = acc * invL;
-    if (p.gated) {
-      const float g = p.qkv[(size_t)qh * 2 * hd + hd + d];
-      o *= sigmoidf_(g);
+  const int chunk = (T + S - 1) / S;
+  const int ns = min(S, (T + chunk - 1) / chunk);      // splits holding positions
+  const float* pm = p.part_m + (size_t)qh * S;
+  const float* pl = p.part_l + (size_t)qh * S;
+  if (tid < 64) {
+    const float mv = tid < ns ? pm[tid] : -INFINITY;
+    const float M = wave_max(mv);
+    const float e = tid < ns ? __expf(mv - M) : 0.f;
+    const float L = wave_sum(tid < ns ? pl[tid] * e : 0.f);
+    wsp[tid] = e / L;
+  }
+  __syncthreads();
+  const float* po = p.part_o + (size_t)qh * S * hd;
+  for (int d = tid; d < hd; d += 256) {
+    float o = 0.f;
+    // Eight independent loads per round keep the memory pipeline full.
+    for (int s0 = 0; s0 < ns; s0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = (s0 + k < ns) ? po[(size_t)(s0 + k) * hd + d] : 0.f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) o += (s0 + k < ns) ? v[k] * wsp[s0 + k] : 0.f;
     }
+    if (p.gated) o *= sigmoidf_(p.qkv[(size_t)qh * 2 * hd + hd + d]);
     p.out[(size_t)qh * hd + d] = o;
   }
 }
@@ -313,6 +417,7 @@ __global__ __launch_bounds__(256) void dense_gemv_kernel(DenseParams p) {
   for (int c = tid; c < p.K; c += 256) xs[c] = p.norm_w ? p.x[c] * rinv * p.norm_w[c] : p.x[c];
   __syncthreads();
   const int lane = tid & 63, wave = tid >> 6;
+  unsigned long long best = 0;   // lane 0: best (ordered value, ~row) key of this wave's rows
   for (int m = blockIdx.x * 4 + wave; m < p.M; m += gridDim.x * 4) {
     const uint8_t* row = p.W + (size_t)m * p.row_bytes;
     float acc = 0.f;
@@ -340,10 +445,12 @@ __global__ __launch_bounds__(256) void dense_gemv_kernel(DenseParams p) {
       if (p.amax_slot) {
         uint32_t u = __float_as_uint(v);
         u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-        atomicMax(p.amax_slot, ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)m));
+        const unsigned long long key = ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)m);
+        best = key > best ? key : best;
       }
     }
   }
+  if (p.amax_slot && lane == 0 && best) atomicMax(p.amax_slot, best);
 }
 
 // Synthetic weights (csrc side of trixium_amd/synth.py's counter-based generator) ---------------
@@ -432,6 +539,8 @@ __global__ void synth_f32_kernel(float* out, long long n, uint32_t seed, uint32_
 // Launchers ------------------------------------------------------------------------------------
 
 int launch_embed(const EmbedParams& p, hipStream_t s) {
+  TRX_CHECK(p.n_embd % kGroup == 0 && p.n_embd / kGroup <= kMaxEmbedGroups, TRX_E_INVALID,
+            "embedding: n_embd %d unsupported", p.n_embd);
   hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(256), 0, s, p);
   TRX_LAUNCHED();
   return TRX_OK;
@@ -444,14 +553,45 @@ int launch_finalize(const int* pos, const int* n_prompt, unsigned long long* slo
   return TRX_OK;
 }
 
-int launch_attention(const AttnParams& p, hipStream_t s) {
-  TRX_CHECK(p.hd % 8 == 0 && p.hd <= kMaxHd && 64 % (p.hd / 8) == 0 && p.n_rep <= kMaxRep &&
-            p.chunk <= 64, TRX_E_INVALID, "attention: unsupported geometry hd=%d rep=%d", p.hd, p.n_rep);
-  hipLaunchKernelGGL(attn_split_kernel, dim3(p.n_kv * p.n_split), dim3(kAttnThreads), 0, s, p);
+int attention_splits(int n_kv, int head_dim, int max_ctx) {
+  // Enough blocks to cover the CUs, and at most the register-held positions per block.
+  int cap = head_dim == 64 ? attn_max_chunk<64>() : head_dim == 128 ? attn_max_chunk<128>()
+                                                                      : attn_max_chunk<256>();
+  int s = min(cdiv(256, n_kv > 0 ? n_kv : 1), 64);
+  if (cdiv(max_ctx, s) > cap) s = cdiv(max_ctx, cap);
+  return s > 64 ? -1 : s;
+}
+
+static int hd_threads(int hd) { return hd < 256 ? (hd < 64 ? 64 : hd) : 256; }
+
+template <int REP>
+static int launch_attn_rep(const AttnParams& p, hipStream_t s) {
+  const dim3 grid(p.n_kv * p.n_split), block(kAttnThreads);
+  switch (p.hd) {
+    case 64: hipLaunchKernelGGL((attn_decode_kernel<REP, 64>), grid, block, 0, s, p); break;
+    case 128: hipLaunchKernelGGL((attn_decode_kernel<REP, 128>), grid, block, 0, s, p); break;
+    case 256: hipLaunchKernelGGL((attn_decode_kernel<REP, 256>), grid, block, 0, s, p); break;
+    default: TRX_CHECK(false, TRX_E_INVALID, "attention: head_dim %d unsupported", p.hd);
+  }
   TRX_LAUNCHED();
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(p.n_head), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(attn_merge_kernel, dim3(p.n_head), dim3(hd_threads(p.hd)), 0, s, p);
   TRX_LAUNCHED();
   return TRX_OK;
+}
+
+int launch_attention(const AttnParams& p, hipStream_t s) {
+  const int cap = p.hd == 64 ? attn_max_chunk<64>() : p.hd == 128 ? attn_max_chunk<128>() : attn_max_chunk<256>();
+  TRX_CHECK(p.rope_n <= p.hd && p.rope_n % 2 == 0, TRX_E_INVALID, "attention: rope dims %d", p.rope_n);
+  TRX_CHECK(p.n_split >= 1 && p.n_split <= 64 && cdiv(p.max_ctx, p.n_split) <= cap,
+            TRX_E_INVALID, "attention: %d splits for context %d", p.n_split, p.max_ctx);
+  switch (p.n_rep) {
+    case 1: return launch_attn_rep<1>(p, s);
+    case 2: return launch_attn_rep<2>(p, s);
+    case 4: return launch_attn_rep<4>(p, s);
+    case 6: return launch_attn_rep<6>(p, s);
+    case 8: return launch_attn_rep<8>(p, s);
+    default: TRX_CHECK(false, TRX_E_INVALID, "attention: %d q heads per kv head unsupported", p.n_rep);
+  }
 }
 
 int launch_dense_gemv(const DenseParams& p, hipStream_t s) {

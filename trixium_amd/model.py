@@ -209,7 +209,8 @@ class Decoder:
     def reset(self):
         _lib.call("trx_model_reset", self._h)
 
-    def _feed(self, tokens, head_from=-1):
+    def feed(self, tokens, head_from=-1):
+        """Queue tokens for the next len(tokens) positions; the forwards run on step()."""
         t = np.ascontiguousarray(np.asarray(tokens, dtype=np.int32).reshape(-1))
         if t.size == 0:
             raise ValueError("no tokens to feed")
@@ -225,7 +226,7 @@ class Decoder:
     def forward(self, tokens, use_graph=None):
         """Feed `tokens` after the current position; logits (vocab,) of the last one
         (FloatModel.forward, golden.py:436-460)."""
-        n = self._feed(tokens)
+        n = self.feed(tokens)
         self.step(n, use_graph)
         return self.logits()
 
@@ -236,12 +237,10 @@ class Decoder:
             return []
         if n > self.cfg.max_new:
             raise ValueError(f"{n} tokens requested, the output buffer holds {self.cfg.max_new}")
-        n_fed = self._feed(tokens)
+        n_fed = self.feed(tokens)
         self.step(n_fed + n - 1, use_graph)
-        _lib.call("trx_model_finalize", self._h)
-        out = np.empty(self.cfg.max_new, dtype=np.int32)
-        self._read(READ_OUT, out)
-        return [int(v) for v in out[:n]]
+        self.finalize()
+        return [int(v) for v in self.outputs()[:n]]
 
     def generate_fresh(self, prompt, n, use_graph=None):
         """reset + generate through the single C entry point (firmware infer_generate)."""
@@ -251,6 +250,14 @@ class Decoder:
         _lib.call("trx_model_generate", self._h, p.ctypes.data_as(ctypes.POINTER(ctypes.c_int)),
                   int(p.size), int(n), out.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), int(bool(g)))
         return [int(v) for v in out]
+
+    def outputs(self):
+        """The generated-token buffer (int32 [max_new]) after finalize()."""
+        return self._read(READ_OUT, np.empty(self.cfg.max_new, dtype=np.int32))
+
+    def finalize(self):
+        """Resolve the argmax of the last forward into the output buffer."""
+        _lib.call("trx_model_finalize", self._h)
 
     def synchronize(self):
         _lib.call("trx_model_sync", self._h)
