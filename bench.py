@@ -51,7 +51,23 @@ def parse_args():
                     help="passes over the 36 layers when timing the dominant kernel")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="launch every kernel eagerly")
+    ap.add_argument("--only-kernel", action="store_true",
+                    help="time only the dominant kernel (for hardware-counter runs)")
+    ap.add_argument("--copy-bytes", type=int, default=0,
+                    help="run a plain device copy of this many bytes, 10 times, and exit (the "
+                         "reference kernel that calibrates the FETCH_SIZE/WRITE_SIZE counters)")
     return ap.parse_args()
+
+
+def copy_calibration(nbytes):
+    """A device-to-device copy kernel of known size (torch's elementwise copy)."""
+    import torch
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").uniform_()
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": nbytes, "launches": 10}), flush=True)
 
 
 def time_dominant_kernel(dec, mc, reps):
@@ -134,10 +150,20 @@ def main():
         print(f"bench.py measures one GPU: the batch-1 decode loop runs on a single MI355X "
               f"(asked for {max(a.gpus, world)}); run it with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+    if a.copy_bytes:
+        copy_calibration(a.copy_bytes)
+        return
     from trixium_amd import configs as C, layout as L, _lib
     from trixium_amd.model import Decoder, INFO_WEIGHT_BYTES
     mc = C.QWEN3_8B
     kind = L.KIND_TERNARY5 if a.kind == "trit5" else L.KIND_TERNARY
+    if a.only_kernel:
+        dec = Decoder.synthetic(mc, a.seed, weight_kind=kind, max_ctx=mc.max_ctx, max_new=8)
+        us, algo, n_launch = time_dominant_kernel(dec, mc, a.kernel_reps)
+        print(json.dumps({"kernel_us": round(us, 3), "bytes_per_launch": algo, "launches": n_launch,
+                          "achieved_GBs": round(algo / (us * 1e-6) / 1e9, 1)}), flush=True)
+        dec.close()
+        return
     n_dec = a.warmup + a.steps
     if a.prompt + n_dec > mc.max_ctx:
         sys.exit(f"prompt {a.prompt} + {n_dec} decode tokens exceed the context {mc.max_ctx}")
