@@ -174,8 +174,8 @@ int trx_model_info(trx_model* m, int what, int64_t* value);
 /* Device address and size of one resident tensor (for benchmarks and tests). */
 int trx_model_tensor_ptr(trx_model* m, int role, int layer, void** ptr, int64_t* bytes);
 
-/* Tuning: force a GEMV launch variant (0 = automatic; 1..5 fixed rows-per-item/block-size
- * pairs). Process-wide; for benchmarks and tests. No counterpart in the reference. */
+/* Tuning: force the GEMV rows per item (0 = automatic; 1: 4 rows, 2: 2 rows, 3: 1 row, 2 for
+ * SwiGLU). Process-wide; for benchmarks and tests. No counterpart in the reference. */
 int trx_gemv_set_variant(int variant);
 
 #ifdef __cplusplus

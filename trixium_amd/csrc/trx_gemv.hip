@@ -30,6 +30,10 @@ namespace trx {
 enum { MODE_F32 = 0, MODE_EXACT = 1, MODE_GSUM = 2 };
 
 constexpr int kLutBytes = 65536;    // 256 entries x 256 bytes
+constexpr int kMaxXRounds = 3;      // x staged in rounds of 8 columns per thread: K <= 24576
+#ifndef GEMV_PRE
+#define GEMV_PRE 1                  // ring items fetched before x arrives (capped at NB - 1)
+#endif
 constexpr int kDynLds = 160 * 1024 - kLutBytes - 512;   // LDS left for the dynamic part
 constexpr int kXStride = 36;        // dwords per half-group in the dot-ready layout
 constexpr int kXDwords5 = 33;       // trit5: 13 x (hi, lo) + 7 d4 pairs
@@ -59,28 +63,6 @@ struct GemvParams {
   const int* gate_from;
 };
 
-// Decode tables, computed at compile time: trit5 byte -> (d0 | d1<<8 | d2<<16 | d3<<24, d4),
-// 2-bit byte -> (c0 | c1<<8 | c2<<16 | c3<<24). Every byte value decodes as
-// digit k = floor(b / 3^k) mod 3 (the numpy decode of the reference, model/bons.py:125-130).
-struct DecodeTables {
-  uint32_t t5lo[256], t5hi[256], c2[256];
-};
-constexpr DecodeTables make_tables() {
-  DecodeTables t{};
-  for (int b = 0; b < 256; ++b) {
-    int v = b;
-    uint32_t lo = 0;
-    for (int k = 0; k < 4; ++k) { lo |= (uint32_t)(v % 3) << (8 * k); v /= 3; }
-    t.t5lo[b] = lo;
-    t.t5hi[b] = (uint32_t)(v % 3);
-    uint32_t c = 0;
-    for (int k = 0; k < 4; ++k) c |= (uint32_t)((b >> (2 * k)) & 3) << (8 * k);
-    t.c2[b] = c;
-  }
-  return t;
-}
-__constant__ const DecodeTables kTables = make_tables();
-
 // Float -> ordered unsigned (monotonic), for the packed argmax.
 __device__ __forceinline__ uint32_t ordered_bits(float f) {
   uint32_t u = __float_as_uint(f);
@@ -95,10 +77,14 @@ struct ItemBuf {
   uint32_t sc[R];
 };
 
-template <int FMT, int MODE, int R, int NT>
-__global__ __launch_bounds__(NT) void gemv_kernel(GemvParams p) {
-  constexpr int kThreads = NT;
-  constexpr int kWaves = NT / 64;
+constexpr int kGemvThreads = 1024;
+
+// R: rows per item; NB: items held in registers (NB - 1 are in flight while one is computed);
+// SW: SwiGLU epilogue (rows [0,F) gate, [F,2F) up; R/2 outputs per item).
+template <int FMT, int MODE, int R, int NB, bool SW>
+__global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvParams p) {
+  constexpr int kThreads = kGemvThreads;
+  constexpr int kWaves = kThreads / 64;
   constexpr bool T5 = (FMT == TRX_KIND_TERNARY5);
   constexpr int NPL = (MODE == MODE_F32) ? 2 : 1;              // int8 planes of x
   // First column of the second half-group of a group (trit5 bytes 13..25 start at column 65).
@@ -127,7 +113,7 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvParams p) {
   // v_perm sources: byte 0 of the address comes from the lane-copy word (selector 0), byte 1
   // from code byte k of the code word (selector 4 + k), bytes 2..3 are zero (selector 0x0c).
   const uint32_t lcopy = T5 ? (uint32_t)((lane & 31) << 3) : (uint32_t)(lane << 2);
-  const bool swiglu = (p.epi == TRX_EPI_SWIGLU);
+  constexpr bool swiglu = SW;
   // Rows of batch bt: plain, bt*R + r; SwiGLU, gate rows bt*R/2 + r and up rows F + bt*R/2 + r.
   const int rows_per_batch = swiglu ? R / 2 : R;
   const uint32_t rb = (uint32_t)p.row_bytes;
@@ -160,18 +146,70 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvParams p) {
     }
   };
 
-  // The first item's codes do not depend on x: fetch them before the prologue.
-  ItemBuf<FMT, R> bufA, bufB;
-  if (first < p.n_batches) load_item(bufA, first, 0);
+  // Items of this row group in order: batch bt = first + k*stride, slot sl = 0..NSLOT-1.
+  auto advance = [&](int& bt, int& sl) {
+    if (++sl == NSLOT) { sl = 0; bt += stride; }
+  };
 
-  // Decode table replicated into LDS: 4096 chunks of 16 bytes, 16 chunks per entry.
+  // x (and the RMSNorm gain) of this thread's 8 columns per round come first: they gate the
+  // prologue, and loads issued after the weight stream would queue behind it.
+  const int rounds = (p.K + kThreads * 8 - 1) / (kThreads * 8);
+  float xv[kMaxXRounds][8], wv[kMaxXRounds][8];
+  uint2 x8v[kMaxXRounds];
+#pragma unroll
+  for (int rd = 0; rd < kMaxXRounds; ++rd) {
+    const int c0 = (rd * kThreads + tid) * 8;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) { xv[rd][k] = 0.f; wv[rd][k] = 1.f; }
+    x8v[rd] = make_uint2(0, 0);
+    if (rd < rounds && c0 < p.K) {
+      if (MODE == MODE_F32) {
+        const float4 a = *(const float4*)(p.x + c0), b = *(const float4*)(p.x + c0 + 4);
+        xv[rd][0] = a.x; xv[rd][1] = a.y; xv[rd][2] = a.z; xv[rd][3] = a.w;
+        xv[rd][4] = b.x; xv[rd][5] = b.y; xv[rd][6] = b.z; xv[rd][7] = b.w;
+        if (p.norm_w) {
+          const float4 c = *(const float4*)(p.norm_w + c0), d = *(const float4*)(p.norm_w + c0 + 4);
+          wv[rd][0] = c.x; wv[rd][1] = c.y; wv[rd][2] = c.z; wv[rd][3] = c.w;
+          wv[rd][4] = d.x; wv[rd][5] = d.y; wv[rd][6] = d.z; wv[rd][7] = d.w;
+        }
+      } else {
+        x8v[rd] = *(const uint2*)(p.x8 + c0);
+      }
+    }
+  }
+
+  // The codes do not depend on x: the first NB - 1 items are fetched before the prologue.
+  ItemBuf<FMT, R> buf[NB];
+  int lbt = first, lsl = 0;            // next item to fetch
+  // Loads are issued unconditionally (an item past the end reads through the descriptor's
+  // bounds check, which returns zeros without touching memory), so the number of loads in
+  // flight is static and every wait counts exactly the loads it needs. kPre items go out
+  // before the prologue, the rest of the ring after x is staged.
+  constexpr int kPre = (GEMV_PRE < NB - 1) ? GEMV_PRE : NB - 1;
+#pragma unroll
+  for (int b = 0; b < kPre; ++b) {
+    load_item(buf[b], lbt, lsl);
+    advance(lbt, lsl);
+  }
+
+  // Decode table replicated into LDS: 4096 chunks of 16 bytes, 16 chunks per entry. Entry b
+  // holds the digits of code byte b, computed here with no memory traffic: trit5 digit k =
+  // floor(b / 3^k) mod 3 (the reference's decode, model/bons.py:125-130), 2-bit code k =
+  // (b >> 2k) & 3.
   {
     uint4* l = (uint4*)lut64;
     for (int i = tid; i < kLutBytes / 16; i += kThreads) {
-      int b = i >> 4;
+      const uint32_t b = (uint32_t)i >> 4;
       uint4 v;
-      if (T5) { v.x = kTables.t5lo[b]; v.y = kTables.t5hi[b]; v.z = v.x; v.w = v.y; }
-      else { v.x = v.y = v.z = v.w = kTables.c2[b]; }
+      if (T5) {
+        const uint32_t b1 = b / 3, b2 = b1 / 3, b3 = b2 / 3, b4 = b3 / 3;
+        const uint32_t lo = (b - 3 * b1) | ((b1 - 3 * b2) << 8) | ((b2 - 3 * b3) << 16) | ((b3 - 3 * b4) << 24);
+        const uint32_t hi = b4 - 3 * (b4 / 3);
+        v = make_uint4(lo, hi, lo, hi);
+      } else {
+        const uint32_t c = (b & 3u) | (((b >> 2) & 3u) << 8) | (((b >> 4) & 3u) << 16) | (((b >> 6) & 3u) << 24);
+        v = make_uint4(c, c, c, c);
+      }
       l[i] = v;
     }
   }
@@ -179,45 +217,53 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvParams p) {
   // x -> int16 per group (float mode, sigma_g = amax/32767) or the int8 vector itself (exact
   // modes), staged in LDS, with the sum of the staged values over every half-group.
   {
+    // The block sum of x^2 also tells every wave that the whole block's x has arrived.
     float rinv = 1.0f;
-    if (MODE == MODE_F32 && p.norm_w) {
+    {
       float ss = 0.f;
-      for (int c = tid * 4; c < p.K; c += kThreads * 4) {
-        float4 v = *(const float4*)(p.x + c);
-        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+      if (MODE == MODE_F32) {
+#pragma unroll
+        for (int rd = 0; rd < kMaxXRounds; ++rd)
+#pragma unroll
+          for (int k = 0; k < 8; ++k) ss += xv[rd][k] * xv[rd][k];
+      } else {
+#pragma unroll
+        for (int rd = 0; rd < kMaxXRounds; ++rd) ss += (float)(x8v[rd].x & 1u) + (float)(x8v[rd].y & 1u);
       }
       ss = block_sum(ss, red);
-      rinv = 1.0f / sqrtf(ss / (float)p.K + p.eps);
+      if (MODE == MODE_F32 && p.norm_w) rinv = 1.0f / sqrtf(ss / (float)p.K + p.eps);
+    }
+    // x has arrived: the rest of the ring goes out now and lands during the staging below.
+#pragma unroll
+    for (int b = kPre; b < NB - 1; ++b) {
+      load_item(buf[b], lbt, lsl);
+      advance(lbt, lsl);
     }
     // 16 threads per group, 8 columns each; every thread runs the same number of rounds.
-    const int rounds = (p.K + kThreads * 8 - 1) / (kThreads * 8);
-    for (int rd = 0; rd < rounds; ++rd) {
+#pragma unroll
+    for (int rd = 0; rd < kMaxXRounds; ++rd) {
+      if (rd >= rounds) break;
       const int c0 = (rd * kThreads + tid) * 8;
       const bool live = c0 < p.K;
       int q[8] = {0, 0, 0, 0, 0, 0, 0, 0};
       float am = 0.f;
       if (MODE == MODE_F32) {
-        float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        if (live) {
-          float4 a = *(const float4*)(p.x + c0), b = *(const float4*)(p.x + c0 + 4);
-          v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-          if (p.norm_w) {
-            float4 wa = *(const float4*)(p.norm_w + c0), wb = *(const float4*)(p.norm_w + c0 + 4);
-            float w[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+        float v[8];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) v[k] = v[k] * rinv * w[k];
-          }
-#pragma unroll
-          for (int k = 0; k < 8; ++k) am = fmaxf(am, fabsf(v[k]));
+        for (int k = 0; k < 8; ++k) {
+          v[k] = p.norm_w ? xv[rd][k] * rinv * wv[rd][k] : xv[rd][k];
+          am = fmaxf(am, fabsf(v[k]));
         }
-#pragma unroll
-        for (int o = 8; o >= 1; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+        am = row16_max(am);               // the 16 lanes of the group
         const float inv = am > 0.f ? 32767.0f / am : 0.f;
 #pragma unroll
         for (int k = 0; k < 8; ++k) q[k] = (int)rintf(v[k] * inv);
-      } else if (live) {
+      } else {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) q[k] = p.x8[c0 + k];
+        for (int k = 0; k < 4; ++k) {
+          q[k] = (int)(int8_t)(x8v[rd].x >> (8 * k));
+          q[k + 4] = (int)(int8_t)(x8v[rd].y >> (8 * k));
+        }
       }
       int s0 = 0, s1 = 0;
       const int lc = c0 & (kGroup - 1);
@@ -234,11 +280,8 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvParams p) {
         pk.w = (uint32_t)(uint16_t)q[6] | ((uint32_t)(uint16_t)q[7] << 16);
         *(uint4*)(stage + c0) = pk;
       }
-#pragma unroll
-      for (int o = 8; o >= 1; o >>= 1) {
-        s0 += __shfl_xor(s0, o, 64);
-        s1 += __shfl_xor(s1, o, 64);
-      }
+      s0 = row16_sum_i(s0);
+      s1 = row16_sum_i(s1);
       if (live && (tid & 15) == 0) {
         gsig[c0 >> 7] = am / 32767.0f;
         usum[2 * (c0 >> 7)] = s0;
@@ -457,24 +500,20 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvParams p) {
   };
 
   if (NSLOT == 1) load_x(0);
-  int bt = first, sl = 0;
-  // Two items per trip so the double buffer needs no register moves.
-  while (bt < p.n_batches) {
-    int nbt = bt, nsl = sl + 1;
-    if (nsl == NSLOT) { nsl = 0; nbt += stride; }
-    if (nbt < p.n_batches) load_item(bufB, nbt, nsl);
-    if (NSLOT > 1) load_x(sl);
-    compute_item(bufA, bt, sl);
-    if (sl == NSLOT - 1) finish_batch(bt);
-    bt = nbt; sl = nsl;
-    if (bt >= p.n_batches) break;
-    nbt = bt; nsl = sl + 1;
-    if (nsl == NSLOT) { nsl = 0; nbt += stride; }
-    if (nbt < p.n_batches) load_item(bufA, nbt, nsl);
-    if (NSLOT > 1) load_x(sl);
-    compute_item(bufB, bt, sl);
-    if (sl == NSLOT - 1) finish_batch(bt);
-    bt = nbt; sl = nsl;
+  int cbt = first, csl = 0;            // item being computed
+  // A ring of NB register buffers: phase ph computes buf[ph] and refills the buffer consumed
+  // one phase earlier with the item NB - 1 ahead.
+  while (cbt < p.n_batches) {
+#pragma unroll
+    for (int ph = 0; ph < NB; ++ph) {
+      if (cbt >= p.n_batches) break;
+      load_item(buf[(ph + NB - 1) % NB], lbt, lsl);
+      advance(lbt, lsl);
+      if (NSLOT > 1) load_x(csl);
+      compute_item(buf[ph], cbt, csl);
+      if (csl == NSLOT - 1) finish_batch(cbt);
+      advance(cbt, csl);
+    }
   }
   if (MODE == MODE_F32 && p.amax_slot) {
     // One atomic per block: wave maximum, then the block's over its waves.
@@ -515,51 +554,62 @@ static int num_cus() {
   return g_num_cus;
 }
 
-template <int FMT, int MODE, int R, int NT>
+template <int FMT, int MODE, int R, int NB, bool SW>
 static int launch_r(GemvParams& p, hipStream_t s) {
-  constexpr int kWaves = NT / 64;
+  constexpr int kWaves = kGemvThreads / 64;
   static bool attr_set = false;
   if (!attr_set) {
-    TRX_HIP(hipFuncSetAttribute((const void*)gemv_kernel<FMT, MODE, R, NT>,
+    TRX_HIP(hipFuncSetAttribute((const void*)gemv_kernel<FMT, MODE, R, NB, SW>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, kDynLds));
     attr_set = true;
   }
-  p.n_batches = (p.epi == TRX_EPI_SWIGLU) ? cdiv(p.n_out, R / 2) : cdiv(p.n_out, R);
+  p.n_batches = SW ? cdiv(p.n_out, R / 2) : cdiv(p.n_out, R);
   const int per_block = kWaves * (64 / p.LPR);
   const int need = cdiv(p.n_batches, per_block);
   const int nb = need < num_cus() ? need : num_cus();
-  hipLaunchKernelGGL((gemv_kernel<FMT, MODE, R, NT>), dim3(nb > 0 ? nb : 1), dim3(NT),
+  hipLaunchKernelGGL((gemv_kernel<FMT, MODE, R, NB, SW>), dim3(nb > 0 ? nb : 1), dim3(kGemvThreads),
                      lds_bytes(p.K, p.G), s, p);
   TRX_LAUNCHED();
   return TRX_OK;
 }
 
-// Variant selection. g_variant (set by trx_gemv_set_variant, for tuning) forces a
-// (rows per item, threads per block) pair; 0 picks automatically: the largest R that still gives
-// every row group of the grid a batch.
+// Variant selection. g_variant (trx_gemv_set_variant, for tuning) forces rows per item
+// (1: R=4, 2: R=2, 3: R=1; SwiGLU takes R=2 for 3); 0 picks the R that minimises
+// (grid rounds rounded up) x R, the time of the slowest row group, preferring the larger R.
 static int g_variant = 0;
+
+static int pick_rows(const GemvParams& p, bool sw) {
+  const int per_block = (kGemvThreads / 64) * (64 / p.LPR);
+  const long long slots = (long long)num_cus() * per_block;
+  int best_r = sw ? 2 : 1;
+  long long best_cost = -1;
+  for (int r : {4, 2, 1}) {
+    if (sw && r < 2) continue;
+    const long long nbat = sw ? cdiv(p.n_out, r / 2) : cdiv(p.n_out, r);
+    const long long cost = ((nbat + slots - 1) / slots) * r;
+    if (best_cost < 0 || cost < best_cost) { best_cost = cost; best_r = r; }
+  }
+  return best_r;
+}
 
 template <int FMT, int MODE>
 static int launch(GemvParams& p, hipStream_t s) {
-  const int outs_per_row = (p.epi == TRX_EPI_SWIGLU) ? 2 : 1;
-  switch (g_variant) {
-    case 1: return launch_r<FMT, MODE, 4, 512>(p, s);
-    case 2: return launch_r<FMT, MODE, 2, 1024>(p, s);
-    case 3: if (outs_per_row == 1) return launch_r<FMT, MODE, 1, 1024>(p, s);
-            return launch_r<FMT, MODE, 2, 1024>(p, s);
-    case 4: return launch_r<FMT, MODE, 2, 512>(p, s);
-    case 5: return launch_r<FMT, MODE, 4, 1024>(p, s);
-    default: break;
+  const bool sw = (p.epi == TRX_EPI_SWIGLU);
+  int r = pick_rows(p, sw);
+  if (g_variant == 1) r = 4;
+  if (g_variant == 2) r = 2;
+  if (g_variant == 3) r = sw ? 2 : 1;
+  if (MODE == MODE_F32 && sw) {
+    if (r == 4) return launch_r<FMT, MODE, 4, 2, true>(p, s);
+    return launch_r<FMT, MODE, 2, 4, true>(p, s);
   }
-  const long long groups_in_grid = (long long)num_cus() * 16 * (64 / p.LPR);
-  const long long rows = (long long)p.n_out * outs_per_row;
-  if (rows >= 4 * groups_in_grid) return launch_r<FMT, MODE, 4, 1024>(p, s);
-  if (rows >= 2 * groups_in_grid || outs_per_row == 2) return launch_r<FMT, MODE, 2, 1024>(p, s);
-  return launch_r<FMT, MODE, 1, 1024>(p, s);
+  if (r == 4) return launch_r<FMT, MODE, 4, 2, false>(p, s);
+  if (r == 2) return launch_r<FMT, MODE, 2, 4, false>(p, s);
+  return launch_r<FMT, MODE, 1, 6, false>(p, s);
 }
 
 int gemv_set_variant(int v) {
-  TRX_CHECK(v >= 0 && v <= 5, TRX_E_INVALID, "gemv variant %d", v);
+  TRX_CHECK(v >= 0 && v <= 3, TRX_E_INVALID, "gemv variant %d", v);
   g_variant = v;
   return TRX_OK;
 }
@@ -569,7 +619,7 @@ int gemv_check(int kind, int M, int K) {
             "gemv: kind %d is not a ternary kind", kind);
   TRX_CHECK(M > 0 && K > 0 && (K % kGroup) == 0, TRX_E_INVALID,
             "gemv: M=%d K=%d (K must be a positive multiple of 128)", M, K);
-  TRX_CHECK(lds_bytes(K, K / kGroup) <= kDynLds, TRX_E_INVALID,
+  TRX_CHECK(lds_bytes(K, K / kGroup) <= kDynLds && K <= kMaxXRounds * kGemvThreads * 8, TRX_E_INVALID,
             "gemv: K=%d exceeds the LDS budget", K);
   RowGeom rg = row_geom(kind, K);
   TRX_CHECK((unsigned long long)M * rg.row_bytes < 0xFFFF0000ull, TRX_E_INVALID,

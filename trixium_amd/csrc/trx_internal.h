@@ -88,10 +88,55 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Cross-lane steps on the DPP path (no LDS round trip), within each row of 16 lanes:
+// quad_perm [1,0,3,2] and [2,3,0,1] pair lanes l ^ 1 and l ^ 2, row_half_mirror pairs l and
+// 7 - l (within 8), row_mirror pairs l and 15 - l. After the four steps every lane of a row holds
+// the row's sum (or maximum).
+constexpr int kDppQuadXor1 = 0xB1, kDppQuadXor2 = 0x4E, kDppRowHalfMirror = 0x141, kDppRowMirror = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, dpp_i<CTRL>(__builtin_bit_cast(int, v)));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f<kDppQuadXor1>(v);
+  v += dpp_f<kDppQuadXor2>(v);
+  v += dpp_f<kDppRowHalfMirror>(v);
+  v += dpp_f<kDppRowMirror>(v);
+  return v;
+}
+__device__ __forceinline__ int row16_sum_i(int v) {
+  v += dpp_i<kDppQuadXor1>(v);
+  v += dpp_i<kDppQuadXor2>(v);
+  v += dpp_i<kDppRowHalfMirror>(v);
+  v += dpp_i<kDppRowMirror>(v);
+  return v;
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f<kDppQuadXor1>(v));
+  v = fmaxf(v, dpp_f<kDppQuadXor2>(v));
+  v = fmaxf(v, dpp_f<kDppRowHalfMirror>(v));
+  v = fmaxf(v, dpp_f<kDppRowMirror>(v));
+  return v;
+}
+// Whole-wave sum through the rows and four lane reads (uniform result; all lanes active).
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v = row16_sum(v);
+  const int b = __builtin_bit_cast(int, v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)) +
+         __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16)) +
+         __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)) +
+         __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+}
+
 // Block-wide sum; `red` is >= 16 floats of shared memory. All threads get the result.
 __device__ __forceinline__ float block_sum(float v, float* red) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
-  v = wave_sum(v);
+  v = wave_sum_dpp(v);
   __syncthreads();
   if (lane == 0) red[w] = v;
   __syncthreads();
