@@ -51,6 +51,8 @@ def parse_args():
                     help="passes over the 36 layers when timing the dominant kernel")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="launch every kernel eagerly")
+    ap.add_argument("--fusion", action="store_true",
+                    help="one kernel per full-attention layer instead of one per operation")
     ap.add_argument("--only-kernel", action="store_true",
                     help="time only the dominant kernel (for hardware-counter runs)")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -169,7 +171,7 @@ def main():
         sys.exit(f"prompt {a.prompt} + {n_dec} decode tokens exceed the context {mc.max_ctx}")
     graph = not a.no_graph
     dec = Decoder.synthetic(mc, a.seed, weight_kind=kind, max_ctx=mc.max_ctx, max_new=n_dec + 8,
-                            use_graph=graph)
+                            use_graph=graph, layer_fusion=a.fusion)
     prompt = np.random.default_rng(a.seed).integers(0, mc.vocab, a.prompt).astype(np.int32)
     dec.reset()
     dec.feed(prompt)
@@ -216,7 +218,8 @@ def main():
                    "n_layer": mc.n_layer, "n_embd": mc.n_embd, "n_head": mc.n_head,
                    "n_kv_head": mc.n_kv_head, "head_dim": mc.head_dim, "ffn_dim": mc.ffn_dim,
                    "vocab": mc.vocab, "max_ctx": mc.max_ctx, "prompt_tokens": a.prompt,
-                   "decode_tokens": n_dec, "weights": a.kind, "hipgraph": graph},
+                   "decode_tokens": n_dec, "weights": a.kind, "hipgraph": graph,
+                   "fused_layers": dec.fused_layers},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profile(a.kind),

@@ -131,6 +131,8 @@ typedef struct {
   int emb_mode;                /* 0: int16 BFP lookup table; 1: ternary token_embd rows */
   int emb_kind;                /* kind of token_embd rows (emb_mode 1 or a tied head) */
   int max_new;                 /* capacity of the generated-token buffer */
+  int layer_fusion;            /* 1: one kernel per full-attention layer where the geometry has
+                                  one (grid barriers between its phases); 0: one per operation */
 } trx_model_config;
 
 typedef struct trx_model trx_model;
@@ -165,11 +167,15 @@ int trx_model_generate(trx_model* m, const int32_t* prompt, int n_prompt, int n_
 #define TRX_READ_TOKEN 3       /* int32: the token of the last forward */
 #define TRX_READ_OUT 4         /* int32 [max_new]: generated tokens */
 #define TRX_READ_SLOT 5        /* uint64: packed argmax */
+#define TRX_READ_QKV 6         /* float32: q|k|v projection of the last attention layer run */
+#define TRX_READ_ATTN 7        /* float32 [n_head*head_dim]: its attention output */
+#define TRX_READ_ACT 8         /* float32 [ffn_dim]: the last layer's SwiGLU activation */
 int trx_model_read(trx_model* m, int what, void* host, size_t bytes);
 #define TRX_INFO_ARENA_BYTES 0
 #define TRX_INFO_DEVICE_BYTES 1
 #define TRX_INFO_STREAM 2
 #define TRX_INFO_WEIGHT_BYTES 3
+#define TRX_INFO_FUSED_LAYERS 4   /* 1 when full-attention layers run as one kernel each */
 int trx_model_info(trx_model* m, int what, int64_t* value);
 /* Device address and size of one resident tensor (for benchmarks and tests). */
 int trx_model_tensor_ptr(trx_model* m, int role, int layer, void** ptr, int64_t* bytes);

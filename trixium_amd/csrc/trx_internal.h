@@ -145,6 +145,24 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   return t;
 }
 
+// A no-op in place of a grid barrier (standalone kernels).
+struct NoWait {
+  __device__ void operator()() const {}
+};
+
+// Loads and stores of vectors that other blocks of the same launch write or read: agent-scope
+// (cross-XCD coherent) relaxed atomics when C, plain accesses otherwise.
+template <bool C>
+__device__ __forceinline__ float ld_vec(const float* p) {
+  if (C) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return *p;
+}
+template <bool C>
+__device__ __forceinline__ void st_vec(float* p, float v) {
+  if (C) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else *p = v;
+}
+
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
 

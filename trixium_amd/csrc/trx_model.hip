@@ -10,9 +10,11 @@
 #include <map>
 #include <vector>
 #include <functional>
+#include <algorithm>
 
 #include "trx_internal.h"
 #include "trx_ops.h"
+#include "trx_layer.h"
 #include "trx_model.h"
 
 namespace trx {
@@ -38,13 +40,19 @@ struct Model {
   float *x = nullptr, *qkv = nullptr, *attn_out = nullptr, *act = nullptr, *logits = nullptr;
   float *part_m = nullptr, *part_l = nullptr, *part_o = nullptr;
   float *dn_io = nullptr, *dn_ba = nullptr, *dn_out = nullptr, *rope_dev = nullptr;
-  int* ctl = nullptr;  // [0] pos, [1] n_fed, [2] cur_tok, [3] head_from, [8..] fed tokens by
+  int* ctl = nullptr;  // [0] pos, [1] n_fed, [2] cur_tok, [3] head_from, [4] error, [8..] fed tokens by
                        // absolute position (max_ctx), then the generated tokens (max_new)
   int host_pos = -1;   // host mirror of the device position after the enqueued steps
   unsigned long long* slot = nullptr;
   int n_attn = 0, n_dn = 0;
   std::vector<int> attn_index, dn_index;           // per layer: index among attn / dn layers
-  int n_split = 0;
+  int n_split = 0;                                 // attention splits of the per-operation kernels
+  // Fused full-attention layers (one kernel per layer, grid barriers between its phases).
+  LayerSetup layer;
+  bool fused = false;
+  int fused_split = 0;
+  unsigned long long* bar = nullptr;                // barrier counters
+  unsigned* xcc_blocks = nullptr;
   hipGraph_t graph = nullptr;
   hipGraphExec_t graph_exec = nullptr;
   size_t dev_bytes = 0;
@@ -57,6 +65,7 @@ struct Model {
   int* head_from() { return ctl + 3; }
   int* prompt() { return ctl + 8; }
   int* out() { return ctl + 8 + cfg.max_ctx; }
+  int* err() { return ctl + 4; }                   // set by a fused layer whose barrier timed out
 };
 
 static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
@@ -199,6 +208,54 @@ int dn_layer_launch(Model& m, int l, hipStream_t s) {
                   TRX_EPI_RESID, m.x, 0, nullptr, s);
 }
 
+// Full-attention layer as one kernel (trx_layer.hip): the same projections, attention and FFN
+// as the per-operation launches below.
+static int fused_layer_launch(Model& m, int l, hipStream_t s) {
+  const trx_model_config& c = m.cfg;
+  const int E = c.n_embd, hd = c.head_dim, F = c.ffn_dim, wk = c.weight_kind;
+  const int qrows = c.n_head * hd * (c.attn_gated ? 2 : 1), kvrows = c.n_kv_head * hd;
+  LayerParams lp = {};
+  int rc;
+  if ((rc = layer_gemv_params(lp.qkv, P(m, TRX_ROLE_ATTN_Q, l), wk, qrows + 2 * kvrows, E, m.x,
+                              PF(m, TRX_ROLE_ATTN_NORM, l), c.rms_eps, m.qkv, TRX_EPI_STORE, nullptr, 2))) return rc;
+  if ((rc = layer_gemv_params(lp.o, P(m, TRX_ROLE_ATTN_OUT, l), wk, E, c.n_head * hd, m.attn_out, nullptr,
+                              c.rms_eps, m.x, TRX_EPI_RESID, m.x, 1))) return rc;
+  if ((rc = layer_gemv_params(lp.gu, P(m, TRX_ROLE_FFN_GATE, l), wk, 2 * F, E, m.x, PF(m, TRX_ROLE_FFN_NORM, l),
+                              c.rms_eps, m.act, TRX_EPI_SWIGLU, nullptr, 2))) return rc;
+  if ((rc = layer_gemv_params(lp.down, P(m, TRX_ROLE_FFN_DOWN, l), wk, E, F, m.act, nullptr, c.rms_eps, m.x,
+                              TRX_EPI_RESID, m.x, 1))) return rc;
+  AttnParams& ap = lp.attn;
+  ap.qkv = m.qkv;
+  ap.q_norm = PF(m, TRX_ROLE_ATTN_Q_NORM, l);
+  ap.k_norm = PF(m, TRX_ROLE_ATTN_K_NORM, l);
+  ap.rope_freq = m.rope_dev;
+  ap.pos = m.pos();
+  const size_t per = (size_t)c.n_kv_head * c.max_ctx * hd;
+  ap.kcache = m.kcache + (size_t)m.attn_index[l] * per;
+  ap.vcache = m.vcache + (size_t)m.attn_index[l] * per;
+  ap.part_m = m.part_m;
+  ap.part_l = m.part_l;
+  ap.part_o = m.part_o;
+  ap.out = m.attn_out;
+  ap.n_head = c.n_head;
+  ap.n_kv = c.n_kv_head;
+  ap.n_rep = c.n_head / c.n_kv_head;
+  ap.hd = hd;
+  ap.rope_n = c.rope_dims ? c.rope_dims : hd;
+  ap.max_ctx = c.max_ctx;
+  ap.n_split = m.fused_split;
+  ap.gated = c.attn_gated;
+  ap.eps = c.rms_eps;
+  lp.bar = m.bar;
+  lp.xcc_blocks = m.xcc_blocks;
+  lp.pos = m.pos();
+  lp.n_layers = m.n_attn;
+  lp.layer_slot = m.attn_index[l];
+  lp.n_xcc = m.layer.n_xcc;
+  lp.err = m.err();
+  return launch_layer(m.layer, lp, s);
+}
+
 static int run_step(Model& m, hipStream_t s) {
   const trx_model_config& c = m.cfg;
   const int E = c.n_embd, hd = c.head_dim, F = c.ffn_dim;
@@ -232,6 +289,10 @@ static int run_step(Model& m, hipStream_t s) {
   for (int l = 0; l < c.n_layer; ++l) {
     if (m.is_dn(l)) {
       if ((rc = dn_layer_launch(m, l, s))) return rc;
+    } else if (m.fused) {
+      // Attention and the FFN in one launch.
+      if ((rc = fused_layer_launch(m, l, s))) return rc;
+      continue;
     } else {
       // q|k|v with the attention RMSNorm fused in the prologue.
       if ((rc = gemv_f32(P(m, TRX_ROLE_ATTN_Q, l), wk, qrows + 2 * kvrows, E, m.x,
@@ -338,6 +399,19 @@ TRX_API int trx_model_create(const trx_model_config* cfg, const float* rope_freq
     set_error("trx_model_create: context %d is too long for the attention kernel", c.max_ctx);
     return fail(TRX_E_INVALID);
   }
+  if ((rc = dalloc(m, (void**)&m.bar, 17 * 32 * sizeof(unsigned long long)))) return fail(rc);
+  if ((rc = dalloc(m, (void**)&m.xcc_blocks, 16 * sizeof(unsigned)))) return fail(rc);
+  if (c.layer_fusion && m.n_attn > 0 && c.n_kv_head > 0) {
+    const int rep = c.n_head / c.n_kv_head;
+    if ((rc = layer_prepare(m.layer, c.weight_kind, rep, hd, c.n_embd, c.n_head * hd, c.ffn_dim, m.xcc_blocks)))
+      return fail(rc);
+    if (m.layer.ok) {
+      m.fused_split = m.layer.blocks / c.n_kv_head;
+      m.fused = m.fused_split >= 1 && m.fused_split <= 256 && c.n_head <= m.layer.blocks &&
+                cdiv(c.max_ctx, m.fused_split) <= attention_max_chunk(hd);
+    }
+  }
+  const int splits = std::max(m.n_split, m.fused ? m.fused_split : 0);
   const size_t kv = (size_t)m.n_attn * c.n_kv_head * c.max_ctx * hd;
   if (m.n_attn) {
     if ((rc = dalloc(m, (void**)&m.kcache, kv * 2))) return fail(rc);
@@ -358,9 +432,9 @@ TRX_API int trx_model_create(const trx_model_config* cfg, const float* rope_freq
   if ((rc = dalloc(m, (void**)&m.attn_out, (size_t)c.n_head * hd * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.act, (size_t)c.ffn_dim * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.logits, (size_t)c.vocab * 4))) return fail(rc);
-  if ((rc = dalloc(m, (void**)&m.part_m, (size_t)c.n_head * m.n_split * 4))) return fail(rc);
-  if ((rc = dalloc(m, (void**)&m.part_l, (size_t)c.n_head * m.n_split * 4))) return fail(rc);
-  if ((rc = dalloc(m, (void**)&m.part_o, (size_t)c.n_head * m.n_split * hd * 4))) return fail(rc);
+  if ((rc = dalloc(m, (void**)&m.part_m, (size_t)c.n_head * splits * 4))) return fail(rc);
+  if ((rc = dalloc(m, (void**)&m.part_l, (size_t)c.n_head * splits * 4))) return fail(rc);
+  if ((rc = dalloc(m, (void**)&m.part_o, (size_t)c.n_head * splits * hd * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.rope_dev, (size_t)rope_n * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.ctl, (size_t)(8 + c.max_ctx + c.max_new) * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.slot, 8))) return fail(rc);
@@ -448,6 +522,7 @@ TRX_API int trx_model_reset(trx_model* h) {
   m.host_pos = -1;
   TRX_HIP(hipMemcpyAsync(m.ctl, init, sizeof init, hipMemcpyHostToDevice, m.stream));
   TRX_HIP(hipMemsetAsync(m.slot, 0, 8, m.stream));
+  TRX_HIP(hipMemsetAsync(m.bar, 0, 17 * 32 * sizeof(unsigned long long), m.stream));
   if (m.n_dn) {
     const int nq = c.dn_num_k_heads * c.dn_k_head_dim, nvh = c.dn_num_v_heads * c.dn_v_head_dim;
     TRX_HIP(hipMemsetAsync(m.conv_state, 0, (size_t)m.n_dn * (c.dn_conv_kernel - 1) * (2 * nq + nvh) * 4, m.stream));
@@ -515,10 +590,22 @@ TRX_API int trx_model_finalize(trx_model* h) {
   return launch_finalize(m.pos(), m.n_prompt(), m.slot, m.out(), m.cfg.max_new, m.stream);
 }
 
+// After the stream has drained: a fused layer whose grid barrier timed out left garbage.
+static int check_err(Model& m) {
+  int e = 0;
+  TRX_HIP(hipMemcpy(&e, m.err(), 4, hipMemcpyDeviceToHost));
+  if (e) {
+    const int zero = 0;
+    TRX_HIP(hipMemcpy(m.err(), &zero, 4, hipMemcpyHostToDevice));
+    TRX_CHECK(false, TRX_E_HIP, "a fused layer's grid barrier timed out (not every block was resident)");
+  }
+  return TRX_OK;
+}
+
 TRX_API int trx_model_sync(trx_model* h) {
   TRX_CHECK(h, TRX_E_INVALID, "trx_model_sync: null");
   TRX_HIP(hipStreamSynchronize(h->m.stream));
-  return TRX_OK;
+  return check_err(h->m);
 }
 
 TRX_API int trx_model_generate(trx_model* h, const int32_t* prompt, int n_prompt, int n_new,
@@ -536,12 +623,13 @@ TRX_API int trx_model_generate(trx_model* h, const int32_t* prompt, int n_prompt
   if ((rc = trx_model_finalize(h))) return rc;
   TRX_HIP(hipMemcpyAsync(out, m.out(), (size_t)n_new * 4, hipMemcpyDeviceToHost, m.stream));
   TRX_HIP(hipStreamSynchronize(m.stream));
-  return TRX_OK;
+  return check_err(m);
 }
 
 TRX_API int trx_model_read(trx_model* h, int what, void* host, size_t bytes) {
   TRX_CHECK(h && host, TRX_E_INVALID, "trx_model_read: null argument");
   Model& m = h->m;
+  int rc;
   const trx_model_config& c = m.cfg;
   const void* src = nullptr;
   size_t n = 0;
@@ -552,10 +640,17 @@ TRX_API int trx_model_read(trx_model* h, int what, void* host, size_t bytes) {
     case TRX_READ_TOKEN: src = m.cur_tok(); n = 4; break;
     case TRX_READ_OUT: src = m.out(); n = (size_t)c.max_new * 4; break;
     case TRX_READ_SLOT: src = m.slot; n = 8; break;
+    case TRX_READ_QKV:
+      src = m.qkv;
+      n = (size_t)(c.n_head * c.head_dim * (c.attn_gated ? 2 : 1) + 2 * c.n_kv_head * c.head_dim) * 4;
+      break;
+    case TRX_READ_ATTN: src = m.attn_out; n = (size_t)c.n_head * c.head_dim * 4; break;
+    case TRX_READ_ACT: src = m.act; n = (size_t)c.ffn_dim * 4; break;
     default: TRX_CHECK(false, TRX_E_INVALID, "trx_model_read: unknown item %d", what);
   }
   TRX_CHECK(bytes <= n, TRX_E_INVALID, "trx_model_read: %zu bytes requested, %zu available", bytes, n);
   TRX_HIP(hipStreamSynchronize(m.stream));
+  if ((rc = check_err(m))) return rc;
   TRX_HIP(hipMemcpy(host, src, bytes, hipMemcpyDeviceToHost));
   return TRX_OK;
 }
@@ -567,6 +662,7 @@ TRX_API int trx_model_info(trx_model* h, int what, int64_t* value) {
     case TRX_INFO_ARENA_BYTES: *value = (int64_t)m.arena_bytes; break;
     case TRX_INFO_DEVICE_BYTES: *value = (int64_t)m.dev_bytes; break;
     case TRX_INFO_STREAM: *value = (int64_t)(intptr_t)m.stream; break;
+    case TRX_INFO_FUSED_LAYERS: *value = m.fused ? 1 : 0; break;
     case TRX_INFO_WEIGHT_BYTES: {
       int64_t s = 0;
       for (auto& kv : m.tensors) s += (int64_t)kv.second.bytes;

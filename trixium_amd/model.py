@@ -22,8 +22,8 @@ from .configs import ModelConfig
 
 f32 = np.float32
 
-READ_LOGITS, READ_HIDDEN, READ_POSITION, READ_TOKEN, READ_OUT, READ_SLOT = range(6)
-INFO_ARENA_BYTES, INFO_DEVICE_BYTES, INFO_STREAM, INFO_WEIGHT_BYTES = range(4)
+READ_LOGITS, READ_HIDDEN, READ_POSITION, READ_TOKEN, READ_OUT, READ_SLOT, READ_QKV, READ_ATTN, READ_ACT = range(9)
+INFO_ARENA_BYTES, INFO_DEVICE_BYTES, INFO_STREAM, INFO_WEIGHT_BYTES, INFO_FUSED_LAYERS = range(5)
 
 # Ranges of the counter-based synthetic weights (the ternary group scales and the RMSNorm gains).
 SYNTH_SCALE = (0.01, 0.05)
@@ -47,7 +47,8 @@ def layer_type_bits(layer_types, n_layer):
     return (bits & (2**64 - 1), bits >> 64)
 
 
-def make_config(mc, weight_kind, head_kind, head_tied, emb_mode, emb_kind, max_ctx=None, max_new=256):
+def make_config(mc, weight_kind, head_kind, head_tied, emb_mode, emb_kind, max_ctx=None, max_new=256,
+                layer_fusion=False):
     """trx_model_config from a ModelConfig (or a BONS header turned into one)."""
     c = _lib.ModelConfig()
     for name in ("n_layer", "n_embd", "n_head", "n_kv_head", "head_dim", "ffn_dim", "vocab",
@@ -61,6 +62,7 @@ def make_config(mc, weight_kind, head_kind, head_tied, emb_mode, emb_kind, max_c
     c.layer_types[0], c.layer_types[1] = lo, hi
     c.weight_kind, c.head_kind, c.head_tied = weight_kind, head_kind, int(bool(head_tied))
     c.emb_mode, c.emb_kind, c.max_new = emb_mode, emb_kind, int(max_new)
+    c.layer_fusion = int(bool(layer_fusion))
     return c
 
 
@@ -94,7 +96,7 @@ class Decoder:
 
     # Construction ------------------------------------------------------------------------------
     @classmethod
-    def from_image(cls, img, max_ctx=None, max_new=256, use_graph=True):
+    def from_image(cls, img, max_ctx=None, max_new=256, use_graph=True, layer_fusion=False):
         """Load a BONS image (path or BONSReader) into HBM."""
         from .bons import BONSReader
         if isinstance(img, str):
@@ -119,7 +121,7 @@ class Decoder:
         else:
             head_kind = L.KIND_F16 if head["kind"] == L.KIND_F32 else head["kind"]
             emb_kind = emb["kind"] if emb is not None and L.is_ternary(emb["kind"]) else weight_kind
-        cfg = make_config(mc, weight_kind, head_kind, head_tied, 0, emb_kind, max_ctx, max_new)
+        cfg = make_config(mc, weight_kind, head_kind, head_tied, 0, emb_kind, max_ctx, max_new, layer_fusion)
         d = cls(mc, cfg, use_graph)
         try:
             d._load_image(img)
@@ -130,13 +132,14 @@ class Decoder:
 
     @classmethod
     def synthetic(cls, mc, seed=0, weight_kind=L.KIND_TERNARY5, max_ctx=None, max_new=256,
-                  use_graph=True):
+                  use_graph=True, layer_fusion=False):
         """Fill every tensor on the device from the counter-based generator (same values as
         trixium_amd.synth.hashed_*): ternary token_embd rows (embedded by decoding the row), an
         untied ternary LM head unless the config ties them."""
         if mc.n_dn_layers:
             raise NotImplementedError("synthetic DeltaNet layers (Q8 beta/alpha) have no device generator")
-        cfg = make_config(mc, weight_kind, weight_kind, mc.tie_embeddings, 1, weight_kind, max_ctx, max_new)
+        cfg = make_config(mc, weight_kind, weight_kind, mc.tie_embeddings, 1, weight_kind, max_ctx, max_new,
+                          layer_fusion)
         d = cls(mc, cfg, use_graph)
         try:
             ranges = np.array([SYNTH_SCALE[0], SYNTH_SCALE[1] - SYNTH_SCALE[0],
@@ -272,6 +275,15 @@ class Decoder:
     def hidden(self):
         return self._read(READ_HIDDEN, np.empty(self.n_embd, dtype=f32))
 
+    def taps(self):
+        """Intermediate vectors of the last forward: the last attention layer's q|k|v projection
+        and attention output, and the last layer's SwiGLU activation (float32)."""
+        c = self.cfg
+        nq = c.n_head * c.head_dim * (2 if c.attn_gated else 1) + 2 * c.n_kv_head * c.head_dim
+        return {"qkv": self._read(READ_QKV, np.empty(nq, dtype=f32)),
+                "attn": self._read(READ_ATTN, np.empty(c.n_head * c.head_dim, dtype=f32)),
+                "act": self._read(READ_ACT, np.empty(c.ffn_dim, dtype=f32))}
+
     def position(self):
         """Position of the last forward (-1 after reset)."""
         return int(self._read(READ_POSITION, np.empty(1, dtype=np.int32))[0])
@@ -280,6 +292,11 @@ class Decoder:
         v = ctypes.c_int64()
         _lib.call("trx_model_info", self._h, what, ctypes.byref(v))
         return v.value
+
+    @property
+    def fused_layers(self):
+        """True when full-attention layers run as one kernel each."""
+        return bool(self.info(INFO_FUSED_LAYERS))
 
     @property
     def stream(self):
