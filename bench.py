@@ -51,6 +51,9 @@ def parse_args():
                     help="passes over the 36 layers when timing the dominant kernel")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="launch every kernel eagerly")
+    ap.add_argument("--packed-ops", type=int, default=-1,
+                    help="projections on the packed GEMV, as TRX_PACK_* bits (-1: the library's "
+                         "choice for the weight kind, 0: none, 63: all)")
     ap.add_argument("--fusion", action="store_true",
                     help="one kernel per full-attention layer instead of one per operation")
     ap.add_argument("--only-kernel", action="store_true",
@@ -80,15 +83,25 @@ def time_dominant_kernel(dec, mc, reps):
     E, F = mc.n_embd, mc.ffn_dim
     x = _lib.DeviceBuffer.from_array(np.random.default_rng(1).standard_normal(E).astype(np.float32))
     y = _lib.DeviceBuffer(F * 4)
+    from trixium_amd.model import PACK_GATE_UP
     s = dec.stream
     kind = dec.cfg.weight_kind
-    mats = [dec.tensor_ptr(L.ROLE_FFN_GATE, l)[0] for l in range(mc.n_layer)]
     norms = [dec.tensor_ptr(L.ROLE_FFN_NORM, l)[0] for l in range(mc.n_layer)]
+    packed = bool(dec.packed_ops & PACK_GATE_UP)
+    if packed:
+        mats = [dec.packed_ptr(PACK_GATE_UP, l) for l in range(mc.n_layer)]
 
-    def launch():
-        for w, g in zip(mats, norms):
-            _lib.call("trx_gemv_ternary_f32", w, kind, 2 * F, E, x.ptr, g, ctypes.c_float(mc.rms_eps),
-                      y.ptr, _lib.EPI_SWIGLU, None, s)
+        def launch():
+            for (w, ws), g in zip(mats, norms):
+                _lib.call("trx_gemv_packed_f32", w, kind, 2 * F, E, x.ptr, g, ctypes.c_float(mc.rms_eps),
+                          y.ptr, _lib.EPI_SWIGLU, None, ws, s)
+    else:
+        mats = [dec.tensor_ptr(L.ROLE_FFN_GATE, l)[0] for l in range(mc.n_layer)]
+
+        def launch():
+            for w, g in zip(mats, norms):
+                _lib.call("trx_gemv_ternary_f32", w, kind, 2 * F, E, x.ptr, g, ctypes.c_float(mc.rms_eps),
+                          y.ptr, _lib.EPI_SWIGLU, None, s)
 
     launch()
     _lib.call("trx_stream_sync", s)
@@ -107,13 +120,15 @@ def time_dominant_kernel(dec, mc, reps):
     n = reps * len(mats)
     rb = L.row_bytes(E, kind)
     algo = 2 * F * rb + E * 4 + E * 4 + F * 4
-    return ms.value * 1e3 / n, algo, n
+    return ms.value * 1e3 / n, algo, n, packed
 
 
-def traffic_from_profile(kind):
+def traffic_from_profile(kind, packed):
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3 counter summary
-    (FETCH_SIZE + WRITE_SIZE, calibrated on a copy kernel), when one exists for this format."""
-    path = os.path.join(ROOT, "profiles", f"gemv_gateup_8b_{kind}_pmc.md")
+    (FETCH_SIZE + WRITE_SIZE, calibrated on a copy kernel), when one exists for this format and
+    kernel."""
+    name = f"gemv_gateup_8b_{kind}_packed_pmc.md" if packed else f"gemv_gateup_8b_{kind}_pmc.md"
+    path = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(path):
         return None
     with open(path) as f:
@@ -160,8 +175,9 @@ def main():
     mc = C.QWEN3_8B
     kind = L.KIND_TERNARY5 if a.kind == "trit5" else L.KIND_TERNARY
     if a.only_kernel:
-        dec = Decoder.synthetic(mc, a.seed, weight_kind=kind, max_ctx=mc.max_ctx, max_new=8)
-        us, algo, n_launch = time_dominant_kernel(dec, mc, a.kernel_reps)
+        dec = Decoder.synthetic(mc, a.seed, weight_kind=kind, max_ctx=mc.max_ctx, max_new=8,
+                                packed_ops=a.packed_ops)
+        us, algo, n_launch, _ = time_dominant_kernel(dec, mc, a.kernel_reps)
         print(json.dumps({"kernel_us": round(us, 3), "bytes_per_launch": algo, "launches": n_launch,
                           "achieved_GBs": round(algo / (us * 1e-6) / 1e9, 1)}), flush=True)
         dec.close()
@@ -171,7 +187,7 @@ def main():
         sys.exit(f"prompt {a.prompt} + {n_dec} decode tokens exceed the context {mc.max_ctx}")
     graph = not a.no_graph
     dec = Decoder.synthetic(mc, a.seed, weight_kind=kind, max_ctx=mc.max_ctx, max_new=n_dec + 8,
-                            use_graph=graph, layer_fusion=a.fusion)
+                            use_graph=graph, layer_fusion=a.fusion, packed_ops=a.packed_ops)
     prompt = np.random.default_rng(a.seed).integers(0, mc.vocab, a.prompt).astype(np.int32)
     dec.reset()
     dec.feed(prompt)
@@ -198,7 +214,7 @@ def main():
     tok_bytes = wbytes - emb_rows + emb_row + kv
     roof_tok_s = HBM_PEAK_GBS * 1e9 / tok_bytes
 
-    us, algo, n_launch = time_dominant_kernel(dec, mc, a.kernel_reps)
+    us, algo, n_launch, gu_packed = time_dominant_kernel(dec, mc, a.kernel_reps)
     achieved = algo / (us * 1e-6) / 1e9
     rec = {
         "metric": "batch-1 decode tok/s (8B shape); ternary matvec HBM GB/s vs ~8 TB/s peak",
@@ -219,12 +235,13 @@ def main():
                    "n_kv_head": mc.n_kv_head, "head_dim": mc.head_dim, "ffn_dim": mc.ffn_dim,
                    "vocab": mc.vocab, "max_ctx": mc.max_ctx, "prompt_tokens": a.prompt,
                    "decode_tokens": n_dec, "weights": a.kind, "hipgraph": graph,
-                   "fused_layers": dec.fused_layers},
+                   "fused_layers": dec.fused_layers, "packed_ops": dec.packed_ops},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic_from_profile(a.kind),
+                     "traffic": traffic_from_profile(a.kind, gu_packed),
                      "kernel": f"ternary GEMV gate|up {2 * mc.ffn_dim}x{mc.n_embd} {a.kind}, "
-                               f"RMSNorm + SwiGLU fused",
+                               f"RMSNorm + SwiGLU fused, "
+                               f"{'packed table-lookup kernel' if gu_packed else 'row-packet kernel'}",
                      "us_per_launch": round(us, 3), "bytes_per_launch": algo, "launches": n_launch},
         "token_roofline": {"bytes_per_token": int(tok_bytes), "tok_s": round(roof_tok_s, 1),
                            "frac": round(tok_s / roof_tok_s, 4)},

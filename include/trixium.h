@@ -85,6 +85,28 @@ int trx_gemv_ternary_f32(const uint8_t* rows, int kind, int M, int K, const floa
                          const float* norm_w, float eps, float* y, int epilogue,
                          const float* resid, trx_stream_t s);
 
+/* Packed float GEMV: the decoder's projection (the same arithmetic as trx_gemv_ternary_f32, with
+ * x kept in fp32) over a GPU-native copy of the rows. The copy cuts K into 256-column slices
+ * (two 128-groups) and stores, per slice, the rows' code bytes and fp16 scales slice-major in
+ * the order the kernel reads them; it holds the same bytes per row as the BONS packets. A block
+ * of the kernel builds, for its slice, the table of every code byte's partial dot product with x
+ * in LDS, so a code byte costs one LDS read and one add; per-slice partial sums are combined in
+ * slice order (deterministic) by the block that completes a tile of rows last.
+ *
+ * trx_pack_geometry: bytes of the packed copy and of the workspace the GEMV needs.
+ * trx_pack_ternary: rows (as for trx_gemv_ternary_f32) -> packed copy. swiglu = 1 packs a
+ *   [gate | up] matrix (M = 2F, F even) for TRX_EPI_SWIGLU.
+ * trx_gemv_packed_f32: y = W xhat, xhat = x or x / rms(x) * norm_w (fastref.py:119-125,143-145)
+ *   with the epilogue; `workspace` holds trx_pack_geometry's workspace bytes, zeroed once before
+ *   its first use (every call leaves it ready for the next); calls sharing a workspace must not
+ *   overlap. x must be 16-byte aligned. */
+int trx_pack_geometry(int kind, int M, int K, size_t* packed_bytes, size_t* workspace_bytes);
+int trx_pack_ternary(const uint8_t* rows, int kind, int M, int K, int swiglu, uint8_t* packed,
+                     trx_stream_t s);
+int trx_gemv_packed_f32(const uint8_t* packed, int kind, int M, int K, const float* x,
+                        const float* norm_w, float eps, float* y, int epilogue,
+                        const float* resid, void* workspace, trx_stream_t s);
+
 /* Decoder ----------------------------------------------------------------------------------------
  * A batch-1 greedy decoder over a BONS model held on the GPU: the GPU counterpart of
  * model/golden.py:FloatModel (reset/forward/generate, golden.py:304-320,436-470) with the
@@ -133,7 +155,21 @@ typedef struct {
   int max_new;                 /* capacity of the generated-token buffer */
   int layer_fusion;            /* 1: one kernel per full-attention layer where the geometry has
                                   one (grid barriers between its phases); 0: one per operation */
+  int packed_ops;              /* projections run by the packed GEMV (trx_gemv_packed_f32) over
+                                  a packed copy of their rows, as TRX_PACK_* bits; the others run
+                                  trx_gemv_ternary_f32's kernel. TRX_PACK_AUTO: the library's
+                                  choice for the weight kind. (With layer_fusion the fused layers
+                                  keep the row-packet kernel.) */
 } trx_model_config;
+
+#define TRX_PACK_QKV 1         /* attention q|k|v */
+#define TRX_PACK_O 2           /* attention output */
+#define TRX_PACK_GATE_UP 4     /* FFN gate|up with SwiGLU */
+#define TRX_PACK_DOWN 8        /* FFN down */
+#define TRX_PACK_HEAD 16       /* ternary LM head (with the argmax) */
+#define TRX_PACK_DN 32         /* Gated DeltaNet qkv|z and out projections */
+#define TRX_PACK_ALL 63
+#define TRX_PACK_AUTO (-1)
 
 typedef struct trx_model trx_model;
 
@@ -176,9 +212,14 @@ int trx_model_read(trx_model* m, int what, void* host, size_t bytes);
 #define TRX_INFO_STREAM 2
 #define TRX_INFO_WEIGHT_BYTES 3
 #define TRX_INFO_FUSED_LAYERS 4   /* 1 when full-attention layers run as one kernel each */
+#define TRX_INFO_PACKED_OPS 5     /* TRX_PACK_* bits in effect */
 int trx_model_info(trx_model* m, int what, int64_t* value);
 /* Device address and size of one resident tensor (for benchmarks and tests). */
 int trx_model_tensor_ptr(trx_model* m, int role, int layer, void** ptr, int64_t* bytes);
+/* Packed copy of one projection (op: TRX_PACK_QKV, _O, _GATE_UP, _DOWN or _HEAD with layer 0) and
+ * the workspace the model's packed GEMVs share, for trx_gemv_packed_f32 (benchmarks and tests;
+ * do not overlap with the model's own work). */
+int trx_model_packed_ptr(trx_model* m, int op, int layer, void** packed, void** workspace);
 
 /* Tuning: force the GEMV rows per item (0 = automatic; 1: 4 rows, 2: 2 rows, 3: 1 row, 2 for
  * SwiGLU). Process-wide; for benchmarks and tests. No counterpart in the reference. */

@@ -183,3 +183,35 @@ def test_fused_layers_match_per_operation_kernels(tiny_images, golden, name):
     assert ta == tb
     assert _rel_err(a.logits(), b.logits()) <= 1e-3
     assert a.generate_fresh(prompt, 16, use_graph=False) == ta
+
+
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-ternemb", "tiny-hybrid"])
+@pytest.mark.parametrize("packed", [0, 63])
+def test_packed_projections_match_oracle(tiny_images, golden, name, packed):
+    """Every projection on the packed GEMV (63 = TRX_PACK_ALL), or none of them: logits at every
+    position against the float oracle and the greedy tokens against the fixture."""
+    from trixium_amd.model import Decoder
+    prompt = golden[f"prompt/{name}"]
+    seq = prompt + golden[f"fastref_tokens/{name}"][:12]
+    img = bons.BONSReader(tiny_images[(name, True)])
+    dec = Decoder.from_image(tiny_images[(name, True)], max_new=N_NEW[name], packed_ops=packed)
+    assert dec.packed_ops == packed
+    lg = _teacher_forced_logits(dec, seq, len(prompt))
+    ref = FloatRef(img, kv_fp16=True)
+    want = [ref.forward(prompt)] + [ref.step(t) for t in seq[len(prompt):]]
+    errs = [_rel_err(g, w) for g, w in zip(lg, want)]
+    print(name, packed, "max rel err", max(errs))
+    assert max(errs) <= 2e-3
+    got = dec.generate_fresh(prompt, N_NEW[name])
+    assert got == golden[f"fastref_tokens/{name}"][:N_NEW[name]]
+
+
+def test_packed_graph_replay_equals_eager(tiny_images, golden):
+    from trixium_amd.model import Decoder
+    name = "tiny-hybrid"
+    prompt = golden[f"prompt/{name}"]
+    a = Decoder.from_image(tiny_images[(name, True)], max_new=16, packed_ops=63, use_graph=True)
+    b = Decoder.from_image(tiny_images[(name, True)], max_new=16, packed_ops=63, use_graph=False)
+    assert a.generate_fresh(prompt, 16) == b.generate_fresh(prompt, 16)
+    a.reset(); b.reset()
+    assert np.array_equal(a.forward(prompt), b.forward(prompt))

@@ -41,6 +41,11 @@ def test_errors_are_reported_without_a_device_call():
     assert b"null" in L.trx_last_error()
     rc = L.trx_gemv_ternary_f32(ctypes.c_void_p(16), 7, 4, 256, None, None, 1e-6, None, 0, None, None)
     assert rc == _lib.TRX_E_INVALID
+    pb, wb = ctypes.c_size_t(), ctypes.c_size_t()
+    rc = L.trx_pack_geometry(7, 4, 256, ctypes.byref(pb), ctypes.byref(wb))
+    assert rc == _lib.TRX_E_INVALID and b"not ternary" in L.trx_last_error()
+    rc = L.trx_pack_geometry(5, 4, 200, ctypes.byref(pb), ctypes.byref(wb))
+    assert rc == _lib.TRX_E_INVALID and b"multiple of 128" in L.trx_last_error()
 
 
 def test_decoder_config_from_images(tiny_images):

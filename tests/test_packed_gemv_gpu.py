@@ -1,0 +1,140 @@
+"""Packed float GEMV (table lookup over the slice-major copy) on the GPU against float64
+evaluations of the same product: plain, RMSNorm prologue, residual and SwiGLU epilogues, odd
+group counts and ragged row counts, both code formats, determinism and workspace reuse."""
+
+import numpy as np
+import pytest
+
+from trixium_amd import layout as L
+
+pytestmark = pytest.mark.gpu
+
+KINDS = [L.KIND_TERNARY5, L.KIND_TERNARY]
+EPI_STORE, EPI_RESID, EPI_SWIGLU = 0, 1, 2
+# fp32 table entries and sums against float64: error relative to sum |w| |x| per row.
+TOL = 2e-6
+
+
+def _rand(M, K, seed, p0=0.4, max_code=2):
+    r = np.random.default_rng(seed)
+    u = r.random((M, K))
+    codes = np.where(u < (1 - p0) / 2, 0, np.where(u < (1 + p0) / 2, 1, 2)).astype(np.uint8)
+    if max_code == 3:
+        codes[r.random((M, K)) < 0.1] = 3
+    scales = r.uniform(0.01, 0.05, (M, K // 128)).astype(np.float16)
+    return codes, scales
+
+
+def _w64(codes, scales):
+    M, K = codes.shape
+    W = (codes.astype(np.float64) - 1).reshape(M, -1, 128) * scales.astype(np.float64)[:, :, None]
+    return W.reshape(M, K)
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    from trixium_amd import _lib
+    if _lib.device_count() < 1:
+        pytest.fail("no GPU visible to libtrixium_hip")
+    from trixium_amd import bitexact
+    return bitexact
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("M,K", [(1, 128), (3, 256), (7, 384), (33, 768), (257, 2048), (1000, 4096),
+                                 (4099, 256), (50, 12288), (130, 4224)])
+def test_packed_matvec_vs_float64(gpu, kind, M, K):
+    print(f"packed matvec kind={kind} M={M} K={K}", flush=True)
+    codes, scales = _rand(M, K, K * 7 + M)
+    x = np.random.default_rng(M + 1).normal(0, 1, K).astype(np.float32)
+    pm = gpu.PackedMatrix(scales, codes, kind)
+    y = pm.matvec(x)
+    W = _w64(codes, scales)
+    ref = W @ x.astype(np.float64)
+    mag = np.abs(W) @ np.abs(x.astype(np.float64))
+    assert np.max(np.abs(y - ref) / mag) < TOL
+
+
+def test_packed_matvec_code3_two_bit(gpu):
+    """2-bit code 3 decodes to weight 2 (code - 1), as the reference's decode does."""
+    M, K = 64, 1024
+    codes, scales = _rand(M, K, 3, max_code=3)
+    x = np.random.default_rng(4).normal(0, 1, K).astype(np.float32)
+    y = gpu.PackedMatrix(scales, codes, L.KIND_TERNARY).matvec(x)
+    W = _w64(codes, scales)
+    assert np.max(np.abs(y - W @ x) / (np.abs(W) @ np.abs(x))) < TOL
+
+
+@pytest.mark.parametrize("kind", KINDS)
+def test_packed_matvec_zero_weights_and_zero_x(gpu, kind):
+    M, K = 40, 512
+    codes = np.ones((M, K), np.uint8)
+    scales = np.full((M, K // 128), 0.03, np.float16)
+    x = np.random.default_rng(0).normal(0, 1, K).astype(np.float32)
+    assert np.all(gpu.PackedMatrix(scales, codes, kind).matvec(x) == 0)
+    codes, scales = _rand(M, K, 1)
+    assert np.all(gpu.PackedMatrix(scales, codes, kind).matvec(np.zeros(K, np.float32)) == 0)
+
+
+@pytest.mark.parametrize("kind", KINDS)
+def test_packed_matvec_rmsnorm_prologue(gpu, kind):
+    M, K = 300, 2048
+    codes, scales = _rand(M, K, 5)
+    r = np.random.default_rng(6)
+    x = r.normal(0, 3, K).astype(np.float32)
+    w = r.uniform(0.8, 1.2, K).astype(np.float32)
+    y = gpu.PackedMatrix(scales, codes, kind).matvec(x, norm_w=w, eps=1e-6)
+    xn = x.astype(np.float64) / np.sqrt(np.mean(x.astype(np.float64) ** 2) + 1e-6) * w
+    W = _w64(codes, scales)
+    assert np.max(np.abs(y - W @ xn) / (np.abs(W) @ np.abs(xn))) < 1e-5
+
+
+@pytest.mark.parametrize("kind", KINDS)
+def test_packed_matvec_residual(gpu, kind):
+    M, K = 515, 1024
+    codes, scales = _rand(M, K, 7)
+    r = np.random.default_rng(8)
+    x = r.normal(0, 1, K).astype(np.float32)
+    res = r.normal(0, 2, M).astype(np.float32)
+    y = gpu.PackedMatrix(scales, codes, kind).matvec(x, epilogue=EPI_RESID, resid=res)
+    W = _w64(codes, scales)
+    ref = res.astype(np.float64) + W @ x
+    assert np.max(np.abs(y - ref) / (np.abs(W) @ np.abs(x) + np.abs(res))) < TOL
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("F,K", [(2, 256), (6, 384), (300, 1024), (1536, 4096)])
+def test_packed_matvec_swiglu(gpu, kind, F, K):
+    codes, scales = _rand(2 * F, K, F + K)
+    x = np.random.default_rng(F).normal(0, 1, K).astype(np.float32)
+    y = gpu.PackedMatrix(scales, codes, kind, swiglu=True).matvec(x, epilogue=EPI_SWIGLU)
+    W = _w64(codes, scales)
+    g, u = W[:F] @ x, W[F:] @ x
+    ref = g / (1 + np.exp(-g)) * u
+    mg, mu = np.abs(W[:F]) @ np.abs(x), np.abs(W[F:]) @ np.abs(x)
+    err = np.abs(y - ref) / (mg * (np.abs(u) + mu) + 1e-30)
+    assert y.shape == (F,) and np.max(err) < 1e-5
+
+
+def test_packed_matvec_deterministic_and_reusable(gpu):
+    """Bitwise identical repeats; the workspace counters are left ready after every call."""
+    codes, scales = _rand(6144, 4096, 9)
+    pm = gpu.PackedMatrix(scales, codes)
+    r = np.random.default_rng(1)
+    xs = [r.normal(0, 1, 4096).astype(np.float32) for _ in range(3)]
+    first = [pm.matvec(x) for x in xs]
+    again = [pm.matvec(x) for x in xs]
+    W = _w64(codes, scales)
+    for x, a, b in zip(xs, first, again):
+        assert np.array_equal(a, b)
+        assert np.max(np.abs(a - W @ x) / (np.abs(W) @ np.abs(x))) < TOL
+
+
+def test_packed_matvec_agrees_with_int16_path(gpu):
+    """The packed path (fp32 x) and the row-packet path (x quantised to int16 per group)."""
+    codes, scales = _rand(512, 4096, 11)
+    x = np.random.default_rng(2).normal(0, 1, 4096).astype(np.float32)
+    a = gpu.PackedMatrix(scales, codes).matvec(x)
+    b = gpu.matvec_float(scales, codes, x)
+    W = _w64(codes, scales)
+    assert np.max(np.abs(a - b) / (np.abs(W) @ np.abs(x))) < 2e-4

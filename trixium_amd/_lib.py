@@ -31,7 +31,7 @@ class ModelConfig(ctypes.Structure):
                                     "dn_v_head_dim", "dn_conv_kernel")] + [
         ("layer_types", ctypes.c_uint64 * 2)] + [
         (n, ctypes.c_int) for n in ("weight_kind", "head_kind", "head_tied", "emb_mode", "emb_kind",
-                                    "max_new", "layer_fusion")]
+                                    "max_new", "layer_fusion", "packed_ops")]
 
 
 _mcp = ctypes.POINTER(ModelConfig)
@@ -59,6 +59,9 @@ SIGNATURES = {
     "trx_gemv_ternary_exact": [_vp, _i, _i, _i, _vp, _i, _i, _vp, _vp, _vp],
     "trx_gemv_ternary_groupsums": [_vp, _i, _i, _i, _vp, _vp, _vp],
     "trx_gemv_ternary_f32": [_vp, _i, _i, _i, _vp, _vp, _f, _vp, _i, _vp, _vp],
+    "trx_pack_geometry": [_i, _i, _i, ctypes.POINTER(_sz), ctypes.POINTER(_sz)],
+    "trx_pack_ternary": [_vp, _i, _i, _i, _i, _vp, _vp],
+    "trx_gemv_packed_f32": [_vp, _i, _i, _i, _vp, _vp, _f, _vp, _i, _vp, _vp, _vp],
     "trx_gemv_set_variant": [_i],
     "trx_model_create": [_mcp, _fp, ctypes.POINTER(_vp)],
     "trx_model_destroy": [_vp],
@@ -73,6 +76,7 @@ SIGNATURES = {
     "trx_model_read": [_vp, _i, _vp, _sz],
     "trx_model_info": [_vp, _i, _i64p],
     "trx_model_tensor_ptr": [_vp, _i, _i, ctypes.POINTER(_vp), _i64p],
+    "trx_model_packed_ptr": [_vp, _i, _i, ctypes.POINTER(_vp), ctypes.POINTER(_vp)],
 }
 _RESTYPES = {"trx_last_error": ctypes.c_char_p}
 

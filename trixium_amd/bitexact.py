@@ -64,3 +64,42 @@ def matvec_float(scales_f16, codes, x, norm_w=None, eps=1e-6, kind=L.KIND_TERNAR
          yb.ptr, 0, None, None)
     synchronize()
     return yb.download(np.float32, M)
+
+
+def pack_geometry(kind, M, K):
+    """(packed bytes, workspace bytes) of the packed float GEMV for an M x K matrix."""
+    import ctypes
+    pb, wb = ctypes.c_size_t(), ctypes.c_size_t()
+    call("trx_pack_geometry", int(kind), int(M), int(K), ctypes.byref(pb), ctypes.byref(wb))
+    return pb.value, wb.value
+
+
+class PackedMatrix:
+    """A ternary matrix packed for the float GEMV (trx_pack_ternary) with its workspace."""
+
+    def __init__(self, scales_f16, codes, kind=L.KIND_TERNARY5, swiglu=False):
+        self.M, self.K = codes.shape
+        self.kind = kind
+        self.swiglu = bool(swiglu)
+        rows = DeviceBuffer.from_array(_packets(scales_f16, codes, kind))
+        pb, wb = pack_geometry(kind, self.M, self.K)
+        self.packed = DeviceBuffer(pb)
+        self.work = DeviceBuffer(wb)
+        self.work.zero()
+        call("trx_pack_ternary", rows.ptr, kind, self.M, self.K, int(self.swiglu), self.packed.ptr, None)
+        synchronize()
+
+    def matvec(self, x, norm_w=None, eps=1e-6, epilogue=0, resid=None):
+        """y = W xhat with the epilogue (TRX_EPI_*); SwiGLU returns M/2 values."""
+        xb = DeviceBuffer.from_array(np.asarray(x, dtype=np.float32))
+        nb = DeviceBuffer.from_array(np.asarray(norm_w, dtype=np.float32)) if norm_w is not None else None
+        n_out = self.M // 2 if epilogue == 2 else self.M
+        if resid is not None:
+            yb = DeviceBuffer.from_array(np.asarray(resid, dtype=np.float32))
+        else:
+            yb = DeviceBuffer(4 * n_out)
+        call("trx_gemv_packed_f32", self.packed.ptr, self.kind, self.M, self.K, xb.ptr,
+             nb.ptr if nb else None, float(eps), yb.ptr, int(epilogue), yb.ptr if resid is not None else None,
+             self.work.ptr, None)
+        synchronize()
+        return yb.download(np.float32, n_out)

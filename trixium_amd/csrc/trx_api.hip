@@ -6,6 +6,7 @@
 #include <string.h>
 
 #include "trx_internal.h"
+#include "trx_tgemv.h"
 
 namespace trx {
 
@@ -167,3 +168,27 @@ TRX_API int trx_gemv_ternary_f32(const uint8_t* rows, int kind, int M, int K, co
 }
 
 TRX_API int trx_gemv_set_variant(int variant) { return gemv_set_variant(variant); }
+
+TRX_API int trx_pack_geometry(int kind, int M, int K, size_t* packed_bytes, size_t* workspace_bytes) {
+  TRX_CHECK(packed_bytes && workspace_bytes, TRX_E_INVALID, "trx_pack_geometry: null argument");
+  PackGeom g;
+  int rc = pack_geom(g, kind, M, K);
+  if (rc) return rc;
+  *packed_bytes = g.bytes;
+  *workspace_bytes = g.work_bytes;
+  return TRX_OK;
+}
+
+TRX_API int trx_pack_ternary(const uint8_t* rows, int kind, int M, int K, int swiglu, uint8_t* packed,
+                             trx_stream_t s) {
+  return pack_ternary(rows, kind, M, K, swiglu, packed, (hipStream_t)s);
+}
+
+TRX_API int trx_gemv_packed_f32(const uint8_t* packed, int kind, int M, int K, const float* x,
+                                const float* norm_w, float eps, float* y, int epilogue,
+                                const float* resid, void* workspace, trx_stream_t s) {
+  TRX_CHECK(epilogue == TRX_EPI_STORE || epilogue == TRX_EPI_RESID || epilogue == TRX_EPI_SWIGLU,
+            TRX_E_INVALID, "trx_gemv_packed_f32: unknown epilogue %d", epilogue);
+  return tgemv_f32(packed, kind, M, K, x, norm_w, eps, y, epilogue, resid, nullptr, workspace,
+                   (hipStream_t)s);
+}

@@ -65,11 +65,6 @@ struct GemvParams {
   const int* gate_from;
 };
 
-// Float -> ordered unsigned (monotonic), for the packed argmax.
-__device__ __forceinline__ uint32_t ordered_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
 
 typedef short s2_t __attribute__((ext_vector_type(2)));
 

@@ -163,6 +163,12 @@ __device__ __forceinline__ void st_vec(float* p, float v) {
   else *p = v;
 }
 
+// Float -> ordered unsigned (monotonic), for the packed argmax.
+__device__ __forceinline__ uint32_t ordered_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
 

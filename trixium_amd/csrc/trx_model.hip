@@ -16,6 +16,7 @@
 #include "trx_ops.h"
 #include "trx_layer.h"
 #include "trx_model.h"
+#include "trx_tgemv.h"
 
 namespace trx {
 
@@ -24,6 +25,16 @@ struct Tensor {
   size_t bytes = 0;
   int rows = 0, cols = 0, kind = 0;
   bool loaded = false;
+};
+
+// Projections that can run on the packed GEMV (trx_tgemv.h), keyed with their layer.
+enum PackedOp { OP_QKV, OP_O, OP_GATE_UP, OP_DOWN, OP_HEAD, OP_DN_QKVZ, OP_DN_OUT };
+
+struct PackedMat {
+  uint8_t* buf = nullptr;          // packed copy
+  const uint8_t* rows = nullptr;   // BONS row packets in the arena
+  int M = 0, K = 0, kind = 0;
+  bool swiglu = false;
 };
 
 struct Model {
@@ -53,6 +64,12 @@ struct Model {
   int fused_split = 0;
   unsigned long long* bar = nullptr;                // barrier counters
   unsigned* xcc_blocks = nullptr;
+  // Packed copies of the projections in packed_ops (repacked from the arena after its tensors
+  // change), and the workspace their GEMVs share.
+  std::map<std::pair<int, int>, PackedMat> packed;
+  int packed_ops = 0;
+  bool pack_dirty = true;
+  void* pack_work = nullptr;
   hipGraph_t graph = nullptr;
   hipGraphExec_t graph_exec = nullptr;
   size_t dev_bytes = 0;
@@ -135,6 +152,83 @@ static void plan_arena(Model& m, size_t& cur) {
   if (!c.head_tied) plan_tensor(m, cur, TRX_ROLE_LM_HEAD, 0, c.head_kind, c.vocab, E);
 }
 
+static int dalloc(Model& m, void** p, size_t bytes);
+static uint8_t* P(Model& m, int role, int layer);
+
+// Packed copies: the projections selected by packed_ops (TRX_PACK_AUTO: the packed GEMV where it
+// is the faster kernel for the weight kind), one device allocation for all of them, and the
+// largest workspace any of them needs.
+static int plan_packed(Model& m) {
+  const trx_model_config& c = m.cfg;
+  int ops = c.packed_ops;
+  if (ops == TRX_PACK_AUTO) ops = c.weight_kind == TRX_KIND_TERNARY5 ? (TRX_PACK_GATE_UP | TRX_PACK_HEAD) : 0;
+  TRX_CHECK(ops >= 0 && (ops & ~TRX_PACK_ALL) == 0, TRX_E_INVALID, "packed_ops %d has unknown bits", c.packed_ops);
+  const int E = c.n_embd, hd = c.head_dim, F = c.ffn_dim, wk = c.weight_kind;
+  const int qrows = c.n_head * hd * (c.attn_gated ? 2 : 1), kvrows = c.n_kv_head * hd;
+  const int nq = c.dn_num_k_heads * c.dn_k_head_dim, nvh = c.dn_num_v_heads * c.dn_v_head_dim;
+  std::vector<std::pair<std::pair<int, int>, PackedMat>> list;
+  auto add = [&](int op, int l, int role, int kind, int M, int K, bool swiglu) {
+    PackedMat pm;
+    pm.rows = P(m, role, l);
+    pm.kind = kind;
+    pm.M = M;
+    pm.K = K;
+    pm.swiglu = swiglu;
+    list.push_back({{op, l}, pm});
+  };
+  for (int l = 0; l < c.n_layer; ++l) {
+    if (m.is_dn(l)) {
+      if (ops & TRX_PACK_DN) {
+        add(OP_DN_QKVZ, l, TRX_ROLE_ATTN_QKV, wk, 2 * nq + 2 * nvh, E, false);
+        add(OP_DN_OUT, l, TRX_ROLE_SSM_OUT, wk, E, nvh, false);
+      }
+    } else {
+      if (ops & TRX_PACK_QKV) add(OP_QKV, l, TRX_ROLE_ATTN_Q, wk, qrows + 2 * kvrows, E, false);
+      if (ops & TRX_PACK_O) add(OP_O, l, TRX_ROLE_ATTN_OUT, wk, E, c.n_head * hd, false);
+    }
+    if (ops & TRX_PACK_GATE_UP) add(OP_GATE_UP, l, TRX_ROLE_FFN_GATE, wk, 2 * F, E, true);
+    if (ops & TRX_PACK_DOWN) add(OP_DOWN, l, TRX_ROLE_FFN_DOWN, wk, E, F, false);
+  }
+  const int head_role = c.head_tied ? TRX_ROLE_TOK_EMB : TRX_ROLE_LM_HEAD;
+  const int head_kind = c.head_tied ? c.emb_kind : c.head_kind;
+  if ((ops & TRX_PACK_HEAD) && (head_kind == TRX_KIND_TERNARY || head_kind == TRX_KIND_TERNARY5))
+    add(OP_HEAD, 0, head_role, head_kind, c.vocab, E, false);
+  size_t total = 0, work = 0;
+  std::vector<size_t> offs;
+  for (auto& e : list) {
+    PackGeom g;
+    int rc = pack_geom(g, e.second.kind, e.second.M, e.second.K);
+    if (rc) return rc;
+    offs.push_back(total);
+    total += (g.bytes + 255) / 256 * 256;
+    work = std::max(work, g.work_bytes);
+  }
+  m.packed_ops = ops;
+  if (list.empty()) return TRX_OK;
+  uint8_t* buf = nullptr;
+  int rc;
+  if ((rc = dalloc(m, (void**)&buf, total))) return rc;
+  if ((rc = dalloc(m, &m.pack_work, work))) return rc;   // zeroed: the tile counters start at 0
+  for (size_t i = 0; i < list.size(); ++i) {
+    list[i].second.buf = buf + offs[i];
+    m.packed[list[i].first] = list[i].second;
+  }
+  return TRX_OK;
+}
+
+// Rebuild the packed copies after the arena's tensors changed.
+static int ensure_packed(Model& m) {
+  if (!m.pack_dirty) return TRX_OK;
+  for (auto& kv : m.packed) {
+    const PackedMat& pm = kv.second;
+    int rc = pack_ternary(pm.rows, pm.kind, pm.M, pm.K, pm.swiglu ? 1 : 0, pm.buf, m.stream);
+    if (rc) return rc;
+  }
+  TRX_HIP(hipStreamSynchronize(m.stream));
+  m.pack_dirty = false;
+  return TRX_OK;
+}
+
 static int dalloc(Model& m, void** p, size_t bytes) {
   hipError_t e = hipMalloc(p, bytes + 256);
   if (e != hipSuccess) {
@@ -153,6 +247,20 @@ static const Tensor& T(Model& m, int role, int layer) { return m.tensors[{role, 
 static uint8_t* P(Model& m, int role, int layer) { return m.arena + T(m, role, layer).off; }
 static float* PF(Model& m, int role, int layer) { return (float*)P(m, role, layer); }
 
+// One ternary projection: the packed GEMV when the model holds a packed copy of it, otherwise the
+// row-packet kernel.
+static int projection(Model& m, int op, int l, const uint8_t* rows, int kind, int M, int K, const float* x,
+                      const float* norm_w, float* y, int epi, const float* resid, hipStream_t s,
+                      unsigned long long* amax = nullptr, const int* gate_pos = nullptr,
+                      const int* gate_from = nullptr) {
+  auto it = m.packed.find({op, l});
+  if (it != m.packed.end())
+    return tgemv_f32(it->second.buf, kind, M, K, x, norm_w, m.cfg.rms_eps, y, epi, resid, amax, m.pack_work, s,
+                     gate_pos, gate_from);
+  return gemv_f32(rows, kind, M, K, x, norm_w, m.cfg.rms_eps, y, epi, resid, epi == TRX_EPI_SWIGLU ? M / 2 : 0,
+                  amax, s, gate_pos, gate_from);
+}
+
 // Gated DeltaNet layer: [qkv|z] GEMV and the beta/alpha Q8 GEMV (both with the attention
 // RMSNorm), conv, recurrence with the gated norm, then the out projection with the residual.
 int dn_layer_launch(Model& m, int l, hipStream_t s) {
@@ -164,8 +272,8 @@ int dn_layer_launch(Model& m, int l, hipStream_t s) {
   int rc;
   float* io = m.dn_io;                  // [C + nvh] projections
   float* conv_out = m.dn_io + C + nvh;  // [C]
-  if ((rc = gemv_f32(P(m, TRX_ROLE_ATTN_QKV, l), c.weight_kind, C + nvh, E, m.x,
-                     PF(m, TRX_ROLE_ATTN_NORM, l), c.rms_eps, io, TRX_EPI_STORE, nullptr, 0, nullptr, s))) return rc;
+  if ((rc = projection(m, OP_DN_QKVZ, l, P(m, TRX_ROLE_ATTN_QKV, l), c.weight_kind, C + nvh, E, m.x,
+                        PF(m, TRX_ROLE_ATTN_NORM, l), io, TRX_EPI_STORE, nullptr, s))) return rc;
   DenseParams dp = {};
   dp.W = P(m, TRX_ROLE_SSM_BETA, l);
   dp.kind = TRX_KIND_Q8;
@@ -204,8 +312,8 @@ int dn_layer_launch(Model& m, int l, hipStream_t s) {
   rp.hv = c.dn_v_head_dim;
   rp.eps = c.rms_eps;
   if ((rc = launch_dn_recur(rp, s))) return rc;
-  return gemv_f32(P(m, TRX_ROLE_SSM_OUT, l), c.weight_kind, E, nvh, m.dn_out, nullptr, c.rms_eps, m.x,
-                  TRX_EPI_RESID, m.x, 0, nullptr, s);
+  return projection(m, OP_DN_OUT, l, P(m, TRX_ROLE_SSM_OUT, l), c.weight_kind, E, nvh, m.dn_out, nullptr,
+                    m.x, TRX_EPI_RESID, m.x, s);
 }
 
 // Full-attention layer as one kernel (trx_layer.hip): the same projections, attention and FFN
@@ -295,9 +403,8 @@ static int run_step(Model& m, hipStream_t s) {
       continue;
     } else {
       // q|k|v with the attention RMSNorm fused in the prologue.
-      if ((rc = gemv_f32(P(m, TRX_ROLE_ATTN_Q, l), wk, qrows + 2 * kvrows, E, m.x,
-                         PF(m, TRX_ROLE_ATTN_NORM, l), c.rms_eps, m.qkv, TRX_EPI_STORE, nullptr, 0,
-                         nullptr, s))) return rc;
+      if ((rc = projection(m, OP_QKV, l, P(m, TRX_ROLE_ATTN_Q, l), wk, qrows + 2 * kvrows, E, m.x,
+                            PF(m, TRX_ROLE_ATTN_NORM, l), m.qkv, TRX_EPI_STORE, nullptr, s))) return rc;
       AttnParams ap = {};
       ap.qkv = m.qkv;
       ap.q_norm = PF(m, TRX_ROLE_ATTN_Q_NORM, l);
@@ -321,14 +428,14 @@ static int run_step(Model& m, hipStream_t s) {
       ap.gated = c.attn_gated;
       ap.eps = c.rms_eps;
       if ((rc = launch_attention(ap, s))) return rc;
-      if ((rc = gemv_f32(P(m, TRX_ROLE_ATTN_OUT, l), wk, E, c.n_head * hd, m.attn_out, nullptr,
-                         c.rms_eps, m.x, TRX_EPI_RESID, m.x, 0, nullptr, s))) return rc;
+      if ((rc = projection(m, OP_O, l, P(m, TRX_ROLE_ATTN_OUT, l), wk, E, c.n_head * hd, m.attn_out, nullptr,
+                            m.x, TRX_EPI_RESID, m.x, s))) return rc;
     }
     // SwiGLU FFN: gate|up with the FFN RMSNorm, then down with the residual add.
-    if ((rc = gemv_f32(P(m, TRX_ROLE_FFN_GATE, l), wk, 2 * F, E, m.x, PF(m, TRX_ROLE_FFN_NORM, l),
-                       c.rms_eps, m.act, TRX_EPI_SWIGLU, nullptr, F, nullptr, s))) return rc;
-    if ((rc = gemv_f32(P(m, TRX_ROLE_FFN_DOWN, l), wk, E, F, m.act, nullptr, c.rms_eps, m.x,
-                       TRX_EPI_RESID, m.x, 0, nullptr, s))) return rc;
+    if ((rc = projection(m, OP_GATE_UP, l, P(m, TRX_ROLE_FFN_GATE, l), wk, 2 * F, E, m.x,
+                          PF(m, TRX_ROLE_FFN_NORM, l), m.act, TRX_EPI_SWIGLU, nullptr, s))) return rc;
+    if ((rc = projection(m, OP_DOWN, l, P(m, TRX_ROLE_FFN_DOWN, l), wk, E, F, m.act, nullptr, m.x,
+                          TRX_EPI_RESID, m.x, s))) return rc;
   }
   // LM head with the output RMSNorm and the greedy argmax; skipped (by the kernel, reading the
   // position) on prefill positions before head_from.
@@ -350,9 +457,9 @@ static int run_step(Model& m, hipStream_t s) {
     dp.gate_from = m.head_from();
     if ((rc = launch_dense_gemv(dp, s))) return rc;
   } else {
-    if ((rc = gemv_f32(P(m, head_role, 0), head_kind, c.vocab, E, m.x, PF(m, TRX_ROLE_OUT_NORM, 0),
-                       c.rms_eps, m.logits, TRX_EPI_STORE, nullptr, 0, m.slot, s, m.pos(),
-                       m.head_from()))) return rc;
+    if ((rc = projection(m, OP_HEAD, 0, P(m, head_role, 0), head_kind, c.vocab, E, m.x,
+                          PF(m, TRX_ROLE_OUT_NORM, 0), m.logits, TRX_EPI_STORE, nullptr, s, m.slot, m.pos(),
+                          m.head_from()))) return rc;
   }
   return TRX_OK;
 }
@@ -393,6 +500,7 @@ TRX_API int trx_model_create(const trx_model_config* cfg, const float* rope_freq
   int rc;
   auto fail = [&](int code) { trx_model_destroy(h); return code; };
   if ((rc = dalloc(m, (void**)&m.arena, m.arena_bytes))) return fail(rc);
+  if ((rc = plan_packed(m))) return fail(rc);
   const int hd = c.head_dim;
   m.n_split = attention_splits(c.n_kv_head, c.head_dim, c.max_ctx);
   if (m.n_split < 0) {
@@ -470,6 +578,7 @@ TRX_API int trx_model_set_tensor(trx_model* h, int role, int layer, const void* 
             bytes, it->second.bytes, it->second.rows, it->second.cols, it->second.kind);
   TRX_HIP(hipMemcpy(m.arena + it->second.off, data, bytes, hipMemcpyHostToDevice));
   it->second.loaded = true;
+  m.pack_dirty = true;
   return TRX_OK;
 }
 
@@ -511,6 +620,7 @@ TRX_API int trx_model_synthesize(trx_model* h, uint32_t seed, const float* range
     }
   }
   TRX_HIP(hipStreamSynchronize(m.stream));
+  m.pack_dirty = true;
   return TRX_OK;
 }
 
@@ -561,6 +671,7 @@ TRX_API int trx_model_step(trx_model* h, int n_steps, int use_graph) {
   Model& m = h->m;
   int rc;
   if ((rc = check_loaded(m))) return rc;
+  if ((rc = ensure_packed(m))) return rc;
   if (use_graph && !m.graph_exec) {
     TRX_HIP(hipStreamBeginCapture(m.stream, hipStreamCaptureModeThreadLocal));
     rc = run_step(m, m.stream);
@@ -663,6 +774,7 @@ TRX_API int trx_model_info(trx_model* h, int what, int64_t* value) {
     case TRX_INFO_DEVICE_BYTES: *value = (int64_t)m.dev_bytes; break;
     case TRX_INFO_STREAM: *value = (int64_t)(intptr_t)m.stream; break;
     case TRX_INFO_FUSED_LAYERS: *value = m.fused ? 1 : 0; break;
+    case TRX_INFO_PACKED_OPS: *value = m.packed_ops; break;
     case TRX_INFO_WEIGHT_BYTES: {
       int64_t s = 0;
       for (auto& kv : m.tensors) s += (int64_t)kv.second.bytes;
@@ -671,6 +783,22 @@ TRX_API int trx_model_info(trx_model* h, int what, int64_t* value) {
     }
     default: TRX_CHECK(false, TRX_E_INVALID, "trx_model_info: unknown item %d", what);
   }
+  return TRX_OK;
+}
+
+TRX_API int trx_model_packed_ptr(trx_model* h, int op, int layer, void** packed, void** workspace) {
+  TRX_CHECK(h && packed && workspace, TRX_E_INVALID, "trx_model_packed_ptr: null argument");
+  Model& m = h->m;
+  int rc;
+  if ((rc = ensure_packed(m))) return rc;
+  const int ids[] = {TRX_PACK_QKV, TRX_PACK_O, TRX_PACK_GATE_UP, TRX_PACK_DOWN, TRX_PACK_HEAD};
+  int id = -1;
+  for (int i = 0; i < 5; ++i) if (op == ids[i]) id = i;
+  TRX_CHECK(id >= 0, TRX_E_INVALID, "trx_model_packed_ptr: op %d is not one TRX_PACK_* bit of a layer projection", op);
+  auto it = m.packed.find({id, layer});
+  TRX_CHECK(it != m.packed.end(), TRX_E_INVALID, "projection %d of layer %d is not packed", op, layer);
+  *packed = it->second.buf;
+  *workspace = m.pack_work;
   return TRX_OK;
 }
 

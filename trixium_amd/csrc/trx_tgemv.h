@@ -1,0 +1,65 @@
+// Table-lookup ternary GEMV over a packed, slice-major weight layout: the float projection of
+// the decoder (model/fastref.py:119-125 HybridRef.matmul for one position).
+//
+// Packed layout of an M x K ternary matrix (built once from BONS row packets by pack_ternary):
+//   K is cut into S = ceil(K/256) slices of two 128-groups; rows into Q = ceil(M/4) quads.
+//   A (slice, row) record holds the slice's code bytes as D dwords (trit5: 13 = 52 bytes, the
+//   two groups' bytes 0..23 in dwords 0..5 and 6..11 and their bytes 24..25 in dword 12; 2-bit:
+//   16 = 64 bytes, one group per 8 dwords).
+//   codes:  uint4 [S][Q][D]: dword d of the quad's four records, in a per-dword row order (the
+//           order the reduction of the lane that owns dword d consumes them in).
+//   scales: uint32 [S][4Q] at codes + align256(code bytes): the slice's two fp16 group scales.
+//   The bytes per row equal the BONS row's (codes + scales) for trit5 and 2-bit alike.
+// SwiGLU matrices ([gate | up], 2F rows) are packed with gate and up rows interleaved per quad:
+//   quad q = [gate 2q, gate 2q+1, up 2q, up 2q+1].
+//
+// Kernel: a block owns one slice and builds in LDS the table T[b][c] = sum_k w_k(b) * xhat[c_k]
+// of every code byte value b at every code position c of the slice (64 positions: 16 lanes x
+// 4 bytes), so a code byte costs one v_perm (the LDS address), one LDS read and one add. Each
+// lane takes one dword of four rows per item; the sixteen lanes of a row reduce over DPP. The
+// block writes per-slice partial sums; the block that completes a 32-quad tile last (agent-scope
+// counter) adds the S partials in slice order (deterministic) and applies the epilogue
+// (store, residual, SwiGLU, or argmax).
+#pragma once
+
+#include "trx_internal.h"
+
+namespace trx {
+
+constexpr int kSliceCols = 256;     // columns per K-slice (two 128-groups)
+constexpr int kTabCols = 64;        // code positions per slice (16 lanes x 4 bytes)
+constexpr int kTileQuads = 32;      // quads per tile: one pass of a block (8 waves x 4 quads)
+constexpr int kTgThreads = 512;
+constexpr int kTgBlocksPerCU = 2;
+
+struct PackGeom {
+  int kind = 0, M = 0, K = 0, G = 0, S = 0, M4 = 0, Q = 0, D = 0, n_tiles = 0;
+  int bps = 0, tpb = 0;       // launch: blocks per slice, tiles per block (tile t -> block t % bps)
+  int rows_p = 0;             // partial sums per slice: bps * tpb tiles of 128 rows
+  size_t code_bytes = 0;      // uint4 [S][Q][D]
+  size_t scale_off = 0;       // byte offset of the scales
+  size_t bytes = 0;           // packed matrix
+  size_t cnt_bytes = 0;       // workspace: tile counters (zero between calls)
+  size_t work_bytes = 0;      // workspace: counters + S x rows_p partial sums
+};
+
+// Geometry of a packed matrix; TRX_E_INVALID for an unsupported kind or shape.
+int pack_geom(PackGeom& g, int kind, int M, int K);
+
+// BONS row packets (M rows back to back) -> packed layout. swiglu: the rows are [gate | up]
+// (M = 2F, F even) and are interleaved per quad.
+int pack_ternary(const uint8_t* rows, int kind, int M, int K, int swiglu, uint8_t* packed,
+                 hipStream_t s);
+
+// y = W xhat with xhat = x (norm_w == nullptr) or x / rms(x) * norm_w, and the epilogue:
+//   TRX_EPI_STORE y[m]; TRX_EPI_RESID y[m] = resid[m] + (W xhat)[m]; TRX_EPI_SWIGLU (matrix
+//   packed with swiglu=1) y[f] = silu(g[f]) * u[f], f < M/2.
+// amax_slot != nullptr: also the packed (ordered value, ~row) maximum of y (atomicMax).
+// gate_pos/gate_from: the launch does nothing while *gate_pos < *gate_from.
+// work: pack_geom().work_bytes of device memory whose counters are zero (the call leaves them
+// zero); calls that share a workspace must not overlap.
+int tgemv_f32(const uint8_t* packed, int kind, int M, int K, const float* x, const float* norm_w,
+              float eps, float* y, int epi, const float* resid, unsigned long long* amax_slot,
+              void* work, hipStream_t s, const int* gate_pos = nullptr, const int* gate_from = nullptr);
+
+}  // namespace trx

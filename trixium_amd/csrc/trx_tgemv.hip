@@ -1,0 +1,528 @@
+// Table-lookup ternary GEMV (float path) and the packing of BONS rows into its layout.
+// The arithmetic is the float projection of model/fastref.py:119-125 with the fused RMSNorm of
+// fastref.py:143-145; the code decode is the reference's (model/bons.py:125-130: trit5 digit k
+// of byte b is floor(b / 3^k) mod 3, 2-bit code k is (b >> 2k) & 3; weight = digit - 1).
+
+#include <algorithm>
+
+#include "trx_tgemv.h"
+
+namespace trx {
+
+// Lane roles inside a 16-lane row group ------------------------------------------------------
+
+// Record dword read by lane l16. trit5: lanes 0..5 take group 0's dwords, 8..13 group 1's,
+// lanes 6 and 14 the shared dword 12 (group 0's bytes 24..25 at its bytes 0..1, group 1's at
+// 2..3); lanes 7 and 15 read dword 12 too but own no byte of it.
+__host__ __device__ inline int tg_lane_dword(bool t5, int l16) {
+  if (!t5) return l16;
+  return l16 < 6 ? l16 : (l16 < 8 ? 12 : (l16 < 14 ? l16 - 2 : 12));
+}
+
+// Row order of lane l16's quad: component k of its uint4 holds row k ^ mask. The masks make the
+// three reduction steps (row_half_mirror, quad xor 2, quad xor 1) pair equal rows without
+// selects; afterwards lane l16 holds row mask(l16) (lanes 0,2,4,6 hold rows 0,1,3,2).
+__host__ __device__ inline int tg_lane_mask(int l16) {
+  const int i = l16 & 7;
+  return (((i >> 2) & 1) << 1) | (((i >> 1) ^ (i >> 2)) & 1);
+}
+
+// Group (0, 1; -1 for no byte) and group byte of table position c = 4 * lane + byte of dword.
+__host__ __device__ inline void tg_position(bool t5, int c, int& g, int& byte) {
+  const int l = c >> 2, jj = c & 3;
+  g = -1;
+  byte = 0;
+  if (!t5) {
+    g = l >> 3;
+    byte = 4 * (l & 7) + jj;
+  } else if (l < 6) {
+    g = 0;
+    byte = 4 * l + jj;
+  } else if (l == 6) {
+    if (jj < 2) { g = 0; byte = 24 + jj; }
+  } else if (l >= 8 && l < 14) {
+    g = 1;
+    byte = 4 * (l - 8) + jj;
+  } else if (l == 14) {
+    if (jj >= 2) { g = 1; byte = 22 + jj; }
+  }
+}
+
+// Group and group byte of record dword d, byte bi.
+__host__ __device__ inline void tg_record_byte(bool t5, int d, int bi, int& g, int& byte) {
+  if (!t5) {
+    g = d >> 3;
+    byte = 4 * (d & 7) + bi;
+  } else if (d < 6) {
+    g = 0;
+    byte = 4 * d + bi;
+  } else if (d < 12) {
+    g = 1;
+    byte = 4 * (d - 6) + bi;
+  } else {
+    g = bi >> 1;
+    byte = 24 + (bi & 1);
+  }
+}
+
+constexpr int kMaxTilesPerBlock = 64;
+
+static int cu_count() {
+  static int cus = 0;
+  if (!cus) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+      set_error("packed GEMV: cannot query the compute units");
+      return 0;
+    }
+  }
+  return cus;
+}
+
+int pack_geom(PackGeom& g, int kind, int M, int K) {
+  TRX_CHECK(kind == TRX_KIND_TERNARY5 || kind == TRX_KIND_TERNARY, TRX_E_INVALID,
+            "packed GEMV: kind %d is not ternary", kind);
+  TRX_CHECK(M >= 1 && K >= kGroup && K % kGroup == 0, TRX_E_INVALID,
+            "packed GEMV: M=%d K=%d (K must be a positive multiple of 128)", M, K);
+  g = PackGeom{};
+  g.kind = kind;
+  g.M = M;
+  g.K = K;
+  g.G = K / kGroup;
+  g.S = cdiv(g.G, 2);
+  g.M4 = cdiv(M, 4) * 4;
+  g.Q = g.M4 / 4;
+  g.D = kind == TRX_KIND_TERNARY5 ? 13 : 16;
+  g.n_tiles = cdiv(g.Q, kTileQuads);
+  // Blocks per slice: fill the resident slots (kTgBlocksPerCU per CU), then even out the tiles.
+  const int cus = cu_count();
+  if (cus <= 0) return TRX_E_HIP;
+  int bps = std::max(1, std::min(g.n_tiles, kTgBlocksPerCU * cus / g.S));
+  int tpb = std::min(cdiv(g.n_tiles, bps), kMaxTilesPerBlock);
+  bps = cdiv(g.n_tiles, tpb);
+  g.tpb = cdiv(g.n_tiles, bps);
+  g.bps = bps;
+  g.rows_p = g.bps * g.tpb * kTileQuads * 4;
+  g.code_bytes = (size_t)g.S * g.Q * g.D * 16;
+  g.scale_off = (g.code_bytes + 255) / 256 * 256;
+  // Lanes of a block's partial last tile read up to (bps * tpb * 32 - Q) quads past their
+  // slice; the padding keeps those reads inside the allocation for the last slice.
+  const size_t over = (size_t)(g.bps * g.tpb * kTileQuads - g.Q) * g.D * 16;
+  g.bytes = g.scale_off + (size_t)g.S * g.M4 * 4 + over;
+  g.cnt_bytes = ((size_t)g.n_tiles * 4 + 255) / 256 * 256;
+  g.work_bytes = g.cnt_bytes + (size_t)g.S * g.rows_p * 4;
+  TRX_CHECK(g.bytes < (1ull << 32), TRX_E_INVALID, "packed GEMV: %zu bytes exceed 4 GiB", g.bytes);
+  return TRX_OK;
+}
+
+// Packing -----------------------------------------------------------------------------------
+
+struct PackParams {
+  const uint8_t* rows;
+  uint8_t* out;
+  size_t scale_off;
+  int M, G, S, M4, Q, D, row_bytes, code_off, swiglu;
+  bool t5;
+};
+
+__device__ inline int pack_src_row(const PackParams& p, int prow) {
+  if (p.swiglu) {
+    const int F = p.M / 2, q = prow >> 2, k = prow & 3;
+    const int f = 2 * q + (k & 1);
+    if (f >= F) return -1;
+    return k < 2 ? f : F + f;
+  }
+  return prow < p.M ? prow : -1;
+}
+
+__global__ void pack_kernel(PackParams p) {
+  const long long n = (long long)p.S * p.Q * p.D;
+  const int gbytes = p.t5 ? kTrit5GroupBytes : 32;
+  for (long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x; idx < n;
+       idx += (long long)gridDim.x * blockDim.x) {
+    const int d = (int)(idx % p.D);
+    const long long r = idx / p.D;
+    const int q = (int)(r % p.Q), s = (int)(r / p.Q);
+    // The lanes that read dword d share one row order.
+    const int owner = p.t5 ? (d < 6 ? d : (d < 12 ? d + 2 : 6)) : d;
+    const int msk = tg_lane_mask(owner);
+    uint32_t v[4];
+    for (int k = 0; k < 4; ++k) {
+      const int src = pack_src_row(p, 4 * q + (k ^ msk));
+      uint32_t word = 0;
+      if (src >= 0) {
+        const uint8_t* row = p.rows + (size_t)src * p.row_bytes + p.code_off;
+        for (int bi = 0; bi < 4; ++bi) {
+          int g, byte;
+          tg_record_byte(p.t5, d, bi, g, byte);
+          const int ga = 2 * s + g;
+          if (ga < p.G) word |= (uint32_t)row[(size_t)gbytes * ga + byte] << (8 * bi);
+        }
+      }
+      v[k] = word;
+    }
+    ((uint4*)p.out)[idx] = make_uint4(v[0], v[1], v[2], v[3]);
+    if (d == 0) {
+      uint32_t* sc = (uint32_t*)(p.out + p.scale_off);
+      for (int k = 0; k < 4; ++k) {
+        const int prow = 4 * q + k;
+        const int src = pack_src_row(p, prow);
+        uint32_t word = 0;
+        if (src >= 0) {
+          const uint16_t* rs = (const uint16_t*)(p.rows + (size_t)src * p.row_bytes);
+          const uint32_t lo = (2 * s < p.G) ? rs[2 * s] : 0u;
+          const uint32_t hi = (2 * s + 1 < p.G) ? rs[2 * s + 1] : 0u;
+          word = lo | (hi << 16);
+        }
+        sc[(size_t)s * p.M4 + prow] = word;
+      }
+    }
+  }
+}
+
+int pack_ternary(const uint8_t* rows, int kind, int M, int K, int swiglu, uint8_t* packed,
+                 hipStream_t s) {
+  PackGeom g;
+  int rc = pack_geom(g, kind, M, K);
+  if (rc) return rc;
+  TRX_CHECK(rows && packed, TRX_E_INVALID, "pack_ternary: null argument");
+  TRX_CHECK(!swiglu || (M % 4 == 0), TRX_E_INVALID, "pack_ternary: SwiGLU needs M = 2F with F even (M=%d)", M);
+  const RowGeom rg = row_geom(kind, K);
+  PackParams p;
+  p.rows = rows;
+  p.out = packed;
+  p.scale_off = g.scale_off;
+  p.M = M;
+  p.G = g.G;
+  p.S = g.S;
+  p.M4 = g.M4;
+  p.Q = g.Q;
+  p.D = g.D;
+  p.row_bytes = rg.row_bytes;
+  p.code_off = rg.code_off;
+  p.swiglu = swiglu ? 1 : 0;
+  p.t5 = kind == TRX_KIND_TERNARY5;
+  const long long n = (long long)g.S * g.Q * g.D;
+  const int blocks = (int)std::min<long long>((n + 255) / 256, 65536);
+  hipLaunchKernelGGL(pack_kernel, dim3(blocks), dim3(256), 0, s, p);
+  TRX_LAUNCHED();
+  return TRX_OK;
+}
+
+// GEMV kernel -------------------------------------------------------------------------------
+
+constexpr int kDppRowRor8 = 0x128;
+constexpr int kCpolSc1 = 16;          // buffer cache policy: device (agent) scope
+constexpr int kMaxNormVec = 6;         // float4 loads per thread of a normalised x: K <= 12288
+
+struct TgParams {
+  const uint8_t* codes;
+  const uint8_t* scales;
+  uint32_t code_bytes, scale_bytes;
+  int K, M, M4, Q, S, D, n_tiles, bps, tpb, rows_p;
+  const float* x;
+  const float* norm_w;
+  float eps;
+  float* y;
+  const float* resid;
+  int epi, n_out;
+  float* part;
+  int* cnt;
+  unsigned long long* amax_slot;
+  const int* gate_pos;
+  const int* gate_from;
+};
+
+template <bool T5>
+struct TgItem {
+  uint4 c;            // dword of four rows
+  uint32_t sc;        // the two fp16 group scales of this lane's row
+};
+
+template <bool T5, int NB>
+__global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgParams p) {
+  constexpr int NLO = T5 ? 9 : 16;     // values of the low digits (trit5: 2 digits; 2-bit: 2 codes)
+  constexpr int NHI = T5 ? 29 : 16;    // values of the rest (b / 9 <= 28; b >> 4)
+  __shared__ __align__(16) float tab[256 * kTabCols];
+  __shared__ __align__(16) float scr[4 * 128];     // reduction: row totals of four tiles
+  __shared__ float xs[kSliceCols];
+  __shared__ float red[16];
+  __shared__ int todo[kMaxTilesPerBlock];
+  __shared__ int n_todo;
+
+  if (p.gate_pos && *p.gate_pos < *p.gate_from) return;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int s = blockIdx.x % p.S, j = blockIdx.x / p.S;
+
+  // 1. x: the slice's 256 values, and the whole vector's sum of squares for the RMSNorm. These
+  //    loads are issued before the weight stream, which would otherwise delay them.
+  const int cs = s * kSliceCols + tid;
+  float xv = 0.f, wv = 1.f;
+  if (tid < kSliceCols && cs < p.K) {
+    xv = p.x[cs];
+    if (p.norm_w) wv = p.norm_w[cs];
+  }
+  float ss = 0.f;
+  if (p.norm_w) {
+    float4 xa[kMaxNormVec];                        // every load in flight before the first use
+#pragma unroll
+    for (int r = 0; r < kMaxNormVec; ++r) {
+      const int c = (r * kTgThreads + tid) * 4;
+      xa[r] = c < p.K ? *(const float4*)(p.x + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int r = 0; r < kMaxNormVec; ++r) ss += xa[r].x * xa[r].x + xa[r].y * xa[r].y + xa[r].z * xa[r].z + xa[r].w * xa[r].w;
+  }
+
+  // 2. The first NB - 1 items of this lane (they do not depend on x).
+  const int rg = lane >> 4, l16 = lane & 15, half = l16 >> 3;
+  const int dw = tg_lane_dword(T5, l16), msk = tg_lane_mask(l16);
+  const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.codes, p.code_bytes);
+  const __amdgpu_buffer_rsrc_t rsc = make_rsrc(p.scales, p.scale_bytes);
+  // Item n of this lane is quad quad0 + n * qstep. The lane's offsets stay in fixed VGPRs and
+  // the item's step goes in the scalar offset, so no VGPR that an in-flight access reads is
+  // rewritten (that would cost a vmcnt wait per item). Only the VGPR offset is relied on for the
+  // descriptor's range check: a quad past the matrix (partial last tile) reads zeros or unused
+  // bytes of the packed matrix, and prefetches past the block's last item re-read that item.
+  constexpr uint32_t kOut = 0x40000000u;     // a VGPR offset past every buffer
+  const int quad0 = j * kTileQuads + w * 4 + rg, qstep = p.bps * kTileQuads;
+  const uint32_t co0 = (((uint32_t)s * p.Q + (uint32_t)quad0) * p.D + dw) * 16u;
+  const uint32_t cstep = (uint32_t)qstep * p.D * 16u;
+  const uint32_t so0 = ((uint32_t)s * p.M4 + 4u * (uint32_t)quad0 + msk) * 4u;
+  const uint32_t sstep = (uint32_t)qstep * 16u;
+  // Partial sums: every lane stores every item (a fixed count of memory events per item keeps
+  // the compiler's waits exact); the lanes that hold no row total store past the buffer (dropped
+  // by the range check), and the items of a partial last tile land in padding rows.
+  const __amdgpu_buffer_rsrc_t rpart = make_rsrc(p.part, (uint32_t)((size_t)p.S * p.rows_p * 4));
+  const uint32_t po0 = (l16 & 9) == 0 ? ((uint32_t)s * p.rows_p + 4u * (uint32_t)quad0 + msk) * 4u : kOut;
+  const uint32_t pstep = (uint32_t)qstep * 16u;
+  auto load_item = [&](TgItem<T5>& it, int n) {
+    const int nn = min(n, p.tpb - 1);
+    const int cso = nn * (int)cstep;
+    const int sso = nn * (int)sstep;
+    const auto a = __builtin_amdgcn_raw_buffer_load_b128(rc, co0, cso, 0);
+    it.c = make_uint4(a[0], a[1], a[2], a[3]);
+    it.sc = __builtin_amdgcn_raw_buffer_load_b32(rsc, so0, sso, 0);
+  };
+  TgItem<T5> buf[NB];
+#pragma unroll
+  for (int b = 0; b < NB - 1; ++b) load_item(buf[b], b);
+
+  // 3. xhat of the slice, the two-level digit sums, then the table.
+  float rinv = 1.f;
+  if (p.norm_w) {
+    ss = block_sum(ss, red);
+    rinv = 1.0f / sqrtf(ss / (float)p.K + p.eps);
+  }
+  if (tid < kSliceCols) xs[tid] = p.norm_w ? xv * rinv * wv : xv;
+  __syncthreads();
+  {
+    // T[b][c] = hi(b) + lo(b): lo from the low digits (trit5: b % 9; 2-bit: b & 15), hi from the
+    // rest (b / 9; b >> 4). A thread owns one column: its x values and its lo sums in registers,
+    // then whole runs of entries sharing one hi (waves take different hi values).
+    const int c = tid & (kTabCols - 1);
+    int g, byte;
+    tg_position(T5, c, g, byte);
+    float u[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
+    if (g >= 0) {
+#pragma unroll
+      for (int k = 0; k < (T5 ? 5 : 4); ++k) {
+        const int cc = (T5 ? 5 : 4) * byte + k;
+        if (cc < kGroup) u[k] = xs[kGroup * g + cc];
+      }
+    }
+    float lo[NLO];
+#pragma unroll
+    for (int e = 0; e < NLO; ++e) {
+      const int d0 = T5 ? e % 3 : (e & 3), d1 = T5 ? e / 3 : (e >> 2);
+      lo[e] = (float)(d0 - 1) * u[0] + (float)(d1 - 1) * u[1];
+    }
+    for (int h = tid >> 6; h < NHI; h += kTgThreads / kTabCols) {
+      float hv;
+      if (T5) {
+        const int h1 = h / 3, h2 = h1 / 3;
+        hv = (float)(h - 3 * h1 - 1) * u[2] + (float)(h1 - 3 * h2 - 1) * u[3] + (float)(h2 % 3 - 1) * u[4];
+      } else {
+        hv = (float)((h & 3) - 1) * u[2] + (float)((h >> 2) - 1) * u[3];
+      }
+      float* col = tab + h * NLO * kTabCols + c;
+#pragma unroll
+      for (int e = 0; e < NLO; ++e)
+        if (h * NLO + e < 256) col[e * kTabCols] = lo[e] + hv;
+    }
+  }
+  __syncthreads();
+
+  // 4. The items: four rows x one dword per lane; sixteen lanes per row group.
+  uint32_t lw[4], sel[4];
+#pragma unroll
+  for (int jq = 0; jq < 4; ++jq) {
+    // Byte jj of the dword at step jq; rotating with the row group and half keeps the 64 lanes
+    // of an LDS read on 64 different table columns (no bank conflicts).
+    const int jj = (jq + rg + 2 * half) & 3;
+    lw[jq] = (uint32_t)(4 * l16 + jj) * 4u;
+    sel[jq] = 0x0c0c0400u | ((uint32_t)jj << 8);
+  }
+  const char* tb = (const char*)tab;
+  const uint32_t sshift = 16u * (uint32_t)half;       // this lane's group scale in the dword
+  auto compute = [&](const TgItem<T5>& it, int n) {
+    float a[4];
+    const uint32_t cw[4] = {it.c.x, it.c.y, it.c.z, it.c.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float t4[4];
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq) {
+        const uint32_t addr = __builtin_amdgcn_perm(cw[k], lw[jq], sel[jq]);  // b * 256 + col * 4
+        t4[jq] = *(const float*)(tb + addr);
+      }
+      a[k] = (t4[0] + t4[1]) + (t4[2] + t4[3]);
+    }
+    a[0] += dpp_f<kDppRowHalfMirror>(a[2]);
+    a[1] += dpp_f<kDppRowHalfMirror>(a[3]);
+    a[0] += dpp_f<kDppQuadXor2>(a[1]);
+    a[0] += dpp_f<kDppQuadXor1>(a[0]);
+    float v = a[0] * __half2float(__ushort_as_half((unsigned short)(it.sc >> sshift)));
+    v += dpp_f<kDppRowRor8>(v);                      // the other group (lane l16 ^ 8)
+    // Agent-scope store (sc1): the tile's reducing block may run on another XCD.
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), rpart, po0, n * (int)pstep, kCpolSc1);
+  };
+  // Whole groups of NB items (a loop with one exit keeps the compiler's vmcnt waits exact: item
+  // n waits only for itself), then the remaining < NB items, already in flight.
+  int n = 0;
+  const int ngroups = p.tpb / NB;
+  for (int gi = 0; gi < ngroups; ++gi) {
+#pragma unroll
+    for (int ph = 0; ph < NB; ++ph) {
+      load_item(buf[(ph + NB - 1) % NB], n + NB - 1);
+      __builtin_amdgcn_sched_barrier(0);     // the prefetch goes out before this item's work
+      compute(buf[ph], n);
+      ++n;
+    }
+  }
+  const int rem = p.tpb - n;
+#pragma unroll
+  for (int ph = 0; ph < NB - 1; ++ph) {
+    if (ph < rem) compute(buf[ph], n + ph);
+  }
+
+  // 5. Count this block's tiles done; the last of a tile's S blocks reduces it.
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0);
+  asm volatile("" ::: "memory");
+  if (tid == 0) n_todo = 0;
+  __syncthreads();
+  if (tid < p.tpb) {
+    const int t = j + tid * p.bps;
+    if (t < p.n_tiles) {
+      const int old = __hip_atomic_fetch_add(p.cnt + t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (old == p.S - 1) {
+        __hip_atomic_store(p.cnt + t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        todo[atomicAdd(&n_todo, 1)] = t;
+      }
+    }
+  }
+  __syncthreads();
+  // Reduction: four tiles per pass, a thread per (tile, row). The S partials of a row are summed
+  // in slice order (the same order whichever block reduces), their loads all in flight together.
+  const int nt = n_todo;
+  const int rl = tid & 127, ti = tid >> 7;
+  for (int i0 = 0; i0 < nt; i0 += 4) {
+    const int i = i0 + ti;
+    const int r0 = (i < nt ? todo[i] : 0) * kTileQuads * 4;
+    const int prow = r0 + rl;
+    const bool live = i < nt && prow < p.M4;
+    float yv = 0.f;
+    if (live) {
+      const uint32_t off = (uint32_t)prow * 4u, step = (uint32_t)p.rows_p * 4u;
+      int q = 0;
+      for (; q + 8 <= p.S; q += 8) {
+        float t[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          t[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rpart, off + (q + k) * step, 0, kCpolSc1));
+#pragma unroll
+        for (int k = 0; k < 8; ++k) yv += t[k];
+      }
+      for (; q < p.S; ++q)
+        yv += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rpart, off + q * step, 0, kCpolSc1));
+    }
+    scr[ti * 128 + rl] = yv;
+    __syncthreads();
+    unsigned long long key = 0;
+    if (live) {
+      if (p.epi == TRX_EPI_SWIGLU) {
+        const int k = prow & 3, f = 2 * (prow >> 2) + k;
+        if (k < 2 && f < p.n_out) p.y[f] = silu(yv) * scr[ti * 128 + rl + 2];
+      } else if (prow < p.M) {
+        float out = yv;
+        if (p.epi == TRX_EPI_RESID) out += p.resid[prow];
+        p.y[prow] = out;
+        key = ((unsigned long long)ordered_bits(out) << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)prow);
+      }
+    }
+    if (p.amax_slot) {
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) {
+        const unsigned long long other = __shfl_xor(key, o, 64);
+        key = other > key ? other : key;
+      }
+      if (lane == 0 && key) atomicMax(p.amax_slot, key);
+    }
+    __syncthreads();
+  }
+}
+
+template <bool T5>
+static const void* tg_fn() {
+  return (const void*)tgemv_kernel<T5, 4>;
+}
+
+int tgemv_f32(const uint8_t* packed, int kind, int M, int K, const float* x, const float* norm_w,
+              float eps, float* y, int epi, const float* resid, unsigned long long* amax_slot,
+              void* work, hipStream_t s, const int* gate_pos, const int* gate_from) {
+  PackGeom g;
+  int rc = pack_geom(g, kind, M, K);
+  if (rc) return rc;
+  TRX_CHECK(packed && x && y && work, TRX_E_INVALID, "packed GEMV: null argument");
+  TRX_CHECK(((uintptr_t)x & 15) == 0, TRX_E_INVALID, "packed GEMV: x must be 16-byte aligned");
+  TRX_CHECK(epi != TRX_EPI_RESID || resid, TRX_E_INVALID, "packed GEMV: residual epilogue without a residual");
+  TRX_CHECK(epi != TRX_EPI_SWIGLU || M % 4 == 0, TRX_E_INVALID, "packed GEMV: SwiGLU needs M = 2F, F even");
+  TRX_CHECK(epi != TRX_EPI_SWIGLU || !amax_slot, TRX_E_INVALID, "packed GEMV: no argmax with SwiGLU");
+  TRX_CHECK(!norm_w || K <= kMaxNormVec * kTgThreads * 4, TRX_E_INVALID,
+            "packed GEMV: the RMSNorm prologue takes K <= %d (K=%d)", kMaxNormVec * kTgThreads * 4, K);
+  TgParams p;
+  p.codes = packed;
+  p.scales = packed + g.scale_off;
+  p.code_bytes = (uint32_t)g.code_bytes;
+  p.scale_bytes = (uint32_t)(g.bytes - g.scale_off);
+  p.K = K;
+  p.M = M;
+  p.M4 = g.M4;
+  p.Q = g.Q;
+  p.S = g.S;
+  p.D = g.D;
+  p.n_tiles = g.n_tiles;
+  p.bps = g.bps;
+  p.tpb = g.tpb;
+  p.rows_p = g.rows_p;
+  p.x = x;
+  p.norm_w = norm_w;
+  p.eps = eps;
+  p.y = y;
+  p.resid = resid;
+  p.epi = epi;
+  p.n_out = epi == TRX_EPI_SWIGLU ? M / 2 : M;
+  p.cnt = (int*)work;
+  p.part = (float*)((uint8_t*)work + g.cnt_bytes);
+  p.amax_slot = amax_slot;
+  p.gate_pos = gate_pos;
+  p.gate_from = gate_from;
+  const void* fn = kind == TRX_KIND_TERNARY5 ? tg_fn<true>() : tg_fn<false>();
+  void* args[] = {(void*)&p};
+  TRX_HIP(hipLaunchKernel(fn, dim3(g.S * g.bps), dim3(kTgThreads), args, 0, s));
+  return TRX_OK;
+}
+
+}  // namespace trx

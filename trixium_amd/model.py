@@ -23,7 +23,11 @@ from .configs import ModelConfig
 f32 = np.float32
 
 READ_LOGITS, READ_HIDDEN, READ_POSITION, READ_TOKEN, READ_OUT, READ_SLOT, READ_QKV, READ_ATTN, READ_ACT = range(9)
-INFO_ARENA_BYTES, INFO_DEVICE_BYTES, INFO_STREAM, INFO_WEIGHT_BYTES, INFO_FUSED_LAYERS = range(5)
+INFO_ARENA_BYTES, INFO_DEVICE_BYTES, INFO_STREAM, INFO_WEIGHT_BYTES, INFO_FUSED_LAYERS, INFO_PACKED_OPS = range(6)
+
+# Projections run by the packed GEMV (TRX_PACK_* bits; PACK_AUTO lets the library choose).
+PACK_QKV, PACK_O, PACK_GATE_UP, PACK_DOWN, PACK_HEAD, PACK_DN = 1, 2, 4, 8, 16, 32
+PACK_ALL, PACK_AUTO = 63, -1
 
 # Ranges of the counter-based synthetic weights (the ternary group scales and the RMSNorm gains).
 SYNTH_SCALE = (0.01, 0.05)
@@ -48,7 +52,7 @@ def layer_type_bits(layer_types, n_layer):
 
 
 def make_config(mc, weight_kind, head_kind, head_tied, emb_mode, emb_kind, max_ctx=None, max_new=256,
-                layer_fusion=False):
+                layer_fusion=False, packed_ops=PACK_AUTO):
     """trx_model_config from a ModelConfig (or a BONS header turned into one)."""
     c = _lib.ModelConfig()
     for name in ("n_layer", "n_embd", "n_head", "n_kv_head", "head_dim", "ffn_dim", "vocab",
@@ -63,6 +67,7 @@ def make_config(mc, weight_kind, head_kind, head_tied, emb_mode, emb_kind, max_c
     c.weight_kind, c.head_kind, c.head_tied = weight_kind, head_kind, int(bool(head_tied))
     c.emb_mode, c.emb_kind, c.max_new = emb_mode, emb_kind, int(max_new)
     c.layer_fusion = int(bool(layer_fusion))
+    c.packed_ops = int(packed_ops)
     return c
 
 
@@ -96,7 +101,8 @@ class Decoder:
 
     # Construction ------------------------------------------------------------------------------
     @classmethod
-    def from_image(cls, img, max_ctx=None, max_new=256, use_graph=True, layer_fusion=False):
+    def from_image(cls, img, max_ctx=None, max_new=256, use_graph=True, layer_fusion=False,
+                   packed_ops=PACK_AUTO):
         """Load a BONS image (path or BONSReader) into HBM."""
         from .bons import BONSReader
         if isinstance(img, str):
@@ -121,7 +127,8 @@ class Decoder:
         else:
             head_kind = L.KIND_F16 if head["kind"] == L.KIND_F32 else head["kind"]
             emb_kind = emb["kind"] if emb is not None and L.is_ternary(emb["kind"]) else weight_kind
-        cfg = make_config(mc, weight_kind, head_kind, head_tied, 0, emb_kind, max_ctx, max_new, layer_fusion)
+        cfg = make_config(mc, weight_kind, head_kind, head_tied, 0, emb_kind, max_ctx, max_new, layer_fusion,
+                          packed_ops)
         d = cls(mc, cfg, use_graph)
         try:
             d._load_image(img)
@@ -132,14 +139,14 @@ class Decoder:
 
     @classmethod
     def synthetic(cls, mc, seed=0, weight_kind=L.KIND_TERNARY5, max_ctx=None, max_new=256,
-                  use_graph=True, layer_fusion=False):
+                  use_graph=True, layer_fusion=False, packed_ops=PACK_AUTO):
         """Fill every tensor on the device from the counter-based generator (same values as
         trixium_amd.synth.hashed_*): ternary token_embd rows (embedded by decoding the row), an
         untied ternary LM head unless the config ties them."""
         if mc.n_dn_layers:
             raise NotImplementedError("synthetic DeltaNet layers (Q8 beta/alpha) have no device generator")
         cfg = make_config(mc, weight_kind, weight_kind, mc.tie_embeddings, 1, weight_kind, max_ctx, max_new,
-                          layer_fusion)
+                          layer_fusion, packed_ops)
         d = cls(mc, cfg, use_graph)
         try:
             ranges = np.array([SYNTH_SCALE[0], SYNTH_SCALE[1] - SYNTH_SCALE[0],
@@ -301,6 +308,17 @@ class Decoder:
     @property
     def stream(self):
         return self.info(INFO_STREAM)
+
+    @property
+    def packed_ops(self):
+        """TRX_PACK_* bits of the projections that run on the packed GEMV."""
+        return self.info(INFO_PACKED_OPS)
+
+    def packed_ptr(self, op, layer=0):
+        """(packed copy, shared workspace) device addresses of one packed projection."""
+        p, w = ctypes.c_void_p(), ctypes.c_void_p()
+        _lib.call("trx_model_packed_ptr", self._h, op, layer, ctypes.byref(p), ctypes.byref(w))
+        return p.value, w.value
 
     def tensor_ptr(self, role, layer=0):
         p, n = ctypes.c_void_p(), ctypes.c_int64()
