@@ -1,0 +1,320 @@
+// Decode attention for one position in one launch (flash decoding): a block per (kv head, split)
+// of the T = pos + 1 cached positions, the split's partial (max, sum, output) per q head, and the
+// merge of a kv head's splits by the block that finishes last. The arithmetic is that of
+// model/fastref.py:216-241 for one position: q and k RMS-normalised per head, NEOX RoPE on the
+// first rope_n dims (angle = pos * freq in fp32), q scaled by 1/sqrt(hd), k (post-RoPE) and v
+// appended to the fp16 cache and read back rounded, softmax over the positions, the output gate
+// of gated attention.
+//
+// Lanes: a position is handled by LPP = hd/8 lanes (8 dims each), a "group"; a block of 256
+// threads has 256/LPP groups. The split's K and V rows are loaded into registers first. q (and
+// the new k, v) are normalised and rotated in registers: sums over a group's lanes by DPP, the
+// rotation partner (dim d +- rope_n/2) from lane li ^ (rope_n/16). Each group keeps an online
+// softmax (max, sum, weighted V) over its positions; the groups are combined through LDS once.
+
+#include "trx_internal.h"
+#include "trx_ops.h"
+#include "trx_attn_dev.h"
+
+namespace trx {
+
+constexpr int kFdMaxSplits = 64;
+constexpr int kCpolSc1 = 16;           // buffer cache policy: device (agent) scope
+constexpr int kDppRowRor8 = 0x128;     // lane l reads lane l ^ 8 within its 16-lane row
+
+// Sum over the LPP lanes of a position group (every lane gets the sum).
+template <int LPP>
+__device__ __forceinline__ float group_sum(float v) {
+  v += dpp_f<kDppQuadXor1>(v);
+  if (LPP >= 4) v += dpp_f<kDppQuadXor2>(v);
+  if (LPP >= 8) v += dpp_f<kDppRowHalfMirror>(v);
+  if (LPP >= 16) v += dpp_f<kDppRowMirror>(v);
+  if (LPP >= 32) v += __shfl_xor(v, 16, 64);
+  return v;
+}
+
+template <int REP, int HD>
+__global__ __launch_bounds__(kAttnThreads) void attn_fd_kernel(AttnParams p) {
+  constexpr int LPP = HD / 8;                         // lanes per position
+  constexpr int PPW = 64 / LPP;                       // groups per wave
+  constexpr int NG = kAttnThreads / LPP;              // groups per block
+  constexpr int PPP = NG;                             // positions per pass
+  __shared__ float cs_s[HD / 2], sn_s[HD / 2];
+  __shared__ float gm[NG][REP], gl[NG][REP];
+  __shared__ __align__(16) float go[NG][REP][HD];
+  __shared__ float wgt[REP][kFdMaxSplits > NG ? kFdMaxSplits : NG];
+  __shared__ float lsp[REP][kFdMaxSplits];
+  __shared__ float tot[REP];
+  __shared__ int last;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int S = p.n_split;
+  const int g = blockIdx.x / S, sp = blockIdx.x - g * S;
+  const int pos = *p.pos, T = pos + 1;
+  const int chunk = (T + S - 1) / S;
+  const int p0 = sp * chunk, p1 = min(T, p0 + chunk), n = max(0, p1 - p0);
+  const int li = lane % LPP, grp = wave * PPW + lane / LPP;
+  const size_t cache0 = (size_t)g * p.max_ctx * HD;
+  const bool owner = n > 0 && pos >= p0 && pos < p1;
+  const int npass = (n + PPP - 1) / PPP;
+  const int qstride = p.gated ? 2 * HD : HD;
+  const int half = p.rope_n / 2;
+
+  // 1. The prologue's inputs first (a later wait for them then does not cover the K/V stream):
+  //    the RoPE frequency of this thread, the q heads, the new k and v, the norm gains.
+  const float fr = tid < half ? p.rope_freq[tid] : 0.f;
+  float q[REP][8], kn[8], vn[8], qw[8], kw[8];
+  const float* kraw = p.qkv + (size_t)p.n_head * qstride + (size_t)g * HD;
+  {
+    const float4* a = (const float4*)(p.q_norm + li * 8);
+    const float4* b = (const float4*)(p.k_norm + li * 8);
+    const float4 a0 = a[0], a1 = a[1], b0 = b[0], b1 = b[1];
+    qw[0] = a0.x; qw[1] = a0.y; qw[2] = a0.z; qw[3] = a0.w; qw[4] = a1.x; qw[5] = a1.y; qw[6] = a1.z; qw[7] = a1.w;
+    kw[0] = b0.x; kw[1] = b0.y; kw[2] = b0.z; kw[3] = b0.w; kw[4] = b1.x; kw[5] = b1.y; kw[6] = b1.z; kw[7] = b1.w;
+  }
+#pragma unroll
+  for (int j = 0; j < REP; ++j) {
+    const float4* src = (const float4*)(p.qkv + (size_t)(g * REP + j) * qstride + li * 8);
+    const float4 a = src[0], b = src[1];
+    q[j][0] = a.x; q[j][1] = a.y; q[j][2] = a.z; q[j][3] = a.w;
+    q[j][4] = b.x; q[j][5] = b.y; q[j][6] = b.z; q[j][7] = b.w;
+  }
+  {
+    const float4* ks = (const float4*)(kraw + li * 8);
+    const float4* vs = (const float4*)(kraw + (size_t)p.n_kv * HD + li * 8);
+    const float4 a = ks[0], b = ks[1], c = vs[0], d = vs[1];
+    kn[0] = a.x; kn[1] = a.y; kn[2] = a.z; kn[3] = a.w; kn[4] = b.x; kn[5] = b.y; kn[6] = b.z; kn[7] = b.w;
+    vn[0] = c.x; vn[1] = c.y; vn[2] = c.z; vn[3] = c.w; vn[4] = d.x; vn[5] = d.y; vn[6] = d.z; vn[7] = d.w;
+  }
+
+  // 2. The split's K and V rows (the new position's come from the projection above).
+  uint4 kr[kMaxPass], vr[kMaxPass];
+#pragma unroll
+  for (int ps = 0; ps < kMaxPass; ++ps) {
+    const int t = ps * PPP + grp;
+    if (ps < npass && t < n && p0 + t != pos) {
+      const size_t off = cache0 + (size_t)(p0 + t) * HD + li * 8;
+      kr[ps] = *(const uint4*)(p.kcache + off);
+      vr[ps] = *(const uint4*)(p.vcache + off);
+    } else {
+      kr[ps] = make_uint4(0, 0, 0, 0);
+      vr[ps] = make_uint4(0, 0, 0, 0);
+    }
+  }
+
+  if (n > 0) {
+    if (tid < half) {
+      float sn, cs;
+      sincosf((float)pos * fr, &sn, &cs);
+      cs_s[tid] = cs;
+      sn_s[tid] = sn;
+    }
+    __syncthreads();
+    // Normalise (gain w), rotate, scale; `post` multiplies the result.
+    auto norm_rope = [&](float* v, const float* w, float post) {
+      float ss = 0.f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) ss += v[k] * v[k];
+      ss = group_sum<LPP>(ss);
+      const float r = 1.0f / sqrtf(ss / (float)HD + p.eps);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = v[k] * r * w[k];
+      const int pxor = half >> 3;                       // partner lane of dim d +- half
+      const int d0 = li * 8;
+      const bool lo = d0 < half, rot = d0 < 2 * half;   // the 8 dims of a lane share the case
+      const int ci = lo ? d0 : (rot ? d0 - half : 0);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float other = pxor == 8 ? dpp_f<kDppRowRor8>(v[k]) : __shfl_xor(v[k], pxor, 64);
+        const float c = cs_s[ci + k], sn = sn_s[ci + k];
+        const float rv = lo ? v[k] * c - other * sn : other * sn + v[k] * c;
+        v[k] = (rot ? rv : v[k]) * post;
+      }
+    };
+    const float qpost = 1.0f / sqrtf((float)HD);
+#pragma unroll
+    for (int j = 0; j < REP; ++j) norm_rope(q[j], qw, qpost);
+    if (owner) {
+      norm_rope(kn, kw, 1.0f);
+      // The cache holds fp16; the score of this position uses the rounded values too.
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        kn[k] = __half2float(__float2half(kn[k]));
+        vn[k] = __half2float(__float2half(vn[k]));
+      }
+      if (grp == 0) {
+        __half kh[8], vh[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) { kh[k] = __float2half(kn[k]); vh[k] = __float2half(vn[k]); }
+        *(uint4*)(p.kcache + cache0 + (size_t)pos * HD + li * 8) = *(const uint4*)kh;
+        *(uint4*)(p.vcache + cache0 + (size_t)pos * HD + li * 8) = *(const uint4*)vh;
+      }
+    }
+
+    // 3. Online softmax over this group's positions.
+    float m[REP], l[REP], acc[REP][8];
+#pragma unroll
+    for (int j = 0; j < REP; ++j) {
+      m[j] = -INFINITY;
+      l[j] = 0.f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) acc[j][k] = 0.f;
+    }
+#pragma unroll
+    for (int ps = 0; ps < kMaxPass; ++ps) {
+      if (ps >= npass) break;
+      const int t = ps * PPP + grp;
+      const bool mine = owner && p0 + t == pos;
+      float kv[8], vv[8];
+      if (mine) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) { kv[k] = kn[k]; vv[k] = vn[k]; }
+      } else {
+        h8_to_f(kr[ps], kv);
+        h8_to_f(vr[ps], vv);
+      }
+      float s[REP];
+#pragma unroll
+      for (int j = 0; j < REP; ++j) {
+        float d = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) d += q[j][k] * kv[k];
+        s[j] = group_sum<LPP>(d);
+      }
+      if (t < n) {
+#pragma unroll
+        for (int j = 0; j < REP; ++j) {
+          const float mn = fmaxf(m[j], s[j]);
+          const float c = __expf(m[j] - mn), e = __expf(s[j] - mn);
+          l[j] = l[j] * c + e;
+#pragma unroll
+          for (int k = 0; k < 8; ++k) acc[j][k] = acc[j][k] * c + e * vv[k];
+          m[j] = mn;
+        }
+      }
+    }
+
+    // 4. The block's groups combined into the split's partial.
+#pragma unroll
+    for (int j = 0; j < REP; ++j) {
+      if (li == 0) { gm[grp][j] = m[j]; gl[grp][j] = l[j]; }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) go[grp][j][li * 8 + k] = acc[j][k];
+    }
+    __syncthreads();
+    if (tid < REP) {
+      float M = -INFINITY;
+      for (int i = 0; i < NG; ++i) M = fmaxf(M, gm[i][tid]);
+      float L = 0.f;
+      for (int i = 0; i < NG; ++i) {
+        const float w = gl[i][tid] > 0.f ? __expf(gm[i][tid] - M) : 0.f;
+        wgt[tid][i] = w;
+        L += gl[i][tid] * w;
+      }
+      st_vec<true>(p.part_m + (size_t)(g * REP + tid) * S + sp, M);
+      st_vec<true>(p.part_l + (size_t)(g * REP + tid) * S + sp, L);
+    }
+    __syncthreads();
+    for (int i = tid; i < REP * HD; i += kAttnThreads) {
+      const int j = i / HD, d = i - j * HD;
+      float o = 0.f;
+#pragma unroll
+      for (int k = 0; k < NG; ++k) o += go[k][j][d] * wgt[j][k];
+      st_vec<true>(p.part_o + ((size_t)(g * REP + j) * S + sp) * HD + d, o);
+    }
+  }
+
+  // 5. The last of kv head g's S blocks merges its splits (the others are done, their partials
+  //    written by agent-scope stores that completed before they counted themselves). Without
+  //    counters the next kernel merges (the packed o projection, trx_tgemv.hip).
+  if (!p.done) return;
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0);
+  asm volatile("" ::: "memory");
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned old = __hip_atomic_fetch_add(p.done + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = old == (unsigned)(S - 1);
+    if (last) __hip_atomic_store(p.done + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!last) return;
+  // Agent-scope (sc1) buffer loads: plain loads could hit stale lines of this XCD's L2, and
+  // atomic loads would be issued one at a time.
+  const int ns = min(S, (T + chunk - 1) / chunk);     // splits holding positions
+  const uint32_t nb = (uint32_t)((size_t)p.n_head * S * 4);
+  const __amdgpu_buffer_rsrc_t rm = make_rsrc(p.part_m, nb), rl = make_rsrc(p.part_l, nb);
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(p.part_o, nb * (uint32_t)HD);
+  for (int i = tid; i < REP * ns; i += kAttnThreads) {
+    const int j = i / ns, k = i - j * ns;
+    const uint32_t off = (uint32_t)(((g * REP + j) * S + k) * 4);
+    wgt[j][k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rm, off, 0, kCpolSc1));
+    lsp[j][k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, off, 0, kCpolSc1));
+  }
+  __syncthreads();
+  if (tid < REP) {
+    float M = -INFINITY;
+    for (int i = 0; i < ns; ++i) M = fmaxf(M, wgt[tid][i]);
+    float L = 0.f;
+    for (int i = 0; i < ns; ++i) {
+      const float w = __expf(wgt[tid][i] - M);
+      wgt[tid][i] = w;
+      L += lsp[tid][i] * w;
+    }
+    tot[tid] = L;
+  }
+  __syncthreads();
+  for (int i = tid; i < REP * HD; i += kAttnThreads) {
+    const int j = i / HD, d = i - j * HD, qh = g * REP + j;
+    const uint32_t base = (uint32_t)(((size_t)qh * S * HD + d) * 4), step = (uint32_t)HD * 4u;
+    float o = 0.f;
+    for (int s0 = 0; s0 < ns; s0 += 32) {
+      float v[32];
+#pragma unroll
+      for (int k = 0; k < 32; ++k)       // past ns: reads of the buffer that get weight 0
+        v[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ro, base + min(s0 + k, ns - 1) * step, 0, kCpolSc1));
+#pragma unroll
+      for (int k = 0; k < 32; ++k) o += s0 + k < ns ? v[k] * wgt[j][s0 + k] : 0.f;
+    }
+    o /= tot[j];
+    if (p.gated) o *= sigmoidf_(p.qkv[(size_t)qh * 2 * HD + HD + d]);
+    p.out[(size_t)qh * HD + d] = o;
+  }
+}
+
+bool attention_fd_supported(int rep, int hd, int rope_n, int n_split) {
+  const int half = rope_n / 2;
+  const bool rope_ok = half >= 8 && half % 8 == 0 && ((half / 8) & (half / 8 - 1)) == 0 && 2 * half <= hd;
+  const bool rep_ok = rep == 1 || rep == 2 || rep == 4 || rep == 6 || rep == 8;
+  return rope_ok && rep_ok && (hd == 64 || hd == 128 || hd == 256) && n_split <= kFdMaxSplits;
+}
+
+template <int REP>
+static int launch_fd_rep(const AttnParams& p, hipStream_t s) {
+  const dim3 grid(p.n_kv * p.n_split), block(kAttnThreads);
+  switch (p.hd) {
+    case 64: hipLaunchKernelGGL((attn_fd_kernel<REP, 64>), grid, block, 0, s, p); break;
+    case 128: hipLaunchKernelGGL((attn_fd_kernel<REP, 128>), grid, block, 0, s, p); break;
+    case 256: hipLaunchKernelGGL((attn_fd_kernel<REP, 256>), grid, block, 0, s, p); break;
+    default: TRX_CHECK(false, TRX_E_INVALID, "attention: head_dim %d unsupported", p.hd);
+  }
+  TRX_LAUNCHED();
+  return TRX_OK;
+}
+
+int launch_attention_fd(const AttnParams& p, hipStream_t s) {
+  TRX_CHECK(attention_fd_supported(p.n_rep, p.hd, p.rope_n, p.n_split), TRX_E_INVALID,
+            "attention: rep %d hd %d rope %d splits %d unsupported", p.n_rep, p.hd, p.rope_n, p.n_split);
+  const int cap = attention_max_chunk(p.hd);
+  TRX_CHECK(p.n_split >= 1 && (p.max_ctx + p.n_split - 1) / p.n_split <= cap, TRX_E_INVALID,
+            "attention: %d splits for context %d", p.n_split, p.max_ctx);
+  switch (p.n_rep) {
+    case 1: return launch_fd_rep<1>(p, s);
+    case 2: return launch_fd_rep<2>(p, s);
+    case 4: return launch_fd_rep<4>(p, s);
+    case 6: return launch_fd_rep<6>(p, s);
+    case 8: return launch_fd_rep<8>(p, s);
+  }
+  return TRX_E_INVALID;
+}
+
+}  // namespace trx

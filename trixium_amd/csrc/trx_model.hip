@@ -50,6 +50,7 @@ struct Model {
   float *conv_state = nullptr, *dn_state = nullptr;
   float *x = nullptr, *qkv = nullptr, *attn_out = nullptr, *act = nullptr, *logits = nullptr;
   float *part_m = nullptr, *part_l = nullptr, *part_o = nullptr;
+  unsigned* attn_done = nullptr;                   // [n_kv] split counters (one-launch attention)
   float *dn_io = nullptr, *dn_ba = nullptr, *dn_out = nullptr, *rope_dev = nullptr;
   int* ctl = nullptr;  // [0] pos, [1] n_fed, [2] cur_tok, [3] head_from, [4] error, [8..] fed tokens by
                        // absolute position (max_ctx), then the generated tokens (max_new)
@@ -161,7 +162,8 @@ static uint8_t* P(Model& m, int role, int layer);
 static int plan_packed(Model& m) {
   const trx_model_config& c = m.cfg;
   int ops = c.packed_ops;
-  if (ops == TRX_PACK_AUTO) ops = c.weight_kind == TRX_KIND_TERNARY5 ? (TRX_PACK_GATE_UP | TRX_PACK_HEAD) : 0;
+  if (ops == TRX_PACK_AUTO)
+    ops = c.weight_kind == TRX_KIND_TERNARY5 ? (TRX_PACK_O | TRX_PACK_GATE_UP | TRX_PACK_HEAD) : TRX_PACK_O;
   TRX_CHECK(ops >= 0 && (ops & ~TRX_PACK_ALL) == 0, TRX_E_INVALID, "packed_ops %d has unknown bits", c.packed_ops);
   const int E = c.n_embd, hd = c.head_dim, F = c.ffn_dim, wk = c.weight_kind;
   const int qrows = c.n_head * hd * (c.attn_gated ? 2 : 1), kvrows = c.n_kv_head * hd;
@@ -427,9 +429,25 @@ static int run_step(Model& m, hipStream_t s) {
       ap.n_split = m.n_split;
       ap.gated = c.attn_gated;
       ap.eps = c.rms_eps;
-      if ((rc = launch_attention(ap, s))) return rc;
-      if ((rc = projection(m, OP_O, l, P(m, TRX_ROLE_ATTN_OUT, l), wk, E, c.n_head * hd, m.attn_out, nullptr,
-                            m.x, TRX_EPI_RESID, m.x, s))) return rc;
+      // One-launch attention; with a packed o projection the splits are merged in that GEMV's
+      // prologue (each of its blocks merges the heads of its column slice).
+      const bool fd = attention_fd_supported(ap.n_rep, hd, ap.rope_n, ap.n_split);
+      auto ito = m.packed.find({OP_O, l});
+      const bool merge_in_o = fd && ito != m.packed.end() && ap.n_split <= 32 && kSliceCols % hd == 0;
+      ap.done = merge_in_o ? nullptr : m.attn_done;
+      if (fd) {
+        if ((rc = launch_attention_fd(ap, s))) return rc;
+      } else if ((rc = launch_attention(ap, s))) {
+        return rc;
+      }
+      if (merge_in_o) {
+        AttnMergeSrc ms = {ap.part_m, ap.part_l, ap.part_o, ap.pos, ap.n_split, hd, ap.gated, ap.qkv, m.attn_out};
+        if ((rc = tgemv_f32(ito->second.buf, wk, E, c.n_head * hd, nullptr, nullptr, c.rms_eps, m.x, TRX_EPI_RESID,
+                            m.x, nullptr, m.pack_work, s, nullptr, nullptr, &ms))) return rc;
+      } else if ((rc = projection(m, OP_O, l, P(m, TRX_ROLE_ATTN_OUT, l), wk, E, c.n_head * hd, m.attn_out,
+                                   nullptr, m.x, TRX_EPI_RESID, m.x, s))) {
+        return rc;
+      }
     }
     // SwiGLU FFN: gate|up with the FFN RMSNorm, then down with the residual add.
     if ((rc = projection(m, OP_GATE_UP, l, P(m, TRX_ROLE_FFN_GATE, l), wk, 2 * F, E, m.x,
@@ -543,6 +561,7 @@ TRX_API int trx_model_create(const trx_model_config* cfg, const float* rope_freq
   if ((rc = dalloc(m, (void**)&m.part_m, (size_t)c.n_head * splits * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.part_l, (size_t)c.n_head * splits * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.part_o, (size_t)c.n_head * splits * hd * 4))) return fail(rc);
+  if ((rc = dalloc(m, (void**)&m.attn_done, (size_t)std::max(c.n_kv_head, 1) * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.rope_dev, (size_t)rope_n * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.ctl, (size_t)(8 + c.max_ctx + c.max_new) * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.slot, 8))) return fail(rc);

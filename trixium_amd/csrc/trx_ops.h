@@ -38,6 +38,7 @@ struct AttnParams {
   float* out;              // [n_head*hd]
   int n_head, n_kv, n_rep, hd, rope_n, max_ctx, n_split, gated;
   float eps;
+  unsigned* done;          // [n_kv] split counters of the one-launch kernel (zero between launches)
 };
 
 struct DenseParams {
@@ -89,6 +90,11 @@ int launch_embed(const EmbedParams& p, hipStream_t s);
 int launch_finalize(const int* pos, const int* n_prompt, unsigned long long* slot, int* out, int max_out,
                     hipStream_t s);
 int launch_attention(const AttnParams& p, hipStream_t s);
+// One-launch attention (trx_attn_fd.hip) for the geometries attention_fd_supported accepts: the
+// split partials, merged by the last split block of each kv head when `done` is set (the output
+// in `out`), left for the consumer to merge otherwise (attn_merge_into_x, the packed o GEMV).
+bool attention_fd_supported(int rep, int hd, int rope_n, int n_split);
+int launch_attention_fd(const AttnParams& p, hipStream_t s);
 int attention_splits(int n_kv, int head_dim, int max_ctx);   // -1: the context is too long
 int attention_max_chunk(int head_dim);                          // positions one split can hold
 int launch_dense_gemv(const DenseParams& p, hipStream_t s);

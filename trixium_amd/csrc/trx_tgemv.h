@@ -58,8 +58,22 @@ int pack_ternary(const uint8_t* rows, int kind, int M, int K, int swiglu, uint8_
 // gate_pos/gate_from: the launch does nothing while *gate_pos < *gate_from.
 // work: pack_geom().work_bytes of device memory whose counters are zero (the call leaves them
 // zero); calls that share a workspace must not overlap.
+// x taken from decode attention's split partials instead (the o projection): x[h*hd + d] =
+// sum_sp o[h][sp][d] exp(m[h][sp] - M) / sum_sp l[h][sp] exp(m[h][sp] - M), times
+// sigmoid(gate) for gated attention; blocks of the first tile column also store x to `out`.
+struct AttnMergeSrc {
+  const float* m;          // [n_head][n_split]
+  const float* l;
+  const float* o;          // [n_head][n_split][hd]
+  const int* pos;          // the position attended (splits of pos + 1 positions)
+  int n_split, hd, gated;
+  const float* qkv;        // gated: the gate after each q head
+  float* out;              // [n_head * hd]
+};
+
 int tgemv_f32(const uint8_t* packed, int kind, int M, int K, const float* x, const float* norm_w,
               float eps, float* y, int epi, const float* resid, unsigned long long* amax_slot,
-              void* work, hipStream_t s, const int* gate_pos = nullptr, const int* gate_from = nullptr);
+              void* work, hipStream_t s, const int* gate_pos = nullptr, const int* gate_from = nullptr,
+              const AttnMergeSrc* merge = nullptr);
 
 }  // namespace trx

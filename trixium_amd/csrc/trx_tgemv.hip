@@ -215,6 +215,7 @@ int pack_ternary(const uint8_t* rows, int kind, int M, int K, int swiglu, uint8_
 constexpr int kDppRowRor8 = 0x128;
 constexpr int kCpolSc1 = 16;          // buffer cache policy: device (agent) scope
 constexpr int kMaxNormVec = 6;         // float4 loads per thread of a normalised x: K <= 12288
+constexpr int kMergeMax = 32;          // attention splits the merging prologue takes
 
 struct TgParams {
   const uint8_t* codes;
@@ -232,6 +233,7 @@ struct TgParams {
   unsigned long long* amax_slot;
   const int* gate_pos;
   const int* gate_from;
+  AttnMergeSrc merge;      // merge.o != nullptr: x from attention partials
 };
 
 template <bool T5>
@@ -249,6 +251,7 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   __shared__ float xs[kSliceCols];
   __shared__ float red[16];
   __shared__ int todo[kMaxTilesPerBlock];
+  __shared__ float amw[kSliceCols / 64][kMergeMax], aml[kSliceCols / 64][kMergeMax], atot[kSliceCols / 64];
   __shared__ int n_todo;
 
   if (p.gate_pos && *p.gate_pos < *p.gate_from) return;
@@ -259,7 +262,29 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   //    loads are issued before the weight stream, which would otherwise delay them.
   const int cs = s * kSliceCols + tid;
   float xv = 0.f, wv = 1.f;
-  if (tid < kSliceCols && cs < p.K) {
+  float ov[kMergeMax];
+  int ns = 0, h0 = 0, nh = 0;
+  if (p.merge.o) {
+    // The slice's attention output from the split partials: every split's o value of this
+    // thread's column in flight, then (m, l) of the slice's heads.
+    const AttnMergeSrc& a = p.merge;
+    const int T = *a.pos + 1, chunk = (T + a.n_split - 1) / a.n_split;
+    ns = min(a.n_split, (T + chunk - 1) / chunk);
+    h0 = (s * kSliceCols) / a.hd;
+    nh = kSliceCols / a.hd;
+    const int h = cs / a.hd, d = cs - h * a.hd;
+    const bool live = tid < kSliceCols && cs < p.K;
+#pragma unroll
+    for (int k = 0; k < kMergeMax; ++k)
+      ov[k] = live && k < ns ? a.o[((size_t)h * a.n_split + k) * a.hd + d] : 0.f;
+    for (int i = tid; i < nh * ns; i += kTgThreads) {
+      const int hl = i / ns, k = i - hl * ns;
+      if ((h0 + hl) * a.hd < p.K) {
+        amw[hl][k] = a.m[(size_t)(h0 + hl) * a.n_split + k];
+        aml[hl][k] = a.l[(size_t)(h0 + hl) * a.n_split + k];
+      }
+    }
+  } else if (tid < kSliceCols && cs < p.K) {
     xv = p.x[cs];
     if (p.norm_w) wv = p.norm_w[cs];
   }
@@ -314,6 +339,31 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   if (p.norm_w) {
     ss = block_sum(ss, red);
     rinv = 1.0f / sqrtf(ss / (float)p.K + p.eps);
+  }
+  if (p.merge.o) {
+    __syncthreads();
+    if (tid < nh && (h0 + tid) * p.merge.hd < p.K) {
+      float M = -INFINITY;
+      for (int k = 0; k < ns; ++k) M = fmaxf(M, amw[tid][k]);
+      float L = 0.f;
+      for (int k = 0; k < ns; ++k) {
+        const float w = __expf(amw[tid][k] - M);
+        amw[tid][k] = w;
+        L += aml[tid][k] * w;
+      }
+      atot[tid] = L;
+    }
+    __syncthreads();
+    if (tid < kSliceCols && cs < p.K) {
+      const int hl = tid / p.merge.hd, h = h0 + hl;
+      float o = 0.f;
+#pragma unroll
+      for (int k = 0; k < kMergeMax; ++k) o += k < ns ? ov[k] * amw[hl][k] : 0.f;
+      o /= atot[hl];
+      if (p.merge.gated) o *= sigmoidf_(p.merge.qkv[(size_t)h * 2 * p.merge.hd + p.merge.hd + (cs - h * p.merge.hd)]);
+      xv = o;
+      if (j == 0) p.merge.out[cs] = o;
+    }
   }
   if (tid < kSliceCols) xs[tid] = p.norm_w ? xv * rinv * wv : xv;
   __syncthreads();
@@ -481,12 +531,20 @@ static const void* tg_fn() {
 
 int tgemv_f32(const uint8_t* packed, int kind, int M, int K, const float* x, const float* norm_w,
               float eps, float* y, int epi, const float* resid, unsigned long long* amax_slot,
-              void* work, hipStream_t s, const int* gate_pos, const int* gate_from) {
+              void* work, hipStream_t s, const int* gate_pos, const int* gate_from,
+              const AttnMergeSrc* merge) {
   PackGeom g;
   int rc = pack_geom(g, kind, M, K);
   if (rc) return rc;
-  TRX_CHECK(packed && x && y && work, TRX_E_INVALID, "packed GEMV: null argument");
+  TRX_CHECK(packed && (x || merge) && y && work, TRX_E_INVALID, "packed GEMV: null argument");
+  TRX_CHECK(!merge || (merge->o && merge->m && merge->l && merge->pos && merge->out && !norm_w &&
+                       (merge->hd == 64 || merge->hd == 128 || merge->hd == 256) &&
+                       merge->n_split >= 1 && merge->n_split <= kMergeMax && K % merge->hd == 0 &&
+                       (!merge->gated || merge->qkv)),
+            TRX_E_INVALID, "packed GEMV: unsupported attention merge (hd %d, %d splits)",
+            merge ? merge->hd : 0, merge ? merge->n_split : 0);
   TRX_CHECK(((uintptr_t)x & 15) == 0, TRX_E_INVALID, "packed GEMV: x must be 16-byte aligned");
+  TRX_CHECK(!norm_w || x, TRX_E_INVALID, "packed GEMV: the RMSNorm prologue needs x");
   TRX_CHECK(epi != TRX_EPI_RESID || resid, TRX_E_INVALID, "packed GEMV: residual epilogue without a residual");
   TRX_CHECK(epi != TRX_EPI_SWIGLU || M % 4 == 0, TRX_E_INVALID, "packed GEMV: SwiGLU needs M = 2F, F even");
   TRX_CHECK(epi != TRX_EPI_SWIGLU || !amax_slot, TRX_E_INVALID, "packed GEMV: no argmax with SwiGLU");
@@ -519,6 +577,7 @@ int tgemv_f32(const uint8_t* packed, int kind, int M, int K, const float* x, con
   p.amax_slot = amax_slot;
   p.gate_pos = gate_pos;
   p.gate_from = gate_from;
+  p.merge = merge ? *merge : AttnMergeSrc{};
   const void* fn = kind == TRX_KIND_TERNARY5 ? tg_fn<true>() : tg_fn<false>();
   void* args[] = {(void*)&p};
   TRX_HIP(hipLaunchKernel(fn, dim3(g.S * g.bps), dim3(kTgThreads), args, 0, s));
