@@ -9,8 +9,9 @@
 // Lanes: a position is handled by LPP = hd/8 lanes (8 dims each), a "group"; a block of 256
 // threads has 256/LPP groups. The split's K and V rows are loaded into registers first. q (and
 // the new k, v) are normalised and rotated in registers: sums over a group's lanes by DPP, the
-// rotation partner (dim d +- rope_n/2) from lane li ^ (rope_n/16). Each group keeps an online
-// softmax (max, sum, weighted V) over its positions; the groups are combined through LDS once.
+// rotation partner (dim d +- rope_n/2) from lane li ^ (rope_n/16). Each group computes the
+// scores of its positions, then their max, sum of exponentials and weighted V; the groups are
+// combined through LDS once.
 
 #include "trx_internal.h"
 #include "trx_ops.h"
@@ -150,11 +151,36 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fd_kernel(AttnParams p) {
       }
     }
 
-    // 3. Online softmax over this group's positions.
+    // 3. This group's positions: every score, then the softmax pieces (max, sum, weighted V).
+    float sc[kMaxPass][REP];
+#pragma unroll
+    for (int ps = 0; ps < kMaxPass; ++ps) {
+#pragma unroll
+      for (int j = 0; j < REP; ++j) sc[ps][j] = -INFINITY;
+      if (ps >= npass) continue;
+      const int t = ps * PPP + grp;
+      float kv[8];
+      if (owner && p0 + t == pos) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) kv[k] = kn[k];
+      } else {
+        h8_to_f(kr[ps], kv);
+      }
+#pragma unroll
+      for (int j = 0; j < REP; ++j) {
+        float d = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) d += q[j][k] * kv[k];
+        d = group_sum<LPP>(d);
+        if (t < n) sc[ps][j] = d;
+      }
+    }
     float m[REP], l[REP], acc[REP][8];
 #pragma unroll
     for (int j = 0; j < REP; ++j) {
       m[j] = -INFINITY;
+#pragma unroll
+      for (int ps = 0; ps < kMaxPass; ++ps) m[j] = fmaxf(m[j], sc[ps][j]);
       l[j] = 0.f;
 #pragma unroll
       for (int k = 0; k < 8; ++k) acc[j][k] = 0.f;
@@ -163,33 +189,20 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fd_kernel(AttnParams p) {
     for (int ps = 0; ps < kMaxPass; ++ps) {
       if (ps >= npass) break;
       const int t = ps * PPP + grp;
-      const bool mine = owner && p0 + t == pos;
-      float kv[8], vv[8];
-      if (mine) {
+      if (t >= n) continue;
+      float vv[8];
+      if (owner && p0 + t == pos) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) { kv[k] = kn[k]; vv[k] = vn[k]; }
+        for (int k = 0; k < 8; ++k) vv[k] = vn[k];
       } else {
-        h8_to_f(kr[ps], kv);
         h8_to_f(vr[ps], vv);
       }
-      float s[REP];
 #pragma unroll
       for (int j = 0; j < REP; ++j) {
-        float d = 0.f;
+        const float e = __expf(sc[ps][j] - m[j]);
+        l[j] += e;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) d += q[j][k] * kv[k];
-        s[j] = group_sum<LPP>(d);
-      }
-      if (t < n) {
-#pragma unroll
-        for (int j = 0; j < REP; ++j) {
-          const float mn = fmaxf(m[j], s[j]);
-          const float c = __expf(m[j] - mn), e = __expf(s[j] - mn);
-          l[j] = l[j] * c + e;
-#pragma unroll
-          for (int k = 0; k < 8; ++k) acc[j][k] = acc[j][k] * c + e * vv[k];
-          m[j] = mn;
-        }
+        for (int k = 0; k < 8; ++k) acc[j][k] += e * vv[k];
       }
     }
 

@@ -251,7 +251,7 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   __shared__ float xs[kSliceCols];
   __shared__ float red[16];
   __shared__ int todo[kMaxTilesPerBlock];
-  __shared__ float amw[kSliceCols / 64][kMergeMax], aml[kSliceCols / 64][kMergeMax], atot[kSliceCols / 64];
+  __shared__ float amw[kSliceCols / 64][kMergeMax], atot[kSliceCols / 64];
   __shared__ int n_todo;
 
   if (p.gate_pos && *p.gate_pos < *p.gate_from) return;
@@ -273,16 +273,25 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
     h0 = (s * kSliceCols) / a.hd;
     nh = kSliceCols / a.hd;
     const int h = cs / a.hd, d = cs - h * a.hd;
-    const bool live = tid < kSliceCols && cs < p.K;
+    if (tid < kSliceCols && cs < p.K) {
+      // Splits past ns re-read the last one; their weight is 0.
 #pragma unroll
-    for (int k = 0; k < kMergeMax; ++k)
-      ov[k] = live && k < ns ? a.o[((size_t)h * a.n_split + k) * a.hd + d] : 0.f;
-    for (int i = tid; i < nh * ns; i += kTgThreads) {
-      const int hl = i / ns, k = i - hl * ns;
-      if ((h0 + hl) * a.hd < p.K) {
-        amw[hl][k] = a.m[(size_t)(h0 + hl) * a.n_split + k];
-        aml[hl][k] = a.l[(size_t)(h0 + hl) * a.n_split + k];
-      }
+      for (int k = 0; k < kMergeMax; ++k) ov[k] = a.o[((size_t)h * a.n_split + min(k, ns - 1)) * a.hd + d];
+    } else {
+#pragma unroll
+      for (int k = 0; k < kMergeMax; ++k) ov[k] = 0.f;
+    }
+    // Split weights of the slice's heads: wave w takes head h0 + w, lane k split k.
+    if (w < nh) {
+      const int hh = h0 + w;
+      const bool ok = lane < ns && hh * a.hd < p.K;
+      const float mv = ok ? a.m[(size_t)hh * a.n_split + lane] : -INFINITY;
+      const float lv = ok ? a.l[(size_t)hh * a.n_split + lane] : 0.f;
+      const float M = wave_max(mv);
+      const float wv = ok ? __expf(mv - M) : 0.f;
+      const float L = wave_sum(lv * wv);
+      if (lane < kMergeMax) amw[w][lane] = wv;
+      if (lane == 0) atot[w] = L;
     }
   } else if (tid < kSliceCols && cs < p.K) {
     xv = p.x[cs];
@@ -342,23 +351,11 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   }
   if (p.merge.o) {
     __syncthreads();
-    if (tid < nh && (h0 + tid) * p.merge.hd < p.K) {
-      float M = -INFINITY;
-      for (int k = 0; k < ns; ++k) M = fmaxf(M, amw[tid][k]);
-      float L = 0.f;
-      for (int k = 0; k < ns; ++k) {
-        const float w = __expf(amw[tid][k] - M);
-        amw[tid][k] = w;
-        L += aml[tid][k] * w;
-      }
-      atot[tid] = L;
-    }
-    __syncthreads();
     if (tid < kSliceCols && cs < p.K) {
       const int hl = tid / p.merge.hd, h = h0 + hl;
       float o = 0.f;
 #pragma unroll
-      for (int k = 0; k < kMergeMax; ++k) o += k < ns ? ov[k] * amw[hl][k] : 0.f;
+      for (int k = 0; k < kMergeMax; ++k) o += ov[k] * amw[hl][k];
       o /= atot[hl];
       if (p.merge.gated) o *= sigmoidf_(p.merge.qkv[(size_t)h * 2 * p.merge.hd + p.merge.hd + (cs - h * p.merge.hd)]);
       xv = o;
