@@ -162,8 +162,12 @@ static uint8_t* P(Model& m, int role, int layer);
 static int plan_packed(Model& m) {
   const trx_model_config& c = m.cfg;
   int ops = c.packed_ops;
+  // Measured on the 8B shape: trit5 gains from the packed GEMV on every large projection; for
+  // 2-bit codes the row-packet kernel is the faster FFN and head, and the packed o projection
+  // still pays for its attention merge.
   if (ops == TRX_PACK_AUTO)
-    ops = c.weight_kind == TRX_KIND_TERNARY5 ? (TRX_PACK_O | TRX_PACK_GATE_UP | TRX_PACK_HEAD) : TRX_PACK_O;
+    ops = c.weight_kind == TRX_KIND_TERNARY5 ? (TRX_PACK_O | TRX_PACK_GATE_UP | TRX_PACK_DOWN | TRX_PACK_HEAD)
+                                             : TRX_PACK_O;
   TRX_CHECK(ops >= 0 && (ops & ~TRX_PACK_ALL) == 0, TRX_E_INVALID, "packed_ops %d has unknown bits", c.packed_ops);
   const int E = c.n_embd, hd = c.head_dim, F = c.ffn_dim, wk = c.weight_kind;
   const int qrows = c.n_head * hd * (c.attn_gated ? 2 : 1), kvrows = c.n_kv_head * hd;

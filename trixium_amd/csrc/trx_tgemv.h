@@ -19,7 +19,9 @@
 // lane takes one dword of four rows per item; the sixteen lanes of a row reduce over DPP. The
 // block writes per-slice partial sums; the block that completes a 32-quad tile last (agent-scope
 // counter) adds the S partials in slice order (deterministic) and applies the epilogue
-// (store, residual, SwiGLU, or argmax).
+// (store, residual, SwiGLU, or argmax). With the RMSNorm prologue the table is built from
+// x * gain and each partial sum is scaled by 1/rms(x) (the block's reduction of sum x^2 then
+// overlaps the table build).
 #pragma once
 
 #include "trx_internal.h"
@@ -28,14 +30,15 @@ namespace trx {
 
 constexpr int kSliceCols = 256;     // columns per K-slice (two 128-groups)
 constexpr int kTabCols = 64;        // code positions per slice (16 lanes x 4 bytes)
-constexpr int kTileQuads = 32;      // quads per tile: one pass of a block (8 waves x 4 quads)
-constexpr int kTgThreads = 512;
-constexpr int kTgBlocksPerCU = 2;
+constexpr int kTgThreads = 1024;    // one block per CU: one 64 KB table per CU
+constexpr int kTgBlocksPerCU = 1;
+constexpr int kTileQuads = kTgThreads / 16;   // quads per tile: one pass of a block (16 waves x 4 quads)
+constexpr int kTileRows = 4 * kTileQuads;
 
 struct PackGeom {
   int kind = 0, M = 0, K = 0, G = 0, S = 0, M4 = 0, Q = 0, D = 0, n_tiles = 0;
   int bps = 0, tpb = 0;       // launch: blocks per slice, tiles per block (tile t -> block t % bps)
-  int rows_p = 0;             // partial sums per slice: bps * tpb tiles of 128 rows
+  int rows_p = 0;             // partial sums per slice: bps * tpb tiles of kTileRows rows
   size_t code_bytes = 0;      // uint4 [S][Q][D]
   size_t scale_off = 0;       // byte offset of the scales
   size_t bytes = 0;           // packed matrix

@@ -65,7 +65,7 @@ __host__ __device__ inline void tg_record_byte(bool t5, int d, int bi, int& g, i
   }
 }
 
-constexpr int kMaxTilesPerBlock = 64;
+constexpr int kMaxTilesPerBlock = 64;   // also bounds the tiles of a reduction pass
 
 static int cu_count() {
   static int cus = 0;
@@ -103,7 +103,7 @@ int pack_geom(PackGeom& g, int kind, int M, int K) {
   bps = cdiv(g.n_tiles, tpb);
   g.tpb = cdiv(g.n_tiles, bps);
   g.bps = bps;
-  g.rows_p = g.bps * g.tpb * kTileQuads * 4;
+  g.rows_p = g.bps * g.tpb * kTileRows;
   g.code_bytes = (size_t)g.S * g.Q * g.D * 16;
   g.scale_off = (g.code_bytes + 255) / 256 * 256;
   // Lanes of a block's partial last tile read up to (bps * tpb * 32 - Q) quads past their
@@ -213,6 +213,7 @@ int pack_ternary(const uint8_t* rows, int kind, int M, int K, int swiglu, uint8_
 // GEMV kernel -------------------------------------------------------------------------------
 
 constexpr int kDppRowRor8 = 0x128;
+constexpr int kDppQuadUp2 = 0xEE;      // quad_perm [2,3,2,3]: lanes 0,1 of a quad read lanes 2,3
 constexpr int kCpolSc1 = 16;          // buffer cache policy: device (agent) scope
 constexpr int kMaxNormVec = 6;         // float4 loads per thread of a normalised x: K <= 12288
 constexpr int kMergeMax = 32;          // attention splits the merging prologue takes
@@ -247,7 +248,6 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   constexpr int NLO = T5 ? 9 : 16;     // values of the low digits (trit5: 2 digits; 2-bit: 2 codes)
   constexpr int NHI = T5 ? 29 : 16;    // values of the rest (b / 9 <= 28; b >> 4)
   __shared__ __align__(16) float tab[256 * kTabCols];
-  __shared__ __align__(16) float scr[4 * 128];     // reduction: row totals of four tiles
   __shared__ float xs[kSliceCols];
   __shared__ float red[16];
   __shared__ int todo[kMaxTilesPerBlock];
@@ -343,12 +343,7 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
 #pragma unroll
   for (int b = 0; b < NB - 1; ++b) load_item(buf[b], b);
 
-  // 3. xhat of the slice, the two-level digit sums, then the table.
-  float rinv = 1.f;
-  if (p.norm_w) {
-    ss = block_sum(ss, red);
-    rinv = 1.0f / sqrtf(ss / (float)p.K + p.eps);
-  }
+  // 3. The slice's x (times the RMSNorm gain; 1/rms(x) scales the partial sums), then the table.
   if (p.merge.o) {
     __syncthreads();
     if (tid < kSliceCols && cs < p.K) {
@@ -362,7 +357,7 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
       if (j == 0) p.merge.out[cs] = o;
     }
   }
-  if (tid < kSliceCols) xs[tid] = p.norm_w ? xv * rinv * wv : xv;
+  if (tid < kSliceCols) xs[tid] = p.norm_w ? xv * wv : xv;
   __syncthreads();
   {
     // T[b][c] = hi(b) + lo(b): lo from the low digits (trit5: b % 9; 2-bit: b & 15), hi from the
@@ -399,7 +394,19 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
         if (h * NLO + e < 256) col[e * kTabCols] = lo[e] + hv;
     }
   }
+  // The block's sum of x^2 (its loads landed during the table build).
+  if (p.norm_w) {
+    ss = wave_sum_dpp(ss);
+    if (lane == 0) red[w] = ss;
+  }
   __syncthreads();
+  float rinv = 1.f;
+  if (p.norm_w) {
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < kTgThreads / 64; ++i) t += red[i];
+    rinv = 1.0f / sqrtf(t / (float)p.K + p.eps);
+  }
 
   // 4. The items: four rows x one dword per lane; sixteen lanes per row group.
   uint32_t lw[4], sel[4];
@@ -430,7 +437,7 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
     a[1] += dpp_f<kDppRowHalfMirror>(a[3]);
     a[0] += dpp_f<kDppQuadXor2>(a[1]);
     a[0] += dpp_f<kDppQuadXor1>(a[0]);
-    float v = a[0] * __half2float(__ushort_as_half((unsigned short)(it.sc >> sshift)));
+    float v = a[0] * (__half2float(__ushort_as_half((unsigned short)(it.sc >> sshift))) * rinv);
     v += dpp_f<kDppRowRor8>(v);                      // the other group (lane l16 ^ 8)
     // Agent-scope store (sc1): the tile's reducing block may run on another XCD.
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), rpart, po0, n * (int)pstep, kCpolSc1);
@@ -471,14 +478,16 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
     }
   }
   __syncthreads();
-  // Reduction: four tiles per pass, a thread per (tile, row). The S partials of a row are summed
-  // in slice order (the same order whichever block reduces), their loads all in flight together.
+  // Reduction: a thread per (tile, row), kTilesPerPass tiles per pass. The S partials of a row
+  // are summed in slice order (the same order whichever block reduces), in batches of 8 loads in
+  // flight. Consecutive threads hold consecutive rows, so a SwiGLU gate row finds its up row two
+  // lanes on (quad_perm).
   const int nt = n_todo;
-  const int rl = tid & 127, ti = tid >> 7;
-  for (int i0 = 0; i0 < nt; i0 += 4) {
+  constexpr int kTilesPerPass = kTgThreads / kTileRows;
+  const int rl = tid % kTileRows, ti = tid / kTileRows;
+  for (int i0 = 0; i0 < nt; i0 += kTilesPerPass) {
     const int i = i0 + ti;
-    const int r0 = (i < nt ? todo[i] : 0) * kTileQuads * 4;
-    const int prow = r0 + rl;
+    const int prow = (i < nt ? todo[i] : 0) * kTileRows + rl;
     const bool live = i < nt && prow < p.M4;
     float yv = 0.f;
     if (live) {
@@ -495,13 +504,12 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
       for (; q < p.S; ++q)
         yv += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rpart, off + q * step, 0, kCpolSc1));
     }
-    scr[ti * 128 + rl] = yv;
-    __syncthreads();
+    const float up = dpp_f<kDppQuadUp2>(yv);             // row prow + 2 (quad lanes 2, 3)
     unsigned long long key = 0;
     if (live) {
       if (p.epi == TRX_EPI_SWIGLU) {
         const int k = prow & 3, f = 2 * (prow >> 2) + k;
-        if (k < 2 && f < p.n_out) p.y[f] = silu(yv) * scr[ti * 128 + rl + 2];
+        if (k < 2 && f < p.n_out) p.y[f] = silu(yv) * up;
       } else if (prow < p.M) {
         float out = yv;
         if (p.epi == TRX_EPI_RESID) out += p.resid[prow];
@@ -517,7 +525,6 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
       }
       if (lane == 0 && key) atomicMax(p.amax_slot, key);
     }
-    __syncthreads();
   }
 }
 
