@@ -215,3 +215,26 @@ def test_packed_graph_replay_equals_eager(tiny_images, golden):
     assert a.generate_fresh(prompt, 16) == b.generate_fresh(prompt, 16)
     a.reset(); b.reset()
     assert np.array_equal(a.forward(prompt), b.forward(prompt))
+
+
+def test_packed_path_at_full_width():
+    """Two layers at Qwen3-1.7B width (2048 wide, ffn 6144, the 151936-row head): row tiles in
+    the hundreds, all projections sharing one packed workspace. Every projection on the packed
+    GEMV against none of them (the row-packet path, itself checked against the oracle above):
+    logits within the int16 activation rounding of the row-packet path, same greedy tokens."""
+    from trixium_amd.model import Decoder
+    cfg = C.QWEN3_1P7B.replace(name="qwen3-1.7b-width-2l", n_layer=2, max_ctx=128)
+    prompt = synth.random_prompt(cfg, 24, 3)
+    a = Decoder.synthetic(cfg, 5, weight_kind=L.KIND_TERNARY5, max_new=16, packed_ops=0)
+    b = Decoder.synthetic(cfg, 5, weight_kind=L.KIND_TERNARY5, max_new=16, packed_ops=63)
+    assert a.packed_ops == 0 and b.packed_ops == 63
+    la, lb = a.forward(prompt), b.forward(prompt)
+    errs = [_rel_err(lb, la)]
+    for t in (17, 90000, 5):
+        errs.append(_rel_err(b.forward([t]), a.forward([t])))
+    print("full width packed vs row-packet rel err", errs)
+    assert max(errs) <= 2e-3
+    a.reset(); b.reset()
+    ta, tb = a.generate_fresh(prompt, 16), b.generate_fresh(prompt, 16)
+    n = next((i for i, (x, y) in enumerate(zip(ta, tb)) if x != y), len(ta))
+    assert n >= 8, (ta, tb)

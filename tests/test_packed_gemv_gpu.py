@@ -138,3 +138,25 @@ def test_packed_matvec_agrees_with_int16_path(gpu):
     b = gpu.matvec_float(scales, codes, x)
     W = _w64(codes, scales)
     assert np.max(np.abs(a - b) / (np.abs(W) @ np.abs(x))) < 2e-4
+
+
+def test_packed_matrices_share_a_workspace(gpu):
+    """Matrices of different row-tile counts interleaved on one workspace (as the decoder's
+    projections share one): every result matches float64."""
+    from trixium_amd import _lib
+    shapes = [(300, 512), (5000, 512), (40, 1024), (9000, 256)]
+    mats, refs = [], []
+    for i, (M, K) in enumerate(shapes):
+        codes, scales = _rand(M, K, 40 + i)
+        mats.append(gpu.PackedMatrix(scales, codes))
+        refs.append(_w64(codes, scales))
+    work = _lib.DeviceBuffer(max(m.work.nbytes for m in mats))
+    work.zero()
+    for m in mats:
+        m.work = work
+    r = np.random.default_rng(5)
+    for rep in range(3):
+        for m, W in zip(mats, refs):
+            x = r.normal(0, 1, m.K).astype(np.float32)
+            y = m.matvec(x)
+            assert np.max(np.abs(y - W @ x) / (np.abs(W) @ np.abs(x))) < TOL, (rep, m.M, m.K)

@@ -565,7 +565,7 @@ TRX_API int trx_model_create(const trx_model_config* cfg, const float* rope_freq
   if ((rc = dalloc(m, (void**)&m.part_m, (size_t)c.n_head * splits * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.part_l, (size_t)c.n_head * splits * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.part_o, (size_t)c.n_head * splits * hd * 4))) return fail(rc);
-  if ((rc = dalloc(m, (void**)&m.attn_done, (size_t)std::max(c.n_kv_head, 1) * 4))) return fail(rc);
+  if ((rc = dalloc(m, (void**)&m.attn_done, (size_t)std::max(c.n_kv_head, 1) * kDoneStride * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.rope_dev, (size_t)rope_n * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.ctl, (size_t)(8 + c.max_ctx + c.max_new) * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.slot, 8))) return fail(rc);

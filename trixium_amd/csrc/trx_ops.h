@@ -38,8 +38,10 @@ struct AttnParams {
   float* out;              // [n_head*hd]
   int n_head, n_kv, n_rep, hd, rope_n, max_ctx, n_split, gated;
   float eps;
-  unsigned* done;          // [n_kv] split counters of the one-launch kernel (zero between launches)
+  unsigned* done;          // [n_kv][kDoneStride] split counters of the one-launch kernel (zero
+                           // between launches), one per 128-byte line
 };
+constexpr int kDoneStride = 32;
 
 struct DenseParams {
   const uint8_t* W;

@@ -60,7 +60,8 @@ int pack_ternary(const uint8_t* rows, int kind, int M, int K, int swiglu, uint8_
 // amax_slot != nullptr: also the packed (ordered value, ~row) maximum of y (atomicMax).
 // gate_pos/gate_from: the launch does nothing while *gate_pos < *gate_from.
 // work: pack_geom().work_bytes of device memory whose counters are zero (the call leaves them
-// zero); calls that share a workspace must not overlap.
+// zero); matrices may share one workspace of the largest work_bytes (the counters sit in a
+// region of one size for all), but calls that share it must not overlap.
 // x taken from decode attention's split partials instead (the o projection): x[h*hd + d] =
 // sum_sp o[h][sp][d] exp(m[h][sp] - M) / sum_sp l[h][sp] exp(m[h][sp] - M), times
 // sigmoid(gate) for gated attention; blocks of the first tile column also store x to `out`.

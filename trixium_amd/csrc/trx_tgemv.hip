@@ -4,6 +4,7 @@
 // of byte b is floor(b / 3^k) mod 3, 2-bit code k is (b >> 2k) & 3; weight = digit - 1).
 
 #include <algorithm>
+#include <type_traits>
 
 #include "trx_tgemv.h"
 
@@ -66,6 +67,10 @@ __host__ __device__ inline void tg_record_byte(bool t5, int d, int bi, int& g, i
 }
 
 constexpr int kMaxTilesPerBlock = 64;   // also bounds the tiles of a reduction pass
+// Tile counters sit 128 bytes apart: the S blocks of a tile count themselves at about the same
+// time, and atomics to one line are serialised.
+constexpr int kCntStride = 32;
+constexpr int kMaxTiles = 4096;          // row tiles of a matrix (4096 x kTileRows rows)
 
 static int cu_count() {
   static int cus = 0;
@@ -110,7 +115,10 @@ int pack_geom(PackGeom& g, int kind, int M, int K) {
   // slice; the padding keeps those reads inside the allocation for the last slice.
   const size_t over = (size_t)(g.bps * g.tpb * kTileQuads - g.Q) * g.D * 16;
   g.bytes = g.scale_off + (size_t)g.S * g.M4 * 4 + over;
-  g.cnt_bytes = ((size_t)g.n_tiles * 4 + 255) / 256 * 256;
+  // The counter region has one size for every matrix, so GEMVs over different matrices can
+  // share a workspace (a matrix's partial sums never cover another's counters).
+  TRX_CHECK(g.n_tiles <= kMaxTiles, TRX_E_INVALID, "packed GEMV: %d row tiles (at most %d)", g.n_tiles, kMaxTiles);
+  g.cnt_bytes = (size_t)kMaxTiles * kCntStride * 4;
   g.work_bytes = g.cnt_bytes + (size_t)g.S * g.rows_p * 4;
   TRX_CHECK(g.bytes < (1ull << 32), TRX_E_INVALID, "packed GEMV: %zu bytes exceed 4 GiB", g.bytes);
   return TRX_OK;
@@ -470,51 +478,74 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   if (tid < p.tpb) {
     const int t = j + tid * p.bps;
     if (t < p.n_tiles) {
-      const int old = __hip_atomic_fetch_add(p.cnt + t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int old = __hip_atomic_fetch_add(p.cnt + t * kCntStride, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (old == p.S - 1) {
-        __hip_atomic_store(p.cnt + t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p.cnt + t * kCntStride, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         todo[atomicAdd(&n_todo, 1)] = t;
       }
     }
   }
   __syncthreads();
-  // Reduction: a thread per (tile, row), kTilesPerPass tiles per pass. The S partials of a row
-  // are summed in slice order (the same order whichever block reduces), in batches of 8 loads in
-  // flight. Consecutive threads hold consecutive rows, so a SwiGLU gate row finds its up row two
-  // lanes on (quad_perm).
+  // Reduction: kRedRows rows per thread, kTilesPerPass tiles per pass. The loads carry no
+  // branches (a row or slice past the end re-reads a valid partial and is masked), so the
+  // kRedRows x kRedChunk loads of a chunk are all in flight together. The S partials of a row
+  // are summed in slice order (the same order whichever block reduces). Consecutive threads hold
+  // consecutive rows, so a SwiGLU gate row finds its up row two lanes on (quad_perm).
   const int nt = n_todo;
-  constexpr int kTilesPerPass = kTgThreads / kTileRows;
-  const int rl = tid % kTileRows, ti = tid / kTileRows;
+  constexpr int kRedRows = 2, kRedChunk = 16;
+  constexpr int kTilesPerPass = kTgThreads * kRedRows / kTileRows;
+  static_assert(kTilesPerPass <= kMaxTilesPerBlock, "reduction pass");
+  const uint32_t step = (uint32_t)p.rows_p * 4u;
   for (int i0 = 0; i0 < nt; i0 += kTilesPerPass) {
-    const int i = i0 + ti;
-    const int prow = (i < nt ? todo[i] : 0) * kTileRows + rl;
-    const bool live = i < nt && prow < p.M4;
-    float yv = 0.f;
-    if (live) {
-      const uint32_t off = (uint32_t)prow * 4u, step = (uint32_t)p.rows_p * 4u;
-      int q = 0;
-      for (; q + 8 <= p.S; q += 8) {
-        float t[8];
+    float yv[kRedRows];
+    int prow[kRedRows];
+    bool live[kRedRows];
+    uint32_t off[kRedRows];
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
-          t[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rpart, off + (q + k) * step, 0, kCpolSc1));
-#pragma unroll
-        for (int k = 0; k < 8; ++k) yv += t[k];
-      }
-      for (; q < p.S; ++q)
-        yv += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rpart, off + q * step, 0, kCpolSc1));
+    for (int r = 0; r < kRedRows; ++r) {
+      const int idx = tid + r * kTgThreads, i = i0 + idx / kTileRows;
+      prow[r] = (i < nt ? todo[i] : todo[0]) * kTileRows + idx % kTileRows;
+      live[r] = i < nt && prow[r] < p.M4;
+      off[r] = (uint32_t)(live[r] ? prow[r] : 0) * 4u;
+      yv[r] = 0.f;
     }
-    const float up = dpp_f<kDppQuadUp2>(yv);             // row prow + 2 (quad lanes 2, 3)
+    // Tiles fill row slot 0 first and are kTileRows (4 waves) apart, so the live tests below are
+    // uniform per wave (but for a partial last tile), and every load of a branch is consumed in
+    // it. Rows of a dead slot issue no load.
+    auto chunks = [&](auto nrows) {
+      constexpr int NR = decltype(nrows)::value;
+      for (int q0 = 0; q0 < p.S; q0 += kRedChunk) {
+        float t[NR][kRedChunk];
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+#pragma unroll
+          for (int k = 0; k < kRedChunk; ++k)
+            t[r][k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                    rpart, off[r] + (uint32_t)min(q0 + k, p.S - 1) * step, 0, kCpolSc1));
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+#pragma unroll
+          for (int k = 0; k < kRedChunk; ++k) yv[r] += q0 + k < p.S ? t[r][k] : 0.f;
+      }
+    };
+    if (live[0] && live[1]) chunks(std::integral_constant<int, 2>{});
+    else if (live[0]) chunks(std::integral_constant<int, 1>{});
     unsigned long long key = 0;
-    if (live) {
-      if (p.epi == TRX_EPI_SWIGLU) {
-        const int k = prow & 3, f = 2 * (prow >> 2) + k;
-        if (k < 2 && f < p.n_out) p.y[f] = silu(yv) * up;
-      } else if (prow < p.M) {
-        float out = yv;
-        if (p.epi == TRX_EPI_RESID) out += p.resid[prow];
-        p.y[prow] = out;
-        key = ((unsigned long long)ordered_bits(out) << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)prow);
+#pragma unroll
+    for (int r = 0; r < kRedRows; ++r) {
+      const float up = dpp_f<kDppQuadUp2>(yv[r]);        // row prow + 2 (quad lanes 2, 3)
+      if (live[r]) {
+        if (p.epi == TRX_EPI_SWIGLU) {
+          const int k = prow[r] & 3, f = 2 * (prow[r] >> 2) + k;
+          if (k < 2 && f < p.n_out) p.y[f] = silu(yv[r]) * up;
+        } else if (prow[r] < p.M) {
+          float out = yv[r];
+          if (p.epi == TRX_EPI_RESID) out += p.resid[prow[r]];
+          p.y[prow[r]] = out;
+          const unsigned long long kr =
+              ((unsigned long long)ordered_bits(out) << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)prow[r]);
+          key = kr > key ? kr : key;
+        }
       }
     }
     if (p.amax_slot) {
