@@ -158,9 +158,9 @@ typedef struct {
   int packed_ops;              /* projections run by the packed GEMV (trx_gemv_packed_f32) over
                                   a packed copy of their rows, as TRX_PACK_* bits; the others run
                                   trx_gemv_ternary_f32's kernel. TRX_PACK_AUTO: the library's
-                                  choice for the weight kind (trit5: o, gate|up, down, LM head;
-                                  2-bit: o). (With layer_fusion the fused layers keep the
-                                  row-packet kernel.) */
+                                  choice (q|k|v, o, gate|up, down, ternary LM head; DeltaNet
+                                  projections on the row-packet kernel). (With layer_fusion the
+                                  fused layers keep the row-packet kernel.) */
 } trx_model_config;
 
 #define TRX_PACK_QKV 1         /* attention q|k|v */

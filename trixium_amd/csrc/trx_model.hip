@@ -71,6 +71,10 @@ struct Model {
   int packed_ops = 0;
   bool pack_dirty = true;
   void* pack_work = nullptr;
+  // Packed gate|up and down: gate|up hands its split-K partial sums to down (ffn_part, geometry
+  // ffn_S x ffn_rows_p), whose prologue sums them and applies SwiGLU.
+  float* ffn_part = nullptr;
+  int ffn_S = 0, ffn_rows_p = 0;
   hipGraph_t graph = nullptr;
   hipGraphExec_t graph_exec = nullptr;
   size_t dev_bytes = 0;
@@ -162,12 +166,11 @@ static uint8_t* P(Model& m, int role, int layer);
 static int plan_packed(Model& m) {
   const trx_model_config& c = m.cfg;
   int ops = c.packed_ops;
-  // Measured on the 8B shape: trit5 gains from the packed GEMV on every large projection; for
-  // 2-bit codes the row-packet kernel is the faster FFN and head, and the packed o projection
-  // still pays for its attention merge.
+  // Measured on the 8B shape: the packed GEMV is the faster kernel for every attention-layer
+  // projection and the head, in both code formats. DeltaNet projections stay on the row-packet
+  // kernel until measured at a hybrid shape.
   if (ops == TRX_PACK_AUTO)
-    ops = c.weight_kind == TRX_KIND_TERNARY5 ? (TRX_PACK_O | TRX_PACK_GATE_UP | TRX_PACK_DOWN | TRX_PACK_HEAD)
-                                             : TRX_PACK_O;
+    ops = TRX_PACK_QKV | TRX_PACK_O | TRX_PACK_GATE_UP | TRX_PACK_DOWN | TRX_PACK_HEAD;
   TRX_CHECK(ops >= 0 && (ops & ~TRX_PACK_ALL) == 0, TRX_E_INVALID, "packed_ops %d has unknown bits", c.packed_ops);
   const int E = c.n_embd, hd = c.head_dim, F = c.ffn_dim, wk = c.weight_kind;
   const int qrows = c.n_head * hd * (c.attn_gated ? 2 : 1), kvrows = c.n_kv_head * hd;
@@ -215,6 +218,15 @@ static int plan_packed(Model& m) {
   int rc;
   if ((rc = dalloc(m, (void**)&buf, total))) return rc;
   if ((rc = dalloc(m, &m.pack_work, work))) return rc;   // zeroed: the tile counters start at 0
+  if ((ops & TRX_PACK_GATE_UP) && (ops & TRX_PACK_DOWN)) {
+    PackGeom g;
+    if ((rc = pack_geom(g, wk, 2 * F, E))) return rc;
+    if (g.S <= tgemv_partial_slices_max()) {
+      if ((rc = dalloc(m, (void**)&m.ffn_part, (size_t)g.S * g.rows_p * 4))) return rc;
+      m.ffn_S = g.S;
+      m.ffn_rows_p = g.rows_p;
+    }
+  }
   for (size_t i = 0; i < list.size(); ++i) {
     list[i].second.buf = buf + offs[i];
     m.packed[list[i].first] = list[i].second;
@@ -454,6 +466,19 @@ static int run_step(Model& m, hipStream_t s) {
       }
     }
     // SwiGLU FFN: gate|up with the FFN RMSNorm, then down with the residual add.
+    auto igu = m.packed.find({OP_GATE_UP, l}), idn = m.packed.find({OP_DOWN, l});
+    if (m.ffn_part && igu != m.packed.end() && idn != m.packed.end()) {
+      // gate|up stores its partial sums; down's prologue reduces them and applies SwiGLU.
+      const PartialSums po = {m.ffn_part, nullptr, 0, 0, 0, nullptr};
+      if ((rc = tgemv_f32(igu->second.buf, wk, 2 * F, E, m.x, PF(m, TRX_ROLE_FFN_NORM, l), c.rms_eps, nullptr,
+                          TRX_EPI_SWIGLU, nullptr, nullptr, m.pack_work, s, nullptr, nullptr, nullptr, &po)))
+        return rc;
+      const PartialSums pi = {nullptr, m.ffn_part, m.ffn_S, m.ffn_rows_p, F, m.act};
+      if ((rc = tgemv_f32(idn->second.buf, wk, E, F, nullptr, nullptr, c.rms_eps, m.x, TRX_EPI_RESID, m.x, nullptr,
+                          m.pack_work, s, nullptr, nullptr, nullptr, &pi)))
+        return rc;
+      continue;
+    }
     if ((rc = projection(m, OP_GATE_UP, l, P(m, TRX_ROLE_FFN_GATE, l), wk, 2 * F, E, m.x,
                           PF(m, TRX_ROLE_FFN_NORM, l), m.act, TRX_EPI_SWIGLU, nullptr, s))) return rc;
     if ((rc = projection(m, OP_DOWN, l, P(m, TRX_ROLE_FFN_DOWN, l), wk, E, F, m.act, nullptr, m.x,

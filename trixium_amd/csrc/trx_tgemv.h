@@ -75,9 +75,25 @@ struct AttnMergeSrc {
   float* out;              // [n_head * hd]
 };
 
+// Split-K partial sums handed to the next GEMV instead of reduced in this one. A GEMV given
+// `out` stores only its partial sums, part[s * rows_p + r] for slice s and packed row r (every
+// slice's partials, already scaled; pack_geom gives S and rows_p), and skips the tile counting
+// and reduction. A GEMV given `in` takes x from such partials of a SwiGLU-packed gate|up matrix:
+// x[f] = silu(g[f]) * u[f] with g and u the sums over the S slices (f < F); blocks of the first
+// tile column also store x to `act`.
+struct PartialSums {
+  float* out;              // producer: [S][rows_p]
+  const float* in;         // consumer: the producer's buffer
+  int S, rows_p, F;        // consumer: the producer's geometry and F = its M / 2
+  float* act;              // consumer: x stored here (may be null)
+};
+
+// The most producer slices (K / 256, rounded up) a partial-sum consumer takes.
+int tgemv_partial_slices_max();
+
 int tgemv_f32(const uint8_t* packed, int kind, int M, int K, const float* x, const float* norm_w,
               float eps, float* y, int epi, const float* resid, unsigned long long* amax_slot,
               void* work, hipStream_t s, const int* gate_pos = nullptr, const int* gate_from = nullptr,
-              const AttnMergeSrc* merge = nullptr);
+              const AttnMergeSrc* merge = nullptr, const PartialSums* parts = nullptr);
 
 }  // namespace trx

@@ -225,6 +225,8 @@ constexpr int kDppQuadUp2 = 0xEE;      // quad_perm [2,3,2,3]: lanes 0,1 of a qu
 constexpr int kCpolSc1 = 16;          // buffer cache policy: device (agent) scope
 constexpr int kMaxNormVec = 6;         // float4 loads per thread of a normalised x: K <= 12288
 constexpr int kMergeMax = 32;          // attention splits the merging prologue takes
+constexpr int kSwiPartMax = 32;        // gate|up slices the SwiGLU prologue takes
+constexpr int kSwiPerThread = kSwiPartMax / (kTgThreads / (2 * kSliceCols));
 
 struct TgParams {
   const uint8_t* codes;
@@ -243,6 +245,7 @@ struct TgParams {
   const int* gate_pos;
   const int* gate_from;
   AttnMergeSrc merge;      // merge.o != nullptr: x from attention partials
+  PartialSums parts;       // parts.out: store the partial sums only; parts.in: x from them
 };
 
 template <bool T5>
@@ -301,6 +304,16 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
       if (lane < kMergeMax) amw[w][lane] = wv;
       if (lane == 0) atot[w] = L;
     }
+  } else if (p.parts.in) {
+    // The gate|up partial sums of this slice's 2 x 256 packed rows: thread t sums row t % 512
+    // over every other slice, starting at slice t / 512.
+    const __amdgpu_buffer_rsrc_t rin = make_rsrc(p.parts.in, (uint32_t)((size_t)p.parts.S * p.parts.rows_p * 4));
+    const uint32_t off = (uint32_t)(2 * kSliceCols * s + (tid & (2 * kSliceCols - 1))) * 4u;
+    const int h = tid / (2 * kSliceCols);
+#pragma unroll
+    for (int k = 0; k < kSwiPerThread; ++k)
+      ov[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                            rin, off + (uint32_t)min(h + 2 * k, p.parts.S - 1) * (uint32_t)p.parts.rows_p * 4u, 0, 0));
   } else if (tid < kSliceCols && cs < p.K) {
     xv = p.x[cs];
     if (p.norm_w) wv = p.norm_w[cs];
@@ -365,7 +378,26 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
       if (j == 0) p.merge.out[cs] = o;
     }
   }
-  if (tid < kSliceCols) xs[tid] = p.norm_w ? xv * wv : xv;
+  if (p.parts.in) {
+    // Sums of the two slice halves (slice order within each) through the table's memory, then
+    // gate row r pairs with up row r + 2 of its quad: x[f] = silu(g) * u.
+    const int h = tid / (2 * kSliceCols);
+    float v = 0.f;
+#pragma unroll
+    for (int k = 0; k < kSwiPerThread; ++k) v += h + 2 * k < p.parts.S ? ov[k] : 0.f;
+    tab[tid] = v;
+    __syncthreads();
+    const float g = tid < 2 * kSliceCols ? tab[tid] + tab[tid + 2 * kSliceCols] : 0.f;
+    const float u = dpp_f<kDppQuadUp2>(g);
+    const int fl = 2 * (tid >> 2) + (tid & 3), f = s * kSliceCols + fl;
+    if (tid < 2 * kSliceCols && (tid & 3) < 2) {
+      const float xf = f < p.K ? silu(g) * u : 0.f;
+      xs[fl] = xf;
+      if (j == 0 && p.parts.act && f < p.K) p.parts.act[f] = xf;
+    }
+  } else if (tid < kSliceCols) {
+    xs[tid] = p.norm_w ? xv * wv : xv;
+  }
   __syncthreads();
   {
     // T[b][c] = hi(b) + lo(b): lo from the low digits (trit5: b % 9; 2-bit: b & 15), hi from the
@@ -469,6 +501,9 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
     if (ph < rem) compute(buf[ph], n + ph);
   }
 
+  // The next GEMV reduces the partial sums (their stores complete before the launch ends).
+  if (p.parts.out) return;
+
   // 5. Count this block's tiles done; the last of a tile's S blocks reduces it.
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(0);
@@ -559,6 +594,8 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   }
 }
 
+int tgemv_partial_slices_max() { return kSwiPartMax; }
+
 template <bool T5>
 static const void* tg_fn() {
   return (const void*)tgemv_kernel<T5, 4>;
@@ -567,11 +604,18 @@ static const void* tg_fn() {
 int tgemv_f32(const uint8_t* packed, int kind, int M, int K, const float* x, const float* norm_w,
               float eps, float* y, int epi, const float* resid, unsigned long long* amax_slot,
               void* work, hipStream_t s, const int* gate_pos, const int* gate_from,
-              const AttnMergeSrc* merge) {
+              const AttnMergeSrc* merge, const PartialSums* parts) {
   PackGeom g;
   int rc = pack_geom(g, kind, M, K);
   if (rc) return rc;
-  TRX_CHECK(packed && (x || merge) && y && work, TRX_E_INVALID, "packed GEMV: null argument");
+  const bool p_in = parts && parts->in, p_out = parts && parts->out;
+  TRX_CHECK(packed && (x || merge || p_in) && (y || p_out) && work, TRX_E_INVALID, "packed GEMV: null argument");
+  TRX_CHECK(!p_in || (!x && !merge && !norm_w && parts->S >= 1 && parts->S <= kSwiPartMax && parts->F == K &&
+                      parts->rows_p >= 2 * kSliceCols * cdiv(K, kSliceCols)),
+            TRX_E_INVALID, "packed GEMV: unsupported partial-sum input (S %d, F %d, K %d)",
+            p_in ? parts->S : 0, p_in ? parts->F : 0, K);
+  TRX_CHECK(!p_out || (!amax_slot && !merge && !p_in), TRX_E_INVALID,
+            "packed GEMV: partial-sum output with an argmax or another source");
   TRX_CHECK(!merge || (merge->o && merge->m && merge->l && merge->pos && merge->out && !norm_w &&
                        (merge->hd == 64 || merge->hd == 128 || merge->hd == 256) &&
                        merge->n_split >= 1 && merge->n_split <= kMergeMax && K % merge->hd == 0 &&
@@ -608,11 +652,12 @@ int tgemv_f32(const uint8_t* packed, int kind, int M, int K, const float* x, con
   p.epi = epi;
   p.n_out = epi == TRX_EPI_SWIGLU ? M / 2 : M;
   p.cnt = (int*)work;
-  p.part = (float*)((uint8_t*)work + g.cnt_bytes);
+  p.part = p_out ? parts->out : (float*)((uint8_t*)work + g.cnt_bytes);
   p.amax_slot = amax_slot;
   p.gate_pos = gate_pos;
   p.gate_from = gate_from;
   p.merge = merge ? *merge : AttnMergeSrc{};
+  p.parts = parts ? *parts : PartialSums{};
   const void* fn = kind == TRX_KIND_TERNARY5 ? tg_fn<true>() : tg_fn<false>();
   void* args[] = {(void*)&p};
   TRX_HIP(hipLaunchKernel(fn, dim3(g.S * g.bps), dim3(kTgThreads), args, 0, s));
