@@ -71,10 +71,18 @@ struct Model {
   int packed_ops = 0;
   bool pack_dirty = true;
   void* pack_work = nullptr;
-  // Packed gate|up and down: gate|up hands its split-K partial sums to down (ffn_part, geometry
-  // ffn_S x ffn_rows_p), whose prologue sums them and applies SwiGLU.
+  // Split-K partial sums handed from a packed GEMV to the next one, which reduces them in its
+  // prologue: gate|up -> down (SwiGLU; with gate|up's slice sums of x^2 for its RMSNorm), and the
+  // residual producers o and down -> the next packed consumer of the residual (x = resid + sums).
   float* ffn_part = nullptr;
+  float* ffn_ss = nullptr;
   int ffn_S = 0, ffn_rows_p = 0;
+  float* o_part = nullptr;
+  int o_S = 0, o_rows_p = 0;
+  float* down_part = nullptr;
+  int down_S = 0, down_rows_p = 0;
+  float* x2 = nullptr;                             // second residual buffer (x alternates)
+  float* hidden = nullptr;                         // the residual after the last layer
   hipGraph_t graph = nullptr;
   hipGraphExec_t graph_exec = nullptr;
   size_t dev_bytes = 0;
@@ -218,15 +226,24 @@ static int plan_packed(Model& m) {
   int rc;
   if ((rc = dalloc(m, (void**)&buf, total))) return rc;
   if ((rc = dalloc(m, &m.pack_work, work))) return rc;   // zeroed: the tile counters start at 0
-  if ((ops & TRX_PACK_GATE_UP) && (ops & TRX_PACK_DOWN)) {
+  // Partial-sum buffers of the producers that hand their sums on.
+  auto part_buf = [&](int M, int K, float** buf, int* S, int* rows_p, float** ss) -> int {
     PackGeom g;
-    if ((rc = pack_geom(g, wk, 2 * F, E))) return rc;
-    if (g.S <= tgemv_partial_slices_max()) {
-      if ((rc = dalloc(m, (void**)&m.ffn_part, (size_t)g.S * g.rows_p * 4))) return rc;
-      m.ffn_S = g.S;
-      m.ffn_rows_p = g.rows_p;
-    }
-  }
+    int rc2 = pack_geom(g, wk, M, K);
+    if (rc2) return rc2;
+    if ((rc2 = dalloc(m, (void**)buf, (size_t)g.S * g.rows_p * 4))) return rc2;
+    if (ss && (rc2 = dalloc(m, (void**)ss, (size_t)g.bps * g.S * 4))) return rc2;
+    *S = g.S;
+    *rows_p = g.rows_p;
+    return TRX_OK;
+  };
+  if ((ops & TRX_PACK_GATE_UP) && (ops & TRX_PACK_DOWN) && cdiv(E, kSliceCols) <= tgemv_partial_slices_max())
+    if ((rc = part_buf(2 * F, E, &m.ffn_part, &m.ffn_S, &m.ffn_rows_p, &m.ffn_ss))) return rc;
+  if ((ops & TRX_PACK_O) && (ops & TRX_PACK_GATE_UP) && m.n_attn > 0 &&
+      cdiv(c.n_head * hd, kSliceCols) <= tgemv_resid_slices_max())
+    if ((rc = part_buf(E, c.n_head * hd, &m.o_part, &m.o_S, &m.o_rows_p, nullptr))) return rc;
+  if ((ops & TRX_PACK_DOWN) && cdiv(F, kSliceCols) <= tgemv_resid_slices_max())
+    if ((rc = part_buf(E, F, &m.down_part, &m.down_S, &m.down_rows_p, nullptr))) return rc;
   for (size_t i = 0; i < list.size(); ++i) {
     list[i].second.buf = buf + offs[i];
     m.packed[list[i].first] = list[i].second;
@@ -412,6 +429,42 @@ static int run_step(Model& m, hipStream_t s) {
   ep.x = m.x;
   if ((rc = launch_embed(ep, s))) return rc;
 
+  // The residual stream between kernels is x = *xc, plus the sums of a producer's partials while
+  // pend.in is set: a packed consumer adds them in its prologue and stores x to the other buffer.
+  // A producer hands on partial sums only when the next consumer is a packed GEMV; otherwise it
+  // reduces them into m.x (the DeltaNet and fused-layer kernels read m.x).
+  float* xc = m.x;
+  PartialSums pend = {};
+  auto other = [&](const float* p) { return p == m.x ? m.x2 : m.x; };
+  PartialSums pin;
+  // Input of a packed consumer: sets x (or nullptr) and returns its partial-sum input (or null).
+  auto take = [&](const float*& x) -> PartialSums* {
+    pin = {};
+    if (!pend.in) {
+      x = xc;
+      return nullptr;
+    }
+    pin.in = pend.in;
+    pin.resid = xc;
+    pin.S = pend.S;
+    pin.rows_p = pend.rows_p;
+    xc = other(xc);
+    pin.act = xc;
+    pend = {};
+    x = nullptr;
+    return &pin;
+  };
+  auto packed = [&](int op, int l) -> const PackedMat* {
+    auto it = m.packed.find({op, l});
+    return it == m.packed.end() ? nullptr : &it->second;
+  };
+  // Whether the residual after layer l goes to a packed GEMV that takes the producer's S slices.
+  auto next_packed = [&](int l, int S) {
+    if (S > tgemv_resid_slices_max()) return false;
+    if (l + 1 < c.n_layer) return !m.is_dn(l + 1) && !m.fused && packed(OP_QKV, l + 1) != nullptr;
+    return packed(OP_HEAD, 0) != nullptr;
+  };
+
   for (int l = 0; l < c.n_layer; ++l) {
     if (m.is_dn(l)) {
       if ((rc = dn_layer_launch(m, l, s))) return rc;
@@ -421,8 +474,16 @@ static int run_step(Model& m, hipStream_t s) {
       continue;
     } else {
       // q|k|v with the attention RMSNorm fused in the prologue.
-      if ((rc = projection(m, OP_QKV, l, P(m, TRX_ROLE_ATTN_Q, l), wk, qrows + 2 * kvrows, E, m.x,
-                            PF(m, TRX_ROLE_ATTN_NORM, l), m.qkv, TRX_EPI_STORE, nullptr, s))) return rc;
+      if (const PackedMat* pq = packed(OP_QKV, l)) {
+        const float* xin;
+        const PartialSums* pp = take(xin);
+        if ((rc = tgemv_f32(pq->buf, wk, qrows + 2 * kvrows, E, xin, PF(m, TRX_ROLE_ATTN_NORM, l), c.rms_eps,
+                            m.qkv, TRX_EPI_STORE, nullptr, nullptr, m.pack_work, s, nullptr, nullptr, nullptr, pp)))
+          return rc;
+      } else if ((rc = projection(m, OP_QKV, l, P(m, TRX_ROLE_ATTN_Q, l), wk, qrows + 2 * kvrows, E, xc,
+                                   PF(m, TRX_ROLE_ATTN_NORM, l), m.qkv, TRX_EPI_STORE, nullptr, s))) {
+        return rc;
+      }
       AttnParams ap = {};
       ap.qkv = m.qkv;
       ap.q_norm = PF(m, TRX_ROLE_ATTN_Q_NORM, l);
@@ -448,8 +509,8 @@ static int run_step(Model& m, hipStream_t s) {
       // One-launch attention; with a packed o projection the splits are merged in that GEMV's
       // prologue (each of its blocks merges the heads of its column slice).
       const bool fd = attention_fd_supported(ap.n_rep, hd, ap.rope_n, ap.n_split);
-      auto ito = m.packed.find({OP_O, l});
-      const bool merge_in_o = fd && ito != m.packed.end() && ap.n_split <= 32 && kSliceCols % hd == 0;
+      const PackedMat* po = packed(OP_O, l);
+      const bool merge_in_o = fd && po && ap.n_split <= 32 && kSliceCols % hd == 0;
       ap.done = merge_in_o ? nullptr : m.attn_done;
       if (fd) {
         if ((rc = launch_attention_fd(ap, s))) return rc;
@@ -458,44 +519,102 @@ static int run_step(Model& m, hipStream_t s) {
       }
       if (merge_in_o) {
         AttnMergeSrc ms = {ap.part_m, ap.part_l, ap.part_o, ap.pos, ap.n_split, hd, ap.gated, ap.qkv, m.attn_out};
-        if ((rc = tgemv_f32(ito->second.buf, wk, E, c.n_head * hd, nullptr, nullptr, c.rms_eps, m.x, TRX_EPI_RESID,
-                            m.x, nullptr, m.pack_work, s, nullptr, nullptr, &ms))) return rc;
-      } else if ((rc = projection(m, OP_O, l, P(m, TRX_ROLE_ATTN_OUT, l), wk, E, c.n_head * hd, m.attn_out,
-                                   nullptr, m.x, TRX_EPI_RESID, m.x, s))) {
-        return rc;
+        if (m.o_part && packed(OP_GATE_UP, l)) {
+          // The o projection's partial sums go to gate|up, which adds them to the residual.
+          PartialSums out = {};
+          out.out = m.o_part;
+          if ((rc = tgemv_f32(po->buf, wk, E, c.n_head * hd, nullptr, nullptr, c.rms_eps, nullptr, TRX_EPI_STORE,
+                              nullptr, nullptr, m.pack_work, s, nullptr, nullptr, &ms, &out))) return rc;
+          pend.in = m.o_part;
+          pend.S = m.o_S;
+          pend.rows_p = m.o_rows_p;
+        } else {
+          if ((rc = tgemv_f32(po->buf, wk, E, c.n_head * hd, nullptr, nullptr, c.rms_eps, m.x, TRX_EPI_RESID, xc,
+                              nullptr, m.pack_work, s, nullptr, nullptr, &ms))) return rc;
+          xc = m.x;
+        }
+      } else {
+        if ((rc = projection(m, OP_O, l, P(m, TRX_ROLE_ATTN_OUT, l), wk, E, c.n_head * hd, m.attn_out, nullptr,
+                             m.x, TRX_EPI_RESID, xc, s))) return rc;
+        xc = m.x;
       }
     }
     // SwiGLU FFN: gate|up with the FFN RMSNorm, then down with the residual add.
-    auto igu = m.packed.find({OP_GATE_UP, l}), idn = m.packed.find({OP_DOWN, l});
-    if (m.ffn_part && igu != m.packed.end() && idn != m.packed.end()) {
-      // gate|up stores its partial sums; down's prologue reduces them and applies SwiGLU.
-      const PartialSums po = {m.ffn_part, nullptr, 0, 0, 0, nullptr};
-      if ((rc = tgemv_f32(igu->second.buf, wk, 2 * F, E, m.x, PF(m, TRX_ROLE_FFN_NORM, l), c.rms_eps, nullptr,
-                          TRX_EPI_SWIGLU, nullptr, nullptr, m.pack_work, s, nullptr, nullptr, nullptr, &po)))
-        return rc;
-      const PartialSums pi = {nullptr, m.ffn_part, m.ffn_S, m.ffn_rows_p, F, m.act};
-      if ((rc = tgemv_f32(idn->second.buf, wk, E, F, nullptr, nullptr, c.rms_eps, m.x, TRX_EPI_RESID, m.x, nullptr,
-                          m.pack_work, s, nullptr, nullptr, nullptr, &pi)))
-        return rc;
+    const PackedMat* pg = packed(OP_GATE_UP, l);
+    const PackedMat* pd = packed(OP_DOWN, l);
+    if (pg && pd && m.ffn_part) {
+      // gate|up stores its partial sums (and slice sums of x^2); down's prologue reduces them,
+      // applies the RMSNorm scale and SwiGLU.
+      const float* xin;
+      PartialSums* pp = take(xin);
+      PartialSums gu = pp ? *pp : PartialSums{};
+      gu.out = m.ffn_part;
+      gu.out_ss = m.ffn_ss;
+      if ((rc = tgemv_f32(pg->buf, wk, 2 * F, E, xin, PF(m, TRX_ROLE_FFN_NORM, l), c.rms_eps, nullptr, TRX_EPI_SWIGLU,
+                          nullptr, nullptr, m.pack_work, s, nullptr, nullptr, nullptr, &gu))) return rc;
+      PartialSums dn = {};
+      dn.in = m.ffn_part;
+      dn.in_ss = m.ffn_ss;
+      dn.S = m.ffn_S;
+      dn.rows_p = m.ffn_rows_p;
+      dn.F = F;
+      dn.in_K = E;
+      dn.act = m.act;
+      if (m.down_part && next_packed(l, m.down_S)) {
+        dn.out = m.down_part;
+        if ((rc = tgemv_f32(pd->buf, wk, E, F, nullptr, nullptr, c.rms_eps, nullptr, TRX_EPI_STORE, nullptr, nullptr,
+                            m.pack_work, s, nullptr, nullptr, nullptr, &dn))) return rc;
+        pend.in = m.down_part;
+        pend.S = m.down_S;
+        pend.rows_p = m.down_rows_p;
+      } else {
+        if ((rc = tgemv_f32(pd->buf, wk, E, F, nullptr, nullptr, c.rms_eps, m.x, TRX_EPI_RESID, xc, nullptr,
+                            m.pack_work, s, nullptr, nullptr, nullptr, &dn))) return rc;
+        xc = m.x;
+      }
       continue;
     }
-    if ((rc = projection(m, OP_GATE_UP, l, P(m, TRX_ROLE_FFN_GATE, l), wk, 2 * F, E, m.x,
-                          PF(m, TRX_ROLE_FFN_NORM, l), m.act, TRX_EPI_SWIGLU, nullptr, s))) return rc;
-    if ((rc = projection(m, OP_DOWN, l, P(m, TRX_ROLE_FFN_DOWN, l), wk, E, F, m.act, nullptr, m.x,
-                          TRX_EPI_RESID, m.x, s))) return rc;
+    if (pg) {
+      const float* xin;
+      const PartialSums* pp = take(xin);
+      if ((rc = tgemv_f32(pg->buf, wk, 2 * F, E, xin, PF(m, TRX_ROLE_FFN_NORM, l), c.rms_eps, m.act, TRX_EPI_SWIGLU,
+                          nullptr, nullptr, m.pack_work, s, nullptr, nullptr, nullptr, pp))) return rc;
+    } else if ((rc = projection(m, OP_GATE_UP, l, P(m, TRX_ROLE_FFN_GATE, l), wk, 2 * F, E, xc,
+                                 PF(m, TRX_ROLE_FFN_NORM, l), m.act, TRX_EPI_SWIGLU, nullptr, s))) {
+      return rc;
+    }
+    if (pd && m.down_part && next_packed(l, m.down_S)) {
+      PartialSums out = {};
+      out.out = m.down_part;
+      if ((rc = tgemv_f32(pd->buf, wk, E, F, m.act, nullptr, c.rms_eps, nullptr, TRX_EPI_STORE, nullptr, nullptr,
+                          m.pack_work, s, nullptr, nullptr, nullptr, &out))) return rc;
+      pend.in = m.down_part;
+      pend.S = m.down_S;
+      pend.rows_p = m.down_rows_p;
+    } else {
+      if ((rc = projection(m, OP_DOWN, l, P(m, TRX_ROLE_FFN_DOWN, l), wk, E, F, m.act, nullptr, m.x, TRX_EPI_RESID,
+                           xc, s))) return rc;
+      xc = m.x;
+    }
   }
   // LM head with the output RMSNorm and the greedy argmax; skipped (by the kernel, reading the
   // position) on prefill positions before head_from.
   const int head_role = c.head_tied ? TRX_ROLE_TOK_EMB : TRX_ROLE_LM_HEAD;
   const int head_kind = c.head_tied ? c.emb_kind : c.head_kind;
-  if (head_kind == TRX_KIND_F16) {
+  if (const PackedMat* ph = packed(OP_HEAD, 0)) {
+    const float* xin;
+    const PartialSums* pp = take(xin);
+    if ((rc = tgemv_f32(ph->buf, head_kind, c.vocab, E, xin, PF(m, TRX_ROLE_OUT_NORM, 0), c.rms_eps, m.logits,
+                        TRX_EPI_STORE, nullptr, m.slot, m.pack_work, s, m.pos(), m.head_from(), nullptr, pp)))
+      return rc;
+  } else if (head_kind == TRX_KIND_F16) {
     DenseParams dp = {};
     dp.W = P(m, head_role, 0);
     dp.kind = TRX_KIND_F16;
     dp.M = c.vocab;
     dp.K = E;
     dp.row_bytes = 2 * E;
-    dp.x = m.x;
+    dp.x = xc;
     dp.norm_w = PF(m, TRX_ROLE_OUT_NORM, 0);
     dp.eps = c.rms_eps;
     dp.y = m.logits;
@@ -504,10 +623,11 @@ static int run_step(Model& m, hipStream_t s) {
     dp.gate_from = m.head_from();
     if ((rc = launch_dense_gemv(dp, s))) return rc;
   } else {
-    if ((rc = projection(m, OP_HEAD, 0, P(m, head_role, 0), head_kind, c.vocab, E, m.x,
+    if ((rc = projection(m, OP_HEAD, 0, P(m, head_role, 0), head_kind, c.vocab, E, xc,
                           PF(m, TRX_ROLE_OUT_NORM, 0), m.logits, TRX_EPI_STORE, nullptr, s, m.slot, m.pos(),
                           m.head_from()))) return rc;
   }
+  m.hidden = xc;
   return TRX_OK;
 }
 
@@ -583,6 +703,8 @@ TRX_API int trx_model_create(const trx_model_config* cfg, const float* rope_freq
   }
   const int qrows = c.n_head * hd * (c.attn_gated ? 2 : 1);
   if ((rc = dalloc(m, (void**)&m.x, (size_t)c.n_embd * 4))) return fail(rc);
+  if ((rc = dalloc(m, (void**)&m.x2, (size_t)c.n_embd * 4))) return fail(rc);
+  m.hidden = m.x;
   if ((rc = dalloc(m, (void**)&m.qkv, (size_t)(qrows + 2 * c.n_kv_head * hd) * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.attn_out, (size_t)c.n_head * hd * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.act, (size_t)c.ffn_dim * 4))) return fail(rc);
@@ -794,7 +916,7 @@ TRX_API int trx_model_read(trx_model* h, int what, void* host, size_t bytes) {
   size_t n = 0;
   switch (what) {
     case TRX_READ_LOGITS: src = m.logits; n = (size_t)c.vocab * 4; break;
-    case TRX_READ_HIDDEN: src = m.x; n = (size_t)c.n_embd * 4; break;
+    case TRX_READ_HIDDEN: src = m.hidden; n = (size_t)c.n_embd * 4; break;
     case TRX_READ_POSITION: src = m.pos(); n = 4; break;
     case TRX_READ_TOKEN: src = m.cur_tok(); n = 4; break;
     case TRX_READ_OUT: src = m.out(); n = (size_t)c.max_new * 4; break;

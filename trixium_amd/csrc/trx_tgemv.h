@@ -43,7 +43,8 @@ struct PackGeom {
   size_t scale_off = 0;       // byte offset of the scales
   size_t bytes = 0;           // packed matrix
   size_t cnt_bytes = 0;       // workspace: tile counters (zero between calls)
-  size_t work_bytes = 0;      // workspace: counters + S x rows_p partial sums
+  size_t ss_bytes = 0;        // workspace: the blocks' slice sums of x^2 (RMSNorm)
+  size_t work_bytes = 0;      // workspace: counters + slice sums + S x rows_p partial sums
 };
 
 // Geometry of a packed matrix; TRX_E_INVALID for an unsupported kind or shape.
@@ -77,19 +78,31 @@ struct AttnMergeSrc {
 
 // Split-K partial sums handed to the next GEMV instead of reduced in this one. A GEMV given
 // `out` stores only its partial sums, part[s * rows_p + r] for slice s and packed row r (every
-// slice's partials, already scaled; pack_geom gives S and rows_p), and skips the tile counting
-// and reduction. A GEMV given `in` takes x from such partials of a SwiGLU-packed gate|up matrix:
-// x[f] = silu(g[f]) * u[f] with g and u the sums over the S slices (f < F); blocks of the first
-// tile column also store x to `act`.
+// slice's partials; pack_geom gives S and rows_p), and skips the tile counting and reduction.
+// With an RMSNorm its sums are of W (x * norm_w) (not yet scaled by 1/rms(x)) and each block
+// stores its slice's sum of x^2 to out_ss[j * S + s]; the consumer applies the scale.
+// A GEMV given `in` takes x from such partials:
+//   F > 0 (a SwiGLU-packed gate|up producer): x[f] = silu(r g[f]) * (r u[f]), f < F = K, with
+//     g and u the sums over the S slices and r = 1/sqrt(sum(in_ss[0..S)) / in_K + eps) (1 when
+//     in_ss is null);
+//   F = 0: x = resid + the sums over the S slices (rows of the producer = columns here).
+// Blocks of the first tile column store that x to `act` (may be null).
 struct PartialSums {
   float* out;              // producer: [S][rows_p]
-  const float* in;         // consumer: the producer's buffer
-  int S, rows_p, F;        // consumer: the producer's geometry and F = its M / 2
+  float* out_ss;           // producer with an RMSNorm: [bps][S]
+  const float* in;         // consumer: the producer's partial sums
+  const float* in_ss;      // consumer, SwiGLU input: the producer's out_ss (may be null)
+  const float* resid;      // consumer, residual input
+  int S, rows_p;           // consumer: the producer's geometry
+  int F;                   // consumer: the producer's M / 2 (SwiGLU input) or 0 (residual input)
+  int in_K;                // consumer with in_ss: the producer's K
   float* act;              // consumer: x stored here (may be null)
 };
 
-// The most producer slices (K / 256, rounded up) a partial-sum consumer takes.
+// The most producer slices (K / 256, rounded up) a partial-sum consumer takes (SwiGLU input).
 int tgemv_partial_slices_max();
+// The same for a residual input.
+int tgemv_resid_slices_max();
 
 int tgemv_f32(const uint8_t* packed, int kind, int M, int K, const float* x, const float* norm_w,
               float eps, float* y, int epi, const float* resid, unsigned long long* amax_slot,

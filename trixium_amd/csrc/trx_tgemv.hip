@@ -71,6 +71,7 @@ constexpr int kMaxTilesPerBlock = 64;   // also bounds the tiles of a reduction 
 // time, and atomics to one line are serialised.
 constexpr int kCntStride = 32;
 constexpr int kMaxTiles = 4096;          // row tiles of a matrix (4096 x kTileRows rows)
+constexpr int kMaxSliceSums = 4096;      // blocks of a launch (one slice sum of x^2 each)
 
 static int cu_count() {
   static int cus = 0;
@@ -119,7 +120,9 @@ int pack_geom(PackGeom& g, int kind, int M, int K) {
   // share a workspace (a matrix's partial sums never cover another's counters).
   TRX_CHECK(g.n_tiles <= kMaxTiles, TRX_E_INVALID, "packed GEMV: %d row tiles (at most %d)", g.n_tiles, kMaxTiles);
   g.cnt_bytes = (size_t)kMaxTiles * kCntStride * 4;
-  g.work_bytes = g.cnt_bytes + (size_t)g.S * g.rows_p * 4;
+  TRX_CHECK(g.bps * g.S <= kMaxSliceSums, TRX_E_INVALID, "packed GEMV: %d blocks (at most %d)", g.bps * g.S, kMaxSliceSums);
+  g.ss_bytes = (size_t)kMaxSliceSums * 4;
+  g.work_bytes = g.cnt_bytes + g.ss_bytes + (size_t)g.S * g.rows_p * 4;
   TRX_CHECK(g.bytes < (1ull << 32), TRX_E_INVALID, "packed GEMV: %zu bytes exceed 4 GiB", g.bytes);
   return TRX_OK;
 }
@@ -223,10 +226,15 @@ int pack_ternary(const uint8_t* rows, int kind, int M, int K, int swiglu, uint8_
 constexpr int kDppRowRor8 = 0x128;
 constexpr int kDppQuadUp2 = 0xEE;      // quad_perm [2,3,2,3]: lanes 0,1 of a quad read lanes 2,3
 constexpr int kCpolSc1 = 16;          // buffer cache policy: device (agent) scope
-constexpr int kMaxNormVec = 6;         // float4 loads per thread of a normalised x: K <= 12288
 constexpr int kMergeMax = 32;          // attention splits the merging prologue takes
 constexpr int kSwiPartMax = 32;        // gate|up slices the SwiGLU prologue takes
 constexpr int kSwiPerThread = kSwiPartMax / (kTgThreads / (2 * kSliceCols));
+constexpr int kResPartMax = 64;        // producer slices the residual prologue takes
+constexpr int kResPerThread = kResPartMax / (kTgThreads / kSliceCols);
+static_assert(kSwiPerThread <= kMergeMax && kResPerThread <= kMergeMax, "prologue registers");
+// Where x comes from: p.x, the attention splits, SwiGLU of gate|up partial sums, or a residual
+// plus a producer's partial sums.
+constexpr int kXPlain = 0, kXMerge = 1, kXSwiglu = 2, kXResid = 3;
 
 struct TgParams {
   const uint8_t* codes;
@@ -240,6 +248,7 @@ struct TgParams {
   const float* resid;
   int epi, n_out;
   float* part;
+  float* ss_out;           // RMSNorm: each block's slice sum of x^2, [bps][S]
   int* cnt;
   unsigned long long* amax_slot;
   const int* gate_pos;
@@ -265,17 +274,20 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   __shared__ float amw[kSliceCols / 64][kMergeMax], atot[kSliceCols / 64];
   __shared__ int n_todo;
 
-  if (p.gate_pos && *p.gate_pos < *p.gate_from) return;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int s = blockIdx.x % p.S, j = blockIdx.x / p.S;
+  const int xmode = p.merge.o ? kXMerge : p.parts.in ? (p.parts.F ? kXSwiglu : kXResid) : kXPlain;
+  // A gated-off launch does nothing, but for storing the residual it was handed in partials.
+  const bool gated_off = p.gate_pos && *p.gate_pos < *p.gate_from;
+  if (gated_off && !(xmode == kXResid && j == 0 && p.parts.act)) return;
 
-  // 1. x: the slice's 256 values, and the whole vector's sum of squares for the RMSNorm. These
-  //    loads are issued before the weight stream, which would otherwise delay them.
+  // 1. The slice's 256 x values, or what they are made of. These loads are issued before the
+  //    weight stream: vmcnt completes in order, so a wait for them would also wait for weights.
   const int cs = s * kSliceCols + tid;
-  float xv = 0.f, wv = 1.f;
+  float xv = 0.f, wv = 1.f, ssin = 0.f;
   float ov[kMergeMax];
   int ns = 0, h0 = 0, nh = 0;
-  if (p.merge.o) {
+  if (xmode == kXMerge) {
     // The slice's attention output from the split partials: every split's o value of this
     // thread's column in flight, then (m, l) of the slice's heads.
     const AttnMergeSrc& a = p.merge;
@@ -304,9 +316,10 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
       if (lane < kMergeMax) amw[w][lane] = wv;
       if (lane == 0) atot[w] = L;
     }
-  } else if (p.parts.in) {
+  } else if (xmode == kXSwiglu) {
     // The gate|up partial sums of this slice's 2 x 256 packed rows: thread t sums row t % 512
-    // over every other slice, starting at slice t / 512.
+    // over every other slice, starting at slice t / 512; and the gate|up input's slice sums of
+    // squares (its RMSNorm scale multiplies g and u).
     const __amdgpu_buffer_rsrc_t rin = make_rsrc(p.parts.in, (uint32_t)((size_t)p.parts.S * p.parts.rows_p * 4));
     const uint32_t off = (uint32_t)(2 * kSliceCols * s + (tid & (2 * kSliceCols - 1))) * 4u;
     const int h = tid / (2 * kSliceCols);
@@ -314,20 +327,24 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
     for (int k = 0; k < kSwiPerThread; ++k)
       ov[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                             rin, off + (uint32_t)min(h + 2 * k, p.parts.S - 1) * (uint32_t)p.parts.rows_p * 4u, 0, 0));
+    if (p.parts.in_ss && tid < p.parts.S) ssin = p.parts.in_ss[tid];
+  } else if (xmode == kXResid) {
+    // x = resid + the producer's partial sums of this slice's 256 rows: thread t sums column
+    // t % 256 over every fourth slice, starting at slice t / 256.
+    const __amdgpu_buffer_rsrc_t rin = make_rsrc(p.parts.in, (uint32_t)((size_t)p.parts.S * p.parts.rows_p * 4));
+    const uint32_t off = (uint32_t)(kSliceCols * s + (tid & (kSliceCols - 1))) * 4u;
+    const int h = tid / kSliceCols;
+#pragma unroll
+    for (int k = 0; k < kResPerThread; ++k)
+      ov[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                            rin, off + (uint32_t)min(h + 4 * k, p.parts.S - 1) * (uint32_t)p.parts.rows_p * 4u, 0, 0));
+    if (tid < kSliceCols && cs < p.K) {
+      xv = p.parts.resid[cs];
+      if (p.norm_w) wv = p.norm_w[cs];
+    }
   } else if (tid < kSliceCols && cs < p.K) {
     xv = p.x[cs];
     if (p.norm_w) wv = p.norm_w[cs];
-  }
-  float ss = 0.f;
-  if (p.norm_w) {
-    float4 xa[kMaxNormVec];                        // every load in flight before the first use
-#pragma unroll
-    for (int r = 0; r < kMaxNormVec; ++r) {
-      const int c = (r * kTgThreads + tid) * 4;
-      xa[r] = c < p.K ? *(const float4*)(p.x + c) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-#pragma unroll
-    for (int r = 0; r < kMaxNormVec; ++r) ss += xa[r].x * xa[r].x + xa[r].y * xa[r].y + xa[r].z * xa[r].z + xa[r].w * xa[r].w;
   }
 
   // 2. The first NB - 1 items of this lane (they do not depend on x).
@@ -364,8 +381,8 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
 #pragma unroll
   for (int b = 0; b < NB - 1; ++b) load_item(buf[b], b);
 
-  // 3. The slice's x (times the RMSNorm gain; 1/rms(x) scales the partial sums), then the table.
-  if (p.merge.o) {
+  // 3. The slice's x (times the RMSNorm gain; 1/rms(x) scales the sums), then the table.
+  if (xmode == kXMerge) {
     __syncthreads();
     if (tid < kSliceCols && cs < p.K) {
       const int hl = tid / p.merge.hd, h = h0 + hl;
@@ -377,8 +394,7 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
       xv = o;
       if (j == 0) p.merge.out[cs] = o;
     }
-  }
-  if (p.parts.in) {
+  } else if (xmode == kXSwiglu) {
     // Sums of the two slice halves (slice order within each) through the table's memory, then
     // gate row r pairs with up row r + 2 of its quad: x[f] = silu(g) * u.
     const int h = tid / (2 * kSliceCols);
@@ -386,8 +402,13 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
 #pragma unroll
     for (int k = 0; k < kSwiPerThread; ++k) v += h + 2 * k < p.parts.S ? ov[k] : 0.f;
     tab[tid] = v;
+    if (w == 0) {
+      const float t = wave_sum_dpp(ssin);
+      if (lane == 0) red[0] = t;
+    }
     __syncthreads();
-    const float g = tid < 2 * kSliceCols ? tab[tid] + tab[tid + 2 * kSliceCols] : 0.f;
+    const float r = p.parts.in_ss ? 1.0f / sqrtf(red[0] / (float)p.parts.in_K + p.eps) : 1.f;
+    const float g = tid < 2 * kSliceCols ? r * (tab[tid] + tab[tid + 2 * kSliceCols]) : 0.f;
     const float u = dpp_f<kDppQuadUp2>(g);
     const int fl = 2 * (tid >> 2) + (tid & 3), f = s * kSliceCols + fl;
     if (tid < 2 * kSliceCols && (tid & 3) < 2) {
@@ -395,10 +416,30 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
       xs[fl] = xf;
       if (j == 0 && p.parts.act && f < p.K) p.parts.act[f] = xf;
     }
-  } else if (tid < kSliceCols) {
-    xs[tid] = p.norm_w ? xv * wv : xv;
+  } else if (xmode == kXResid) {
+    const int h = tid / kSliceCols;
+    float v = 0.f;
+#pragma unroll
+    for (int k = 0; k < kResPerThread; ++k) v += h + 4 * k < p.parts.S ? ov[k] : 0.f;
+    tab[tid] = v;
+    __syncthreads();
+    if (tid < kSliceCols && cs < p.K) {
+      xv += (tab[tid] + tab[tid + kSliceCols]) + (tab[tid + 2 * kSliceCols] + tab[tid + 3 * kSliceCols]);
+      if (j == 0 && p.parts.act) p.parts.act[cs] = xv;
+    }
+    if (gated_off) return;
+    __syncthreads();                                // the table's memory is rewritten below
+  }
+  if (xmode != kXSwiglu && tid < kSliceCols) xs[tid] = p.norm_w ? xv * wv : xv;
+  // The slice's sum of x^2 (x before the gain), for whoever applies the RMSNorm scale.
+  if (p.norm_w && w < kSliceCols / 64) {
+    const float q = wave_sum_dpp(xv * xv);
+    if (lane == 0) red[w] = q;
   }
   __syncthreads();
+  if (p.norm_w && tid == 0)
+    __hip_atomic_store(p.ss_out + j * p.S + s, (red[0] + red[1]) + (red[2] + red[3]), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
   {
     // T[b][c] = hi(b) + lo(b): lo from the low digits (trit5: b % 9; 2-bit: b & 15), hi from the
     // rest (b / 9; b >> 4). A thread owns one column: its x values and its lo sums in registers,
@@ -434,19 +475,7 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
         if (h * NLO + e < 256) col[e * kTabCols] = lo[e] + hv;
     }
   }
-  // The block's sum of x^2 (its loads landed during the table build).
-  if (p.norm_w) {
-    ss = wave_sum_dpp(ss);
-    if (lane == 0) red[w] = ss;
-  }
   __syncthreads();
-  float rinv = 1.f;
-  if (p.norm_w) {
-    float t = 0.f;
-#pragma unroll
-    for (int i = 0; i < kTgThreads / 64; ++i) t += red[i];
-    rinv = 1.0f / sqrtf(t / (float)p.K + p.eps);
-  }
 
   // 4. The items: four rows x one dword per lane; sixteen lanes per row group.
   uint32_t lw[4], sel[4];
@@ -477,7 +506,7 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
     a[1] += dpp_f<kDppRowHalfMirror>(a[3]);
     a[0] += dpp_f<kDppQuadXor2>(a[1]);
     a[0] += dpp_f<kDppQuadXor1>(a[0]);
-    float v = a[0] * (__half2float(__ushort_as_half((unsigned short)(it.sc >> sshift))) * rinv);
+    float v = a[0] * __half2float(__ushort_as_half((unsigned short)(it.sc >> sshift)));
     v += dpp_f<kDppRowRor8>(v);                      // the other group (lane l16 ^ 8)
     // Agent-scope store (sc1): the tile's reducing block may run on another XCD.
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), rpart, po0, n * (int)pstep, kCpolSc1);
@@ -527,6 +556,14 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   // are summed in slice order (the same order whichever block reduces). Consecutive threads hold
   // consecutive rows, so a SwiGLU gate row finds its up row two lanes on (quad_perm).
   const int nt = n_todo;
+  // The RMSNorm scale from the slice sums the tile's S blocks stored (each wave reads them).
+  float rr = 1.f;
+  if (p.norm_w && nt > 0) {
+    float t = 0.f;
+    for (int i = lane; i < p.S; i += 64)
+      t += __hip_atomic_load(p.ss_out + j * p.S + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    rr = 1.0f / sqrtf(wave_sum_dpp(t) / (float)p.K + p.eps);
+  }
   constexpr int kRedRows = 2, kRedChunk = 16;
   constexpr int kTilesPerPass = kTgThreads * kRedRows / kTileRows;
   static_assert(kTilesPerPass <= kMaxTilesPerBlock, "reduction pass");
@@ -565,6 +602,8 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
     };
     if (live[0] && live[1]) chunks(std::integral_constant<int, 2>{});
     else if (live[0]) chunks(std::integral_constant<int, 1>{});
+#pragma unroll
+    for (int r = 0; r < kRedRows; ++r) yv[r] *= rr;
     unsigned long long key = 0;
 #pragma unroll
     for (int r = 0; r < kRedRows; ++r) {
@@ -595,6 +634,7 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
 }
 
 int tgemv_partial_slices_max() { return kSwiPartMax; }
+int tgemv_resid_slices_max() { return kResPartMax; }
 
 template <bool T5>
 static const void* tg_fn() {
@@ -609,26 +649,22 @@ int tgemv_f32(const uint8_t* packed, int kind, int M, int K, const float* x, con
   int rc = pack_geom(g, kind, M, K);
   if (rc) return rc;
   const bool p_in = parts && parts->in, p_out = parts && parts->out;
+  const bool p_swi = p_in && parts->F > 0;
   TRX_CHECK(packed && (x || merge || p_in) && (y || p_out) && work, TRX_E_INVALID, "packed GEMV: null argument");
-  TRX_CHECK(!p_in || (!x && !merge && !norm_w && parts->S >= 1 && parts->S <= kSwiPartMax && parts->F == K &&
-                      parts->rows_p >= 2 * kSliceCols * cdiv(K, kSliceCols)),
-            TRX_E_INVALID, "packed GEMV: unsupported partial-sum input (S %d, F %d, K %d)",
-            p_in ? parts->S : 0, p_in ? parts->F : 0, K);
-  TRX_CHECK(!p_out || (!amax_slot && !merge && !p_in), TRX_E_INVALID,
-            "packed GEMV: partial-sum output with an argmax or another source");
-  TRX_CHECK(!merge || (merge->o && merge->m && merge->l && merge->pos && merge->out && !norm_w &&
-                       (merge->hd == 64 || merge->hd == 128 || merge->hd == 256) &&
-                       merge->n_split >= 1 && merge->n_split <= kMergeMax && K % merge->hd == 0 &&
-                       (!merge->gated || merge->qkv)),
-            TRX_E_INVALID, "packed GEMV: unsupported attention merge (hd %d, %d splits)",
-            merge ? merge->hd : 0, merge ? merge->n_split : 0);
+  TRX_CHECK(!p_in || (!x && !merge && parts->S >= 1 && parts->S <= (p_swi ? kSwiPartMax : kResPartMax) &&
+                      parts->rows_p >= (p_swi ? 2 : 1) * kSliceCols * cdiv(K, kSliceCols)),
+            TRX_E_INVALID, "packed GEMV: unsupported partial-sum input (S %d, rows %d, K %d)",
+            p_in ? parts->S : 0, p_in ? parts->rows_p : 0, K);
+  TRX_CHECK(!p_swi || (parts->F == K && !norm_w && (!parts->in_ss || parts->in_K > 0)), TRX_E_INVALID,
+            "packed GEMV: SwiGLU partial-sum input needs F = K, no RMSNorm of its own and in_K");
+  TRX_CHECK(!p_in || p_swi || parts->resid, TRX_E_INVALID, "packed GEMV: residual partial-sum input without resid");
+  TRX_CHECK(!p_out || (!amax_slot && (!norm_w || parts->out_ss)), TRX_E_INVALID,
+            "packed GEMV: partial-sum output with an argmax, or with an RMSNorm but no out_ss");
   TRX_CHECK(((uintptr_t)x & 15) == 0, TRX_E_INVALID, "packed GEMV: x must be 16-byte aligned");
-  TRX_CHECK(!norm_w || x, TRX_E_INVALID, "packed GEMV: the RMSNorm prologue needs x");
+  TRX_CHECK(!norm_w || x || (p_in && !p_swi), TRX_E_INVALID, "packed GEMV: the RMSNorm prologue needs x");
   TRX_CHECK(epi != TRX_EPI_RESID || resid, TRX_E_INVALID, "packed GEMV: residual epilogue without a residual");
   TRX_CHECK(epi != TRX_EPI_SWIGLU || M % 4 == 0, TRX_E_INVALID, "packed GEMV: SwiGLU needs M = 2F, F even");
   TRX_CHECK(epi != TRX_EPI_SWIGLU || !amax_slot, TRX_E_INVALID, "packed GEMV: no argmax with SwiGLU");
-  TRX_CHECK(!norm_w || K <= kMaxNormVec * kTgThreads * 4, TRX_E_INVALID,
-            "packed GEMV: the RMSNorm prologue takes K <= %d (K=%d)", kMaxNormVec * kTgThreads * 4, K);
   TgParams p;
   p.codes = packed;
   p.scales = packed + g.scale_off;
@@ -652,7 +688,8 @@ int tgemv_f32(const uint8_t* packed, int kind, int M, int K, const float* x, con
   p.epi = epi;
   p.n_out = epi == TRX_EPI_SWIGLU ? M / 2 : M;
   p.cnt = (int*)work;
-  p.part = p_out ? parts->out : (float*)((uint8_t*)work + g.cnt_bytes);
+  p.part = p_out ? parts->out : (float*)((uint8_t*)work + g.cnt_bytes + g.ss_bytes);
+  p.ss_out = p_out ? parts->out_ss : (float*)((uint8_t*)work + g.cnt_bytes);
   p.amax_slot = amax_slot;
   p.gate_pos = gate_pos;
   p.gate_from = gate_from;
