@@ -238,3 +238,38 @@ def test_packed_path_at_full_width():
     ta, tb = a.generate_fresh(prompt, 16), b.generate_fresh(prompt, 16)
     n = next((i for i, (x, y) in enumerate(zip(ta, tb)) if x != y), len(ta))
     assert n >= 8, (ta, tb)
+
+
+@pytest.fixture(scope="module")
+def h_geometry_image(tmp_path_factory):
+    """The two-layer 27B-hybrid-geometry model of tests/golden/make_golden_h.py, written by this
+    repository's writer (its sha256 is the reference writer's, checked below)."""
+    import hashlib
+    import os
+    fx = dict(np.load(os.path.join(os.path.dirname(__file__), "golden", "golden_h_geometry.npz")))
+    cfg = C.QWEN35_27B.replace(name="qwen3.5-27b-geometry-2l", n_layer=2, layer_types=("deltanet", "attn"),
+                               vocab=512, max_ctx=64)
+    p = str(tmp_path_factory.mktemp("h") / "h.img")
+    print("writing the 27B-geometry image", flush=True)
+    bons.write_image(cfg, synth.small_model_tensors(cfg, 7, True), 1, p, trit5=True)
+    sha = hashlib.sha256(open(p, "rb").read()).hexdigest()
+    assert sha == bytes(fx["image_sha256"]).decode()
+    return p, fx
+
+
+@pytest.mark.parametrize("packed", [-1, 0])
+def test_hybrid_27b_geometry_matches_fixture(h_geometry_image, packed):
+    """A Gated DeltaNet layer and a gated attention layer at the 27B hybrid's geometry (width
+    5120, 24 q / 4 kv heads of 256 with 64 RoPE dims, 48 v / 16 k DeltaNet heads of 128, FFN
+    17408): logits at the last prompt position and every generated one within 2e-3 of the
+    reference's fastref logits, and its greedy tokens, with the library's kernel choice (-1) and
+    with every projection on the row-packet kernel (0)."""
+    from trixium_amd.model import Decoder
+    p, fx = h_geometry_image
+    prompt, tokens = [int(t) for t in fx["prompt"]], [int(t) for t in fx["tokens"]]
+    dec = Decoder.from_image(p, max_new=8, packed_ops=packed)
+    lg = _teacher_forced_logits(dec, prompt + tokens, len(prompt))
+    errs = [_rel_err(g, w) for g, w in zip(lg, fx["logits"])]
+    print("27B geometry, packed", dec.packed_ops, "rel errs", errs)
+    assert max(errs) <= 2e-3
+    assert dec.generate_fresh(prompt, len(tokens)) == tokens
