@@ -76,25 +76,38 @@ def copy_calibration(nbytes):
 
 
 def time_dominant_kernel(dec, mc, reps):
-    """Average duration of the gate|up GEMV over the resident layer matrices (HIP events on
-    the model stream)."""
+    """Average duration of the gate|up GEMV over the resident layer matrices (HIP events on the
+    model stream), launched as the decode launches it: with the packed gate|up and down, the
+    partial sums and slice sums of x^2 that down's prologue reduces."""
     import ctypes
     from trixium_amd import _lib, layout as L
+    from trixium_amd.model import PACK_GATE_UP, PACK_DOWN
     E, F = mc.n_embd, mc.ffn_dim
     x = _lib.DeviceBuffer.from_array(np.random.default_rng(1).standard_normal(E).astype(np.float32))
     y = _lib.DeviceBuffer(F * 4)
-    from trixium_amd.model import PACK_GATE_UP
     s = dec.stream
     kind = dec.cfg.weight_kind
     norms = [dec.tensor_ptr(L.ROLE_FFN_NORM, l)[0] for l in range(mc.n_layer)]
-    packed = bool(dec.packed_ops & PACK_GATE_UP)
-    if packed:
+    mode = "row-packet"
+    if dec.packed_ops & PACK_GATE_UP:
         mats = [dec.packed_ptr(PACK_GATE_UP, l) for l in range(mc.n_layer)]
+        mode = "packed partials" if dec.packed_ops & PACK_DOWN else "packed"
+        if mode == "packed partials":
+            S, rp, bps = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+            _lib.call("trx_pack_partials_geometry", kind, 2 * F, E, ctypes.byref(S), ctypes.byref(rp), ctypes.byref(bps))
+            part = _lib.DeviceBuffer(4 * S.value * rp.value)
+            ss = _lib.DeviceBuffer(4 * S.value * bps.value)
+            parts = _lib.PartialSums(out=part.ptr, out_ss=ss.ptr)
 
-        def launch():
-            for (w, ws), g in zip(mats, norms):
-                _lib.call("trx_gemv_packed_f32", w, kind, 2 * F, E, x.ptr, g, ctypes.c_float(mc.rms_eps),
-                          y.ptr, _lib.EPI_SWIGLU, None, ws, s)
+            def launch():
+                for (w, ws), g in zip(mats, norms):
+                    _lib.call("trx_gemv_packed_parts_f32", w, kind, 2 * F, E, x.ptr, g, ctypes.c_float(mc.rms_eps),
+                              None, _lib.EPI_SWIGLU, None, ws, ctypes.byref(parts), s)
+        else:
+            def launch():
+                for (w, ws), g in zip(mats, norms):
+                    _lib.call("trx_gemv_packed_f32", w, kind, 2 * F, E, x.ptr, g, ctypes.c_float(mc.rms_eps),
+                              y.ptr, _lib.EPI_SWIGLU, None, ws, s)
     else:
         mats = [dec.tensor_ptr(L.ROLE_FFN_GATE, l)[0] for l in range(mc.n_layer)]
 
@@ -120,15 +133,15 @@ def time_dominant_kernel(dec, mc, reps):
     n = reps * len(mats)
     rb = L.row_bytes(E, kind)
     algo = 2 * F * rb + E * 4 + E * 4 + F * 4
-    return ms.value * 1e3 / n, algo, n, packed
+    return ms.value * 1e3 / n, algo, n, mode
 
 
-def traffic_from_profile(kind, packed):
+def traffic_from_profile(kind, mode):
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3 counter summary
     (FETCH_SIZE + WRITE_SIZE, calibrated on a copy kernel), when one exists for this format and
     kernel."""
-    name = f"gemv_gateup_8b_{kind}_packed_pmc.md" if packed else f"gemv_gateup_8b_{kind}_pmc.md"
-    path = os.path.join(ROOT, "profiles", name)
+    tag = {"row-packet": "", "packed": "_packed", "packed partials": "_packed_partials"}[mode]
+    path = os.path.join(ROOT, "profiles", f"gemv_gateup_8b_{kind}{tag}_pmc.md")
     if not os.path.exists(path):
         return None
     with open(path) as f:
@@ -214,8 +227,16 @@ def main():
     tok_bytes = wbytes - emb_rows + emb_row + kv
     roof_tok_s = HBM_PEAK_GBS * 1e9 / tok_bytes
 
-    us, algo, n_launch, gu_packed = time_dominant_kernel(dec, mc, a.kernel_reps)
+    us, algo, n_launch, gu_mode = time_dominant_kernel(dec, mc, a.kernel_reps)
     achieved = algo / (us * 1e-6) / 1e9
+    from trixium_amd.model import PACK_QKV, PACK_O, PACK_GATE_UP, PACK_DOWN
+    layer_ops = PACK_QKV | PACK_O | PACK_GATE_UP | PACK_DOWN
+    acts = ("fp32 activations" if dec.packed_ops & layer_ops == layer_ops
+            else "fp32 activations (packed GEMV) / int16 per 128-group (row-packet GEMV)")
+    kdesc = {"packed partials": "RMSNorm fused (its scale applied by the consumer), split-K partial sums "
+                                "handed to down's prologue (SwiGLU there), packed table-lookup kernel",
+             "packed": "RMSNorm + SwiGLU fused, packed table-lookup kernel",
+             "row-packet": "RMSNorm + SwiGLU fused, row-packet kernel"}[gu_mode]
     rec = {
         "metric": "batch-1 decode tok/s (8B shape); ternary matvec HBM GB/s vs ~8 TB/s peak",
         "value": round(tok_s, 2),
@@ -227,7 +248,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "ternary weights (fp16 group scales), int16 activations, fp32 accumulate, fp16 KV",
+        "dtype": f"ternary weights (fp16 group scales), {acts}, fp32 accumulate, fp16 KV",
         "data": "synthetic: random ternary weights from a counter-based hash, random prompt",
         "config": {"workload": "qwen3-8b-shape ternary decoder, batch-1 greedy decode after a "
                                f"{a.prompt}-token prompt",
@@ -238,10 +259,8 @@ def main():
                    "fused_layers": dec.fused_layers, "packed_ops": dec.packed_ops},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic_from_profile(a.kind, gu_packed),
-                     "kernel": f"ternary GEMV gate|up {2 * mc.ffn_dim}x{mc.n_embd} {a.kind}, "
-                               f"RMSNorm + SwiGLU fused, "
-                               f"{'packed table-lookup kernel' if gu_packed else 'row-packet kernel'}",
+                     "traffic": traffic_from_profile(a.kind, gu_mode),
+                     "kernel": f"ternary GEMV gate|up {2 * mc.ffn_dim}x{mc.n_embd} {a.kind}, {kdesc}",
                      "us_per_launch": round(us, 3), "bytes_per_launch": algo, "launches": n_launch},
         "token_roofline": {"bytes_per_token": int(tok_bytes), "tok_s": round(roof_tok_s, 1),
                            "frac": round(tok_s / roof_tok_s, 4)},

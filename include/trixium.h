@@ -107,6 +107,35 @@ int trx_gemv_packed_f32(const uint8_t* packed, int kind, int M, int K, const flo
                         const float* norm_w, float eps, float* y, int epilogue,
                         const float* resid, void* workspace, trx_stream_t s);
 
+/* Split-K partial sums handed from one packed GEMV to the next, as the decoder chains its
+ * projections (no counterpart in the reference: its engine returns whole results; these let a
+ * caller skip the per-GEMV reduction the same way).
+ * trx_pack_partials_geometry: S (slices), rows_p (partial rows per slice) and bps (blocks per
+ *   slice) of a matrix: a producer's partial buffer holds S * rows_p floats, its slice-sum
+ *   buffer bps * S floats.
+ * trx_gemv_packed_parts_f32: trx_gemv_packed_f32 with the partial-sum fields of `parts`
+ *   (null: none). out != null: store the partial sums (part[s * rows_p + r] for slice s, packed
+ *   row r) instead of y and skip the reduction; with norm_w the sums are of W (x * norm_w), not
+ *   yet scaled by 1/rms(x), and each block stores its slice's sum of x^2 to out_ss. in != null:
+ *   x is taken from a producer's partials (x must be null): F > 0 for a SwiGLU-packed gate|up
+ *   producer (x[f] = silu(r g[f]) * (r u[f]), f < F = K, r from in_ss and in_K, or 1 without
+ *   in_ss; no norm_w); F = 0 for a residual (x = resid + the slice sums, S <= 64). act != null:
+ *   that x is also stored there. */
+typedef struct trx_partial_sums {
+  float* out;
+  float* out_ss;
+  const float* in;
+  const float* in_ss;
+  const float* resid;
+  int S, rows_p, F, in_K;
+  float* act;
+} trx_partial_sums;
+int trx_pack_partials_geometry(int kind, int M, int K, int* S, int* rows_p, int* bps);
+int trx_gemv_packed_parts_f32(const uint8_t* packed, int kind, int M, int K, const float* x,
+                              const float* norm_w, float eps, float* y, int epilogue,
+                              const float* resid, void* workspace, const trx_partial_sums* parts,
+                              trx_stream_t s);
+
 /* Decoder ----------------------------------------------------------------------------------------
  * A batch-1 greedy decoder over a BONS model held on the GPU: the GPU counterpart of
  * model/golden.py:FloatModel (reset/forward/generate, golden.py:304-320,436-470) with the

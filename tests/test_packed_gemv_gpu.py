@@ -160,3 +160,59 @@ def test_packed_matrices_share_a_workspace(gpu):
             x = r.normal(0, 1, m.K).astype(np.float32)
             y = m.matvec(x)
             assert np.max(np.abs(y - W @ x) / (np.abs(W) @ np.abs(x))) < TOL, (rep, m.M, m.K)
+
+
+def _silu(v):
+    return v / (1 + np.exp(-v))
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("E,F", [(256, 256), (1024, 768), (2048, 6144), (5120, 4352), (384, 640)])
+def test_partial_sums_gate_up_to_down(gpu, kind, E, F):
+    """gate|up (RMSNorm) stores its partial sums; down takes them: SwiGLU with the RMSNorm scale
+    applied to g and u, then the residual epilogue. y, and the activation down stores, against
+    float64."""
+    print(f"gate|up -> down kind={kind} E={E} F={F}", flush=True)
+    cg, sg = _rand(2 * F, E, E + F)
+    cd, sd = _rand(E, F, F + 3)
+    r = np.random.default_rng(E)
+    x = r.normal(0, 2, E).astype(np.float32)
+    w = r.uniform(0.8, 1.2, E).astype(np.float32)
+    res = r.normal(0, 1, E).astype(np.float32)
+    gu = gpu.PackedMatrix(sg, cg, kind, swiglu=True)
+    dn = gpu.PackedMatrix(sd, cd, kind)
+    src = gu.partials(x, norm_w=w, eps=1e-6)
+    y, h = dn.matvec_from(src, epilogue=EPI_RESID, resid=res)
+    xn = x.astype(np.float64) / np.sqrt(np.mean(x.astype(np.float64) ** 2) + 1e-6) * w
+    Wg = _w64(cg, sg)
+    g, u = Wg[:F] @ xn, Wg[F:] @ xn
+    h64 = _silu(g) * u
+    hmag = (np.abs(Wg[:F]) @ np.abs(xn)) * (np.abs(u) + np.abs(Wg[F:]) @ np.abs(xn))
+    assert np.max(np.abs(h - h64) / (hmag + 1e-30)) < 1e-5
+    Wd = _w64(cd, sd)
+    ref = res + Wd @ h64
+    assert np.max(np.abs(y - ref) / (np.abs(Wd) @ np.abs(h64) + np.abs(res))) < 1e-5
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("E,K", [(256, 256), (2048, 2048), (4096, 6144), (1152, 640)])
+def test_partial_sums_residual_to_normed_gemv(gpu, kind, E, K):
+    """A residual producer (o: E x K) stores its partial sums; the next GEMV (E -> 3E/2 rows, with
+    an RMSNorm) takes x = resid + their sums and stores that x. Both against float64."""
+    print(f"residual -> normed kind={kind} E={E} K={K}", flush=True)
+    co, so = _rand(E, K, E * 3 + K)
+    M2 = 3 * E // 2
+    c2, s2 = _rand(M2, E, E + 11)
+    r = np.random.default_rng(K)
+    xo = r.normal(0, 1, K).astype(np.float32)
+    resid = r.normal(0, 3, E).astype(np.float32)
+    w = r.uniform(0.8, 1.2, E).astype(np.float32)
+    o = gpu.PackedMatrix(so, co, kind)
+    m2 = gpu.PackedMatrix(s2, c2, kind)
+    y, xnew = m2.matvec_from(o.partials(xo), resid_x=resid, norm_w=w, eps=1e-6)
+    Wo = _w64(co, so)
+    x64 = resid.astype(np.float64) + Wo @ xo
+    assert np.max(np.abs(xnew - x64) / (np.abs(Wo) @ np.abs(xo) + np.abs(resid))) < 2e-6
+    xn = x64 / np.sqrt(np.mean(x64 ** 2) + 1e-6) * w
+    W2 = _w64(c2, s2)
+    assert np.max(np.abs(y - W2 @ xn) / (np.abs(W2) @ np.abs(xn))) < 1e-5

@@ -37,6 +37,14 @@ class ModelConfig(ctypes.Structure):
 _mcp = ctypes.POINTER(ModelConfig)
 
 # name -> argtypes (restype is int unless listed in _RESTYPES)
+class PartialSums(ctypes.Structure):
+    """trx_partial_sums (include/trixium.h): split-K partial sums handed between packed GEMVs."""
+    _fields_ = [("out", ctypes.c_void_p), ("out_ss", ctypes.c_void_p), ("in_", ctypes.c_void_p),
+                ("in_ss", ctypes.c_void_p), ("resid", ctypes.c_void_p), ("S", ctypes.c_int),
+                ("rows_p", ctypes.c_int), ("F", ctypes.c_int), ("in_K", ctypes.c_int),
+                ("act", ctypes.c_void_p)]
+
+
 SIGNATURES = {
     "trx_last_error": [],
     "trx_version": [],
@@ -62,6 +70,8 @@ SIGNATURES = {
     "trx_pack_geometry": [_i, _i, _i, ctypes.POINTER(_sz), ctypes.POINTER(_sz)],
     "trx_pack_ternary": [_vp, _i, _i, _i, _i, _vp, _vp],
     "trx_gemv_packed_f32": [_vp, _i, _i, _i, _vp, _vp, _f, _vp, _i, _vp, _vp, _vp],
+    "trx_pack_partials_geometry": [_i, _i, _i, _ip, _ip, _ip],
+    "trx_gemv_packed_parts_f32": [_vp, _i, _i, _i, _vp, _vp, _f, _vp, _i, _vp, _vp, _vp, _vp],
     "trx_gemv_set_variant": [_i],
     "trx_model_create": [_mcp, _fp, ctypes.POINTER(_vp)],
     "trx_model_destroy": [_vp],

@@ -7,11 +7,13 @@ matvec runs on the GPU through libtrixium_hip (trx_gemv_ternary_exact) on row pa
 from the arguments (trit5 by default). `group_sums` exposes the engine's exact per-group sums.
 """
 
+import ctypes
+
 import numpy as np
 
 from . import layout as L
 from .bons import encode_rows
-from ._lib import DeviceBuffer, call, synchronize
+from ._lib import DeviceBuffer, PartialSums, call, synchronize
 
 
 def _packets(scales_f16, codes, kind):
@@ -68,7 +70,6 @@ def matvec_float(scales_f16, codes, x, norm_w=None, eps=1e-6, kind=L.KIND_TERNAR
 
 def pack_geometry(kind, M, K):
     """(packed bytes, workspace bytes) of the packed float GEMV for an M x K matrix."""
-    import ctypes
     pb, wb = ctypes.c_size_t(), ctypes.c_size_t()
     call("trx_pack_geometry", int(kind), int(M), int(K), ctypes.byref(pb), ctypes.byref(wb))
     return pb.value, wb.value
@@ -103,3 +104,45 @@ class PackedMatrix:
              self.work.ptr, None)
         synchronize()
         return yb.download(np.float32, n_out)
+
+    def partials_geometry(self):
+        """(S, rows_p, bps) of trx_pack_partials_geometry."""
+        S, rp, bps = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        call("trx_pack_partials_geometry", self.kind, self.M, self.K, ctypes.byref(S), ctypes.byref(rp), ctypes.byref(bps))
+        return S.value, rp.value, bps.value
+
+    def partials(self, x, norm_w=None, eps=1e-6):
+        """The split-K partial sums only (trx_gemv_packed_parts_f32 with `out`): a dict with the
+        device buffers part ([S][rows_p]) and ss (the slice sums of x^2 with an RMSNorm), S,
+        rows_p and K, for a consumer's matvec_from."""
+        S, rp, bps = self.partials_geometry()
+        xb = DeviceBuffer.from_array(np.asarray(x, dtype=np.float32))
+        nb = DeviceBuffer.from_array(np.asarray(norm_w, dtype=np.float32)) if norm_w is not None else None
+        part, ss = DeviceBuffer(4 * S * rp), DeviceBuffer(4 * bps * S)
+        ps = PartialSums(out=part.ptr, out_ss=ss.ptr if nb else None)
+        call("trx_gemv_packed_parts_f32", self.packed.ptr, self.kind, self.M, self.K, xb.ptr, nb.ptr if nb else None,
+             float(eps), None, 2 if self.swiglu else 0, None, self.work.ptr, ctypes.byref(ps), None)
+        synchronize()
+        return {"part": part, "ss": ss if nb else None, "S": S, "rows_p": rp, "K": self.K, "swiglu": self.swiglu}
+
+    def matvec_from(self, src, resid_x=None, norm_w=None, eps=1e-6, epilogue=0, resid=None):
+        """y = W xhat with x from a producer's partial sums (`src` from partials): SwiGLU of a
+        gate|up producer's sums, or resid_x plus a residual producer's sums. Returns (y, x)."""
+        ps = PartialSums(in_=src["part"].ptr, S=src["S"], rows_p=src["rows_p"])
+        if src["swiglu"]:
+            ps.F = self.K
+            if src["ss"] is not None:
+                ps.in_ss = src["ss"].ptr
+                ps.in_K = src["K"]
+        else:
+            rb = DeviceBuffer.from_array(np.asarray(resid_x, dtype=np.float32))
+            ps.resid = rb.ptr
+        act = DeviceBuffer(4 * self.K)
+        ps.act = act.ptr
+        nb = DeviceBuffer.from_array(np.asarray(norm_w, dtype=np.float32)) if norm_w is not None else None
+        yb = DeviceBuffer.from_array(np.asarray(resid, dtype=np.float32)) if resid is not None else DeviceBuffer(4 * self.M)
+        call("trx_gemv_packed_parts_f32", self.packed.ptr, self.kind, self.M, self.K, None, nb.ptr if nb else None,
+             float(eps), yb.ptr, int(epilogue), yb.ptr if resid is not None else None, self.work.ptr,
+             ctypes.byref(ps), None)
+        synchronize()
+        return yb.download(np.float32, self.M), act.download(np.float32, self.K)

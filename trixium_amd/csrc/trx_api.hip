@@ -184,6 +184,40 @@ TRX_API int trx_pack_ternary(const uint8_t* rows, int kind, int M, int K, int sw
   return pack_ternary(rows, kind, M, K, swiglu, packed, (hipStream_t)s);
 }
 
+TRX_API int trx_pack_partials_geometry(int kind, int M, int K, int* S, int* rows_p, int* bps) {
+  TRX_CHECK(S && rows_p && bps, TRX_E_INVALID, "trx_pack_partials_geometry: null argument");
+  PackGeom g;
+  int rc = pack_geom(g, kind, M, K);
+  if (rc) return rc;
+  *S = g.S;
+  *rows_p = g.rows_p;
+  *bps = g.bps;
+  return TRX_OK;
+}
+
+TRX_API int trx_gemv_packed_parts_f32(const uint8_t* packed, int kind, int M, int K, const float* x,
+                                      const float* norm_w, float eps, float* y, int epilogue,
+                                      const float* resid, void* workspace, const trx_partial_sums* parts,
+                                      trx_stream_t s) {
+  TRX_CHECK(epilogue == TRX_EPI_STORE || epilogue == TRX_EPI_RESID || epilogue == TRX_EPI_SWIGLU,
+            TRX_E_INVALID, "trx_gemv_packed_parts_f32: unknown epilogue %d", epilogue);
+  PartialSums ps = {};
+  if (parts) {
+    ps.out = parts->out;
+    ps.out_ss = parts->out_ss;
+    ps.in = parts->in;
+    ps.in_ss = parts->in_ss;
+    ps.resid = parts->resid;
+    ps.S = parts->S;
+    ps.rows_p = parts->rows_p;
+    ps.F = parts->F;
+    ps.in_K = parts->in_K;
+    ps.act = parts->act;
+  }
+  return tgemv_f32(packed, kind, M, K, x, norm_w, eps, y, epilogue, resid, nullptr, workspace, (hipStream_t)s,
+                   nullptr, nullptr, nullptr, parts ? &ps : nullptr);
+}
+
 TRX_API int trx_gemv_packed_f32(const uint8_t* packed, int kind, int M, int K, const float* x,
                                 const float* norm_w, float eps, float* y, int epilogue,
                                 const float* resid, void* workspace, trx_stream_t s) {

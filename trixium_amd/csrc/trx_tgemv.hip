@@ -652,7 +652,7 @@ int tgemv_f32(const uint8_t* packed, int kind, int M, int K, const float* x, con
   const bool p_swi = p_in && parts->F > 0;
   TRX_CHECK(packed && (x || merge || p_in) && (y || p_out) && work, TRX_E_INVALID, "packed GEMV: null argument");
   TRX_CHECK(!p_in || (!x && !merge && parts->S >= 1 && parts->S <= (p_swi ? kSwiPartMax : kResPartMax) &&
-                      parts->rows_p >= (p_swi ? 2 : 1) * kSliceCols * cdiv(K, kSliceCols)),
+                      parts->rows_p >= (p_swi ? 2 : 1) * K),
             TRX_E_INVALID, "packed GEMV: unsupported partial-sum input (S %d, rows %d, K %d)",
             p_in ? parts->S : 0, p_in ? parts->rows_p : 0, K);
   TRX_CHECK(!p_swi || (parts->F == K && !norm_w && (!parts->in_ss || parts->in_K > 0)), TRX_E_INVALID,
