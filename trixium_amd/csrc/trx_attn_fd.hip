@@ -34,7 +34,9 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
-template <int REP, int HD>
+// ROR8: the RoPE partner lane is li ^ 8 (rope_n = 128), a DPP row_ror:8; otherwise a shuffle. A
+// template parameter, so the choice is not a branch around every element.
+template <int REP, int HD, bool ROR8>
 __global__ __launch_bounds__(kAttnThreads) void attn_fd_kernel(AttnParams p) {
   constexpr int LPP = HD / 8;                         // lanes per position
   constexpr int PPW = 64 / LPP;                       // groups per wave
@@ -50,18 +52,14 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fd_kernel(AttnParams p) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int S = p.n_split;
   const int g = blockIdx.x / S, sp = blockIdx.x - g * S;
-  const int pos = *p.pos, T = pos + 1;
-  const int chunk = (T + S - 1) / S;
-  const int p0 = sp * chunk, p1 = min(T, p0 + chunk), n = max(0, p1 - p0);
   const int li = lane % LPP, grp = wave * PPW + lane / LPP;
   const size_t cache0 = (size_t)g * p.max_ctx * HD;
-  const bool owner = n > 0 && pos >= p0 && pos < p1;
-  const int npass = (n + PPP - 1) / PPP;
   const int qstride = p.gated ? 2 * HD : HD;
   const int half = p.rope_n / 2;
 
-  // 1. The prologue's inputs first (a later wait for them then does not cover the K/V stream):
-  //    the RoPE frequency of this thread, the q heads, the new k and v, the norm gains.
+  // 1. The prologue's inputs first: the RoPE frequency of this thread, the q heads, the new k
+  //    and v, the norm gains. None depends on the position, so they are in flight while the
+  //    position is read, and a later wait for them does not cover the K/V stream.
   const float fr = tid < half ? p.rope_freq[tid] : 0.f;
   float q[REP][8], kn[8], vn[8], qw[8], kw[8];
   const float* kraw = p.qkv + (size_t)p.n_head * qstride + (size_t)g * HD;
@@ -87,19 +85,31 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fd_kernel(AttnParams p) {
     vn[0] = c.x; vn[1] = c.y; vn[2] = c.z; vn[3] = c.w; vn[4] = d.x; vn[5] = d.y; vn[6] = d.z; vn[7] = d.w;
   }
 
+  const int pos = *p.pos, T = pos + 1;
+  const int chunk = (T + S - 1) / S;
+  const int p0 = sp * chunk, p1 = min(T, p0 + chunk), n = max(0, p1 - p0);
+  const bool owner = n > 0 && pos >= p0 && pos < p1;
+  const int npass = (n + PPP - 1) / PPP;
+
   // 2. The split's K and V rows (the new position's come from the projection above).
+  //    Every pass issues its loads: a position outside the split (or the new one) gets an offset
+  //    past the buffer, which the range check turns into zeros without a memory access. With no
+  //    branch around them the compiler's wait for the prologue's inputs counts these loads
+  //    exactly (after a conditional load it would also wait for some of them).
+  constexpr uint32_t kOut = 0x40000000u;
+  const uint32_t head_bytes = (uint32_t)p.max_ctx * HD * 2u;
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.kcache + cache0, head_bytes);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.vcache + cache0, head_bytes);
   uint4 kr[kMaxPass], vr[kMaxPass];
 #pragma unroll
   for (int ps = 0; ps < kMaxPass; ++ps) {
     const int t = ps * PPP + grp;
-    if (ps < npass && t < n && p0 + t != pos) {
-      const size_t off = cache0 + (size_t)(p0 + t) * HD + li * 8;
-      kr[ps] = *(const uint4*)(p.kcache + off);
-      vr[ps] = *(const uint4*)(p.vcache + off);
-    } else {
-      kr[ps] = make_uint4(0, 0, 0, 0);
-      vr[ps] = make_uint4(0, 0, 0, 0);
-    }
+    const bool ok = ps < npass && t < n && p0 + t != pos;
+    const uint32_t off = ok ? ((uint32_t)(p0 + t) * HD + li * 8) * 2u : kOut;
+    const auto a = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0);
+    const auto b = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0);
+    kr[ps] = make_uint4(a[0], a[1], a[2], a[3]);
+    vr[ps] = make_uint4(b[0], b[1], b[2], b[3]);
   }
 
   if (n > 0) {
@@ -116,7 +126,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fd_kernel(AttnParams p) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) ss += v[k] * v[k];
       ss = group_sum<LPP>(ss);
-      const float r = 1.0f / sqrtf(ss / (float)HD + p.eps);
+      const float r = rsqrtf(ss / (float)HD + p.eps);
 #pragma unroll
       for (int k = 0; k < 8; ++k) v[k] = v[k] * r * w[k];
       const int pxor = half >> 3;                       // partner lane of dim d +- half
@@ -125,7 +135,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fd_kernel(AttnParams p) {
       const int ci = lo ? d0 : (rot ? d0 - half : 0);
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        const float other = pxor == 8 ? dpp_f<kDppRowRor8>(v[k]) : __shfl_xor(v[k], pxor, 64);
+        const float other = ROR8 ? dpp_f<kDppRowRor8>(v[k]) : __shfl_xor(v[k], pxor, 64);
         const float c = cs_s[ci + k], sn = sn_s[ci + k];
         const float rv = lo ? v[k] * c - other * sn : other * sn + v[k] * c;
         v[k] = (rot ? rv : v[k]) * post;
@@ -304,10 +314,17 @@ bool attention_fd_supported(int rep, int hd, int rope_n, int n_split) {
 template <int REP>
 static int launch_fd_rep(const AttnParams& p, hipStream_t s) {
   const dim3 grid(p.n_kv * p.n_split), block(kAttnThreads);
+  const bool ror8 = p.rope_n == 128;       // partner lane li ^ (rope_n / 16) = li ^ 8
   switch (p.hd) {
-    case 64: hipLaunchKernelGGL((attn_fd_kernel<REP, 64>), grid, block, 0, s, p); break;
-    case 128: hipLaunchKernelGGL((attn_fd_kernel<REP, 128>), grid, block, 0, s, p); break;
-    case 256: hipLaunchKernelGGL((attn_fd_kernel<REP, 256>), grid, block, 0, s, p); break;
+    case 64: hipLaunchKernelGGL((attn_fd_kernel<REP, 64, false>), grid, block, 0, s, p); break;
+    case 128:
+      if (ror8) hipLaunchKernelGGL((attn_fd_kernel<REP, 128, true>), grid, block, 0, s, p);
+      else hipLaunchKernelGGL((attn_fd_kernel<REP, 128, false>), grid, block, 0, s, p);
+      break;
+    case 256:
+      if (ror8) hipLaunchKernelGGL((attn_fd_kernel<REP, 256, true>), grid, block, 0, s, p);
+      else hipLaunchKernelGGL((attn_fd_kernel<REP, 256, false>), grid, block, 0, s, p);
+      break;
     default: TRX_CHECK(false, TRX_E_INVALID, "attention: head_dim %d unsupported", p.hd);
   }
   TRX_LAUNCHED();
