@@ -57,32 +57,25 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fd_kernel(AttnParams p) {
   const int qstride = p.gated ? 2 * HD : HD;
   const int half = p.rope_n / 2;
 
-  // 1. The prologue's inputs first: the RoPE frequency of this thread, the q heads, the new k
-  //    and v, the norm gains. None depends on the position, so they are in flight while the
-  //    position is read, and a later wait for them does not cover the K/V stream.
+  // 1. The prologue's inputs first: the RoPE frequency of this thread, then, loaded once by the
+  //    block (every position group uses the same values), the q heads, the new k and v and the
+  //    two norm gains. None depends on the position, so they are in flight while the position
+  //    is read, and a later wait for them does not cover the K/V stream.
   const float fr = tid < half ? p.rope_freq[tid] : 0.f;
-  float q[REP][8], kn[8], vn[8], qw[8], kw[8];
   const float* kraw = p.qkv + (size_t)p.n_head * qstride + (size_t)g * HD;
-  {
-    const float4* a = (const float4*)(p.q_norm + li * 8);
-    const float4* b = (const float4*)(p.k_norm + li * 8);
-    const float4 a0 = a[0], a1 = a[1], b0 = b[0], b1 = b[1];
-    qw[0] = a0.x; qw[1] = a0.y; qw[2] = a0.z; qw[3] = a0.w; qw[4] = a1.x; qw[5] = a1.y; qw[6] = a1.z; qw[7] = a1.w;
-    kw[0] = b0.x; kw[1] = b0.y; kw[2] = b0.z; kw[3] = b0.w; kw[4] = b1.x; kw[5] = b1.y; kw[6] = b1.z; kw[7] = b1.w;
-  }
+  constexpr int NST = REP + 4, STV = NST * HD / 4;                 // rows, float4s staged
+  constexpr int SPT = (STV + kAttnThreads - 1) / kAttnThreads;     // float4s per thread
+  __shared__ __align__(16) float stg[NST][HD];
+  float4 sv[SPT];
 #pragma unroll
-  for (int j = 0; j < REP; ++j) {
-    const float4* src = (const float4*)(p.qkv + (size_t)(g * REP + j) * qstride + li * 8);
-    const float4 a = src[0], b = src[1];
-    q[j][0] = a.x; q[j][1] = a.y; q[j][2] = a.z; q[j][3] = a.w;
-    q[j][4] = b.x; q[j][5] = b.y; q[j][6] = b.z; q[j][7] = b.w;
-  }
-  {
-    const float4* ks = (const float4*)(kraw + li * 8);
-    const float4* vs = (const float4*)(kraw + (size_t)p.n_kv * HD + li * 8);
-    const float4 a = ks[0], b = ks[1], c = vs[0], d = vs[1];
-    kn[0] = a.x; kn[1] = a.y; kn[2] = a.z; kn[3] = a.w; kn[4] = b.x; kn[5] = b.y; kn[6] = b.z; kn[7] = b.w;
-    vn[0] = c.x; vn[1] = c.y; vn[2] = c.z; vn[3] = c.w; vn[4] = d.x; vn[5] = d.y; vn[6] = d.z; vn[7] = d.w;
+  for (int k = 0; k < SPT; ++k) {
+    const int e = min(tid + k * kAttnThreads, STV - 1);            // past the end: a repeat
+    const int row = 4 * e / HD, d = 4 * e - row * HD;
+    const float* src = row < REP ? p.qkv + (size_t)(g * REP + row) * qstride + d
+                       : row == REP ? kraw + d
+                       : row == REP + 1 ? kraw + (size_t)p.n_kv * HD + d
+                       : row == REP + 2 ? p.q_norm + d : p.k_norm + d;
+    sv[k] = *(const float4*)src;
   }
 
   const int pos = *p.pos, T = pos + 1;
@@ -112,6 +105,13 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fd_kernel(AttnParams p) {
     vr[ps] = make_uint4(b[0], b[1], b[2], b[3]);
   }
 
+  // The staged inputs into LDS (the loads are waited for here, after the K/V loads went out).
+#pragma unroll
+  for (int k = 0; k < SPT; ++k) {
+    const int e = min(tid + k * kAttnThreads, STV - 1);
+    *(float4*)(&stg[0][0] + 4 * e) = sv[k];
+  }
+  float q[REP][8], kn[8], vn[8], qw[8], kw[8];
   if (n > 0) {
     if (tid < half) {
       float sn, cs;
@@ -120,6 +120,15 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fd_kernel(AttnParams p) {
       sn_s[tid] = sn;
     }
     __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+#pragma unroll
+      for (int j = 0; j < REP; ++j) q[j][k] = stg[j][li * 8 + k];
+      kn[k] = stg[REP][li * 8 + k];
+      vn[k] = stg[REP + 1][li * 8 + k];
+      qw[k] = stg[REP + 2][li * 8 + k];
+      kw[k] = stg[REP + 3][li * 8 + k];
+    }
     // Normalise (gain w), rotate, scale; `post` multiplies the result.
     auto norm_rope = [&](float* v, const float* w, float post) {
       float ss = 0.f;
@@ -224,17 +233,19 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fd_kernel(AttnParams p) {
       for (int k = 0; k < 8; ++k) go[grp][j][li * 8 + k] = acc[j][k];
     }
     __syncthreads();
-    if (tid < REP) {
-      float M = -INFINITY;
-      for (int i = 0; i < NG; ++i) M = fmaxf(M, gm[i][tid]);
-      float L = 0.f;
-      for (int i = 0; i < NG; ++i) {
-        const float w = gl[i][tid] > 0.f ? __expf(gm[i][tid] - M) : 0.f;
-        wgt[tid][i] = w;
-        L += gl[i][tid] * w;
+    // Wave w combines q heads w, w + 4, ...: lane i holds group i's (max, sum) of the head.
+    static_assert(NG <= 64, "one lane per group");
+    for (int j = wave; j < REP; j += kAttnThreads / 64) {
+      const float gmv = lane < NG ? gm[lane][j] : -INFINITY;
+      const float glv = lane < NG ? gl[lane][j] : 0.f;
+      const float M = wave_max(gmv);
+      const float w = glv > 0.f ? __expf(gmv - M) : 0.f;
+      if (lane < NG) wgt[j][lane] = w;
+      const float L = wave_sum(glv * w);
+      if (lane == 0) {
+        st_vec<true>(p.part_m + (size_t)(g * REP + j) * S + sp, M);
+        st_vec<true>(p.part_l + (size_t)(g * REP + j) * S + sp, L);
       }
-      st_vec<true>(p.part_m + (size_t)(g * REP + tid) * S + sp, M);
-      st_vec<true>(p.part_l + (size_t)(g * REP + tid) * S + sp, L);
     }
     __syncthreads();
     for (int i = tid; i < REP * HD; i += kAttnThreads) {
