@@ -81,6 +81,9 @@ struct Model {
   int o_S = 0, o_rows_p = 0;
   float* down_part = nullptr;
   int down_S = 0, down_rows_p = 0;
+  float* head_part = nullptr;                      // LM head: partial sums reduced by many blocks
+  float* head_ss = nullptr;
+  int head_S = 0, head_rows_p = 0;
   float* x2 = nullptr;                             // second residual buffer (x alternates)
   float* hidden = nullptr;                         // the residual after the last layer
   hipGraph_t graph = nullptr;
@@ -227,9 +230,9 @@ static int plan_packed(Model& m) {
   if ((rc = dalloc(m, (void**)&buf, total))) return rc;
   if ((rc = dalloc(m, &m.pack_work, work))) return rc;   // zeroed: the tile counters start at 0
   // Partial-sum buffers of the producers that hand their sums on.
-  auto part_buf = [&](int M, int K, float** buf, int* S, int* rows_p, float** ss) -> int {
+  auto part_buf = [&](int M, int K, float** buf, int* S, int* rows_p, float** ss, int kind) -> int {
     PackGeom g;
-    int rc2 = pack_geom(g, wk, M, K);
+    int rc2 = pack_geom(g, kind, M, K);
     if (rc2) return rc2;
     if ((rc2 = dalloc(m, (void**)buf, (size_t)g.S * g.rows_p * 4))) return rc2;
     if (ss && (rc2 = dalloc(m, (void**)ss, (size_t)g.bps * g.S * 4))) return rc2;
@@ -238,12 +241,16 @@ static int plan_packed(Model& m) {
     return TRX_OK;
   };
   if ((ops & TRX_PACK_GATE_UP) && (ops & TRX_PACK_DOWN) && cdiv(E, kSliceCols) <= tgemv_partial_slices_max())
-    if ((rc = part_buf(2 * F, E, &m.ffn_part, &m.ffn_S, &m.ffn_rows_p, &m.ffn_ss))) return rc;
+    if ((rc = part_buf(2 * F, E, &m.ffn_part, &m.ffn_S, &m.ffn_rows_p, &m.ffn_ss, wk))) return rc;
   if ((ops & TRX_PACK_O) && (ops & TRX_PACK_GATE_UP) && m.n_attn > 0 &&
       cdiv(c.n_head * hd, kSliceCols) <= tgemv_resid_slices_max())
-    if ((rc = part_buf(E, c.n_head * hd, &m.o_part, &m.o_S, &m.o_rows_p, nullptr))) return rc;
+    if ((rc = part_buf(E, c.n_head * hd, &m.o_part, &m.o_S, &m.o_rows_p, nullptr, wk))) return rc;
   if ((ops & TRX_PACK_DOWN) && cdiv(F, kSliceCols) <= tgemv_resid_slices_max())
-    if ((rc = part_buf(E, F, &m.down_part, &m.down_S, &m.down_rows_p, nullptr))) return rc;
+    if ((rc = part_buf(E, F, &m.down_part, &m.down_S, &m.down_rows_p, nullptr, wk))) return rc;
+  for (auto& e : list)
+    if (e.first.first == OP_HEAD &&
+        (rc = part_buf(c.vocab, E, &m.head_part, &m.head_S, &m.head_rows_p, &m.head_ss, e.second.kind)))
+      return rc;
   for (size_t i = 0; i < list.size(); ++i) {
     list[i].second.buf = buf + offs[i];
     m.packed[list[i].first] = list[i].second;
@@ -602,10 +609,18 @@ static int run_step(Model& m, hipStream_t s) {
   const int head_role = c.head_tied ? TRX_ROLE_TOK_EMB : TRX_ROLE_LM_HEAD;
   const int head_kind = c.head_tied ? c.emb_kind : c.head_kind;
   if (const PackedMat* ph = packed(OP_HEAD, 0)) {
+    // The head GEMV stores its partial sums; a second launch spreads their reduction (and the
+    // argmax) over the whole GPU instead of the tile columns' last blocks.
     const float* xin;
     const PartialSums* pp = take(xin);
-    if ((rc = tgemv_f32(ph->buf, head_kind, c.vocab, E, xin, PF(m, TRX_ROLE_OUT_NORM, 0), c.rms_eps, m.logits,
-                        TRX_EPI_STORE, nullptr, m.slot, m.pack_work, s, m.pos(), m.head_from(), nullptr, pp)))
+    PartialSums hp = pp ? *pp : PartialSums{};
+    hp.out = m.head_part;
+    hp.out_ss = m.head_ss;
+    if ((rc = tgemv_f32(ph->buf, head_kind, c.vocab, E, xin, PF(m, TRX_ROLE_OUT_NORM, 0), c.rms_eps, nullptr,
+                        TRX_EPI_STORE, nullptr, nullptr, m.pack_work, s, m.pos(), m.head_from(), nullptr, &hp)))
+      return rc;
+    if ((rc = tgemv_reduce_f32(m.head_part, m.head_ss, m.head_S, m.head_rows_p, c.vocab, E, c.rms_eps, m.logits,
+                               m.slot, s, m.pos(), m.head_from())))
       return rc;
   } else if (head_kind == TRX_KIND_F16) {
     DenseParams dp = {};

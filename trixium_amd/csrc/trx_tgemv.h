@@ -99,6 +99,15 @@ struct PartialSums {
   float* act;              // consumer: x stored here (may be null)
 };
 
+// y[m] = r * sum_s part[s * rows_p + m] for m < M (part and ss from a producer GEMV given
+// PartialSums.out / out_ss; r = 1/sqrt(sum(ss[0..S)) / K + eps), or 1 without ss), with the
+// packed (ordered value, ~row) maximum of y into amax_slot (atomicMax, one per block) when given.
+// Spreads the reduction over the whole GPU: the LM head's rows. gate_pos/gate_from as for
+// tgemv_f32.
+int tgemv_reduce_f32(const float* part, const float* ss, int S, int rows_p, int M, int K, float eps, float* y,
+                     unsigned long long* amax_slot, hipStream_t s, const int* gate_pos = nullptr,
+                     const int* gate_from = nullptr);
+
 // The most producer slices (K / 256, rounded up) a partial-sum consumer takes (SwiGLU input).
 int tgemv_partial_slices_max();
 // The same for a residual input.

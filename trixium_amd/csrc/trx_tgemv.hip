@@ -633,6 +633,104 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   }
 }
 
+// Reduction of partial sums over many blocks ------------------------------------------------
+
+constexpr int kRdThreads = 256, kRdBlocks = 256, kRdRowsMax = 4, kRdChunk = 16;
+
+struct RdParams {
+  const float* part;
+  const float* ss;
+  int S, rows_p, M, K, rpb;   // rpb: rows per block
+  float eps;
+  float* y;
+  unsigned long long* amax_slot;
+  const int* gate_pos;
+  const int* gate_from;
+};
+
+__global__ __launch_bounds__(kRdThreads) void tgemv_reduce_kernel(RdParams p) {
+  __shared__ unsigned long long kmax[kRdThreads / 64];
+  if (p.gate_pos && *p.gate_pos < *p.gate_from) return;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int r0 = blockIdx.x * p.rpb;
+  // Rows r0 + tid + i * 256 (i < kRdRowsMax): every partial of every row in flight per chunk of
+  // slices; a row past the block's range or M re-reads row r0 and is not stored.
+  int row[kRdRowsMax];
+  bool live[kRdRowsMax];
+#pragma unroll
+  for (int i = 0; i < kRdRowsMax; ++i) {
+    const int r = r0 + tid + i * kRdThreads;
+    live[i] = tid + i * kRdThreads < p.rpb && r < p.M;
+    row[i] = live[i] ? r : min(r0, p.M - 1);
+  }
+  float rs = 1.f;
+  if (p.ss) {
+    float t = 0.f;
+    for (int i = lane; i < p.S; i += 64) t += p.ss[i];
+    rs = rsqrtf(wave_sum_dpp(t) / (float)p.K + p.eps);
+  }
+  float acc[kRdRowsMax] = {};
+  for (int q0 = 0; q0 < p.S; q0 += kRdChunk) {
+    float v[kRdRowsMax][kRdChunk];
+#pragma unroll
+    for (int i = 0; i < kRdRowsMax; ++i)
+#pragma unroll
+      for (int k = 0; k < kRdChunk; ++k) v[i][k] = p.part[(size_t)min(q0 + k, p.S - 1) * p.rows_p + row[i]];
+#pragma unroll
+    for (int i = 0; i < kRdRowsMax; ++i)
+#pragma unroll
+      for (int k = 0; k < kRdChunk; ++k) acc[i] += q0 + k < p.S ? v[i][k] : 0.f;
+  }
+  unsigned long long key = 0;
+#pragma unroll
+  for (int i = 0; i < kRdRowsMax; ++i) {
+    if (!live[i]) continue;
+    const float out = acc[i] * rs;
+    p.y[row[i]] = out;
+    const unsigned long long kr =
+        ((unsigned long long)ordered_bits(out) << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)row[i]);
+    key = kr > key ? kr : key;
+  }
+  if (!p.amax_slot) return;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const unsigned long long other = __shfl_xor(key, o, 64);
+    key = other > key ? other : key;
+  }
+  if (lane == 0) kmax[w] = key;
+  __syncthreads();
+  if (tid == 0) {
+    unsigned long long k = kmax[0];
+    for (int i = 1; i < kRdThreads / 64; ++i) k = kmax[i] > k ? kmax[i] : k;
+    if (k) atomicMax(p.amax_slot, k);
+  }
+}
+
+int tgemv_reduce_f32(const float* part, const float* ss, int S, int rows_p, int M, int K, float eps, float* y,
+                     unsigned long long* amax_slot, hipStream_t s, const int* gate_pos, const int* gate_from) {
+  TRX_CHECK(part && y && S >= 1 && M >= 1 && rows_p >= M && K >= 1, TRX_E_INVALID,
+            "partial-sum reduction: bad arguments (S %d, rows %d, M %d)", S, rows_p, M);
+  RdParams p;
+  p.part = part;
+  p.ss = ss;
+  p.S = S;
+  p.rows_p = rows_p;
+  p.M = M;
+  p.K = K;
+  p.eps = eps;
+  p.y = y;
+  p.amax_slot = amax_slot;
+  p.gate_pos = gate_pos;
+  p.gate_from = gate_from;
+  const int blocks = std::min(kRdBlocks, cdiv(M, kRdThreads));
+  p.rpb = cdiv(M, blocks);
+  TRX_CHECK(p.rpb <= kRdRowsMax * kRdThreads, TRX_E_INVALID, "partial-sum reduction: %d rows (at most %d)", M,
+            kRdBlocks * kRdRowsMax * kRdThreads);
+  hipLaunchKernelGGL(tgemv_reduce_kernel, dim3(cdiv(M, p.rpb)), dim3(kRdThreads), 0, s, p);
+  TRX_LAUNCHED();
+  return TRX_OK;
+}
+
 int tgemv_partial_slices_max() { return kSwiPartMax; }
 int tgemv_resid_slices_max() { return kResPartMax; }
 
