@@ -27,6 +27,9 @@ __device__ __forceinline__ float bfp_scale(int e) { return ldexpf(1.0f, e); }
 //   204-236): every group's (code-1)*m11 aligned to the row's smallest exponent (capped at 20),
 //   the live absmax normalised into [2^14, 2^15), truncated to int16.
 constexpr int kMaxEmbedGroups = 128;
+constexpr int kEmbedRowMax = 32 * (kMaxEmbedGroups / 16 + kMaxEmbedGroups);   // 2-bit row bytes
+constexpr int kEmbedVecs = kEmbedRowMax / 16;
+constexpr int kEmbedThreads = 1024;       // 16 waves: the row's columns over a whole CU
 
 __device__ __forceinline__ int wave_min_i(int v) {
 #pragma unroll
@@ -34,19 +37,23 @@ __device__ __forceinline__ int wave_min_i(int v) {
   return v;
 }
 
-__global__ __launch_bounds__(256) void embed_kernel(EmbedParams p) {
+__global__ __launch_bounds__(kEmbedThreads) void embed_kernel(EmbedParams p) {
   __shared__ int s_tok;
-  __shared__ int s_red[8];
+  __shared__ int s_red[kEmbedThreads / 64];
+  __shared__ __align__(16) uint8_t s_row[kEmbedRowMax];
   const int tid = threadIdx.x;
   if (tid == 0) {
-    int pos = *p.pos + 1;
+    // The control words are read together (one round trip), before the position is written.
+    const int pos0 = *p.pos, np = *p.n_prompt;
+    const unsigned long long key = *p.slot;
+    const int pos = pos0 + 1;
     *p.pos = pos;
     int tok;
-    if (pos < *p.n_prompt) {
+    if (pos < np) {
       tok = p.prompt[pos];
     } else {
-      tok = slot_token(*p.slot);
-      const int k = pos - *p.n_prompt;
+      tok = slot_token(key);
+      const int k = pos - np;
       if (k < p.max_out) p.out[k] = tok;
     }
     if (tok < 0 || tok >= p.vocab) tok = 0;
@@ -59,13 +66,24 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedParams p) {
   if (p.mode == EMBED_TABLE) {
     const float sc = bfp_scale(p.exps[tok]);
     const int16_t* m = p.mant + (size_t)tok * p.n_embd;
-    for (int c = tid; c < p.n_embd; c += 256) p.x[c] = (float)m[c] * sc;
+    for (int c = tid; c < p.n_embd; c += kEmbedThreads) p.x[c] = (float)m[c] * sc;
     return;
   }
-  // Ternary row: scales at the head of the row packet, codes after code_off.
+  // Ternary row: scales at the head of the row packet, codes after code_off. The whole packet
+  // comes into LDS with one 16-byte load per thread; every later read is from LDS.
   __shared__ int s_live[kMaxEmbedGroups];
-  __shared__ long long s_lred[4];
-  const uint8_t* row = p.rows + (size_t)tok * p.row_bytes;
+  __shared__ long long s_lred[kEmbedThreads / 64];
+  {
+    const uint4* src = (const uint4*)(p.rows + (size_t)tok * p.row_bytes);
+    const int nvec = p.row_bytes / 16;
+#pragma unroll
+    for (int k = 0; k < (kEmbedVecs + kEmbedThreads - 1) / kEmbedThreads; ++k) {
+      const int i = min(tid + kEmbedThreads * k, nvec - 1);
+      ((uint4*)s_row)[i] = src[i];
+    }
+  }
+  __syncthreads();
+  const uint8_t* row = s_row;
   const uint16_t* sc = (const uint16_t*)row;
   const int G = p.n_embd / kGroup;
   auto code_of = [&](int c) -> int {
@@ -79,7 +97,7 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedParams p) {
   };
   // Smallest scale exponent of the row, and which groups hold a nonzero weight.
   int emin = 1 << 20;
-  for (int g = tid; g < G; g += 256) {
+  for (int g = tid; g < G; g += kEmbedThreads) {
     int m11, e16;
     fp16_split(sc[g], m11, e16);
     emin = min(emin, e16);
@@ -88,13 +106,14 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedParams p) {
   emin = wave_min_i(emin);
   if ((tid & 63) == 0) s_red[tid >> 6] = emin;
   __syncthreads();
-  emin = min(min(s_red[0], s_red[1]), min(s_red[2], s_red[3]));
-  for (int c = tid; c < p.n_embd; c += 256)
+  emin = s_red[0];
+  for (int i = 1; i < kEmbedThreads / 64; ++i) emin = min(emin, s_red[i]);
+  for (int c = tid; c < p.n_embd; c += kEmbedThreads)
     if (code_of(c) != 1) s_live[c >> 7] = 1;
   __syncthreads();
   // Largest aligned |m11| over the live groups.
   long long amax = 0;
-  for (int g = tid; g < G; g += 256) {
+  for (int g = tid; g < G; g += kEmbedThreads) {
     if (!s_live[g]) continue;
     int m11, e16;
     fp16_split(sc[g], m11, e16);
@@ -109,12 +128,12 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedParams p) {
   if ((tid & 63) == 0) s_lred[tid >> 6] = amax;
   __syncthreads();
   amax = s_lred[0];
-  for (int i = 1; i < 4; ++i) amax = s_lred[i] > amax ? s_lred[i] : amax;
+  for (int i = 1; i < kEmbedThreads / 64; ++i) amax = s_lred[i] > amax ? s_lred[i] : amax;
   int bl = 0;
   while (bl < 63 && (amax >> bl) != 0) ++bl;
   const int k2 = bl - 15;
   const float scale = bfp_scale(emin + k2);
-  for (int c = tid; c < p.n_embd; c += 256) {
+  for (int c = tid; c < p.n_embd; c += kEmbedThreads) {
     int m11, e16;
     fp16_split(sc[c >> 7], m11, e16);
     const int sh = min(e16 - emin, 20) - k2;
@@ -274,7 +293,9 @@ __global__ void synth_f32_kernel(float* out, long long n, uint32_t seed, uint32_
 int launch_embed(const EmbedParams& p, hipStream_t s) {
   TRX_CHECK(p.n_embd % kGroup == 0 && p.n_embd / kGroup <= kMaxEmbedGroups, TRX_E_INVALID,
             "embedding: n_embd %d unsupported", p.n_embd);
-  hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(256), 0, s, p);
+  TRX_CHECK(p.mode == EMBED_TABLE || (p.row_bytes % 16 == 0 && p.row_bytes <= kEmbedRowMax), TRX_E_INVALID,
+            "embedding: row of %d bytes unsupported", p.row_bytes);
+  hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(kEmbedThreads), 0, s, p);
   TRX_LAUNCHED();
   return TRX_OK;
 }

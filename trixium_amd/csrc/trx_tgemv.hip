@@ -277,9 +277,10 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int s = blockIdx.x % p.S, j = blockIdx.x / p.S;
   const int xmode = p.merge.o ? kXMerge : p.parts.in ? (p.parts.F ? kXSwiglu : kXResid) : kXPlain;
-  // A gated-off launch does nothing, but for storing the residual it was handed in partials.
-  const bool gated_off = p.gate_pos && *p.gate_pos < *p.gate_from;
-  if (gated_off && !(xmode == kXResid && j == 0 && p.parts.act)) return;
+  // A gated-off launch does nothing but store the residual it was handed in partials. The gate
+  // is read here and tested after the prologue's loads and the first weight loads are issued,
+  // so its round trip does not delay them.
+  const int gpos = p.gate_pos ? *p.gate_pos : 0, gfrom = p.gate_pos ? *p.gate_from : 0;
 
   // 1. The slice's 256 x values, or what they are made of. These loads are issued before the
   //    weight stream: vmcnt completes in order, so a wait for them would also wait for weights.
@@ -380,6 +381,8 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   TgItem<T5> buf[NB];
 #pragma unroll
   for (int b = 0; b < NB - 1; ++b) load_item(buf[b], b);
+  const bool gated_off = gpos < gfrom;
+  if (gated_off && !(xmode == kXResid && j == 0 && p.parts.act)) return;
 
   // 3. The slice's x (times the RMSNorm gain; 1/rms(x) scales the sums), then the table.
   if (xmode == kXMerge) {
@@ -650,7 +653,8 @@ struct RdParams {
 
 __global__ __launch_bounds__(kRdThreads) void tgemv_reduce_kernel(RdParams p) {
   __shared__ unsigned long long kmax[kRdThreads / 64];
-  if (p.gate_pos && *p.gate_pos < *p.gate_from) return;
+  // The gate is read with the partials (a gated-off launch drops them) rather than before them.
+  const int gpos = p.gate_pos ? *p.gate_pos : 0, gfrom = p.gate_pos ? *p.gate_from : 0;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int r0 = blockIdx.x * p.rpb;
   // Rows r0 + tid + i * 256 (i < kRdRowsMax): every partial of every row in flight per chunk of
@@ -662,12 +666,6 @@ __global__ __launch_bounds__(kRdThreads) void tgemv_reduce_kernel(RdParams p) {
     const int r = r0 + tid + i * kRdThreads;
     live[i] = tid + i * kRdThreads < p.rpb && r < p.M;
     row[i] = live[i] ? r : min(r0, p.M - 1);
-  }
-  float rs = 1.f;
-  if (p.ss) {
-    float t = 0.f;
-    for (int i = lane; i < p.S; i += 64) t += p.ss[i];
-    rs = rsqrtf(wave_sum_dpp(t) / (float)p.K + p.eps);
   }
   float acc[kRdRowsMax] = {};
   for (int q0 = 0; q0 < p.S; q0 += kRdChunk) {
@@ -681,6 +679,13 @@ __global__ __launch_bounds__(kRdThreads) void tgemv_reduce_kernel(RdParams p) {
 #pragma unroll
       for (int k = 0; k < kRdChunk; ++k) acc[i] += q0 + k < p.S ? v[i][k] : 0.f;
   }
+  float rs = 1.f;
+  if (p.ss) {
+    float t = 0.f;
+    for (int i = lane; i < p.S; i += 64) t += p.ss[i];
+    rs = rsqrtf(wave_sum_dpp(t) / (float)p.K + p.eps);
+  }
+  if (gpos < gfrom) return;
   unsigned long long key = 0;
 #pragma unroll
   for (int i = 0; i < kRdRowsMax; ++i) {
@@ -702,7 +707,9 @@ __global__ __launch_bounds__(kRdThreads) void tgemv_reduce_kernel(RdParams p) {
   if (tid == 0) {
     unsigned long long k = kmax[0];
     for (int i = 1; i < kRdThreads / 64; ++i) k = kmax[i] > k ? kmax[i] : k;
-    if (k) atomicMax(p.amax_slot, k);
+    // The slot only grows: a block whose key does not beat the value it reads needs no atomic
+    // (same-address atomics from every block serialise).
+    if (k && k > __hip_atomic_load(p.amax_slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) atomicMax(p.amax_slot, k);
   }
 }
 
