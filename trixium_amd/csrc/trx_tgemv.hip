@@ -228,10 +228,12 @@ constexpr int kDppQuadUp2 = 0xEE;      // quad_perm [2,3,2,3]: lanes 0,1 of a qu
 constexpr int kCpolSc1 = 16;          // buffer cache policy: device (agent) scope
 constexpr int kMergeMax = 32;          // attention splits the merging prologue takes
 constexpr int kSwiPartMax = 32;        // gate|up slices the SwiGLU prologue takes
-constexpr int kSwiPerThread = kSwiPartMax / (kTgThreads / (2 * kSliceCols));
 constexpr int kResPartMax = 64;        // producer slices the residual prologue takes
-constexpr int kResPerThread = kResPartMax / (kTgThreads / kSliceCols);
-static_assert(kSwiPerThread <= kMergeMax && kResPerThread <= kMergeMax, "prologue registers");
+// Partial-sum prologues load 16 bytes per thread and slice: the SwiGLU one a packed row quad
+// (128 per slice, so 8 slices per pass of the block), the residual one 4 columns (64 per slice,
+// 16 slices per pass).
+constexpr int kSwiSlicesPerPass = kTgThreads / (2 * kSliceCols / 4), kSwiVec = kSwiPartMax / kSwiSlicesPerPass;
+constexpr int kResSlicesPerPass = kTgThreads / (kSliceCols / 4), kResVec = kResPartMax / kResSlicesPerPass;
 // Where x comes from: p.x, the attention splits, SwiGLU of gate|up partial sums, or a residual
 // plus a producer's partial sums.
 constexpr int kXPlain = 0, kXMerge = 1, kXSwiglu = 2, kXResid = 3;
@@ -287,6 +289,7 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   const int cs = s * kSliceCols + tid;
   float xv = 0.f, wv = 1.f, ssin = 0.f;
   float ov[kMergeMax];
+  float4 pv[kSwiVec > kResVec ? kSwiVec : kResVec];
   int ns = 0, h0 = 0, nh = 0;
   if (xmode == kXMerge) {
     // The slice's attention output from the split partials: every split's o value of this
@@ -318,27 +321,33 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
       if (lane == 0) atot[w] = L;
     }
   } else if (xmode == kXSwiglu) {
-    // The gate|up partial sums of this slice's 2 x 256 packed rows: thread t sums row t % 512
-    // over every other slice, starting at slice t / 512; and the gate|up input's slice sums of
-    // squares (its RMSNorm scale multiplies g and u).
+    // The gate|up partial sums of this slice's 128 packed row quads ([g 2q, g 2q+1, u 2q,
+    // u 2q+1]): thread t loads quad t % 128 of slices t / 128, t / 128 + 8, ...; and the gate|up
+    // input's slice sums of squares (its RMSNorm scale multiplies g and u). Slices past S
+    // re-read the last one and are not added.
     const __amdgpu_buffer_rsrc_t rin = make_rsrc(p.parts.in, (uint32_t)((size_t)p.parts.S * p.parts.rows_p * 4));
-    const uint32_t off = (uint32_t)(2 * kSliceCols * s + (tid & (2 * kSliceCols - 1))) * 4u;
-    const int h = tid / (2 * kSliceCols);
+    const uint32_t off = (uint32_t)(2 * kSliceCols * s + 4 * (tid % (2 * kSliceCols / 4))) * 4u;
+    const int sl = tid / (2 * kSliceCols / 4);
 #pragma unroll
-    for (int k = 0; k < kSwiPerThread; ++k)
-      ov[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                            rin, off + (uint32_t)min(h + 2 * k, p.parts.S - 1) * (uint32_t)p.parts.rows_p * 4u, 0, 0));
+    for (int k = 0; k < kSwiVec; ++k) {
+      const auto a = __builtin_amdgcn_raw_buffer_load_b128(
+          rin, off + (uint32_t)min(sl + kSwiSlicesPerPass * k, p.parts.S - 1) * (uint32_t)p.parts.rows_p * 4u, 0, 0);
+      pv[k] = make_float4(__uint_as_float(a[0]), __uint_as_float(a[1]), __uint_as_float(a[2]), __uint_as_float(a[3]));
+    }
     if (p.parts.in_ss && tid < p.parts.S) ssin = p.parts.in_ss[tid];
   } else if (xmode == kXResid) {
-    // x = resid + the producer's partial sums of this slice's 256 rows: thread t sums column
-    // t % 256 over every fourth slice, starting at slice t / 256.
+    // x = resid + the producer's partial sums of this slice's 256 rows: thread t loads columns
+    // 4 (t % 64) .. + 3 of slices t / 64, t / 64 + 16, ... Slices past S re-read the last one and
+    // are not added.
     const __amdgpu_buffer_rsrc_t rin = make_rsrc(p.parts.in, (uint32_t)((size_t)p.parts.S * p.parts.rows_p * 4));
-    const uint32_t off = (uint32_t)(kSliceCols * s + (tid & (kSliceCols - 1))) * 4u;
-    const int h = tid / kSliceCols;
+    const uint32_t off = (uint32_t)(kSliceCols * s + 4 * (tid % (kSliceCols / 4))) * 4u;
+    const int sl = tid / (kSliceCols / 4);
 #pragma unroll
-    for (int k = 0; k < kResPerThread; ++k)
-      ov[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                            rin, off + (uint32_t)min(h + 4 * k, p.parts.S - 1) * (uint32_t)p.parts.rows_p * 4u, 0, 0));
+    for (int k = 0; k < kResVec; ++k) {
+      const auto a = __builtin_amdgcn_raw_buffer_load_b128(
+          rin, off + (uint32_t)min(sl + kResSlicesPerPass * k, p.parts.S - 1) * (uint32_t)p.parts.rows_p * 4u, 0, 0);
+      pv[k] = make_float4(__uint_as_float(a[0]), __uint_as_float(a[1]), __uint_as_float(a[2]), __uint_as_float(a[3]));
+    }
     if (tid < kSliceCols && cs < p.K) {
       xv = p.parts.resid[cs];
       if (p.norm_w) wv = p.norm_w[cs];
@@ -398,36 +407,56 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
       if (j == 0) p.merge.out[cs] = o;
     }
   } else if (xmode == kXSwiglu) {
-    // Sums of the two slice halves (slice order within each) through the table's memory, then
-    // gate row r pairs with up row r + 2 of its quad: x[f] = silu(g) * u.
-    const int h = tid / (2 * kSliceCols);
-    float v = 0.f;
+    // Each thread's slices summed, the 8 slice groups through the table's memory (in group
+    // order), then per quad x[2q] = silu(r g0) * (r u0), x[2q + 1] = silu(r g1) * (r u1).
+    constexpr int NQ = 2 * kSliceCols / 4;
+    const int sl = tid / NQ;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int k = 0; k < kSwiPerThread; ++k) v += h + 2 * k < p.parts.S ? ov[k] : 0.f;
-    tab[tid] = v;
+    for (int k = 0; k < kSwiVec; ++k)
+      if (sl + kSwiSlicesPerPass * k < p.parts.S)
+        v = make_float4(v.x + pv[k].x, v.y + pv[k].y, v.z + pv[k].z, v.w + pv[k].w);
+    *(float4*)(tab + sl * 2 * kSliceCols + 4 * (tid % NQ)) = v;
     if (w == 0) {
       const float t = wave_sum_dpp(ssin);
       if (lane == 0) red[0] = t;
     }
     __syncthreads();
-    const float r = p.parts.in_ss ? 1.0f / sqrtf(red[0] / (float)p.parts.in_K + p.eps) : 1.f;
-    const float g = tid < 2 * kSliceCols ? r * (tab[tid] + tab[tid + 2 * kSliceCols]) : 0.f;
-    const float u = dpp_f<kDppQuadUp2>(g);
-    const int fl = 2 * (tid >> 2) + (tid & 3), f = s * kSliceCols + fl;
-    if (tid < 2 * kSliceCols && (tid & 3) < 2) {
-      const float xf = f < p.K ? silu(g) * u : 0.f;
-      xs[fl] = xf;
-      if (j == 0 && p.parts.act && f < p.K) p.parts.act[f] = xf;
+    if (tid < NQ) {
+      const float r = p.parts.in_ss ? 1.0f / sqrtf(red[0] / (float)p.parts.in_K + p.eps) : 1.f;
+      float4 a = *(const float4*)(tab + 4 * tid);
+#pragma unroll
+      for (int i = 1; i < kSwiSlicesPerPass; ++i) {
+        const float4 b = *(const float4*)(tab + i * 2 * kSliceCols + 4 * tid);
+        a = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+      }
+      const int fl = 2 * tid, f = s * kSliceCols + fl;
+      const float x0 = f < p.K ? silu(r * a.x) * (r * a.z) : 0.f;
+      const float x1 = f + 1 < p.K ? silu(r * a.y) * (r * a.w) : 0.f;
+      xs[fl] = x0;
+      xs[fl + 1] = x1;
+      if (j == 0 && p.parts.act) {
+        if (f < p.K) p.parts.act[f] = x0;
+        if (f + 1 < p.K) p.parts.act[f + 1] = x1;
+      }
     }
   } else if (xmode == kXResid) {
-    const int h = tid / kSliceCols;
-    float v = 0.f;
+    // Each thread's slices summed, then the 16 slice groups through the table's memory (in
+    // group order).
+    constexpr int NQ = kSliceCols / 4;
+    const int sl = tid / NQ;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int k = 0; k < kResPerThread; ++k) v += h + 4 * k < p.parts.S ? ov[k] : 0.f;
-    tab[tid] = v;
+    for (int k = 0; k < kResVec; ++k)
+      if (sl + kResSlicesPerPass * k < p.parts.S)
+        v = make_float4(v.x + pv[k].x, v.y + pv[k].y, v.z + pv[k].z, v.w + pv[k].w);
+    *(float4*)(tab + sl * kSliceCols + 4 * (tid % NQ)) = v;
     __syncthreads();
     if (tid < kSliceCols && cs < p.K) {
-      xv += (tab[tid] + tab[tid + kSliceCols]) + (tab[tid + 2 * kSliceCols] + tab[tid + 3 * kSliceCols]);
+      float a = 0.f;
+#pragma unroll
+      for (int i = 0; i < kResSlicesPerPass; ++i) a += tab[i * kSliceCols + tid];
+      xv += a;
       if (j == 0 && p.parts.act) p.parts.act[cs] = xv;
     }
     if (gated_off) return;
