@@ -273,3 +273,21 @@ def test_hybrid_27b_geometry_matches_fixture(h_geometry_image, packed):
     print("27B geometry, packed", dec.packed_ops, "rel errs", errs)
     assert max(errs) <= 2e-3
     assert dec.generate_fresh(prompt, len(tokens)) == tokens
+
+
+@pytest.mark.parametrize("case", ["qwen3_ch1", "qwen35_hybrid_kseg"])
+def test_converted_gguf_decodes_like_the_oracle(tmp_path, case):
+    """A synthetic Bonsai GGUF (PTQ1_0/PQ2_0/Q2_0/Q1_0 ternary blocks, Q8_0 and BF16 DeltaNet head
+    projections) converted to a trit5 image decodes on the GPU like the oracle reads the image."""
+    import synth_gguf
+    from trixium_amd import convert
+    c = next(x for x in synth_gguf.CASES if x["id"] == case)
+    g, p = str(tmp_path / "m.gguf"), str(tmp_path / "m.bons")
+    synth_gguf.build(g, c["cfg"], c["seed"], c["arch"])
+    convert.convert(g, 1, p, kseg_max=c["kseg_max"], trit5=True, log=lambda *a: None)
+    prompt = synth.random_prompt(c["cfg"], 8, c["seed"])
+    dec = _decoder(p)
+    ref = FloatRef(bons.BONSReader(p), kv_fp16=True)
+    assert _rel_err(dec.forward(prompt), ref.forward(prompt)) <= 2e-3
+    for t in (5, 700, 11, 42):
+        assert _rel_err(dec.forward([t]), ref.step(t)) <= 2e-3

@@ -20,13 +20,15 @@ from .fixedpoint import fp16_split, scale_bias, result_shift, GS_MAX, GS_MAX_Q8
 
 class TensorSpec:
     """One tensor to write. Ternary: scales (rows, cols/128) fp16 and codes (rows, cols) uint8 in
-    {0,1,2} (w = code - 1); Q8: scales (rows, cols/32) and int8 values; F16/F32/NORM16: values."""
+    {0,1,2} (w = code - 1); Q8: scales (rows, cols/32) and int8 values; F16/F32/NORM16: values.
+    `loader`, in place of values, returns them when the writer reaches the tensor, so a converter
+    holds one tensor's codes at a time (the reference's TensorSpec.loader, model/bons.py)."""
 
     def __init__(self, name, role, layer, kind, rows, cols, scales=None, values=None, flags=0,
-                 bias=None, kseg=0, fixed_point=None):
+                 bias=None, kseg=0, fixed_point=None, loader=None):
         self.name, self.role, self.layer, self.kind = name, role, layer, kind
         self.rows, self.cols, self.flags, self.kseg = rows, cols, flags, kseg
-        self.scales, self.values = scales, values
+        self.scales, self.values, self.loader = scales, values, loader
         if values is not None and tuple(values.shape) != (rows, cols):
             raise ValueError(f"{name}: values {values.shape} != {(rows, cols)}")
         if kind in (L.KIND_TERNARY, L.KIND_TERNARY5, L.KIND_Q8):
@@ -41,6 +43,42 @@ class TensorSpec:
         else:
             self.bias = (bias & 0xFF) if bias is not None else 0
             self.rshift = 0
+
+    def load(self):
+        """The values, from the loader when none are held."""
+        if self.values is not None:
+            return self.values
+        v = self.loader()
+        if tuple(v.shape) != (self.rows, self.cols):
+            raise ValueError(f"{self.name}: loaded values {v.shape} != {(self.rows, self.cols)}")
+        return v
+
+
+def split_wide(spec, kseg_max=L.KSEG_MAX):
+    """A ternary or Q8 matrix wider than kseg_max as K-segments (model/bons.py:83-115): nseg =
+    ceil(cols / kseg_max) column ranges on whole scale groups (segment k ends at group
+    floor(G k / nseg)), each flagged FLAG_KSEG with its index, named `<name>.k<k>`, and every one
+    keeping the whole tensor's bias/rshift so the segment results add up. The token embedding
+    stays whole (a lookup reads whole rows)."""
+    if spec.kind == L.KIND_Q8:
+        kseg_max = min(kseg_max, L.KSEG_MAX_Q8)
+    if spec.kind not in (L.KIND_TERNARY, L.KIND_Q8) or spec.cols <= kseg_max or spec.role == L.ROLE_TOK_EMB:
+        return [spec]
+    g = L.KIND_GROUP[spec.kind]
+    if kseg_max < g:
+        raise ValueError(f"kseg_max {kseg_max} is narrower than the {g}-weight scale group")
+    nseg, ngrp = -(-spec.cols // kseg_max), spec.cols // g
+    edges = [ngrp * k // nseg * g for k in range(nseg + 1)]
+    out = []
+    for k in range(nseg):
+        c0, c1 = edges[k], edges[k + 1]
+        vals = None if spec.values is None else np.ascontiguousarray(spec.values[:, c0:c1])
+        ld = None if spec.loader is None else (lambda c0=c0, c1=c1, f=spec.loader: np.ascontiguousarray(f()[:, c0:c1]))
+        out.append(TensorSpec(f"{spec.name}.k{k}", spec.role, spec.layer, spec.kind, spec.rows, c1 - c0,
+                              scales=np.ascontiguousarray(spec.scales[:, c0 // g:c1 // g]), values=vals,
+                              flags=spec.flags | L.FLAG_KSEG, kseg=k, fixed_point=(spec.bias, spec.rshift),
+                              loader=ld))
+    return out
 
 
 # Row-packet codecs -----------------------------------------------------------------------------
@@ -220,7 +258,7 @@ def write_image(cfg, tensors, n_channels, path, tokenizer_sha256=b"", manifest_p
     if emb16 and emb and not any(t.role == L.ROLE_TOK_EMB16 for t in tensors):
         if cfg.hadamard_block:
             raise NotImplementedError("rotated (Hadamard) embedding tables are not written here")
-        tensors.extend(emb16_specs(*embed_bfp_rows(emb[0].values, emb[0].scales)))
+        tensors.extend(emb16_specs(*embed_bfp_rows(emb[0].load(), emb[0].scales)))
     if trit5:
         has16 = any(t.role == L.ROLE_TOK_EMB16 for t in tensors)
         for spec in tensors:
@@ -242,7 +280,7 @@ def write_image(cfg, tensors, n_channels, path, tokenizer_sha256=b"", manifest_p
     image = np.zeros(payload_off + n_channels * chan_bytes, dtype=np.uint8)
     entries, man = [], []
     for spec, (b0, nb) in zip(tensors, per_chan):
-        packets = encode_rows(spec.kind, spec.cols, spec.scales, spec.values)
+        packets = encode_rows(spec.kind, spec.cols, spec.scales, spec.load())
         crc = 0
         for c in range(n_channels):
             r0, nr = (0, spec.rows) if spec.flags & L.FLAG_REPLICATED else L.shard_rows(spec.rows, n_channels, c)

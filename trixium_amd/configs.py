@@ -36,6 +36,11 @@ class ModelConfig:
     hadamard_block: int = 0
     hadamard_signs: dict = None
 
+    def vocab_padded(self, n_channels):
+        """The vocabulary rounded up to a multiple of the channel count: row-sharded embedding and
+        LM head tensors get zero rows there (model/configs.py:69-72)."""
+        return -(-self.vocab // n_channels) * n_channels
+
     def layer_type(self, l):
         return self.layer_types[l] if self.layer_types else "attn"
 

@@ -32,6 +32,7 @@ KIND_GROUP = {KIND_TERNARY: GROUP, KIND_TERNARY5: GROUP, KIND_Q8: GROUP_Q8}
 FLAG_REPLICATED = 0x01
 FLAG_KSEG = 0x02
 KSEG_MAX = 16384
+KSEG_MAX_Q8 = 255 * 32      # a Q8 segment: at most 255 code beats of 32 columns
 
 # Tensor roles (model/layout.py:95-115).
 ROLE_TOK_EMB, ROLE_OUT_NORM, ROLE_LM_HEAD = 0, 1, 2
