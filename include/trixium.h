@@ -168,6 +168,8 @@ int trx_gemv_packed_parts_f32(const uint8_t* packed, int kind, int M, int K, con
 #define TRX_ROLE_SSM_A 23
 #define TRX_ROLE_SSM_DT 24
 #define TRX_ROLE_SSM_NORM 25
+#define TRX_ROLE_HADAMARD 26   /* model tensor (role, layer = width index): that input width's
+                                  PrismML rotation signs, float32 +-1 (trx_model_set_tensor) */
 
 typedef struct {
   int n_layer, n_embd, n_head, n_kv_head, head_dim, ffn_dim, vocab, max_ctx;
@@ -190,6 +192,16 @@ typedef struct {
                                   choice (q|k|v, o, gate|up, down, ternary LM head; DeltaNet
                                   projections on the row-packet kernel). (With layer_fusion the
                                   fused layers keep the row-packet kernel.) */
+  /* PrismML's rotated weight basis (model/golden.py:250-289, model/fastref.py:127-140): every
+     ternary projection but the DeltaNet beta/alpha takes x' = hadamard_scale * H (s * xhat)
+     blockwise over hadamard_block columns (H the +-1 Sylvester matrix, s the width's signs,
+     xhat the normalised input), computed by a fast Walsh-Hadamard transform before the GEMV.
+     0 = plain basis. A rotated model runs every projection on the row-packet kernel, one per
+     operation (packed_ops and layer_fusion must be 0). */
+  int hadamard_block;          /* 0, or a power of two in [64, 1024] dividing every width */
+  float hadamard_scale;        /* the rotation tensors' scale (a power of two) */
+  int hadamard_widths[4];      /* the rotated input widths (0 = unused); signs per width as
+                                  model tensors TRX_ROLE_HADAMARD, layer = index here */
 } trx_model_config;
 
 #define TRX_PACK_QKV 1         /* attention q|k|v */

@@ -30,8 +30,9 @@ class FloatRef:
         self.gated = bool(h["attn_gated"])
         self.vocab = h["vocab"]
         self.dn = [t == "deltanet" for t in h["layer_types"]]
-        if h["hadamard_block"]:
-            raise NotImplementedError("rotated-basis images are outside this reference")
+        # PrismML's rotated basis: every ternary projection's input goes through the image's
+        # rotation tensors first (fastref.py:127-140), the DeltaNet beta/alpha excepted.
+        self.hb, self.hwidths = h["hadamard_block"], list(h["hadamard_widths"])
         self.kv_fp16 = kv_fp16
         self.wcache = {}
         # fastref.py:62-63: theta**(-2i/n) evaluated in float32.
@@ -80,9 +81,21 @@ class FloatRef:
             self.wcache[key] = np.concatenate(ws, axis=1).astype(np.float16)
         return self.wcache[key]
 
+    def rotate(self, x, width):
+        """x' = the rotation blocks (ternary block x block tensors) applied blockwise."""
+        out = np.empty(width, f32)
+        wi = self.hwidths.index(width)
+        for b in range(width // self.hb):
+            W = self.weight(L.ROLE_HADAMARD, L.hadamard_layer(wi, b))
+            out[b * self.hb:(b + 1) * self.hb] = W.astype(f32) @ x[b * self.hb:(b + 1) * self.hb]
+        return out
+
     def proj(self, role, l, x):
         W = self.weight(role, l)
-        return (W.astype(f32) @ np.asarray(x, dtype=f32)).astype(f32)
+        x = np.asarray(x, dtype=f32)
+        if self.hb and role not in (L.ROLE_SSM_BETA, L.ROLE_SSM_ALPHA):
+            x = self.rotate(x, W.shape[1])
+        return (W.astype(f32) @ x).astype(f32)
 
     # Elementwise ops (fastref.py:143-156) ----------------------------------------------------
     def rmsnorm(self, x, w):

@@ -7,7 +7,7 @@ alpha in BF16, everything else F32. Shapes keep every payload but the embedding 
 import numpy as np
 
 from trixium_amd import configs as C, layout as L, qformats as Q, synth
-from trixium_amd.gguf import T_ARR, T_F32, T_I32, T_STR, Typed, write_gguf
+from trixium_amd.gguf import T_ARR, T_F32, T_I8, T_I32, T_STR, Typed, write_gguf
 
 TERNARY_CYCLE = (Q.GGML_PTQ1_0, Q.GGML_PQ2_0, Q.GGML_Q2_0)
 
@@ -22,6 +22,22 @@ CASES = [
     {"id": "qwen35_hybrid_kseg", "cfg": C.TINY_HYBRID.replace(name="tiny-hybrid-gguf"), "arch": "qwen35",
      "seed": 5, "channels": 1, "trit5": True, "kseg_max": 256},
 ]
+# PrismML-rotated files: qwen3 with 128-blocks (an odd power of two: the converter folds 2^-0.5
+# into the weights) and the hybrid with 256-blocks.
+ROT_CASES = [
+    {"id": "qwen3_rot128", "cfg": C.TINY.replace(name="tiny-gguf-rot"), "arch": "qwen3", "seed": 6, "channels": 1,
+     "trit5": True, "kseg_max": 16384, "hadamard": 128},
+    {"id": "qwen35_rot256", "cfg": C.TINY_HYBRID.replace(name="tiny-hybrid-gguf-rot"), "arch": "qwen35", "seed": 7,
+     "channels": 1, "trit5": True, "kseg_max": 16384, "hadamard": 256},
+]
+
+
+def input_widths(cfg):
+    """The input widths of the model's ternary projections (what a rotation must cover)."""
+    w = {cfg.n_embd, cfg.q_dim, cfg.ffn_dim}
+    if any(cfg.layer_type(l) == "deltanet" for l in range(cfg.n_layer)):
+        w.add(cfg.dn_num_v_heads * cfg.dn_v_head_dim)
+    return sorted(w)
 
 
 def _meta(cfg, arch):
@@ -50,9 +66,11 @@ def _bf16(w):
     return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16).tobytes()
 
 
-def build(path, cfg, seed, arch="qwen3", one_bit="blk.0.attn_k.weight"):
+def build(path, cfg, seed, arch="qwen3", one_bit="blk.0.attn_k.weight", hadamard=0):
     """Write the GGUF; returns {name: (scales, codes)} of its ternary matrices as the file holds
-    them (the 1-bit matrix as codes 0/2)."""
+    them (the 1-bit matrix as codes 0/2). hadamard: the block of a PrismML rotation declared in
+    the metadata, with seeded signs for every projection input width (the weights stand for
+    folded ones)."""
     specs = synth.small_model_tensors(cfg, seed, fp16_embedding=False)
     rng = np.random.default_rng(seed + 1)
     tensors, truth, k = [], {}, 0
@@ -85,5 +103,14 @@ def build(path, cfg, seed, arch="qwen3", one_bit="blk.0.attn_k.weight"):
     # The embedding goes last: with an odd vocabulary its payload is not a multiple of the
     # alignment, and only the last tensor's size is exact from the offsets alone.
     tensors.sort(key=lambda t: t[0] == "token_embd.weight")
-    write_gguf(path, _meta(cfg, arch), tensors)
+    md = _meta(cfg, arch)
+    if hadamard:
+        widths = input_widths(cfg)
+        signs = np.concatenate([np.where(rng.random(w) < 0.5, -1, 1) for w in widths]).astype(np.int8)
+        md.update({"prism.hadamard.block_size": hadamard,
+                   "prism.hadamard.transform": "normalized-sylvester-walsh-hadamard",
+                   "prism.hadamard.axis": "input-last-dimension",
+                   "prism.hadamard.sign_widths": Typed(T_ARR, np.array(widths, np.int32), T_I32),
+                   "prism.hadamard.sign_values": Typed(T_ARR, signs, T_I8)})
+    write_gguf(path, md, tensors)
     return truth

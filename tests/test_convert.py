@@ -11,8 +11,8 @@ import numpy as np
 import pytest
 
 import synth_gguf
-from synth_gguf import CASES
-from trixium_amd import bons, configs as C, convert, gguf, layout as L, qformats as Q
+from synth_gguf import CASES, ROT_CASES
+from trixium_amd import bons, configs as C, convert, gguf, hadamard as H, layout as L, qformats as Q
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 
@@ -242,6 +242,85 @@ def test_beta_alpha_become_q8_rows(converted):
     assert np.all(np.abs(q * step - w) <= 0.5 * step * (1 + 1e-3) + 1e-7)
 
 
+# PrismML rotation --------------------------------------------------------------------------------
+
+def test_sylvester_matrix_and_restore():
+    """H_2n = [[H_n, H_n], [H_n, -H_n]] with H_1 = [1]; R = H / sqrt(n) is orthonormal; restore
+    undoes the fold z = R diag(s) e."""
+    h = np.ones((1, 1), np.float32)
+    while h.shape[0] < 256:
+        h = np.block([[h, h], [h, -h]])
+    assert np.array_equal(H.sign_matrix(256), h)
+    R = H.matrix(256).astype(np.float64)
+    assert np.allclose(R @ R.T, np.eye(256), atol=1e-6)
+    rng = np.random.default_rng(0)
+    s = np.where(rng.random(512) < 0.5, -1.0, 1.0).astype(np.float32)
+    e = rng.normal(0, 1, (3, 512)).astype(np.float32)
+    z = ((e * s).reshape(3, 2, 256) @ R.T.astype(np.float32)).reshape(3, 512)
+    assert np.allclose(H.restore(z, s, 256), e, atol=1e-5)
+    assert H.image_scales(1024) == (2.0 ** -5, 1.0) and H.image_scales(512) == (2.0 ** -4, 2.0 ** -0.5)
+    assert H.image_gain(1024) == 1.0 and abs(H.image_gain(512) - np.sqrt(2)) < 1e-12
+
+
+def test_restored_table_rows():
+    """restored_bfp_rows: mantissas with the row absmax in [2^14, 2^15) whose value is the
+    restored row times the image gain within half a mantissa step."""
+    rng = np.random.default_rng(1)
+    codes = rng.integers(0, 3, (5, 256), dtype=np.uint8)
+    scales = rng.uniform(0.01, 0.05, (5, 2)).astype(np.float16)
+    s = np.where(rng.random(256) < 0.5, -1.0, 1.0).astype(np.float32)
+    mant, exps = H.restored_bfp_rows(scales, codes, s, 128)
+    z = ((codes.astype(np.float64) - 1).reshape(5, 2, 128) * scales.astype(np.float64)[:, :, None]).reshape(5, 256)
+    e = H.restore(z.astype(np.float32), s, 128).astype(np.float64) * H.image_gain(128)
+    amax = np.abs(mant.astype(np.int64)).max(axis=1)
+    assert ((amax >= 2 ** 14 - 1) & (amax <= 32767)).all()
+    assert np.all(np.abs(mant * 2.0 ** exps[:, None] - e) <= 0.5 * 2.0 ** exps[:, None] * (1 + 1e-6))
+
+
+@pytest.fixture(scope="module")
+def rotated(tmp_path_factory):
+    d = tmp_path_factory.mktemp("rot")
+    out = {}
+    for c in ROT_CASES:
+        g, img = str(d / (c["id"] + ".gguf")), str(d / (c["id"] + ".bons"))
+        synth_gguf.build(g, c["cfg"], c["seed"], c["arch"], hadamard=c["hadamard"])
+        convert.convert(g, c["channels"], img, kseg_max=c["kseg_max"], trit5=c["trit5"], log=lambda *a: None)
+        out[c["id"]] = (c, g, img)
+    return out
+
+
+@pytest.mark.parametrize("case", [c["id"] for c in ROT_CASES])
+def test_rotated_image_equals_the_reference_converters(rotated, case):
+    """Rotation tensors, the odd-block fold and the restored embedding table, byte for byte."""
+    with open(os.path.join(HERE, "golden", "golden_convert.json")) as f:
+        want = json.load(f)[case]
+    c, g, img = rotated[case]
+    assert _sha(g) == want["gguf_sha256"], "the synthetic GGUF changed: regenerate the fixture"
+    assert _sha(img) == want["image_sha256"]
+    blk, scale, signs = H.image_rotation(bons.BONSReader(img))
+    gg = gguf.GGUFReader(g)
+    assert blk == c["hadamard"] and scale == H.image_scales(blk)[0]
+    at = 0
+    for w in gg.metadata["prism.hadamard.sign_widths"]:
+        assert np.array_equal(signs[int(w)], gg.metadata["prism.hadamard.sign_values"][at:at + int(w)])
+        at += int(w)
+
+
+@pytest.mark.parametrize("case", [c["id"] for c in ROT_CASES])
+def test_oracle_rotates_like_fastref(rotated, case):
+    """The oracle's rotation (the image's rotation tensors before every ternary projection but
+    beta/alpha) against the reference's HybridRef logits on the reference's image, every position
+    of the prompt (tests/golden/golden_rot_logits.npz)."""
+    from oracle.floatref import FloatRef
+    z = np.load(os.path.join(HERE, "golden", "golden_rot_logits.npz"))
+    prompt, want = [int(t) for t in z[case + "/prompt"]], z[case + "/logits"]
+    ref = FloatRef(bons.BONSReader(rotated[case][2]))
+    got = [ref.forward(prompt[:1])] + [ref.step(t) for t in prompt[1:]]
+    for g, w in zip(got, want):
+        assert np.max(np.abs(g - w)) <= 1e-4 * np.max(np.abs(w))
+        assert np.argmax(g) == np.argmax(w)
+
+
 def test_unsupported_inputs_are_errors(tmp_path):
     cfg = C.TINY.replace(name="t", n_layer=1)
     g = str(tmp_path / "g64.gguf")
@@ -258,8 +337,10 @@ def test_unsupported_inputs_are_errors(tmp_path):
     h = str(tmp_path / "had.gguf")
     gguf.write_gguf(h, md, [("token_embd.weight", (cfg.vocab, 256), Q.GGML_PQ2_0, bytes(cfg.vocab * 2 * 34))])
     assert convert.config_from_gguf(gguf.GGUFReader(h)).hadamard_block == 256
-    with pytest.raises(NotImplementedError, match="Hadamard"):
-        convert.convert(h, 1, str(tmp_path / "x.bons"), log=lambda *a: None)
+    md["prism.hadamard.axis"] = "output"
+    gguf.write_gguf(h, md, [("token_embd.weight", (cfg.vocab, 256), Q.GGML_PQ2_0, bytes(cfg.vocab * 2 * 34))])
+    with pytest.raises(ValueError, match="transform or axis"):
+        convert.config_from_gguf(gguf.GGUFReader(h))
 
 
 def test_command_line(converted, tmp_path, capsys):

@@ -291,3 +291,32 @@ def test_converted_gguf_decodes_like_the_oracle(tmp_path, case):
     assert _rel_err(dec.forward(prompt), ref.forward(prompt)) <= 2e-3
     for t in (5, 700, 11, 42):
         assert _rel_err(dec.forward([t]), ref.step(t)) <= 2e-3
+
+
+@pytest.mark.parametrize("case", ["qwen3_rot128", "qwen35_rot256"])
+def test_rotated_image_decodes_like_fastref(tmp_path, case):
+    """A PrismML-rotated model (rotation tensors, folded weights, restored embedding table) on the
+    GPU: the fast Walsh-Hadamard transform before every projection against the oracle's rotation
+    tensors on the same image, and against the reference's HybridRef logits on the reference
+    converter's image (tests/golden/golden_rot_logits.npz), every prompt position."""
+    import os
+    import synth_gguf
+    from trixium_amd import convert
+    c = next(x for x in synth_gguf.ROT_CASES if x["id"] == case)
+    g, p = str(tmp_path / "m.gguf"), str(tmp_path / "m.bons")
+    synth_gguf.build(g, c["cfg"], c["seed"], c["arch"], hadamard=c["hadamard"])
+    convert.convert(g, 1, p, trit5=c["trit5"], log=lambda *a: None)
+    z = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden_rot_logits.npz"))
+    prompt, want = [int(t) for t in z[case + "/prompt"]], z[case + "/logits"]
+    dec = _decoder(p)
+    ref = FloatRef(bons.BONSReader(p), kv_fp16=True)
+    got = [dec.forward(prompt[:1])] + [dec.forward([t]) for t in prompt[1:]]
+    oracle = [ref.forward(prompt[:1])] + [ref.step(t) for t in prompt[1:]]
+    for gl, o, w in zip(got, oracle, want):
+        assert _rel_err(gl, o) <= 2e-3
+        assert _rel_err(gl, w) <= LOGIT_RTOL
+        assert np.argmax(gl) == np.argmax(w)
+    dec.reset()
+    toks = dec.generate(prompt, 6)
+    dec2 = _decoder(p, use_graph=False)
+    assert toks == dec2.generate(prompt, 6)

@@ -257,8 +257,14 @@ def write_image(cfg, tensors, n_channels, path, tokenizer_sha256=b"", manifest_p
     emb = [t for t in tensors if t.role == L.ROLE_TOK_EMB and t.kind == L.KIND_TERNARY]
     if emb16 and emb and not any(t.role == L.ROLE_TOK_EMB16 for t in tensors):
         if cfg.hadamard_block:
-            raise NotImplementedError("rotated (Hadamard) embedding tables are not written here")
-        tensors.extend(emb16_specs(*embed_bfp_rows(emb[0].load(), emb[0].scales)))
+            # A rotated table is restored to the plain basis here, in row blocks.
+            from .hadamard import restored_bfp_rows
+            codes, sig = emb[0].load(), cfg.hadamard_signs[emb[0].cols]
+            parts = [restored_bfp_rows(emb[0].scales[r:r + 8192], codes[r:r + 8192], sig, cfg.hadamard_block)
+                     for r in range(0, emb[0].rows, 8192)]
+            tensors.extend(emb16_specs(np.concatenate([p[0] for p in parts]), np.concatenate([p[1] for p in parts])))
+        else:
+            tensors.extend(emb16_specs(*embed_bfp_rows(emb[0].load(), emb[0].scales)))
     if trit5:
         has16 = any(t.role == L.ROLE_TOK_EMB16 for t in tensors)
         for spec in tensors:

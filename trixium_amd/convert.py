@@ -12,12 +12,13 @@ The conversion of model/convert.py:120-343 for the images this decoder reads:
   32 weights, fp16 scales, round half to even); Q8_0 tensors taken as they are; F32 tensors as
   F32 rows (the conv taps as rows of 1024);
 - matrices wider than kseg_max split into K-segments;
-- written with write_image (rope table, int16 embedding table, optional trit5 storage).
+- written with write_image (rope table, int16 embedding table, optional trit5 storage);
+- PrismML's Hadamard-rotated files: the rotation tensors of every input width, the odd-block
+  scale fold, and the token table restored to the plain basis in the int16 embedding table.
 
 Not done here: the FPGA board's channel-window fit check (model/convert.py:260-312: HBM windows,
 per-channel KV and DeltaNet budgets), which can drop the int16 embedding table for an FPGA
-image; and PrismML's Hadamard-rotated files (the rotation tensors and the restored embedding
-table), which the GPU decoder does not run either - they raise NotImplementedError.
+image.
 
     python -m trixium_amd.convert inspect FILE.gguf
     python -m trixium_amd.convert convert --gguf F --channels 1 --out IMG [--trit5] [--check] ...
@@ -31,6 +32,7 @@ import time
 
 import numpy as np
 
+from . import hadamard
 from . import layout as L
 from . import qformats as Q
 from .bons import BONSReader, TensorSpec, split_wide, write_image
@@ -258,8 +260,6 @@ def convert(gguf_path, n_channels, out_path, manifest_path=None, tokenizer_path=
     """Write the BONS image of a GGUF file; returns the manifest."""
     reader = GGUFReader(gguf_path)
     cfg = config_from_gguf(reader)
-    if cfg.hadamard_block:
-        raise NotImplementedError(f"{gguf_path}: Hadamard-rotated (PrismML) files are not converted here")
     try:
         check_engine_support(cfg)
     except SystemExit as e:
@@ -269,6 +269,18 @@ def convert(gguf_path, n_channels, out_path, manifest_path=None, tokenizer_path=
         cfg.name = f"{cfg.name}-l{cfg.n_layer}"
     vocab_pad = cfg.vocab_padded(n_channels)
     specs = [spec_from_gguf(reader, n, n_channels, vocab_pad) for n in tensor_names(reader, cfg)]
+    if cfg.hadamard_block:
+        # An odd power-of-two block: the rotation tensors carry 2^-floor(k/2), so every rotated
+        # ternary tensor (the projections, the head and the token table) takes the remaining
+        # 2^-0.5 in its scales. As in model/convert.py:229-239 the fold comes after the entries'
+        # bias/rshift were chosen from the unfolded scales.
+        fold = hadamard.image_scales(cfg.hadamard_block)[1]
+        if fold != 1.0:
+            for sp in specs:
+                if sp.kind == L.KIND_TERNARY:
+                    sp.scales = (sp.scales.astype(np.float32) * np.float32(fold)).astype(np.float16)
+            log(f"  hadamard block {cfg.hadamard_block}: weights x 2**-0.5")
+        specs += hadamard.rotation_specs(cfg)
     specs = [seg for sp in specs for seg in split_wide(sp, kseg_max)]
     nseg = sum(1 for sp in specs if sp.flags & L.FLAG_KSEG)
     if nseg:

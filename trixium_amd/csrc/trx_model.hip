@@ -85,6 +85,7 @@ struct Model {
   float* head_ss = nullptr;
   int head_S = 0, head_rows_p = 0;
   float* x2 = nullptr;                             // second residual buffer (x alternates)
+  float* xrot = nullptr;                           // a rotated model's projection input
   float* hidden = nullptr;                         // the residual after the last layer
   hipGraph_t graph = nullptr;
   hipGraphExec_t graph_exec = nullptr;
@@ -166,6 +167,9 @@ static void plan_arena(Model& m, size_t& cur) {
   }
   if (c.emb_mode == 1 || c.head_tied) plan_tensor(m, cur, TRX_ROLE_TOK_EMB, 0, c.emb_kind, c.vocab, E);
   if (!c.head_tied) plan_tensor(m, cur, TRX_ROLE_LM_HEAD, 0, c.head_kind, c.vocab, E);
+  if (c.hadamard_block)
+    for (int i = 0; i < 4; ++i)
+      if (c.hadamard_widths[i]) plan_tensor(m, cur, TRX_ROLE_HADAMARD, i, TRX_KIND_F32, 1, c.hadamard_widths[i]);
 }
 
 static int dalloc(Model& m, void** p, size_t bytes);
@@ -290,11 +294,23 @@ static uint8_t* P(Model& m, int role, int layer) { return m.arena + T(m, role, l
 static float* PF(Model& m, int role, int layer) { return (float*)P(m, role, layer); }
 
 // One ternary projection: the packed GEMV when the model holds a packed copy of it, otherwise the
-// row-packet kernel.
+// row-packet kernel. In a rotated model the input (normalised first, with a norm) goes through
+// the width's rotation into xrot, and the GEMV takes that.
 static int projection(Model& m, int op, int l, const uint8_t* rows, int kind, int M, int K, const float* x,
                       const float* norm_w, float* y, int epi, const float* resid, hipStream_t s,
                       unsigned long long* amax = nullptr, const int* gate_pos = nullptr,
                       const int* gate_from = nullptr) {
+  if (m.cfg.hadamard_block) {
+    int wi = 0;
+    while (wi < 4 && m.cfg.hadamard_widths[wi] != K) ++wi;
+    TRX_CHECK(wi < 4, TRX_E_INVALID, "rotated model: no rotation for input width %d", K);
+    RotParams rp = {x, norm_w, m.cfg.rms_eps, K, m.cfg.hadamard_block, PF(m, TRX_ROLE_HADAMARD, wi),
+                    m.cfg.hadamard_scale, m.xrot};
+    int rc;
+    if ((rc = launch_rotate(rp, s))) return rc;
+    x = m.xrot;
+    norm_w = nullptr;
+  }
   auto it = m.packed.find({op, l});
   if (it != m.packed.end())
     return tgemv_f32(it->second.buf, kind, M, K, x, norm_w, m.cfg.rms_eps, y, epi, resid, amax, m.pack_work, s,
@@ -666,6 +682,17 @@ TRX_API int trx_model_create(const trx_model_config* cfg, const float* rope_freq
             "trx_model_create: unsupported geometry");
   TRX_CHECK(c.weight_kind == TRX_KIND_TERNARY || c.weight_kind == TRX_KIND_TERNARY5, TRX_E_INVALID,
             "trx_model_create: weight_kind must be ternary");
+  if (c.hadamard_block) {
+    const int B = c.hadamard_block;
+    TRX_CHECK(B >= 64 && B <= 1024 && (B & (B - 1)) == 0 && c.hadamard_scale > 0.f, TRX_E_INVALID,
+              "trx_model_create: Hadamard block %d unsupported", B);
+    TRX_CHECK(c.packed_ops == 0 && !c.layer_fusion && (c.head_tied || c.head_kind != TRX_KIND_F16),
+              TRX_E_INVALID, "trx_model_create: a rotated model runs the row-packet kernel, one per operation, "
+              "with a ternary head (packed_ops 0, layer_fusion 0)");
+    for (int i = 0; i < 4; ++i)
+      TRX_CHECK(c.hadamard_widths[i] >= 0 && c.hadamard_widths[i] % B == 0, TRX_E_INVALID,
+                "trx_model_create: rotation width %d is not a multiple of the block", c.hadamard_widths[i]);
+  }
   trx_model* h = new trx_model();
   Model& m = h->m;
   m.cfg = c;
@@ -719,6 +746,11 @@ TRX_API int trx_model_create(const trx_model_config* cfg, const float* rope_freq
   const int qrows = c.n_head * hd * (c.attn_gated ? 2 : 1);
   if ((rc = dalloc(m, (void**)&m.x, (size_t)c.n_embd * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.x2, (size_t)c.n_embd * 4))) return fail(rc);
+  if (c.hadamard_block) {
+    const int wmax = std::max({c.hadamard_widths[0], c.hadamard_widths[1], c.hadamard_widths[2],
+                               c.hadamard_widths[3]});
+    if ((rc = dalloc(m, (void**)&m.xrot, (size_t)wmax * 4))) return fail(rc);
+  }
   m.hidden = m.x;
   if ((rc = dalloc(m, (void**)&m.qkv, (size_t)(qrows + 2 * c.n_kv_head * hd) * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.attn_out, (size_t)c.n_head * hd * 4))) return fail(rc);

@@ -86,6 +86,19 @@ struct DnRecurParams {
   float eps;
 };
 
+// PrismML rotation of a projection input: y = scale * H (s * xhat) per block of B columns (H the
+// +-1 Sylvester matrix), xhat = x, or x / rms(x) * norm_w with a norm. y must not alias x.
+struct RotParams {
+  const float* x;
+  const float* norm_w;   // RMSNorm gain, or null
+  float eps;
+  int K, B;              // columns; block (a power of two in [64, 1024] dividing K)
+  const float* signs;    // +-1 per column
+  float scale;
+  float* y;
+};
+
+int launch_rotate(const RotParams& p, hipStream_t s);
 int launch_dn_conv(const DnConvParams& p, hipStream_t s);
 int launch_dn_recur(const DnRecurParams& p, hipStream_t s);
 int launch_embed(const EmbedParams& p, hipStream_t s);

@@ -288,7 +288,54 @@ __global__ void synth_f32_kernel(float* out, long long n, uint32_t seed, uint32_
   }
 }
 
+// PrismML rotation ------------------------------------------------------------------------------
+
+// One workgroup of B threads per block of columns. With a norm every workgroup sums x^2 over the
+// whole vector (K <= a few tens of thousands: a few KB from L2 each). The butterflies of span
+// below 64 exchange within a wave by shuffles, the wider ones through LDS; the natural-order
+// butterfly (a + b, a - b) over spans 1, 2, 4, ... yields H v with H[i][j] = (-1)^popcount(i & j).
+__global__ __launch_bounds__(1024) void rotate_kernel(RotParams p) {
+  __shared__ float v[1024];
+  __shared__ float red[16];
+  const int t = threadIdx.x, B = blockDim.x, c = blockIdx.x * B + t;
+  const int lane = t & 63, w = t >> 6;
+  float a = p.x[c] * p.signs[c];
+  if (p.norm_w) {
+    float ss = 0.f;
+    for (int i = t; i < p.K; i += B) {
+      const float e = p.x[i];
+      ss += e * e;
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) red[w] = ss;
+    __syncthreads();
+    float tot = 0.f;
+    for (int k = 0; k < B / 64; ++k) tot += red[k];
+    a *= p.norm_w[c] / sqrtf(tot / (float)p.K + p.eps);
+  }
+  for (int h = 1; h < 64; h <<= 1) {
+    const float o = __shfl_xor(a, h, 64);
+    a = (lane & h) ? o - a : a + o;
+  }
+  for (int h = 64; h < B; h <<= 1) {
+    v[t] = a;
+    __syncthreads();
+    const float o = v[t ^ h];
+    __syncthreads();
+    a = (t & h) ? o - a : a + o;
+  }
+  p.y[c] = a * p.scale;
+}
+
 // Launchers ------------------------------------------------------------------------------------
+
+int launch_rotate(const RotParams& p, hipStream_t s) {
+  TRX_CHECK(p.B >= 64 && p.B <= 1024 && (p.B & (p.B - 1)) == 0 && p.K > 0 && p.K % p.B == 0 && p.x != p.y,
+            TRX_E_INVALID, "rotation: block %d over %d columns unsupported", p.B, p.K);
+  hipLaunchKernelGGL(rotate_kernel, dim3(p.K / p.B), dim3(p.B), 0, s, p);
+  TRX_LAUNCHED();
+  return TRX_OK;
+}
 
 int launch_embed(const EmbedParams& p, hipStream_t s) {
   TRX_CHECK(p.n_embd % kGroup == 0 && p.n_embd / kGroup <= kMaxEmbedGroups, TRX_E_INVALID,

@@ -43,6 +43,13 @@ ROLE_ROPE_TAB, ROLE_TOK_EMB16, ROLE_TOK_EMB16_EXP = 14, 15, 16
 ROLE_ATTN_QKV, ROLE_ATTN_ZGATE, ROLE_SSM_OUT, ROLE_SSM_BETA, ROLE_SSM_ALPHA = 17, 18, 19, 20, 21
 ROLE_SSM_CONV, ROLE_SSM_A, ROLE_SSM_DT, ROLE_SSM_NORM, ROLE_HADAMARD = 22, 23, 24, 25, 26
 
+def hadamard_layer(width_index, block_index):
+    """The entry `layer` of a rotation block tensor: width index * 256 + block (model/layout.py:124-128)."""
+    if not (0 <= width_index < 4 and 0 <= block_index < 256):
+        raise ValueError("rotation block out of range")
+    return width_index * 256 + block_index
+
+
 # Roles whose ternary weights the writer stores as trit5 when asked (model/layout.py:131-133).
 TRIT5_ROLES = (ROLE_ATTN_Q, ROLE_ATTN_K, ROLE_ATTN_V, ROLE_ATTN_OUT, ROLE_FFN_GATE,
                ROLE_FFN_UP, ROLE_FFN_DOWN, ROLE_LM_HEAD, ROLE_ATTN_QKV, ROLE_ATTN_ZGATE,

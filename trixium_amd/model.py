@@ -19,6 +19,7 @@ import numpy as np
 from . import _lib
 from . import layout as L
 from .configs import ModelConfig
+from .hadamard import image_rotation
 
 f32 = np.float32
 
@@ -72,8 +73,6 @@ def make_config(mc, weight_kind, head_kind, head_tied, emb_mode, emb_kind, max_c
 
 
 def config_from_header(h, name="bons-image"):
-    if h["hadamard_block"]:
-        raise NotImplementedError("rotated-basis (Hadamard) images are not supported by the GPU decoder")
     return ModelConfig(name=name, n_layer=h["n_layer"], n_embd=h["n_embd"], n_head=h["n_head"],
                        n_kv_head=h["n_kv_head"], head_dim=h["head_dim"], ffn_dim=h["ffn_dim"],
                        vocab=h["vocab"], rope_theta=float(h["rope_theta"]), rms_eps=float(h["rms_eps"]),
@@ -127,8 +126,20 @@ class Decoder:
         else:
             head_kind = L.KIND_F16 if head["kind"] == L.KIND_F32 else head["kind"]
             emb_kind = emb["kind"] if emb is not None and L.is_ternary(emb["kind"]) else weight_kind
+        rot = image_rotation(img)
+        if rot is not None:
+            # A rotated model: every projection on the row-packet kernel, one kernel per operation,
+            # its input rotated first (the packed GEMV's partial-sum handoffs skip the rotation).
+            if packed_ops not in (PACK_AUTO, 0) or layer_fusion:
+                raise ValueError("a rotated (Hadamard) image runs with packed_ops=0 and no layer fusion")
+            packed_ops, layer_fusion = 0, False
         cfg = make_config(mc, weight_kind, head_kind, head_tied, 0, emb_kind, max_ctx, max_new, layer_fusion,
                           packed_ops)
+        if rot is not None:
+            block, scale, signs = rot
+            cfg.hadamard_block, cfg.hadamard_scale = block, scale
+            for i, w in enumerate(signs):
+                cfg.hadamard_widths[i] = w
         d = cls(mc, cfg, use_graph)
         try:
             d._load_image(img)
@@ -201,6 +212,10 @@ class Decoder:
             for r in roles + _LAYER_MATRICES_FFN:
                 self.set_tensor(r, l, self._rows(img, img.find(r, l), wk))
         self.set_tensor(L.ROLE_OUT_NORM, 0, self._f32(img, L.ROLE_OUT_NORM, 0))
+        rot = image_rotation(img)
+        if rot is not None:
+            for i, (w, sg) in enumerate(rot[2].items()):
+                self.set_tensor(L.ROLE_HADAMARD, i, sg.astype(f32))
         _, mant = img.entry_tensor(img.find(L.ROLE_TOK_EMB16, 0))
         _, ex = img.entry_tensor(img.find(L.ROLE_TOK_EMB16_EXP, 0))
         self.set_tensor(L.ROLE_TOK_EMB16, 0, np.asarray(mant, dtype=np.int16))
