@@ -91,9 +91,12 @@ def trit5_pack(codes):
     byte i within every 128-group, lanes 128 and 129 zero."""
     rows, cols = codes.shape
     g = cols // L.GROUP
-    c = np.zeros((rows, g, 130), dtype=np.uint16)
-    c[:, :, :128] = codes.reshape(rows, g, 128)
-    return (c.reshape(rows, g, 26, 5) * _POW3).sum(axis=3).astype(np.uint8).reshape(rows, g * 26)
+    c = np.asarray(codes, np.uint8).reshape(rows, g, 128)
+    out = np.empty((rows, g, 26), np.uint8)
+    d = c[:, :, :125].reshape(rows, g, 25, 5)
+    out[:, :, :25] = d[..., 0] + 3 * d[..., 1] + 9 * d[..., 2] + 27 * d[..., 3] + 81 * d[..., 4]
+    out[:, :, 25] = c[:, :, 125] + 3 * c[:, :, 126] + 9 * c[:, :, 127]
+    return out.reshape(rows, g * 26)
 
 
 def trit5_unpack(body, cols):
@@ -201,17 +204,20 @@ def embed_bfp_rows(codes, scales):
     m11, e16 = fp16_split(scales)
     rows, cols = codes.shape
     g = cols // L.GROUP
-    q = codes.astype(np.int64).reshape(rows, g, L.GROUP) - 1
+    c = np.asarray(codes, np.uint8).reshape(rows, g, L.GROUP)
     emin = e16.min(axis=1, keepdims=True)
     sh = np.minimum(e16 - emin, 20)
-    live = (q != 0).any(axis=2)
+    live = (c != 1).any(axis=2)
     amax = np.where(live, np.abs(m11) << sh, 0).max(axis=1)
     blen = np.array([int(a).bit_length() for a in amax], dtype=np.int64)
     k2 = blen - 15
-    net = (sh - k2[:, None])[:, :, None]
-    v = q * m11[:, :, None]
-    mant = np.where(net >= 0, v << np.maximum(net, 0), v >> np.maximum(-net, 0))
-    return mant.reshape(rows, cols).astype(np.int16), (emin[:, 0] + k2).astype(np.int32)
+    net = sh - k2[:, None]
+    # A group's mantissas take three values, (code - 1) * m11 shifted by the group's net exponent
+    # (an arithmetic right shift rounds the negative one down): gather them per code.
+    tab = np.stack([-m11, np.zeros_like(m11), m11], axis=2).astype(np.int64)
+    tab = np.where(net[:, :, None] >= 0, tab << np.maximum(net, 0)[:, :, None], tab >> np.maximum(-net, 0)[:, :, None])
+    mant = np.take_along_axis(tab.astype(np.int16), c.astype(np.intp), axis=2)
+    return mant.reshape(rows, cols), (emin[:, 0] + k2).astype(np.int32)
 
 
 def float_bfp_rows(values):

@@ -105,6 +105,21 @@ def _ptq1_order():
 
 
 _QS_IDX, _QH_IDX = _ptq1_order()
+
+
+def _ptq1_runs():
+    """(first byte, bytes, first weight) of each run of five-trit bytes: within a run, trit n of
+    byte j + m is weight base + n c + m, i.e. the run's weights are its bytes' trits digit-major."""
+    runs, e, j = [], 0, 0
+    for c in (32, 16, 8):
+        while j + c <= 24:
+            runs.append((j, c, e))
+            e += 5 * c
+            j += c
+    return runs
+
+
+_RUNS = _ptq1_runs()
 _POW3 = np.array([1, 3, 9, 27, 81], np.uint16)
 
 
@@ -117,9 +132,11 @@ def _trits(q, n):
 def ptq1_0_unpack(raw):
     """(scales fp16 (nb,), codes uint8 (nb, 128) in 0..2)."""
     b = _blocks(raw, BLOCK_PTQ1_0, "PTQ1_0")
-    codes = np.empty((b.shape[0], QK_PTQ1_0), np.uint8)
-    codes[:, _QS_IDX] = _trits(b[:, :24], 5)
-    codes[:, _QH_IDX] = _trits(b[:, 24:26], 4)
+    nb = b.shape[0]
+    codes = np.empty((nb, QK_PTQ1_0), np.uint8)
+    for j, c, e in _RUNS:
+        codes[:, e:e + 5 * c] = _trits(b[:, j:j + c], 5).transpose(0, 2, 1).reshape(nb, 5 * c)
+    codes[:, 120:128] = _trits(b[:, 24:26], 4).transpose(0, 2, 1).reshape(nb, 8)   # weight 120 + 2n + h
     return _scales(b, 26), codes
 
 
