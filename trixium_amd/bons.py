@@ -214,9 +214,19 @@ def embed_bfp_rows(codes, scales):
     net = sh - k2[:, None]
     # A group's mantissas take three values, (code - 1) * m11 shifted by the group's net exponent
     # (an arithmetic right shift rounds the negative one down): gather them per code.
-    tab = np.stack([-m11, np.zeros_like(m11), m11], axis=2).astype(np.int64)
-    tab = np.where(net[:, :, None] >= 0, tab << np.maximum(net, 0)[:, :, None], tab >> np.maximum(-net, 0)[:, :, None])
-    mant = np.take_along_axis(tab.astype(np.int16), c.astype(np.intp), axis=2)
+    # A group's mantissas are (code - 1) * pos, pos = m11 shifted by the group's net exponent,
+    # except that an arithmetic right shift of -m11 rounds down: one less when bits drop out.
+    m = m11.astype(np.int64)
+    up, down = np.maximum(net, 0), np.maximum(-net, 0)
+    pos = np.where(net >= 0, m << up, m >> down).astype(np.int16)
+    low = (np.where(net >= 0, 0, m & ((np.int64(1) << down) - 1)) != 0).astype(np.int16)
+    mant = np.empty((rows, g, L.GROUP), np.int16)
+    for r in range(0, rows, 8192):
+        q = c[r:r + 8192].astype(np.int16) - 1
+        blk = q * pos[r:r + 8192, :, None]
+        if low[r:r + 8192].any():
+            blk -= (q < 0).view(np.int8).astype(np.int16) * low[r:r + 8192, :, None]
+        mant[r:r + 8192] = blk
     return mant.reshape(rows, cols), (emin[:, 0] + k2).astype(np.int32)
 
 

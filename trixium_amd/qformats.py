@@ -124,9 +124,14 @@ _POW3 = np.array([1, 3, 9, 27, 81], np.uint16)
 
 
 def _trits(q, n):
-    """The first n base-3 digits of fixed-point bytes q: digit k = ((q 3^k) mod 256) 3 >> 8."""
-    q = q.astype(np.uint16)[..., None]
-    return ((((q * _POW3[:n]) & 0xFF) * 3) >> 8).astype(np.uint8)
+    """The first n base-3 digits of fixed-point bytes q, (nb, bytes, n): digit k = ((q 3^k) mod
+    256) 3 >> 8, computed in uint8 (the multiply wraps mod 256; t 3 >> 8 is (t >= 86) + (t >= 171))."""
+    q = np.asarray(q, np.uint8)
+    out = np.empty(q.shape + (n,), np.uint8)
+    for k in range(n):
+        t = q * np.uint8(3 ** k)
+        out[..., k] = (t >= 86).view(np.uint8) + (t >= 171).view(np.uint8)
+    return out
 
 
 def ptq1_0_unpack(raw):
