@@ -205,6 +205,52 @@ __global__ __launch_bounds__(256) void dense_gemv_kernel(DenseParams p) {
   if (p.amax_slot && lane == 0 && best) atomicMax(p.amax_slot, best);
 }
 
+// Q8 GEMV for a few rows (the DeltaNet beta|alpha head projections): one block per row, thread t
+// takes the 32-column groups t, t + 256, ... whole (two 16-byte code loads, its scale, x and the
+// gain from global memory), every load issued before the products. With a norm the row's sum is
+// scaled by 1/rms(x) at the end: x^2 and the products reduce together. The weight q*s is rounded
+// to fp16 as the float reference caches every dequantised matrix in fp16.
+__global__ __launch_bounds__(256) void q8_gemv_kernel(DenseParams p) {
+  __shared__ float red[2][4];
+  if (p.gate_pos && *p.gate_pos < *p.gate_from) return;
+  const int m = blockIdx.x, t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const uint8_t* row = p.W + (size_t)m * p.row_bytes;
+  const uint16_t* sc = (const uint16_t*)row;
+  const int8_t* q = (const int8_t*)(row + p.code_off);
+  float acc = 0.f, ss = 0.f;
+  for (int g = t; g < p.K / 32; g += 256) {
+    const int4 c4[2] = {*(const int4*)(q + 32 * g), *(const int4*)(q + 32 * g + 16)};
+    const float s = __half2float(__ushort_as_half(sc[g]));
+    const float4* xv = (const float4*)(p.x + 32 * g);
+    const float4* gv = p.norm_w ? (const float4*)(p.norm_w + 32 * g) : nullptr;
+    const int8_t* cb = (const int8_t*)c4;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float4 x4 = xv[k];
+      const float4 g4 = gv ? gv[k] : make_float4(1.f, 1.f, 1.f, 1.f);
+      const float xs[4] = {x4.x, x4.y, x4.z, x4.w}, gs[4] = {g4.x, g4.y, g4.z, g4.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        ss += xs[i] * xs[i];
+        acc += __half2float(__float2half((float)cb[4 * k + i] * s)) * (xs[i] * gs[i]);
+      }
+    }
+  }
+  acc = wave_sum(acc);
+  ss = wave_sum(ss);
+  if (lane == 0) {
+    red[0][w] = acc;
+    red[1][w] = ss;
+  }
+  __syncthreads();
+  if (t == 0) {
+    float v = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
+    if (p.norm_w) v *= 1.0f / sqrtf(((red[1][0] + red[1][1]) + (red[1][2] + red[1][3])) / (float)p.K + p.eps);
+    if (p.sigmoid) v = sigmoidf_(v);
+    p.y[m] = v;
+  }
+}
+
 // Synthetic weights (csrc side of trixium_amd/synth.py's counter-based generator) ---------------
 
 __device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
@@ -409,6 +455,12 @@ int launch_attention(const AttnParams& p, hipStream_t s) {
 }
 
 int launch_dense_gemv(const DenseParams& p, hipStream_t s) {
+  if (p.kind == TRX_KIND_Q8 && !p.amax_slot && p.K % 32 == 0 && p.code_off % 16 == 0 && p.row_bytes % 16 == 0 &&
+      ((uintptr_t)p.W | (uintptr_t)p.x | (uintptr_t)p.norm_w) % 16 == 0) {
+    hipLaunchKernelGGL(q8_gemv_kernel, dim3(p.M), dim3(256), 0, s, p);
+    TRX_LAUNCHED();
+    return TRX_OK;
+  }
   int blocks = (p.M + 3) / 4;
   if (blocks > 1024) blocks = 1024;
   hipLaunchKernelGGL(dense_gemv_kernel, dim3(blocks), dim3(256), p.K * sizeof(float), s, p);
