@@ -234,6 +234,7 @@ constexpr int kResPartMax = 64;        // producer slices the residual prologue 
 // 16 slices per pass).
 constexpr int kSwiSlicesPerPass = kTgThreads / (2 * kSliceCols / 4), kSwiVec = kSwiPartMax / kSwiSlicesPerPass;
 constexpr int kResSlicesPerPass = kTgThreads / (kSliceCols / 4), kResVec = kResPartMax / kResSlicesPerPass;
+constexpr int kMergeSlicesPerPass = kTgThreads / (kSliceCols / 4), kMergeVec = kMergeMax / kMergeSlicesPerPass;
 // Where x comes from: p.x, the attention splits, SwiGLU of gate|up partial sums, or a residual
 // plus a producer's partial sums.
 constexpr int kXPlain = 0, kXMerge = 1, kXSwiglu = 2, kXResid = 3;
@@ -288,26 +289,24 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   //    weight stream: vmcnt completes in order, so a wait for them would also wait for weights.
   const int cs = s * kSliceCols + tid;
   float xv = 0.f, wv = 1.f, ssin = 0.f;
-  float ov[kMergeMax];
-  float4 pv[kSwiVec > kResVec ? kSwiVec : kResVec];
+  float4 pv[kSwiVec > kResVec ? (kSwiVec > kMergeVec ? kSwiVec : kMergeVec) : (kResVec > kMergeVec ? kResVec : kMergeVec)];
   int ns = 0, h0 = 0, nh = 0;
   if (xmode == kXMerge) {
-    // The slice's attention output from the split partials: every split's o value of this
-    // thread's column in flight, then (m, l) of the slice's heads.
+    // The slice's attention output from the split partials: the splits' o values in flight,
+    // then (m, l) of the slice's heads.
     const AttnMergeSrc& a = p.merge;
     const int T = *a.pos + 1, chunk = (T + a.n_split - 1) / a.n_split;
     ns = min(a.n_split, (T + chunk - 1) / chunk);
     h0 = (s * kSliceCols) / a.hd;
     nh = kSliceCols / a.hd;
-    const int h = cs / a.hd, d = cs - h * a.hd;
-    if (tid < kSliceCols && cs < p.K) {
-      // Splits past ns re-read the last one; their weight is 0.
+    // Thread t loads columns 4 (t % 64) .. + 3 of splits t / 64 and t / 64 + 16 (16 bytes each;
+    // splits past ns re-read the last one, their weight is 0).
+    const int c0 = s * kSliceCols + 4 * (tid % (kSliceCols / 4)), sl = tid / (kSliceCols / 4);
+    const int h = c0 / a.hd, d = c0 - h * a.hd;
 #pragma unroll
-      for (int k = 0; k < kMergeMax; ++k) ov[k] = a.o[((size_t)h * a.n_split + min(k, ns - 1)) * a.hd + d];
-    } else {
-#pragma unroll
-      for (int k = 0; k < kMergeMax; ++k) ov[k] = 0.f;
-    }
+    for (int k = 0; k < kMergeVec; ++k)
+      pv[k] = c0 < p.K ? *(const float4*)(a.o + ((size_t)h * a.n_split + min(sl + kMergeSlicesPerPass * k, ns - 1)) * a.hd + d)
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
     // Split weights of the slice's heads: wave w takes head h0 + w, lane k split k.
     if (w < nh) {
       const int hh = h0 + w;
@@ -395,17 +394,33 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
 
   // 3. The slice's x (times the RMSNorm gain; 1/rms(x) scales the sums), then the table.
   if (xmode == kXMerge) {
+    // Each thread's two splits weighted, the 16 split groups summed through the table's memory
+    // (in group order), then scaled by the heads' 1 / L.
+    __syncthreads();
+    {
+      constexpr int NQ = kSliceCols / 4;
+      const int sl = tid / NQ, hl = (4 * (tid % NQ)) / p.merge.hd;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int k = 0; k < kMergeVec; ++k) {
+        const int sp = sl + kMergeSlicesPerPass * k;
+        const float wk = sp < ns ? amw[hl][sp] : 0.f;
+        v = make_float4(v.x + pv[k].x * wk, v.y + pv[k].y * wk, v.z + pv[k].z * wk, v.w + pv[k].w * wk);
+      }
+      *(float4*)(tab + sl * kSliceCols + 4 * (tid % NQ)) = v;
+    }
     __syncthreads();
     if (tid < kSliceCols && cs < p.K) {
       const int hl = tid / p.merge.hd, h = h0 + hl;
       float o = 0.f;
 #pragma unroll
-      for (int k = 0; k < kMergeMax; ++k) o += ov[k] * amw[hl][k];
+      for (int i = 0; i < kMergeSlicesPerPass; ++i) o += tab[i * kSliceCols + tid];
       o /= atot[hl];
       if (p.merge.gated) o *= sigmoidf_(p.merge.qkv[(size_t)h * 2 * p.merge.hd + p.merge.hd + (cs - h * p.merge.hd)]);
       xv = o;
       if (j == 0) p.merge.out[cs] = o;
     }
+    __syncthreads();                                // the table's memory is rewritten below
   } else if (xmode == kXSwiglu) {
     // Each thread's slices summed, the 8 slice groups through the table's memory (in group
     // order), then per quad x[2q] = silu(r g0) * (r u0), x[2q + 1] = silu(r g1) * (r u1).
