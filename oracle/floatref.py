@@ -259,6 +259,7 @@ class ShapeSample(FloatRef):
         self.rope_n = mc.rope_dims or mc.head_dim
         self.eps = f32(mc.rms_eps)
         self.gated = False
+        self.hb, self.hwidths = 0, []          # plain basis
         self.vocab = mc.vocab
         self.dn = [False] * n_layer
         self.nk = self.hk = self.nv = self.hv = 0

@@ -149,3 +149,14 @@ def test_floatref_mirror_loop_contract(tiny_images, golden):
     b = FloatRef(bons.BONSReader(tiny_images[("tiny-hybrid", False)]))
     p = golden["prompt/tiny-hybrid"]
     assert a.generate(p, 8) == b.generate(p, 8) == golden["mirror_exact_tokens/tiny-hybrid"]
+
+
+def test_shape_sample_steps_like_the_cpu_baseline():
+    """The CPU baseline's sampled decode step (bench.py's cpu_baseline leg) runs on a small shape:
+    a plain-basis reference with random weights and a filled KV cache, logits of the vocabulary."""
+    from oracle.floatref import ShapeSample
+    mc = C.TINY.replace(n_layer=2)
+    s = ShapeSample(mc, 2, 20, seed=0)
+    lg = s.step(1)
+    assert lg.shape == (mc.vocab,) and np.isfinite(lg).all()
+    s.step(2, want_logits=False)
