@@ -93,6 +93,62 @@ __global__ __launch_bounds__(256) void dn_recur_kernel(DnRecurParams p) {
     p.out[(size_t)gpos * hv + i] = o_s[i] * r * p.norm_w[i] * silu(p.z[(size_t)h * hv + i]);
 }
 
+// The same recurrence for head geometries known at compile time: a row's HK columns across HK/4
+// lanes (one float4 each), 64/(HK/4) rows per wave pass, so a load instruction covers whole
+// consecutive rows; each thread keeps its HV/(4*rows per pass) float4 of the state in registers.
+// Row sums (S k and S q) by shuffles within the row's lanes. NW waves per head: more state
+// loads in flight per CU (the grid has only one block per value head).
+template <int HK, int HV, int NW>
+__global__ __launch_bounds__(NW * 64) void dn_recur_fixed_kernel(DnRecurParams p) {
+  constexpr int LPR = HK / 4, RPP = 64 / LPR, NIT = HV / (NW * RPP);
+  static_assert(HK % 4 == 0 && 64 % LPR == 0 && NIT >= 1 && HV % (NW * RPP) == 0, "head geometry");
+  __shared__ float o_s[HV];
+  __shared__ float red[NW];
+  const int h = blockIdx.x, t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const int sub = lane / LPR, c4 = lane % LPR;
+  const int nk = p.nk, nq = nk * HK, kh = h % nk;
+  const float4 k4 = *(const float4*)(p.conv + nq + kh * HK + 4 * c4);
+  const float4 q4 = *(const float4*)(p.conv + kh * HK + 4 * c4);
+  float4* S = (float4*)(p.S + (size_t)h * HV * HK);
+  float4 sv[NIT];
+  float vj[NIT];
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int j = (it * NW + w) * RPP + sub;
+    sv[it] = S[j * LPR + c4];
+    vj[it] = p.conv[2 * nq + h * HV + j];
+  }
+  const float a = p.ba[p.nv + h] + p.dt[h];
+  const float sp = a > 20.f ? a : log1pf(expf(a));
+  const float decay = expf(sp * p.A[h]);
+  const float beta = sigmoidf_(p.ba[h]);
+  const float qs = 1.0f / sqrtf((float)HK);
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int j = (it * NW + w) * RPP + sub;
+    float4 s4 = make_float4(sv[it].x * decay, sv[it].y * decay, sv[it].z * decay, sv[it].w * decay);
+    float dot = (s4.x * k4.x + s4.y * k4.y) + (s4.z * k4.z + s4.w * k4.w);
+#pragma unroll
+    for (int o = LPR >> 1; o >= 1; o >>= 1) dot += __shfl_xor(dot, o, 64);
+    const float delta = (vj[it] - dot) * beta;
+    s4 = make_float4(s4.x + delta * k4.x, s4.y + delta * k4.y, s4.z + delta * k4.z, s4.w + delta * k4.w);
+    S[j * LPR + c4] = s4;
+    float oq = (s4.x * q4.x + s4.y * q4.y) + (s4.z * q4.z + s4.w * q4.w);
+#pragma unroll
+    for (int o = LPR >> 1; o >= 1; o >>= 1) oq += __shfl_xor(oq, o, 64);
+    if (c4 == 0) o_s[j] = oq * qs;
+  }
+  __syncthreads();
+  // Gated RMSNorm over the head, then the grouped output position.
+  float ss = 0.f;
+  for (int i = t; i < HV; i += NW * 64) ss += o_s[i] * o_s[i];
+  ss = block_sum(ss, red);
+  const float r = 1.0f / sqrtf(ss / (float)HV + p.eps);
+  const int gpos = kh * (p.nv / nk) + h / nk;
+  for (int i = t; i < HV; i += NW * 64)
+    p.out[(size_t)gpos * HV + i] = o_s[i] * r * p.norm_w[i] * silu(p.z[(size_t)h * HV + i]);
+}
+
 int launch_dn_conv(const DnConvParams& p, hipStream_t s) {
   TRX_CHECK(p.hk <= 256 && p.C % p.hk == 0, TRX_E_INVALID, "deltanet conv: head dim %d", p.hk);
   hipLaunchKernelGGL(dn_conv_kernel, dim3(p.C / p.hk), dim3(p.hk), 8 * sizeof(float), s, p);
@@ -104,7 +160,13 @@ int launch_dn_recur(const DnRecurParams& p, hipStream_t s) {
   TRX_CHECK(p.hv <= 256 && 256 % p.hv == 0 && p.hk % (256 / p.hv) == 0 && p.hk / (256 / p.hv) <= 64 &&
             p.hk <= 512 && p.hv <= 512 && p.nv % p.nk == 0, TRX_E_INVALID,
             "deltanet recurrence: unsupported head geometry hk=%d hv=%d", p.hk, p.hv);
-  hipLaunchKernelGGL(dn_recur_kernel, dim3(p.nv), dim3(256), 0, s, p);
+  const bool aligned = ((uintptr_t)p.S | (uintptr_t)p.conv) % 16 == 0 && (p.nk * p.hk) % 4 == 0;
+  if (aligned && p.hk == 128 && p.hv == 128)
+    hipLaunchKernelGGL((dn_recur_fixed_kernel<128, 128, 16>), dim3(p.nv), dim3(1024), 0, s, p);
+  else if (aligned && p.hk == 64 && p.hv == 64)
+    hipLaunchKernelGGL((dn_recur_fixed_kernel<64, 64, 16>), dim3(p.nv), dim3(1024), 0, s, p);
+  else
+    hipLaunchKernelGGL(dn_recur_kernel, dim3(p.nv), dim3(256), 0, s, p);
   TRX_LAUNCHED();
   return TRX_OK;
 }
