@@ -298,13 +298,13 @@ __device__ __forceinline__ void attn_merge_body(const AttnParams& p, int qh) {
   const float* po = p.part_o + (size_t)qh * S * hd;
   for (int d = tid; d < hd; d += blockDim.x) {
     float o = 0.f;
-    // Eight independent loads per round keep the memory pipeline full.
-    for (int s0 = 0; s0 < ns; s0 += 8) {
-      float v[8];
+    // 32 independent loads per round: 64 splits in two round trips.
+    for (int s0 = 0; s0 < ns; s0 += 32) {
+      float v[32];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = (s0 + k < ns) ? ld_vec<FUSED>(po + (size_t)(s0 + k) * hd + d) : 0.f;
+      for (int k = 0; k < 32; ++k) v[k] = (s0 + k < ns) ? ld_vec<FUSED>(po + (size_t)(s0 + k) * hd + d) : 0.f;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) o += (s0 + k < ns) ? v[k] * wsp[s0 + k] : 0.f;
+      for (int k = 0; k < 32; ++k) o += (s0 + k < ns) ? v[k] * wsp[s0 + k] : 0.f;
     }
     if (p.gated) o *= sigmoidf_(ld_vec<FUSED>(p.qkv + (size_t)qh * 2 * hd + hd + d));
     st_vec<FUSED>(p.out + (size_t)qh * hd + d, o);

@@ -534,9 +534,13 @@ static int run_step(Model& m, hipStream_t s) {
       const bool fd = attention_fd_supported(ap.n_rep, hd, ap.rope_n, ap.n_split);
       const PackedMat* po = packed(OP_O, l);
       const bool merge_in_o = fd && po && ap.n_split <= 32 && kSliceCols % hd == 0;
-      ap.done = merge_in_o ? nullptr : m.attn_done;
+      // Otherwise the splits are merged by the last split block of each kv head, or, when that
+      // block would read many partials alone, by a merge launch with one block per q head.
+      const bool merge_apart = !merge_in_o && ap.n_split * ap.n_rep * hd > 8192;
+      ap.done = merge_in_o || merge_apart ? nullptr : m.attn_done;
       if (fd) {
         if ((rc = launch_attention_fd(ap, s))) return rc;
+        if (merge_apart && (rc = launch_attention_merge(ap, s))) return rc;
       } else if ((rc = launch_attention(ap, s))) {
         return rc;
       }

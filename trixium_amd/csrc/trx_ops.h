@@ -110,6 +110,8 @@ int launch_attention(const AttnParams& p, hipStream_t s);
 // in `out`), left for the consumer to merge otherwise (attn_merge_into_x, the packed o GEMV).
 bool attention_fd_supported(int rep, int hd, int rope_n, int n_split);
 int launch_attention_fd(const AttnParams& p, hipStream_t s);
+// The split partials of attention_fd merged by one block per q head (into `out`).
+int launch_attention_merge(const AttnParams& p, hipStream_t s);
 int attention_splits(int n_kv, int head_dim, int max_ctx);   // -1: the context is too long
 int attention_max_chunk(int head_dim);                          // positions one split can hold
 int launch_dense_gemv(const DenseParams& p, hipStream_t s);

@@ -439,6 +439,12 @@ static int launch_attn_rep(const AttnParams& p, hipStream_t s) {
   return TRX_OK;
 }
 
+int launch_attention_merge(const AttnParams& p, hipStream_t s) {
+  hipLaunchKernelGGL(attn_merge_kernel, dim3(p.n_head), dim3(hd_threads(p.hd)), 0, s, p);
+  TRX_LAUNCHED();
+  return TRX_OK;
+}
+
 int launch_attention(const AttnParams& p, hipStream_t s) {
   const int cap = p.hd == 64 ? attn_max_chunk<64>() : p.hd == 128 ? attn_max_chunk<128>() : attn_max_chunk<256>();
   TRX_CHECK(p.rope_n <= p.hd && p.rope_n % 2 == 0, TRX_E_INVALID, "attention: rope dims %d", p.rope_n);
