@@ -196,8 +196,9 @@ typedef struct {
      ternary projection but the DeltaNet beta/alpha takes x' = hadamard_scale * H (s * xhat)
      blockwise over hadamard_block columns (H the +-1 Sylvester matrix, s the width's signs,
      xhat the normalised input), computed by a fast Walsh-Hadamard transform before the GEMV.
-     0 = plain basis. A rotated model runs every projection on the row-packet kernel, one per
-     operation (packed_ops and layer_fusion must be 0). */
+     0 = plain basis. A rotated model runs one kernel per operation (layer_fusion 0): its
+     projections take the rotated input as a plain vector, on the packed GEMV where packed_ops
+     selects it, without the partial-sum handoffs between packed GEMVs. */
   int hadamard_block;          /* 0, or a power of two in [64, 1024] dividing every width */
   float hadamard_scale;        /* the rotation tensors' scale (a power of two) */
   int hadamard_widths[4];      /* the rotated input widths (0 = unused); signs per width as

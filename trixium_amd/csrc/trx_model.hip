@@ -477,7 +477,10 @@ static int run_step(Model& m, hipStream_t s) {
     x = nullptr;
     return &pin;
   };
+  // The packed GEMV's own launches below (partial-sum handoffs, the attention merge in o's
+  // prologue) take no rotation: a rotated model runs every projection through projection().
   auto packed = [&](int op, int l) -> const PackedMat* {
+    if (c.hadamard_block) return nullptr;
     auto it = m.packed.find({op, l});
     return it == m.packed.end() ? nullptr : &it->second;
   };
@@ -690,9 +693,8 @@ TRX_API int trx_model_create(const trx_model_config* cfg, const float* rope_freq
     const int B = c.hadamard_block;
     TRX_CHECK(B >= 64 && B <= 1024 && (B & (B - 1)) == 0 && c.hadamard_scale > 0.f, TRX_E_INVALID,
               "trx_model_create: Hadamard block %d unsupported", B);
-    TRX_CHECK(c.packed_ops == 0 && !c.layer_fusion && (c.head_tied || c.head_kind != TRX_KIND_F16),
-              TRX_E_INVALID, "trx_model_create: a rotated model runs the row-packet kernel, one per operation, "
-              "with a ternary head (packed_ops 0, layer_fusion 0)");
+    TRX_CHECK(!c.layer_fusion && (c.head_tied || c.head_kind != TRX_KIND_F16), TRX_E_INVALID,
+              "trx_model_create: a rotated model runs one kernel per operation with a ternary head");
     for (int i = 0; i < 4; ++i)
       TRX_CHECK(c.hadamard_widths[i] >= 0 && c.hadamard_widths[i] % B == 0, TRX_E_INVALID,
                 "trx_model_create: rotation width %d is not a multiple of the block", c.hadamard_widths[i]);

@@ -128,11 +128,10 @@ class Decoder:
             emb_kind = emb["kind"] if emb is not None and L.is_ternary(emb["kind"]) else weight_kind
         rot = image_rotation(img)
         if rot is not None:
-            # A rotated model: every projection on the row-packet kernel, one kernel per operation,
-            # its input rotated first (the packed GEMV's partial-sum handoffs skip the rotation).
-            if packed_ops not in (PACK_AUTO, 0) or layer_fusion:
-                raise ValueError("a rotated (Hadamard) image runs with packed_ops=0 and no layer fusion")
-            packed_ops, layer_fusion = 0, False
+            # A rotated model: one kernel per operation, every projection's input rotated first
+            # (no partial-sum handoffs between packed GEMVs, no fused layers).
+            if layer_fusion:
+                raise ValueError("a rotated (Hadamard) image runs without layer fusion")
         cfg = make_config(mc, weight_kind, head_kind, head_tied, 0, emb_kind, max_ctx, max_new, layer_fusion,
                           packed_ops)
         if rot is not None:
