@@ -189,8 +189,8 @@ typedef struct {
   int packed_ops;              /* projections run by the packed GEMV (trx_gemv_packed_f32) over
                                   a packed copy of their rows, as TRX_PACK_* bits; the others run
                                   trx_gemv_ternary_f32's kernel. TRX_PACK_AUTO: the library's
-                                  choice (q|k|v, o, gate|up, down, ternary LM head; DeltaNet
-                                  projections on the row-packet kernel). (With layer_fusion the
+                                  choice (every projection: q|k|v, o, gate|up, down, the ternary
+                                  LM head, the DeltaNet qkv|z and out). (With layer_fusion the
                                   fused layers keep the row-packet kernel.) */
   /* PrismML's rotated weight basis (model/golden.py:250-289, model/fastref.py:127-140): every
      ternary projection but the DeltaNet beta/alpha takes x' = hadamard_scale * H (s * xhat)

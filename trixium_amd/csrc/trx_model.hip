@@ -181,11 +181,10 @@ static uint8_t* P(Model& m, int role, int layer);
 static int plan_packed(Model& m) {
   const trx_model_config& c = m.cfg;
   int ops = c.packed_ops;
-  // Measured on the 8B shape: the packed GEMV is the faster kernel for every attention-layer
-  // projection and the head, in both code formats. DeltaNet projections stay on the row-packet
-  // kernel until measured at a hybrid shape.
-  if (ops == TRX_PACK_AUTO)
-    ops = TRX_PACK_QKV | TRX_PACK_O | TRX_PACK_GATE_UP | TRX_PACK_DOWN | TRX_PACK_HEAD;
+  // Measured: the packed GEMV is the faster kernel for every attention-layer projection and the
+  // head at the 8B shape, in both code formats, and for the DeltaNet qkv|z and out projections
+  // at the 27B hybrid's widths.
+  if (ops == TRX_PACK_AUTO) ops = TRX_PACK_ALL;
   TRX_CHECK(ops >= 0 && (ops & ~TRX_PACK_ALL) == 0, TRX_E_INVALID, "packed_ops %d has unknown bits", c.packed_ops);
   const int E = c.n_embd, hd = c.head_dim, F = c.ffn_dim, wk = c.weight_kind;
   const int qrows = c.n_head * hd * (c.attn_gated ? 2 : 1), kvrows = c.n_kv_head * hd;
