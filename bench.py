@@ -50,6 +50,9 @@ def parse_args():
     ap.add_argument("--kernel-reps", type=int, default=10,
                     help="passes over the 36 layers when timing the dominant kernel")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--sampling", default=None, metavar="T,P,R",
+                    help="sample with temperature T, top-p P and repetition penalty R instead of the "
+                         "greedy argmax (the firmware's sampler; not the headline workload)")
     ap.add_argument("--no-graph", action="store_true", help="launch every kernel eagerly")
     ap.add_argument("--packed-ops", type=int, default=-1,
                     help="projections on the packed GEMV, as TRX_PACK_* bits (-1: the library's "
@@ -202,6 +205,9 @@ def main():
     dec = Decoder.synthetic(mc, a.seed, weight_kind=kind, max_ctx=mc.max_ctx, max_new=n_dec + 8,
                             use_graph=graph, layer_fusion=a.fusion, packed_ops=a.packed_ops)
     prompt = np.random.default_rng(a.seed).integers(0, mc.vocab, a.prompt).astype(np.int32)
+    if a.sampling:
+        t, p_, r = (float(v) for v in a.sampling.split(","))
+        dec.set_sampling(t, p_, r, seed=a.seed + 1)
     dec.reset()
     dec.feed(prompt)
     dec.step(a.prompt)                           # prefill, one position per forward
@@ -250,8 +256,9 @@ def main():
         "vs_baseline": None,
         "dtype": f"ternary weights (fp16 group scales), {acts}, fp32 accumulate, fp16 KV",
         "data": "synthetic: random ternary weights from a counter-based hash, random prompt",
-        "config": {"workload": "qwen3-8b-shape ternary decoder, batch-1 greedy decode after a "
-                               f"{a.prompt}-token prompt",
+        "config": {"workload": "qwen3-8b-shape ternary decoder, batch-1 "
+                               + (f"sampled (T,P,R={a.sampling})" if a.sampling else "greedy")
+                               + f" decode after a {a.prompt}-token prompt",
                    "n_layer": mc.n_layer, "n_embd": mc.n_embd, "n_head": mc.n_head,
                    "n_kv_head": mc.n_kv_head, "head_dim": mc.head_dim, "ffn_dim": mc.ffn_dim,
                    "vocab": mc.vocab, "max_ctx": mc.max_ctx, "prompt_tokens": a.prompt,

@@ -218,6 +218,15 @@ typedef struct trx_model trx_model;
 
 /* rope_freq: rope_dims/2 float32 frequencies theta^(-2i/rope_dims) (fastref.py:62-63). */
 int trx_model_create(const trx_model_config* cfg, const float* rope_freq, trx_model** out);
+/* Sampling instead of the greedy argmax (firmware/infer.c:385-488, infer_set_sampling): the
+   candidates are the maxima of 32 row ranges of each of n_channels vocabulary shards (the
+   image's channel count reproduces the FPGA's candidate set); a repetition penalty
+   (logit / repetition above zero, logit * repetition below) on candidates among the last 64
+   tokens; then softmax(logit / temperature), the smallest top_p prefix of the sorted mass, one
+   xorshift32 draw (seed 0 keeps the stream). temperature 0 with repetition 1 is the greedy
+   argmax (no extra launch). */
+int trx_model_set_sampling(trx_model* m, float temperature, float top_p, float repetition, uint32_t seed,
+                           int n_channels);
 int trx_model_destroy(trx_model* m);
 /* Upload one tensor (synchronous). Ternary and Q8: BONS row packets of the model's kind; F32:
  * float32 values; F16 head: fp16 values; TOK_EMB16: int16 [vocab, n_embd]; TOK_EMB16_EXP: int32

@@ -78,6 +78,7 @@ SIGNATURES = {
     "trx_model_create": [_mcp, _fp, ctypes.POINTER(_vp)],
     "trx_model_destroy": [_vp],
     "trx_model_set_tensor": [_vp, _i, _i, _vp, _sz],
+    "trx_model_set_sampling": [_vp, ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_uint32, _i],
     "trx_model_synthesize": [_vp, ctypes.c_uint32, _fp],
     "trx_model_reset": [_vp],
     "trx_model_set_prompt": [_vp, _ip, _i, _i],

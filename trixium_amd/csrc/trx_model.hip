@@ -86,6 +86,11 @@ struct Model {
   int head_S = 0, head_rows_p = 0;
   float* x2 = nullptr;                             // second residual buffer (x alternates)
   float* xrot = nullptr;                           // a rotated model's projection input
+  // Sampling (trx_model_set_sampling): temperature, top_p, repetition, then the xorshift32 state.
+  float* smp = nullptr;
+  unsigned long long* smp_cand = nullptr;          // [32] slice candidates, then the counter
+  bool sampling = false;
+  int smp_channels = 1;
   float* hidden = nullptr;                         // the residual after the last layer
   hipGraph_t graph = nullptr;
   hipGraphExec_t graph_exec = nullptr;
@@ -664,6 +669,12 @@ static int run_step(Model& m, hipStream_t s) {
                           PF(m, TRX_ROLE_OUT_NORM, 0), m.logits, TRX_EPI_STORE, nullptr, s, m.slot, m.pos(),
                           m.head_from()))) return rc;
   }
+  if (m.sampling) {
+    SampleParams sp = {m.logits, c.vocab, m.smp_channels, 64, m.pos(), m.head_from(), m.n_prompt(), m.prompt(),
+                       m.out(), c.max_new, m.smp, (uint32_t*)(m.smp + 3), m.slot, m.smp_cand,
+                       (unsigned*)(m.smp_cand + 32)};
+    if ((rc = launch_sample(sp, s))) return rc;
+  }
   m.hidden = xc;
   return TRX_OK;
 }
@@ -768,6 +779,15 @@ TRX_API int trx_model_create(const trx_model_config* cfg, const float* rope_freq
   if ((rc = dalloc(m, (void**)&m.rope_dev, (size_t)rope_n * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.ctl, (size_t)(8 + c.max_ctx + c.max_new) * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.slot, 8))) return fail(rc);
+  if ((rc = dalloc(m, (void**)&m.smp, 16))) return fail(rc);
+  if ((rc = dalloc(m, (void**)&m.smp_cand, 33 * 8))) return fail(rc);
+  TRX_HIP(hipMemset(m.smp_cand, 0, 33 * 8));
+  {
+    const float cfg0[4] = {0.f, 1.f, 1.f, 0.f};
+    const uint32_t rng0 = 0x9E3779B9u;         // the firmware's initial stream
+    TRX_HIP(hipMemcpy(m.smp, cfg0, 16, hipMemcpyHostToDevice));
+    TRX_HIP(hipMemcpy(m.smp + 3, &rng0, 4, hipMemcpyHostToDevice));
+  }
   TRX_HIP(hipMemcpy(m.rope_dev, m.rope_freq.data(), m.rope_freq.size() * 4, hipMemcpyHostToDevice));
   {
     hipError_t e = hipStreamCreateWithFlags(&m.stream, hipStreamNonBlocking);
@@ -787,6 +807,30 @@ TRX_API int trx_model_destroy(trx_model* h) {
   for (void* p : m.allocs) (void)hipFree(p);
   if (m.stream) (void)hipStreamDestroy(m.stream);
   delete h;
+  return TRX_OK;
+}
+
+TRX_API int trx_model_set_sampling(trx_model* h, float temperature, float top_p, float repetition,
+                                   uint32_t seed, int n_channels) {
+  TRX_CHECK(h && n_channels >= 1, TRX_E_INVALID, "trx_model_set_sampling: bad argument");
+  Model& m = h->m;
+  // firmware/infer.c:401-407: a negative temperature is 0, top_p outside (0, 1] is 1, a
+  // repetition below 1 is 1, seed 0 keeps the stream.
+  const float cfg[3] = {temperature < 0.f ? 0.f : temperature, (top_p <= 0.f || top_p > 1.f) ? 1.f : top_p,
+                        repetition < 1.f ? 1.f : repetition};
+  TRX_HIP(hipStreamSynchronize(m.stream));
+  TRX_HIP(hipMemcpy(m.smp, cfg, 12, hipMemcpyHostToDevice));
+  if (seed) TRX_HIP(hipMemcpy(m.smp + 3, &seed, 4, hipMemcpyHostToDevice));
+  const bool on = cfg[0] > 0.f || cfg[2] > 1.f;
+  if (on != m.sampling || n_channels != m.smp_channels) {
+    // The captured position has (or lacks) the sampling launch: capture again.
+    if (m.graph_exec) (void)hipGraphExecDestroy(m.graph_exec);
+    if (m.graph) (void)hipGraphDestroy(m.graph);
+    m.graph_exec = nullptr;
+    m.graph = nullptr;
+  }
+  m.sampling = on;
+  m.smp_channels = n_channels;
   return TRX_OK;
 }
 

@@ -101,7 +101,28 @@ struct RotParams {
 int launch_rotate(const RotParams& p, hipStream_t s);
 int launch_dn_conv(const DnConvParams& p, hipStream_t s);
 int launch_dn_recur(const DnRecurParams& p, hipStream_t s);
+// Sampling of the next token (firmware/infer.c:385-488): the candidates are the maxima of 32 row
+// ranges of every channel's vocabulary shard; a repetition penalty over the last `window` tokens,
+// then temperature, top-p over the candidates and one xorshift32 draw. The pick replaces the
+// argmax in *slot. Nothing on positions before head_from.
+struct SampleParams {
+  const float* logits;
+  int vocab, n_ch, window;
+  const int* pos;
+  const int* head_from;
+  const int* n_prompt;
+  const int* prompt;
+  const int* out;
+  int max_out;
+  const float* cfg;        // temperature, top_p, repetition
+  uint32_t* rng;           // xorshift32 state
+  unsigned long long* slot;
+  unsigned long long* cand;  // [32] the slices' (value bits, token) between the blocks
+  unsigned* done;            // blocks finished (zero between launches)
+};
+
 int launch_embed(const EmbedParams& p, hipStream_t s);
+int launch_sample(const SampleParams& p, hipStream_t s);
 int launch_finalize(const int* pos, const int* n_prompt, unsigned long long* slot, int* out, int max_out,
                     hipStream_t s);
 int launch_attention(const AttnParams& p, hipStream_t s);

@@ -334,6 +334,150 @@ __global__ void synth_f32_kernel(float* out, long long n, uint32_t seed, uint32_
   }
 }
 
+// Sampling ----------------------------------------------------------------------------------------
+
+constexpr int kSmpSlices = 32, kSmpWindowMax = 960;
+
+// One block per slice: its maximum over every channel's rows of the slice (first maximum in
+// channel-major order, i.e. the smallest token) into cand; the block that finishes last (an
+// agent-scope counter) picks among the 32.
+__global__ __launch_bounds__(1024) void sample_kernel(SampleParams p) {
+  __shared__ float cval[kSmpSlices], wv[16];
+  __shared__ int ctok[kSmpSlices], wi[16];
+  __shared__ int win[kSmpWindowMax];
+  __shared__ float lg[kSmpSlices], pr[kSmpSlices];
+  __shared__ int tk[kSmpSlices], ord[kSmpSlices], seen[kSmpSlices], n_s;
+  __shared__ bool last;
+  const int pos = *p.pos;
+  if (pos < *p.head_from) return;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, k = blockIdx.x;
+  const int rpc = (p.vocab + p.n_ch - 1) / p.n_ch, srows = (rpc + kSmpSlices - 1) / kSmpSlices;
+  const int r0 = k * srows, rows = max(0, min(srows, rpc - r0));
+  float best = -INFINITY;
+  int btok = 0x7FFFFFFF;
+  for (int c = 0; c < p.n_ch; ++c) {
+    const int base = c * rpc + r0;
+    for (int i0 = 0; i0 < rows; i0 += 4 * 1024) {
+      float v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = i0 + u * 1024 + t, tok = base + i;
+        v[u] = i < rows && tok < p.vocab ? p.logits[tok] : -INFINITY;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int tok = base + i0 + u * 1024 + t;
+        if (v[u] > best || (v[u] == best && v[u] > -INFINITY && tok < btok)) best = v[u], btok = tok;
+      }
+    }
+  }
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float ob = __shfl_xor(best, o, 64);
+    const int ot = __shfl_xor(btok, o, 64);
+    if (ob > best || (ob == best && ot < btok)) best = ob, btok = ot;
+  }
+  if (lane == 0) {
+    wv[w] = best;
+    wi[w] = btok;
+  }
+  __syncthreads();
+  if (t == 0) {
+    for (int i = 1; i < 16; ++i)
+      if (wv[i] > wv[0] || (wv[i] == wv[0] && wi[i] < wi[0])) wv[0] = wv[i], wi[0] = wi[i];
+    __hip_atomic_store(p.cand + k, ((unsigned long long)__float_as_uint(wv[0]) << 32) |
+                                       (unsigned)(wi[0] == 0x7FFFFFFF ? 0xFFFFFFFFu : (unsigned)wi[0]),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __atomic_thread_fence(__ATOMIC_RELEASE);
+    const unsigned old = __hip_atomic_fetch_add(p.done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    last = old == kSmpSlices - 1;
+    if (last) __hip_atomic_store(p.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!last) return;
+  // The candidates and the token window staged by the block's threads (one load each); the
+  // penalty's membership tests and the sort ranks in parallel; the sums and the draw on thread 0
+  // in the firmware's order (the same float rounding).
+  const int np = *p.n_prompt, j0 = max(0, pos + 1 - p.window), nwin = pos + 1 - j0;
+  if (t < kSmpSlices) {
+    const unsigned long long c = __hip_atomic_load(p.cand + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    cval[t] = __uint_as_float((uint32_t)(c >> 32));
+    ctok[t] = (uint32_t)c == 0xFFFFFFFFu ? -1 : (int)(uint32_t)c;
+    seen[t] = 0;
+  } else if (t >= 64 && t - 64 < nwin) {
+    const int j = j0 + t - 64, g = j - np;   // position j: a prompt token or generated token g
+    win[t - 64] = j < np ? p.prompt[j] : (g < p.max_out ? p.out[g] : -1);
+  }
+  __syncthreads();
+  const float temp = p.cfg[0], top_p = p.cfg[1], rep = p.cfg[2];
+  if (rep > 1.0f)
+    for (int idx = t; idx < kSmpSlices * nwin; idx += 1024) {
+      const int q = idx / nwin;
+      if (ctok[q] >= 0 && win[idx - q * nwin] == ctok[q]) seen[q] = 1;
+    }
+  __syncthreads();
+  if (t == 0) {
+    int n = 0, bi = 0;
+    for (int q = 0; q < kSmpSlices; ++q) {
+      if (ctok[q] < 0) continue;
+      float v = cval[q];
+      if (rep > 1.0f && seen[q]) v = v > 0.f ? v / rep : v * rep;
+      lg[n] = v;
+      tk[n] = ctok[q];
+      if (v > lg[bi]) bi = n;
+      ++n;
+    }
+    n_s = n;
+    if (n == 0) {
+      n_s = -1;
+    } else if (temp <= 0.0f) {
+      n_s = -1;
+      *p.slot = (1ull << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)tk[bi]);
+    }
+  }
+  __syncthreads();
+  const int n = n_s;
+  if (n <= 0) return;
+  if (t < n) {
+    // Rank in the stable descending order: the larger values, then the equal ones before it.
+    const float v = lg[t];
+    int r = 0;
+    for (int i = 0; i < n; ++i) r += lg[i] > v || (lg[i] == v && i < t);
+    ord[r] = t;
+  }
+  __syncthreads();
+  if (t < n) pr[t] = expf((lg[ord[t]] - lg[ord[0]]) / temp);
+  __syncthreads();
+  if (t != 0) return;
+  float sum = 0.f;
+  for (int i = 0; i < n; ++i) sum += pr[i];
+  float acc = 0.f;
+  const float cut = top_p * sum;
+  int keep = n;
+  for (int i = 0; i < n; ++i) {              // the smallest prefix holding top_p of the mass
+    acc += pr[i];
+    if (acc >= cut) {
+      keep = i + 1;
+      break;
+    }
+  }
+  uint32_t x = *p.rng;
+  x ^= x << 13;
+  x ^= x >> 17;
+  x ^= x << 5;
+  *p.rng = x;
+  const float r = (float)(x >> 8) * (1.0f / 16777216.0f) * acc;
+  float c = 0.f;
+  int pick = tk[ord[keep - 1]];
+  for (int i = 0; i < keep; ++i) {
+    c += pr[i];
+    if (r < c) {
+      pick = tk[ord[i]];
+      break;
+    }
+  }
+  *p.slot = (1ull << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)pick);
+}
+
 // PrismML rotation ------------------------------------------------------------------------------
 
 // One workgroup of B threads per block of columns. With a norm every workgroup sums x^2 over the
@@ -374,6 +518,14 @@ __global__ __launch_bounds__(1024) void rotate_kernel(RotParams p) {
 }
 
 // Launchers ------------------------------------------------------------------------------------
+
+int launch_sample(const SampleParams& p, hipStream_t s) {
+  TRX_CHECK(p.n_ch >= 1 && p.vocab > 0 && p.window >= 0 && p.window <= kSmpWindowMax, TRX_E_INVALID,
+            "sampling: bad parameters");
+  hipLaunchKernelGGL(sample_kernel, dim3(kSmpSlices), dim3(1024), 0, s, p);
+  TRX_LAUNCHED();
+  return TRX_OK;
+}
 
 int launch_rotate(const RotParams& p, hipStream_t s) {
   TRX_CHECK(p.B >= 64 && p.B <= 1024 && (p.B & (p.B - 1)) == 0 && p.K > 0 && p.K % p.B == 0 && p.x != p.y,

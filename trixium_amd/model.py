@@ -140,6 +140,7 @@ class Decoder:
             for i, w in enumerate(signs):
                 cfg.hadamard_widths[i] = w
         d = cls(mc, cfg, use_graph)
+        d.n_channels = img.header["n_channels"]
         try:
             d._load_image(img)
         except Exception:
@@ -228,6 +229,16 @@ class Decoder:
                 self.set_tensor(L.ROLE_LM_HEAD, 0, w.astype(np.float16))
             else:
                 self.set_tensor(L.ROLE_LM_HEAD, 0, self._rows(img, head, cfg.head_kind))
+
+    def set_sampling(self, temperature=0.0, top_p=1.0, repetition=1.0, seed=0, n_channels=None):
+        """Sample instead of the greedy argmax, as the firmware's `sample` does
+        (firmware/infer.c:385-488): candidates are the maxima of 32 row ranges of each of
+        n_channels vocabulary shards (default: the image's channel count), a repetition penalty
+        over the last 64 tokens, temperature, top-p, an xorshift32 stream (seed 0 keeps it).
+        temperature 0 and repetition 1 restore the greedy argmax."""
+        n = int(n_channels or getattr(self, "n_channels", 1))
+        _lib.call("trx_model_set_sampling", self._h, float(temperature), float(top_p), float(repetition),
+                  int(seed) & 0xFFFFFFFF, n)
 
     # State and decoding ------------------------------------------------------------------------
     def reset(self):
