@@ -320,3 +320,28 @@ def test_rotated_image_decodes_like_fastref(tmp_path, case):
     toks = dec.generate(prompt, 6)
     dec2 = _decoder(p, use_graph=False)
     assert toks == dec2.generate(prompt, 6)
+
+
+@pytest.mark.parametrize("block", [512, 1024])
+def test_rotation_in_the_gemv_prologue(tmp_path, block):
+    """Rotation blocks wider than the packed GEMV's 256-column slice: every GEMV block transforms
+    the whole rotation block holding its slice. The packed path (rotation in the GEMV prologue)
+    against the oracle's rotation tensors and against the row-packet path (a separate rotation
+    launch), every position of a teacher-forced run."""
+    from trixium_amd import hadamard as H
+    cfg = C.TINY.replace(name="rot-wide", n_layer=2, n_embd=1024, n_head=8, n_kv_head=2, head_dim=128,
+                         ffn_dim=2048, vocab=512, max_ctx=64, tie_embeddings=False)
+    rng = np.random.default_rng(block)
+    signs = {w: tuple(int(v) for v in np.where(rng.random(w) < 0.5, -1, 1)) for w in (1024, 2048)}
+    rcfg = cfg.replace(hadamard_block=block, hadamard_signs=signs)
+    specs = synth.small_model_tensors(cfg, 9, fp16_embedding=False) + H.rotation_specs(rcfg)
+    p = str(tmp_path / "rot.bons")
+    bons.write_image(rcfg, specs, 1, p, trit5=True)
+    prompt = synth.random_prompt(cfg, 6, 9)
+    ref = FloatRef(bons.BONSReader(p), kv_fp16=True)
+    want = [ref.forward(prompt[:1])] + [ref.step(t) for t in prompt[1:]]
+    for packed in (-1, 0):
+        dec = _decoder(p, packed_ops=packed)
+        got = [dec.forward(prompt[:1])] + [dec.forward([t]) for t in prompt[1:]]
+        for g, w in zip(got, want):
+            assert _rel_err(g, w) <= 2e-3, (packed, _rel_err(g, w))

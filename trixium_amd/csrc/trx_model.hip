@@ -304,18 +304,25 @@ static int projection(Model& m, int op, int l, const uint8_t* rows, int kind, in
                       const float* norm_w, float* y, int epi, const float* resid, hipStream_t s,
                       unsigned long long* amax = nullptr, const int* gate_pos = nullptr,
                       const int* gate_from = nullptr) {
+  auto it = m.packed.find({op, l});
   if (m.cfg.hadamard_block) {
     int wi = 0;
     while (wi < 4 && m.cfg.hadamard_widths[wi] != K) ++wi;
     TRX_CHECK(wi < 4, TRX_E_INVALID, "rotated model: no rotation for input width %d", K);
-    RotParams rp = {x, norm_w, m.cfg.rms_eps, K, m.cfg.hadamard_block, PF(m, TRX_ROLE_HADAMARD, wi),
-                    m.cfg.hadamard_scale, m.xrot};
+    const float* signs = PF(m, TRX_ROLE_HADAMARD, wi);
+    const int B = m.cfg.hadamard_block;
+    if (it != m.packed.end() && K % std::max(B, kSliceCols) == 0) {
+      // The packed GEMV rotates its own slice of x in its prologue.
+      const RotSrc rs = {signs, B, m.cfg.hadamard_scale};
+      return tgemv_f32(it->second.buf, kind, M, K, x, norm_w, m.cfg.rms_eps, y, epi, resid, amax, m.pack_work, s,
+                       gate_pos, gate_from, nullptr, nullptr, &rs);
+    }
+    RotParams rp = {x, norm_w, m.cfg.rms_eps, K, B, signs, m.cfg.hadamard_scale, m.xrot};
     int rc;
     if ((rc = launch_rotate(rp, s))) return rc;
     x = m.xrot;
     norm_w = nullptr;
   }
-  auto it = m.packed.find({op, l});
   if (it != m.packed.end())
     return tgemv_f32(it->second.buf, kind, M, K, x, norm_w, m.cfg.rms_eps, y, epi, resid, amax, m.pack_work, s,
                      gate_pos, gate_from);

@@ -113,9 +113,19 @@ int tgemv_partial_slices_max();
 // The same for a residual input.
 int tgemv_resid_slices_max();
 
+// A PrismML rotation of the GEMV's input, applied in its prologue: x' = scale * H (signs * xhat)
+// per block of B columns (H the +-1 Sylvester matrix; B a power of two <= 1024 with K a multiple
+// of max(B, 256)). Each GEMV block transforms the rotation block(s) holding its 256 columns.
+struct RotSrc {
+  const float* signs;
+  int B;
+  float scale;
+};
+
 int tgemv_f32(const uint8_t* packed, int kind, int M, int K, const float* x, const float* norm_w,
               float eps, float* y, int epi, const float* resid, unsigned long long* amax_slot,
               void* work, hipStream_t s, const int* gate_pos = nullptr, const int* gate_from = nullptr,
-              const AttnMergeSrc* merge = nullptr, const PartialSums* parts = nullptr);
+              const AttnMergeSrc* merge = nullptr, const PartialSums* parts = nullptr,
+              const RotSrc* rot = nullptr);
 
 }  // namespace trx

@@ -258,6 +258,9 @@ struct TgParams {
   const int* gate_from;
   AttnMergeSrc merge;      // merge.o != nullptr: x from attention partials
   PartialSums parts;       // parts.out: store the partial sums only; parts.in: x from them
+  const float* rot_signs;  // a rotation of x in the prologue (RotSrc), or null
+  int rot_B;
+  float rot_scale;
 };
 
 template <bool T5>
@@ -354,6 +357,18 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   } else if (tid < kSliceCols && cs < p.K) {
     xv = p.x[cs];
     if (p.norm_w) wv = p.norm_w[cs];
+  }
+  // A rotated input: this thread's element of the rotation span holding the slice (the slice
+  // itself for blocks of <= 256 columns, else the rotation block containing it), times the gain
+  // and its sign.
+  const bool rot = p.rot_signs && xmode == kXPlain;
+  const int rL = p.rot_B > kSliceCols ? p.rot_B : kSliceCols;
+  const int rbase = s * kSliceCols - (s * kSliceCols) % rL;
+  float rv = 0.f;
+  if (rot && tid < rL) {
+    const int c = rbase + tid;
+    rv = p.x[c] * p.rot_signs[c];
+    if (p.norm_w) rv *= p.norm_w[c];
   }
 
   // 2. The first NB - 1 items of this lane (they do not depend on x).
@@ -477,7 +492,26 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
     if (gated_off) return;
     __syncthreads();                                // the table's memory is rewritten below
   }
-  if (xmode != kXSwiglu && tid < kSliceCols) xs[tid] = p.norm_w ? xv * wv : xv;
+  if (rot) {
+    // H over each rotation block of the span: butterflies of span < 64 by wave shuffles, the
+    // wider ones through the table's memory; then the slice's 256 values, scaled.
+    for (int h = 1; h < 64 && h < p.rot_B; h <<= 1) {
+      const float o = __shfl_xor(rv, h, 64);
+      rv = (lane & h) ? o - rv : rv + o;
+    }
+    for (int h = 64; h < p.rot_B; h <<= 1) {
+      tab[tid] = rv;
+      __syncthreads();
+      const float o = tab[tid ^ h];
+      __syncthreads();
+      rv = (tid & h) ? o - rv : rv + o;
+    }
+    tab[tid] = rv * p.rot_scale;
+    __syncthreads();
+    if (tid < kSliceCols) xs[tid] = tab[s * kSliceCols - rbase + tid];
+  } else if (xmode != kXSwiglu && tid < kSliceCols) {
+    xs[tid] = p.norm_w ? xv * wv : xv;
+  }
   // The slice's sum of x^2 (x before the gain), for whoever applies the RMSNorm scale.
   if (p.norm_w && w < kSliceCols / 64) {
     const float q = wave_sum_dpp(xv * xv);
@@ -793,7 +827,7 @@ static const void* tg_fn() {
 int tgemv_f32(const uint8_t* packed, int kind, int M, int K, const float* x, const float* norm_w,
               float eps, float* y, int epi, const float* resid, unsigned long long* amax_slot,
               void* work, hipStream_t s, const int* gate_pos, const int* gate_from,
-              const AttnMergeSrc* merge, const PartialSums* parts) {
+              const AttnMergeSrc* merge, const PartialSums* parts, const RotSrc* rot) {
   PackGeom g;
   int rc = pack_geom(g, kind, M, K);
   if (rc) return rc;
@@ -844,6 +878,12 @@ int tgemv_f32(const uint8_t* packed, int kind, int M, int K, const float* x, con
   p.gate_from = gate_from;
   p.merge = merge ? *merge : AttnMergeSrc{};
   p.parts = parts ? *parts : PartialSums{};
+  p.rot_signs = rot ? rot->signs : nullptr;
+  p.rot_B = rot ? rot->B : 0;
+  p.rot_scale = rot ? rot->scale : 1.f;
+  TRX_CHECK(!rot || (x && !merge && !p_in && rot->signs && rot->B >= 1 && rot->B <= kTgThreads &&
+                     (rot->B & (rot->B - 1)) == 0 && K % std::max(rot->B, kSliceCols) == 0),
+            TRX_E_INVALID, "packed GEMV: rotation of block %d over %d columns unsupported", rot ? rot->B : 0, K);
   const void* fn = kind == TRX_KIND_TERNARY5 ? tg_fn<true>() : tg_fn<false>();
   void* args[] = {(void*)&p};
   TRX_HIP(hipLaunchKernel(fn, dim3(g.S * g.bps), dim3(kTgThreads), args, 0, s));
