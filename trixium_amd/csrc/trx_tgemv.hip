@@ -303,7 +303,8 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
     h0 = (s * kSliceCols) / a.hd;
     nh = kSliceCols / a.hd;
     // Thread t loads columns 4 (t % 64) .. + 3 of splits t / 64 and t / 64 + 16 (16 bytes each;
-    // splits past ns re-read the last one, their weight is 0).
+    // splits past ns re-read the last one, their weight is 0: unconditional loads measured faster
+    // here, at long contexts every split holds positions).
     const int c0 = s * kSliceCols + 4 * (tid % (kSliceCols / 4)), sl = tid / (kSliceCols / 4);
     const int h = c0 / a.hd, d = c0 - h * a.hd;
 #pragma unroll
@@ -325,30 +326,35 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   } else if (xmode == kXSwiglu) {
     // The gate|up partial sums of this slice's 128 packed row quads ([g 2q, g 2q+1, u 2q,
     // u 2q+1]): thread t loads quad t % 128 of slices t / 128, t / 128 + 8, ...; and the gate|up
-    // input's slice sums of squares (its RMSNorm scale multiplies g and u). Slices past S
-    // re-read the last one and are not added.
+    // input's slice sums of squares (its RMSNorm scale multiplies g and u). Slices past S are
+    // not loaded (these loads precede the ring prefetch, so the wait for them stays exact).
     const __amdgpu_buffer_rsrc_t rin = make_rsrc(p.parts.in, (uint32_t)((size_t)p.parts.S * p.parts.rows_p * 4));
     const uint32_t off = (uint32_t)(2 * kSliceCols * s + 4 * (tid % (2 * kSliceCols / 4))) * 4u;
     const int sl = tid / (2 * kSliceCols / 4);
 #pragma unroll
     for (int k = 0; k < kSwiVec; ++k) {
-      const auto a = __builtin_amdgcn_raw_buffer_load_b128(
-          rin, off + (uint32_t)min(sl + kSwiSlicesPerPass * k, p.parts.S - 1) * (uint32_t)p.parts.rows_p * 4u, 0, 0);
-      pv[k] = make_float4(__uint_as_float(a[0]), __uint_as_float(a[1]), __uint_as_float(a[2]), __uint_as_float(a[3]));
+      pv[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (sl + kSwiSlicesPerPass * k < p.parts.S) {
+        const auto a = __builtin_amdgcn_raw_buffer_load_b128(
+            rin, off + (uint32_t)(sl + kSwiSlicesPerPass * k) * (uint32_t)p.parts.rows_p * 4u, 0, 0);
+        pv[k] = make_float4(__uint_as_float(a[0]), __uint_as_float(a[1]), __uint_as_float(a[2]), __uint_as_float(a[3]));
+      }
     }
     if (p.parts.in_ss && tid < p.parts.S) ssin = p.parts.in_ss[tid];
   } else if (xmode == kXResid) {
     // x = resid + the producer's partial sums of this slice's 256 rows: thread t loads columns
-    // 4 (t % 64) .. + 3 of slices t / 64, t / 64 + 16, ... Slices past S re-read the last one and
-    // are not added.
+    // 4 (t % 64) .. + 3 of slices t / 64, t / 64 + 16, ... Slices past S are not loaded.
     const __amdgpu_buffer_rsrc_t rin = make_rsrc(p.parts.in, (uint32_t)((size_t)p.parts.S * p.parts.rows_p * 4));
     const uint32_t off = (uint32_t)(kSliceCols * s + 4 * (tid % (kSliceCols / 4))) * 4u;
     const int sl = tid / (kSliceCols / 4);
 #pragma unroll
     for (int k = 0; k < kResVec; ++k) {
-      const auto a = __builtin_amdgcn_raw_buffer_load_b128(
-          rin, off + (uint32_t)min(sl + kResSlicesPerPass * k, p.parts.S - 1) * (uint32_t)p.parts.rows_p * 4u, 0, 0);
-      pv[k] = make_float4(__uint_as_float(a[0]), __uint_as_float(a[1]), __uint_as_float(a[2]), __uint_as_float(a[3]));
+      pv[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (sl + kResSlicesPerPass * k < p.parts.S) {
+        const auto a = __builtin_amdgcn_raw_buffer_load_b128(
+            rin, off + (uint32_t)(sl + kResSlicesPerPass * k) * (uint32_t)p.parts.rows_p * 4u, 0, 0);
+        pv[k] = make_float4(__uint_as_float(a[0]), __uint_as_float(a[1]), __uint_as_float(a[2]), __uint_as_float(a[3]));
+      }
     }
     if (tid < kSliceCols && cs < p.K) {
       xv = p.parts.resid[cs];
