@@ -352,3 +352,32 @@ def test_command_line(converted, tmp_path, capsys):
     assert convert.main(["verify", "--image", out]) == 0
     convert.main(["inspect", g])
     assert "token_embd.weight" in capsys.readouterr().out
+
+
+def test_split_wide_segments():
+    """K-segments (model/bons.py:83-115): nseg = ceil(cols / kseg_max) ranges ending at group
+    floor(G k / nseg), FLAG_KSEG with the index, the whole tensor's bias/rshift on every segment,
+    and the pieces joining back to the tensor; Q8 capped at 255 code beats of 32 columns; the token
+    embedding never split."""
+    rng = np.random.default_rng(4)
+    sc = rng.uniform(0.01, 0.05, (3, 40)).astype(np.float16)
+    codes = rng.integers(0, 3, (3, 5120), dtype=np.uint8)
+    t = bons.TensorSpec("w", L.ROLE_FFN_DOWN, 2, L.KIND_TERNARY, 3, 5120, scales=sc, values=codes)
+    segs = bons.split_wide(t, 1536)
+    assert [s.cols for s in segs] == [1280, 1280, 1280, 1280]           # 40 groups / 4 segments
+    assert [s.kseg for s in segs] == [0, 1, 2, 3] and all(s.flags & L.FLAG_KSEG for s in segs)
+    assert all((s.bias, s.rshift) == (t.bias, t.rshift) for s in segs)
+    assert [s.name for s in segs] == ["w.k0", "w.k1", "w.k2", "w.k3"]
+    assert np.array_equal(np.concatenate([s.values for s in segs], axis=1), codes)
+    assert np.array_equal(np.concatenate([s.scales for s in segs], axis=1), sc)
+    odd = bons.split_wide(t, 2000)                                        # 3 segments of 40 groups
+    assert [s.cols for s in odd] == [13 * 128, 13 * 128, 14 * 128]
+    lazy = bons.TensorSpec("w", L.ROLE_FFN_DOWN, 2, L.KIND_TERNARY, 3, 5120, scales=sc, loader=lambda: codes)
+    assert np.array_equal(np.concatenate([s.load() for s in bons.split_wide(lazy, 1536)], axis=1), codes)
+    q = rng.integers(-127, 128, (2, 16384), dtype=np.int8)
+    q8 = bons.TensorSpec("b", L.ROLE_SSM_BETA, 0, L.KIND_Q8, 2, 16384,
+                         scales=rng.uniform(0.01, 0.05, (2, 512)).astype(np.float16), values=q)
+    # 16384 columns > 255 * 32 = 8160: 3 segments, edges at groups floor(512 k / 3) = 0, 170, 341, 512
+    assert [s.cols for s in bons.split_wide(q8)] == [5440, 5472, 5472]
+    emb = bons.TensorSpec("token_embd.weight", L.ROLE_TOK_EMB, 0, L.KIND_TERNARY, 3, 5120, scales=sc, values=codes)
+    assert bons.split_wide(emb, 1536) == [emb]
