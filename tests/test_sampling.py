@@ -11,7 +11,7 @@ def test_xorshift32_stream():
     """x ^= x << 13; x ^= x >> 17; x ^= x << 5 (32-bit): from 1, 270369, then 67634689."""
     assert S.xorshift32(1) == 270369
     assert S.xorshift32(270369) == 67634689
-    assert S.xorshift32(0x9E3779B9) == S.xorshift32(0x9E3779B9)
+    assert all(S.xorshift32(x) != 0 for x in (1, 0x9E3779B9, 0xFFFFFFFF))   # never leaves a nonzero state
 
 
 def test_candidates_are_slice_maxima():
