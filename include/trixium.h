@@ -232,7 +232,8 @@ int trx_model_destroy(trx_model* m);
  * float32 values; F16 head: fp16 values; TOK_EMB16: int16 [vocab, n_embd]; TOK_EMB16_EXP: int32
  * [vocab]. The fused groups (q|k|v, gate|up, qkv|z, beta|alpha) are laid out adjacent. */
 int trx_model_set_tensor(trx_model* m, int role, int layer, const void* data, size_t bytes);
-/* Fill every tensor from the counter-based generator (trixium_amd/synth.py's hash). ranges:
+/* Fill every tensor from the counter-based generator (trixium_amd/synth.py's hash) but the Q8
+ * rows (a hybrid's DeltaNet beta|alpha), which the caller sets with trx_model_set_tensor. ranges:
  * float32 {scale_lo, scale_span, gain_lo, gain_span}. */
 int trx_model_synthesize(trx_model* m, uint32_t seed, const float* ranges);
 /* Clear the position, the argmax slot and the DeltaNet state (golden.py:304-320). */

@@ -345,3 +345,17 @@ def test_rotation_in_the_gemv_prologue(tmp_path, block):
         got = [dec.forward(prompt[:1])] + [dec.forward([t]) for t in prompt[1:]]
         for g, w in zip(got, want):
             assert _rel_err(g, w) <= 2e-3, (packed, _rel_err(g, w))
+
+
+def test_synthetic_hybrid_decodes():
+    """A synthetic hybrid (device-generated ternary and float tensors, host Q8 beta|alpha rows):
+    finite logits, and the graph replay generates what eager launches generate."""
+    from trixium_amd.model import Decoder
+    mc = C.TINY_HYBRID.replace(max_ctx=64)
+    a = Decoder.synthetic(mc, 3, max_new=16)
+    b = Decoder.synthetic(mc, 3, max_new=16, use_graph=False)
+    prompt = synth.random_prompt(mc, 8, 3)
+    assert np.isfinite(a.forward(prompt)).all()
+    a.reset()
+    assert a.generate(prompt, 8) == b.generate(prompt, 8)
+    assert np.array_equal(a.read_tensor(L.ROLE_SSM_BETA, 1), b.read_tensor(L.ROLE_SSM_BETA, 1))

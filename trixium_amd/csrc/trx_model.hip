@@ -888,9 +888,11 @@ TRX_API int trx_model_synthesize(trx_model* h, uint32_t seed, const float* range
       if ((rc = launch_synth_f32((float*)(m.arena + t.off), (long long)t.rows * t.cols, seed, tid, lo,
                                  span, transform, m.stream))) return rc;
       t.loaded = true;
-    } else {
+    } else if (t.kind != TRX_KIND_Q8) {
       TRX_CHECK(false, TRX_E_INVALID, "synthesize: tensor role=%d kind=%d has no generator", role, t.kind);
     }
+    // Q8 rows (the DeltaNet beta|alpha, a few KB a layer) are left to the caller's
+    // trx_model_set_tensor; a step refuses to run while any tensor is unset.
   }
   TRX_HIP(hipStreamSynchronize(m.stream));
   m.pack_dirty = true;

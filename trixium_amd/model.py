@@ -153,9 +153,8 @@ class Decoder:
                   use_graph=True, layer_fusion=False, packed_ops=PACK_AUTO):
         """Fill every tensor on the device from the counter-based generator (same values as
         trixium_amd.synth.hashed_*): ternary token_embd rows (embedded by decoding the row), an
-        untied ternary LM head unless the config ties them."""
-        if mc.n_dn_layers:
-            raise NotImplementedError("synthetic DeltaNet layers (Q8 beta/alpha) have no device generator")
+        untied ternary LM head unless the config ties them. A hybrid's DeltaNet beta|alpha Q8
+        rows come from the host (seeded int8 values, fp16 scales U(0.01, 0.05))."""
         cfg = make_config(mc, weight_kind, weight_kind, mc.tie_embeddings, 1, weight_kind, max_ctx, max_new,
                           layer_fusion, packed_ops)
         d = cls(mc, cfg, use_graph)
@@ -164,6 +163,17 @@ class Decoder:
                                SYNTH_GAIN[0], SYNTH_GAIN[1] - SYNTH_GAIN[0]], dtype=f32)
             _lib.call("trx_model_synthesize", d._h, seed & 0xFFFFFFFF,
                       ranges.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+            if mc.n_dn_layers:
+                from .bons import encode_rows
+                rng = np.random.default_rng(seed)
+                nv = mc.dn_num_v_heads
+                for l in range(mc.n_layer):
+                    if mc.layer_type(l) != "deltanet":
+                        continue
+                    for r in (L.ROLE_SSM_BETA, L.ROLE_SSM_ALPHA):
+                        q = rng.integers(-127, 128, (nv, mc.n_embd), dtype=np.int8)
+                        sc = rng.uniform(0.01, 0.05, (nv, mc.n_embd // L.GROUP_Q8)).astype(np.float16)
+                        d.set_tensor(r, l, encode_rows(L.KIND_Q8, mc.n_embd, sc, q))
         except Exception:
             d.close()
             raise
