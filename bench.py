@@ -46,10 +46,11 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--prompt", type=int, default=None,
                     help="prompt tokens (default 2048 for the 8B shape, 1024 for the 27B hybrid)")
-    ap.add_argument("--model", choices=("8b", "27b"), default="8b",
-                    help="8b: the Qwen3-8B shape (the headline workload); 27b: the Qwen3.5-27B hybrid "
-                         "shape (48 Gated DeltaNet + 16 gated attention layers), tok/s and the "
-                         "bytes-per-token roofline only")
+    ap.add_argument("--model", choices=("8b", "1.7b", "27b"), default="8b",
+                    help="8b: the Qwen3-8B shape (the headline workload); 1.7b: the Qwen3-1.7B shape "
+                         "(512-token prompt); 27b: the Qwen3.5-27B hybrid shape (48 Gated DeltaNet + 16 "
+                         "gated attention layers); the last two report tok/s and the bytes-per-token "
+                         "roofline only")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--kind", choices=("trit5", "2bit"), default="trit5")
     ap.add_argument("--kernel-reps", type=int, default=10,
@@ -193,9 +194,9 @@ def main():
         return
     from trixium_amd import configs as C, layout as L, _lib
     from trixium_amd.model import Decoder, INFO_WEIGHT_BYTES
-    mc = C.QWEN3_8B if a.model == "8b" else C.QWEN35_27B
+    mc = {"8b": C.QWEN3_8B, "1.7b": C.QWEN3_1P7B, "27b": C.QWEN35_27B}[a.model]
     if a.prompt is None:
-        a.prompt = 2048 if a.model == "8b" else 1024
+        a.prompt = {"8b": 2048, "1.7b": 512, "27b": 1024}[a.model]
     kind = L.KIND_TERNARY5 if a.kind == "trit5" else L.KIND_TERNARY
     if a.only_kernel:
         dec = Decoder.synthetic(mc, a.seed, weight_kind=kind, max_ctx=mc.max_ctx, max_new=8,
@@ -240,21 +241,22 @@ def main():
     tok_bytes = wbytes - emb_rows + emb_row + kv
     roof_tok_s = HBM_PEAK_GBS * 1e9 / tok_bytes
 
-    if a.model == "27b":
-        # Bytes per token of the hybrid: the weights, one embedding row, K/V of the 16 attention
-        # layers up to the mean position, every DeltaNet layer's recurrent state read and written.
+    if a.model != "8b":
+        # Bytes per token: the weights, one embedding row, K/V of the attention layers up to the
+        # mean position, every DeltaNet layer's recurrent state read and written.
         n_attn = mc.n_layer - mc.n_dn_layers
         kv = 2 * n_attn * mc.n_kv_head * mc.head_dim * 2 * (mean_pos + 1)
         dn = 2 * mc.n_dn_layers * mc.dn_num_v_heads * mc.dn_v_head_dim * mc.dn_k_head_dim * 4
-        tok_bytes = wbytes - emb_rows + emb_row + kv + dn
+        # A tied head reads the whole embedding table every token.
+        tok_bytes = wbytes + (0 if mc.tie_embeddings else emb_row - emb_rows) + kv + dn
         print(json.dumps({
-            "metric": "batch-1 decode tok/s (27B hybrid shape)", "value": round(tok_s, 2), "unit": "tok/s",
+            "metric": f"batch-1 decode tok/s ({mc.name})", "value": round(tok_s, 2), "unit": "tok/s",
             "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(1e3 / tok_s, 4),
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-            "dtype": "ternary weights (fp16 group scales), fp32 activations, fp32 accumulate, fp16 KV, "
-                     "fp32 DeltaNet state",
+            "dtype": "ternary weights (fp16 group scales), fp32 activations, fp32 accumulate, fp16 KV"
+                     + (", fp32 DeltaNet state" if mc.n_dn_layers else ""),
             "data": "synthetic: random ternary weights from a counter-based hash, random prompt",
-            "config": {"workload": f"qwen3.5-27b-shape hybrid ternary decoder, batch-1 greedy decode after a "
+            "config": {"workload": f"{mc.name} ternary decoder, batch-1 greedy decode after a "
                                    f"{a.prompt}-token prompt", "n_layer": mc.n_layer, "n_embd": mc.n_embd,
                        "ffn_dim": mc.ffn_dim, "vocab": mc.vocab, "prompt_tokens": a.prompt,
                        "decode_tokens": n_dec, "weights": a.kind, "hipgraph": graph,
