@@ -70,7 +70,65 @@ def parse_args():
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="run a plain device copy of this many bytes, 10 times, and exit (the "
                          "reference kernel that calibrates the FETCH_SIZE/WRITE_SIZE counters)")
+    ap.add_argument("--exact-rows", type=int, default=0, metavar="N",
+                    help="time the engine matvec at the 8B gate|up shape on N int8 rows in one "
+                         "weight pass (trx_gemv_ternary_exact_rows) against N single-row calls, "
+                         "and exit")
     return ap.parse_args()
+
+
+def time_exact_rows(n, kind, reps=50):
+    """The multi-row engine matvec (one weight pass for n int8 rows) against n single-row engine
+    matvecs, at the Qwen3-8B gate|up shape (24576 x 4096), HIP events on one stream."""
+    import ctypes
+    from trixium_amd import _lib, layout as L
+    from trixium_amd.bons import encode_rows
+    M, K = 24576, 4096
+    r = np.random.default_rng(3)
+    codes = r.integers(0, 3, (M, K), dtype=np.uint8)
+    scales = r.uniform(0.01, 0.05, (M, K // 128)).astype(np.float16)
+    rows = _lib.DeviceBuffer.from_array(encode_rows(kind, K, scales, codes))
+    xs = _lib.DeviceBuffer.from_array(r.integers(-127, 128, (n, K), dtype=np.int8))
+    y = _lib.DeviceBuffer(4 * n * M)
+    st = _lib.DeviceBuffer(4)
+    st.zero()
+    B, R = 27, 24
+    e0, e1 = ctypes.c_void_p(), ctypes.c_void_p()
+    _lib.call("trx_event_create", ctypes.byref(e0))
+    _lib.call("trx_event_create", ctypes.byref(e1))
+
+    def timed(one):
+        for _ in range(5):
+            one()
+        _lib.call("trx_event_record", e0, None)
+        for _ in range(reps):
+            one()
+        _lib.call("trx_event_record", e1, None)
+        ms = ctypes.c_float()
+        _lib.call("trx_event_elapsed_ms", e0, e1, ctypes.byref(ms))
+        return ms.value * 1e3 / reps
+
+    def multi():
+        _lib.call("trx_gemv_ternary_exact_rows", rows.ptr, kind, M, K, xs.ptr, n, B, R, y.ptr,
+                  st.ptr, None)
+
+    def singles():
+        for i in range(n):
+            _lib.call("trx_gemv_ternary_exact", rows.ptr, kind, M, K, xs.ptr + i * K, B, R,
+                      y.ptr + 4 * i * M, st.ptr, None)
+
+    us_multi, us_single = timed(multi), timed(singles)
+    _lib.synchronize()
+    _lib.call("trx_event_destroy", e0)
+    _lib.call("trx_event_destroy", e1)
+    wbytes = M * L.row_bytes(K, kind)
+    algo = wbytes + n * K + 4 * n * M
+    print(json.dumps({"kernel": "gemv_rows_kernel", "shape": [M, K], "x_rows": n,
+                      "kind": "trit5" if kind == L.KIND_TERNARY5 else "2bit",
+                      "us_one_pass": round(us_multi, 3), "us_single_row_calls": round(us_single, 3),
+                      "speedup": round(us_single / us_multi, 2), "bytes_per_launch": algo,
+                      "achieved_GBs": round(algo / (us_multi * 1e-6) / 1e9, 1), "peak_GBs": 8000,
+                      "status": int(st.download(np.int32)[0])}), flush=True)
 
 
 def copy_calibration(nbytes):
@@ -194,6 +252,9 @@ def main():
         return
     from trixium_amd import configs as C, layout as L, _lib
     from trixium_amd.model import Decoder, INFO_WEIGHT_BYTES
+    if a.exact_rows:
+        time_exact_rows(a.exact_rows, L.KIND_TERNARY5 if a.kind == "trit5" else L.KIND_TERNARY)
+        return
     mc = {"8b": C.QWEN3_8B, "1.7b": C.QWEN3_1P7B, "27b": C.QWEN35_27B}[a.model]
     if a.prompt is None:
         a.prompt = {"8b": 2048, "1.7b": 512, "27b": 1024}[a.model]

@@ -72,6 +72,14 @@ int trx_event_elapsed_ms(void* start, void* stop, float* ms);
 int trx_gemv_ternary_exact(const uint8_t* rows, int kind, int M, int K, const int8_t* x8, int B,
                            int R, int32_t* y, int32_t* status, trx_stream_t s);
 
+/* Multi-row exact engine matvec (model/bitexact.py:121-125 matvec_ternary_rows): one pass over
+ * the rows against n_rows (1..8) int8 vectors x8_rows[n_rows][K] (16-byte aligned,
+ * n_rows * K <= 114688), y[n_rows][M]; row r equals trx_gemv_ternary_exact on x8_rows[r], and
+ * *status is OR-ed the same way. */
+int trx_gemv_ternary_exact_rows(const uint8_t* rows, int kind, int M, int K, const int8_t* x8_rows,
+                                int n_rows, int B, int R, int32_t* y, int32_t* status,
+                                trx_stream_t s);
+
 /* Exact per-group sums gs[m*G + g] = sum (code-1)*x8 over group g (the engine's adder-tree
  * output, model/bitexact.py:110; debug form of engine op 0). */
 int trx_gemv_ternary_groupsums(const uint8_t* rows, int kind, int M, int K, const int8_t* x8,

@@ -85,6 +85,12 @@ def matvec_ternary(scales_f16, codes, x8, B, R):
     return _shift_accumulate(group_sums(codes, x8), scales_f16, B, R)[0]
 
 
+def matvec_ternary_rows(scales_f16, codes, x8_rows, B, R):
+    """Multi-row engine matvec (model/bitexact.py:121-125): every row of x8_rows (n, K) is the
+    single-row matvec of that row -> int32 (n, M)."""
+    return np.stack([matvec_ternary(scales_f16, codes, x8, B, R) for x8 in x8_rows])
+
+
 def matvec_q8(scales_f16, q8w, x8, B, R):
     """Q8 row-dot mode (model/bitexact.py:127-144): group 32, w = q8 * scale."""
     return _shift_accumulate(group_sums(q8w, x8, group=32, offset=0), scales_f16, B, R)[0]

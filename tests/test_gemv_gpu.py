@@ -70,6 +70,63 @@ def test_matvec_exact_microbench_fixtures(gpu, golden, kind):
 
 
 @pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("M,K,n", [(1, 128, 1), (3, 640, 8), (33, 768, 3), (100, 4096, 8),
+                                   (17, 6144, 5), (9, 12288, 8), (5, 17408, 8), (70, 2048, 2)])
+def test_matvec_rows_vs_oracle(gpu, kind, M, K, n):
+    """One weight pass against n x8 rows: every row bit-exact with the oracle's single-row matvec
+    (wide-exponent scales, so both shift directions occur) and with the single-row GPU call."""
+    r = np.random.default_rng(M * 31 + K + n)
+    codes = r.integers(0, 3, (M, K), dtype=np.uint8)
+    scales = (np.exp2(r.uniform(-20, 3, (M, K // 128))) * r.choice([-1, 1], (M, K // 128))).astype(np.float16)
+    xs = r.integers(-128, 128, (n, K), dtype=np.int8)
+    xs[0, : K // 2] = 127
+    _, e16 = ob.fp16_decompose(scales)
+    B = ob.choose_scale_bias(e16)
+    R = ob.choose_result_shift(scales, B)
+    print(f"multi-row matvec kind={kind} {M}x{K} n={n}", flush=True)
+    got = gpu.matvec_ternary_rows(scales, codes, xs, B, R, kind=kind)
+    assert got.shape == (n, M)
+    assert np.array_equal(got, ob.matvec_ternary_rows(scales, codes, xs, B, R))
+    assert np.array_equal(got[-1], gpu.matvec_ternary(scales, codes, xs[-1], B, R, kind=kind))
+
+
+@pytest.mark.parametrize("kind", KINDS)
+def test_matvec_rows_microbench_fixtures(gpu, golden, kind):
+    """The microbench shapes in a 7-row pass (11 rows: passes of 8 and 3): the fixture's x at rows
+    0 and 9 matches the sha256 the reference's matvec_ternary produced. Every group shift is a
+    left shift at these scales, so the negated x gives the negated accumulator and results that
+    differ from the negated ones by the final floor shift alone (at most 1)."""
+    for (M, K) in C.MICROBENCH_SHAPES:
+        r = np.random.default_rng(M * 7919 + K)
+        u = r.random((M, K))
+        codes = np.where(u < 0.3, 0, np.where(u < 0.7, 1, 2)).astype(np.uint8)
+        scales = r.uniform(0.01, 0.05, (M, K // 128)).astype(np.float16)
+        x8 = r.integers(-127, 128, K, dtype=np.int8)
+        g = golden[f"matvec/{M}x{K}"]
+        xs = np.random.default_rng(K).integers(-127, 128, (11, K), dtype=np.int8)
+        xs[0] = x8
+        xs[9] = x8
+        xs[4] = -x8
+        print(f"multi-row microbench kind={kind} {M}x{K}", flush=True)
+        res = gpu.matvec_ternary_rows(scales, codes, xs, g["B"], g["R"], kind=kind)
+        for i in (0, 9):
+            assert hashlib.sha256(res[i].astype("<i4").tobytes()).hexdigest() == g["sha256"]
+        assert np.all(np.abs(res[4].astype(np.int64) + res[0]) <= 1)
+
+
+def test_matvec_rows_overflow_asserts(gpu):
+    """An overflowing row among good ones trips the reference's int32 result assertion."""
+    codes = np.full((2, 12288), 2, np.uint8)
+    scales = np.full((2, 96), 0.5, np.float16)
+    xs = np.zeros((3, 12288), np.int8)
+    xs[1] = 127
+    _, e16 = ob.fp16_decompose(scales)
+    B = ob.choose_scale_bias(e16)
+    with pytest.raises(AssertionError, match="int32 result overflow"):
+        gpu.matvec_ternary_rows(scales, codes, xs, B, 0)
+
+
+@pytest.mark.parametrize("kind", KINDS)
 @pytest.mark.parametrize("M,K", [(5, 256), (129, 4096), (31, 12288)])
 def test_matvec_exact_wide_scales(gpu, kind, M, K):
     """Scales over a wide exponent range (negative and positive per-group shifts)."""

@@ -41,6 +41,12 @@ def test_errors_are_reported_without_a_device_call():
     assert b"null" in L.trx_last_error()
     rc = L.trx_gemv_ternary_f32(ctypes.c_void_p(16), 7, 4, 256, None, None, 1e-6, None, 0, None, None)
     assert rc == _lib.TRX_E_INVALID
+    fake = ctypes.c_void_p(256)
+    for n, K, what in ((0, 256, b"x rows"), (9, 256, b"x rows"), (8, 19456, b"staged bytes")):
+        rc = L.trx_gemv_ternary_exact_rows(fake, 5, 4, K, fake, n, 0, 0, fake, fake, None)
+        assert rc == _lib.TRX_E_INVALID and what in L.trx_last_error(), (n, K, L.trx_last_error())
+    rc = L.trx_gemv_ternary_exact_rows(fake, 5, 4, 256, ctypes.c_void_p(264), 2, 0, 0, fake, fake, None)
+    assert rc == _lib.TRX_E_INVALID and b"16-byte aligned" in L.trx_last_error()
     pb, wb = ctypes.c_size_t(), ctypes.c_size_t()
     rc = L.trx_pack_geometry(7, 4, 256, ctypes.byref(pb), ctypes.byref(wb))
     assert rc == _lib.TRX_E_INVALID and b"not ternary" in L.trx_last_error()

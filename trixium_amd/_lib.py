@@ -67,6 +67,7 @@ SIGNATURES = {
     "trx_event_record": [_vp, _vp],
     "trx_event_elapsed_ms": [_vp, _vp, _fp],
     "trx_gemv_ternary_exact": [_vp, _i, _i, _i, _vp, _i, _i, _vp, _vp, _vp],
+    "trx_gemv_ternary_exact_rows": [_vp, _i, _i, _i, _vp, _i, _i, _i, _vp, _vp, _vp],
     "trx_gemv_ternary_groupsums": [_vp, _i, _i, _i, _vp, _vp, _vp],
     "trx_gemv_ternary_f32": [_vp, _i, _i, _i, _vp, _vp, _f, _vp, _i, _vp, _vp],
     "trx_pack_geometry": [_i, _i, _i, ctypes.POINTER(_sz), ctypes.POINTER(_sz)],

@@ -43,6 +43,40 @@ def matvec_ternary(scales_f16, codes, x8, B, R, kind=L.KIND_TERNARY5):
     return matvec_ternary_rows_gpu(rows, kind, M, K, x8, B, R)
 
 
+ROWS_STAGED_BYTES = 114688   # n * K bound of one trx_gemv_ternary_exact_rows call
+
+
+def matvec_ternary_rows_multi_gpu(rows_dev, kind, M, K, x8_rows, B, R):
+    """Multi-row exact matvec on resident row packets: x8_rows (n, K) int8, n in 1..8 -> int32
+    (n, M), one weight pass (trx_gemv_ternary_exact_rows)."""
+    x = np.ascontiguousarray(x8_rows, dtype=np.int8)
+    assert x.ndim == 2 and x.shape[1] == K
+    n = x.shape[0]
+    xb = DeviceBuffer.from_array(x)
+    yb = DeviceBuffer(4 * n * M)
+    st = DeviceBuffer(4)
+    st.zero()
+    call("trx_gemv_ternary_exact_rows", rows_dev.ptr, kind, M, K, xb.ptr, n, int(B), int(R), yb.ptr,
+         st.ptr, None)
+    synchronize()
+    status = int(st.download(np.int32)[0])
+    assert not (status & 1), "int48 accumulator overflow"
+    assert not (status & 2), "int32 result overflow"
+    return yb.download(np.int32, n * M).reshape(n, M)
+
+
+def matvec_ternary_rows(scales_f16, codes, x8_rows, B, R, kind=L.KIND_TERNARY5):
+    """The engine's multi-row matvec (model/bitexact.py:121-125) on the GPU: x8_rows (n, K) int8
+    -> int32 (n, M), each row the single-row matvec of its x. One pass takes at most 8 rows and
+    ROWS_STAGED_BYTES of x; more run in several passes."""
+    M, K = codes.shape
+    rows = DeviceBuffer.from_array(_packets(scales_f16, codes, kind))
+    x = np.asarray(x8_rows, dtype=np.int8)
+    step = max(1, min(8, ROWS_STAGED_BYTES // K))
+    return np.concatenate([matvec_ternary_rows_multi_gpu(rows, kind, M, K, x[i:i + step], B, R)
+                           for i in range(0, x.shape[0], step)])
+
+
 def group_sums(scales_f16, codes, x8, kind=L.KIND_TERNARY5):
     """Exact per-group sums (M, K/128) of (code - 1) * x8 on the GPU."""
     M, K = codes.shape
