@@ -192,19 +192,17 @@ typedef struct {
   int emb_mode;                /* 0: int16 BFP lookup table; 1: ternary token_embd rows */
   int emb_kind;                /* kind of token_embd rows (emb_mode 1 or a tied head) */
   int max_new;                 /* capacity of the generated-token buffer */
-  int layer_fusion;            /* 1: one kernel per full-attention layer where the geometry has
-                                  one (grid barriers between its phases); 0: one per operation */
+  int persistent;              /* 1: each position runs as one persistent kernel (reserved) */
   int packed_ops;              /* projections run by the packed GEMV (trx_gemv_packed_f32) over
                                   a packed copy of their rows, as TRX_PACK_* bits; the others run
                                   trx_gemv_ternary_f32's kernel. TRX_PACK_AUTO: the library's
                                   choice (every projection: q|k|v, o, gate|up, down, the ternary
-                                  LM head, the DeltaNet qkv|z and out). (With layer_fusion the
-                                  fused layers keep the row-packet kernel.) */
+                                  LM head, the DeltaNet qkv|z and out). */
   /* PrismML's rotated weight basis (model/golden.py:250-289, model/fastref.py:127-140): every
      ternary projection but the DeltaNet beta/alpha takes x' = hadamard_scale * H (s * xhat)
      blockwise over hadamard_block columns (H the +-1 Sylvester matrix, s the width's signs,
      xhat the normalised input), computed by a fast Walsh-Hadamard transform before the GEMV.
-     0 = plain basis. A rotated model runs one kernel per operation (layer_fusion 0): its
+     0 = plain basis. A rotated model runs one kernel per operation: its
      projections take the rotated input as a plain vector, on the packed GEMV where packed_ops
      selects it, without the partial-sum handoffs between packed GEMVs. */
   int hadamard_block;          /* 0, or a power of two in [64, 1024] dividing every width */
@@ -272,7 +270,7 @@ int trx_model_read(trx_model* m, int what, void* host, size_t bytes);
 #define TRX_INFO_DEVICE_BYTES 1
 #define TRX_INFO_STREAM 2
 #define TRX_INFO_WEIGHT_BYTES 3
-#define TRX_INFO_FUSED_LAYERS 4   /* 1 when full-attention layers run as one kernel each */
+#define TRX_INFO_PERSISTENT 4     /* 1 when each position runs as one persistent kernel */
 #define TRX_INFO_PACKED_OPS 5     /* TRX_PACK_* bits in effect */
 int trx_model_info(trx_model* m, int what, int64_t* value);
 /* Device address and size of one resident tensor (for benchmarks and tests). */

@@ -171,20 +171,6 @@ def test_device_generator_matches_host_hash(tmp_path):
         assert _rel_err(dec.forward([t]), ref.step(t)) <= 2e-3
 
 
-@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-hybrid"])
-def test_fused_layers_match_per_operation_kernels(tiny_images, golden, name):
-    """One kernel per full-attention layer (grid barriers between its phases) against one kernel
-    per operation: the same greedy tokens, logits equal to float rounding."""
-    prompt = golden[f"prompt/{name}"]
-    a = _decoder(tiny_images[(name, True)], max_new=16, layer_fusion=True)
-    b = _decoder(tiny_images[(name, True)], max_new=16, layer_fusion=False)
-    assert a.fused_layers and not b.fused_layers
-    ta, tb = a.generate_fresh(prompt, 16), b.generate_fresh(prompt, 16)
-    assert ta == tb
-    assert _rel_err(a.logits(), b.logits()) <= 1e-3
-    assert a.generate_fresh(prompt, 16, use_graph=False) == ta
-
-
 @pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-ternemb", "tiny-hybrid"])
 @pytest.mark.parametrize("packed", [0, 63])
 def test_packed_projections_match_oracle(tiny_images, golden, name, packed):

@@ -1,12 +1,10 @@
-// Device code of decode attention, shared by the per-operation kernels (trx_ops.hip) and the
-// fused decoder-layer kernel (trx_layer.hip).
+// Device code of decode attention for the split kernel and the merge kernel (trx_ops.hip).
 //
 // Split body: the work of one (kv head g, split sp) pair. It owns the positions
 // [sp*chunk, (sp+1)*chunk) of the T = pos + 1 cached ones (chunk = ceil(T / n_split)), for the
 // REP q heads sharing g (model/fastref.py:216-241):
 //   - the split's K and V rows are loaded into registers first (16-byte loads, HD/8 lanes per
-//     position), so one memory round trip overlaps the rest of the prologue (fused: the grid
-//     barrier that makes q, k and v ready);
+//     position), so one memory round trip overlaps the rest of the prologue;
 //   - q: RMS-normalised per head, rotated (NEOX pairs on the first rope_n dims, angle =
 //     pos * freq in fp32) and scaled by 1/sqrt(hd); the block holding `pos` does the same for
 //     the new k and appends k (post-RoPE) and v to the fp16 cache;

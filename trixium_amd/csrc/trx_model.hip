@@ -14,7 +14,6 @@
 
 #include "trx_internal.h"
 #include "trx_ops.h"
-#include "trx_layer.h"
 #include "trx_model.h"
 #include "trx_tgemv.h"
 
@@ -59,12 +58,6 @@ struct Model {
   int n_attn = 0, n_dn = 0;
   std::vector<int> attn_index, dn_index;           // per layer: index among attn / dn layers
   int n_split = 0;                                 // attention splits of the per-operation kernels
-  // Fused full-attention layers (one kernel per layer, grid barriers between its phases).
-  LayerSetup layer;
-  bool fused = false;
-  int fused_split = 0;
-  unsigned long long* bar = nullptr;                // barrier counters
-  unsigned* xcc_blocks = nullptr;
   // Packed copies of the projections in packed_ops (repacked from the arena after its tensors
   // change), and the workspace their GEMVs share.
   std::map<std::pair<int, int>, PackedMat> packed;
@@ -104,7 +97,7 @@ struct Model {
   int* head_from() { return ctl + 3; }
   int* prompt() { return ctl + 8; }
   int* out() { return ctl + 8 + cfg.max_ctx; }
-  int* err() { return ctl + 4; }                   // set by a fused layer whose barrier timed out
+  int* err() { return ctl + 4; }                   // set by a kernel whose bounded wait timed out
 };
 
 static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
@@ -385,54 +378,6 @@ int dn_layer_launch(Model& m, int l, hipStream_t s) {
                     m.x, TRX_EPI_RESID, m.x, s);
 }
 
-// Full-attention layer as one kernel (trx_layer.hip): the same projections, attention and FFN
-// as the per-operation launches below.
-static int fused_layer_launch(Model& m, int l, hipStream_t s) {
-  const trx_model_config& c = m.cfg;
-  const int E = c.n_embd, hd = c.head_dim, F = c.ffn_dim, wk = c.weight_kind;
-  const int qrows = c.n_head * hd * (c.attn_gated ? 2 : 1), kvrows = c.n_kv_head * hd;
-  LayerParams lp = {};
-  int rc;
-  if ((rc = layer_gemv_params(lp.qkv, P(m, TRX_ROLE_ATTN_Q, l), wk, qrows + 2 * kvrows, E, m.x,
-                              PF(m, TRX_ROLE_ATTN_NORM, l), c.rms_eps, m.qkv, TRX_EPI_STORE, nullptr, 2))) return rc;
-  if ((rc = layer_gemv_params(lp.o, P(m, TRX_ROLE_ATTN_OUT, l), wk, E, c.n_head * hd, m.attn_out, nullptr,
-                              c.rms_eps, m.x, TRX_EPI_RESID, m.x, 1))) return rc;
-  if ((rc = layer_gemv_params(lp.gu, P(m, TRX_ROLE_FFN_GATE, l), wk, 2 * F, E, m.x, PF(m, TRX_ROLE_FFN_NORM, l),
-                              c.rms_eps, m.act, TRX_EPI_SWIGLU, nullptr, 2))) return rc;
-  if ((rc = layer_gemv_params(lp.down, P(m, TRX_ROLE_FFN_DOWN, l), wk, E, F, m.act, nullptr, c.rms_eps, m.x,
-                              TRX_EPI_RESID, m.x, 1))) return rc;
-  AttnParams& ap = lp.attn;
-  ap.qkv = m.qkv;
-  ap.q_norm = PF(m, TRX_ROLE_ATTN_Q_NORM, l);
-  ap.k_norm = PF(m, TRX_ROLE_ATTN_K_NORM, l);
-  ap.rope_freq = m.rope_dev;
-  ap.pos = m.pos();
-  const size_t per = (size_t)c.n_kv_head * c.max_ctx * hd;
-  ap.kcache = m.kcache + (size_t)m.attn_index[l] * per;
-  ap.vcache = m.vcache + (size_t)m.attn_index[l] * per;
-  ap.part_m = m.part_m;
-  ap.part_l = m.part_l;
-  ap.part_o = m.part_o;
-  ap.out = m.attn_out;
-  ap.n_head = c.n_head;
-  ap.n_kv = c.n_kv_head;
-  ap.n_rep = c.n_head / c.n_kv_head;
-  ap.hd = hd;
-  ap.rope_n = c.rope_dims ? c.rope_dims : hd;
-  ap.max_ctx = c.max_ctx;
-  ap.n_split = m.fused_split;
-  ap.gated = c.attn_gated;
-  ap.eps = c.rms_eps;
-  lp.bar = m.bar;
-  lp.xcc_blocks = m.xcc_blocks;
-  lp.pos = m.pos();
-  lp.n_layers = m.n_attn;
-  lp.layer_slot = m.attn_index[l];
-  lp.n_xcc = m.layer.n_xcc;
-  lp.err = m.err();
-  return launch_layer(m.layer, lp, s);
-}
-
 static int run_step(Model& m, hipStream_t s) {
   const trx_model_config& c = m.cfg;
   const int E = c.n_embd, hd = c.head_dim, F = c.ffn_dim;
@@ -466,7 +411,7 @@ static int run_step(Model& m, hipStream_t s) {
   // The residual stream between kernels is x = *xc, plus the sums of a producer's partials while
   // pend.in is set: a packed consumer adds them in its prologue and stores x to the other buffer.
   // A producer hands on partial sums only when the next consumer is a packed GEMV; otherwise it
-  // reduces them into m.x (the DeltaNet and fused-layer kernels read m.x).
+  // reduces them into m.x (the DeltaNet kernels read m.x).
   float* xc = m.x;
   PartialSums pend = {};
   auto other = [&](const float* p) { return p == m.x ? m.x2 : m.x; };
@@ -498,17 +443,13 @@ static int run_step(Model& m, hipStream_t s) {
   // Whether the residual after layer l goes to a packed GEMV that takes the producer's S slices.
   auto next_packed = [&](int l, int S) {
     if (S > tgemv_resid_slices_max()) return false;
-    if (l + 1 < c.n_layer) return !m.is_dn(l + 1) && !m.fused && packed(OP_QKV, l + 1) != nullptr;
+    if (l + 1 < c.n_layer) return !m.is_dn(l + 1) && packed(OP_QKV, l + 1) != nullptr;
     return packed(OP_HEAD, 0) != nullptr;
   };
 
   for (int l = 0; l < c.n_layer; ++l) {
     if (m.is_dn(l)) {
       if ((rc = dn_layer_launch(m, l, s))) return rc;
-    } else if (m.fused) {
-      // Attention and the FFN in one launch.
-      if ((rc = fused_layer_launch(m, l, s))) return rc;
-      continue;
     } else {
       // q|k|v with the attention RMSNorm fused in the prologue.
       if (const PackedMat* pq = packed(OP_QKV, l)) {
@@ -706,11 +647,12 @@ TRX_API int trx_model_create(const trx_model_config* cfg, const float* rope_freq
             "trx_model_create: unsupported geometry");
   TRX_CHECK(c.weight_kind == TRX_KIND_TERNARY || c.weight_kind == TRX_KIND_TERNARY5, TRX_E_INVALID,
             "trx_model_create: weight_kind must be ternary");
+  TRX_CHECK(c.persistent == 0, TRX_E_INVALID, "trx_model_create: persistent %d is not supported", c.persistent);
   if (c.hadamard_block) {
     const int B = c.hadamard_block;
     TRX_CHECK(B >= 64 && B <= 1024 && (B & (B - 1)) == 0 && c.hadamard_scale > 0.f, TRX_E_INVALID,
               "trx_model_create: Hadamard block %d unsupported", B);
-    TRX_CHECK(!c.layer_fusion && (c.head_tied || c.head_kind != TRX_KIND_F16), TRX_E_INVALID,
+    TRX_CHECK(c.head_tied || c.head_kind != TRX_KIND_F16, TRX_E_INVALID,
               "trx_model_create: a rotated model runs one kernel per operation with a ternary head");
     for (int i = 0; i < 4; ++i)
       TRX_CHECK(c.hadamard_widths[i] >= 0 && c.hadamard_widths[i] % B == 0, TRX_E_INVALID,
@@ -739,19 +681,7 @@ TRX_API int trx_model_create(const trx_model_config* cfg, const float* rope_freq
     set_error("trx_model_create: context %d is too long for the attention kernel", c.max_ctx);
     return fail(TRX_E_INVALID);
   }
-  if ((rc = dalloc(m, (void**)&m.bar, 17 * 32 * sizeof(unsigned long long)))) return fail(rc);
-  if ((rc = dalloc(m, (void**)&m.xcc_blocks, 16 * sizeof(unsigned)))) return fail(rc);
-  if (c.layer_fusion && m.n_attn > 0 && c.n_kv_head > 0) {
-    const int rep = c.n_head / c.n_kv_head;
-    if ((rc = layer_prepare(m.layer, c.weight_kind, rep, hd, c.n_embd, c.n_head * hd, c.ffn_dim, m.xcc_blocks)))
-      return fail(rc);
-    if (m.layer.ok) {
-      m.fused_split = m.layer.blocks / c.n_kv_head;
-      m.fused = m.fused_split >= 1 && m.fused_split <= 256 && c.n_head <= m.layer.blocks &&
-                cdiv(c.max_ctx, m.fused_split) <= attention_max_chunk(hd);
-    }
-  }
-  const int splits = std::max(m.n_split, m.fused ? m.fused_split : 0);
+  const int splits = m.n_split;
   const size_t kv = (size_t)m.n_attn * c.n_kv_head * c.max_ctx * hd;
   if (m.n_attn) {
     if ((rc = dalloc(m, (void**)&m.kcache, kv * 2))) return fail(rc);
@@ -907,7 +837,6 @@ TRX_API int trx_model_reset(trx_model* h) {
   m.host_pos = -1;
   TRX_HIP(hipMemcpyAsync(m.ctl, init, sizeof init, hipMemcpyHostToDevice, m.stream));
   TRX_HIP(hipMemsetAsync(m.slot, 0, 8, m.stream));
-  TRX_HIP(hipMemsetAsync(m.bar, 0, 17 * 32 * sizeof(unsigned long long), m.stream));
   if (m.n_dn) {
     const int nq = c.dn_num_k_heads * c.dn_k_head_dim, nvh = c.dn_num_v_heads * c.dn_v_head_dim;
     TRX_HIP(hipMemsetAsync(m.conv_state, 0, (size_t)m.n_dn * (c.dn_conv_kernel - 1) * (2 * nq + nvh) * 4, m.stream));
@@ -976,14 +905,14 @@ TRX_API int trx_model_finalize(trx_model* h) {
   return launch_finalize(m.pos(), m.n_prompt(), m.slot, m.out(), m.cfg.max_new, m.stream);
 }
 
-// After the stream has drained: a fused layer whose grid barrier timed out left garbage.
+// After the stream has drained: a kernel whose bounded wait timed out left garbage.
 static int check_err(Model& m) {
   int e = 0;
   TRX_HIP(hipMemcpy(&e, m.err(), 4, hipMemcpyDeviceToHost));
   if (e) {
     const int zero = 0;
     TRX_HIP(hipMemcpy(m.err(), &zero, 4, hipMemcpyHostToDevice));
-    TRX_CHECK(false, TRX_E_HIP, "a fused layer's grid barrier timed out (not every block was resident)");
+    TRX_CHECK(false, TRX_E_HIP, "a bounded wait timed out on the device (results of this call are invalid)");
   }
   return TRX_OK;
 }
@@ -1048,7 +977,7 @@ TRX_API int trx_model_info(trx_model* h, int what, int64_t* value) {
     case TRX_INFO_ARENA_BYTES: *value = (int64_t)m.arena_bytes; break;
     case TRX_INFO_DEVICE_BYTES: *value = (int64_t)m.dev_bytes; break;
     case TRX_INFO_STREAM: *value = (int64_t)(intptr_t)m.stream; break;
-    case TRX_INFO_FUSED_LAYERS: *value = m.fused ? 1 : 0; break;
+    case TRX_INFO_PERSISTENT: *value = 0; break;
     case TRX_INFO_PACKED_OPS: *value = m.packed_ops; break;
     case TRX_INFO_WEIGHT_BYTES: {
       int64_t s = 0;

@@ -24,7 +24,7 @@ from .hadamard import image_rotation
 f32 = np.float32
 
 READ_LOGITS, READ_HIDDEN, READ_POSITION, READ_TOKEN, READ_OUT, READ_SLOT, READ_QKV, READ_ATTN, READ_ACT = range(9)
-INFO_ARENA_BYTES, INFO_DEVICE_BYTES, INFO_STREAM, INFO_WEIGHT_BYTES, INFO_FUSED_LAYERS, INFO_PACKED_OPS = range(6)
+INFO_ARENA_BYTES, INFO_DEVICE_BYTES, INFO_STREAM, INFO_WEIGHT_BYTES, INFO_PERSISTENT, INFO_PACKED_OPS = range(6)
 
 # Projections run by the packed GEMV (TRX_PACK_* bits; PACK_AUTO lets the library choose).
 PACK_QKV, PACK_O, PACK_GATE_UP, PACK_DOWN, PACK_HEAD, PACK_DN = 1, 2, 4, 8, 16, 32
@@ -53,7 +53,7 @@ def layer_type_bits(layer_types, n_layer):
 
 
 def make_config(mc, weight_kind, head_kind, head_tied, emb_mode, emb_kind, max_ctx=None, max_new=256,
-                layer_fusion=False, packed_ops=PACK_AUTO):
+                persistent=False, packed_ops=PACK_AUTO):
     """trx_model_config from a ModelConfig (or a BONS header turned into one)."""
     c = _lib.ModelConfig()
     for name in ("n_layer", "n_embd", "n_head", "n_kv_head", "head_dim", "ffn_dim", "vocab",
@@ -67,7 +67,7 @@ def make_config(mc, weight_kind, head_kind, head_tied, emb_mode, emb_kind, max_c
     c.layer_types[0], c.layer_types[1] = lo, hi
     c.weight_kind, c.head_kind, c.head_tied = weight_kind, head_kind, int(bool(head_tied))
     c.emb_mode, c.emb_kind, c.max_new = emb_mode, emb_kind, int(max_new)
-    c.layer_fusion = int(bool(layer_fusion))
+    c.persistent = int(persistent)
     c.packed_ops = int(packed_ops)
     return c
 
@@ -100,7 +100,7 @@ class Decoder:
 
     # Construction ------------------------------------------------------------------------------
     @classmethod
-    def from_image(cls, img, max_ctx=None, max_new=256, use_graph=True, layer_fusion=False,
+    def from_image(cls, img, max_ctx=None, max_new=256, use_graph=True, persistent=False,
                    packed_ops=PACK_AUTO):
         """Load a BONS image (path or BONSReader) into HBM."""
         from .bons import BONSReader
@@ -129,10 +129,10 @@ class Decoder:
         rot = image_rotation(img)
         if rot is not None:
             # A rotated model: one kernel per operation, every projection's input rotated first
-            # (no partial-sum handoffs between packed GEMVs, no fused layers).
-            if layer_fusion:
-                raise ValueError("a rotated (Hadamard) image runs without layer fusion")
-        cfg = make_config(mc, weight_kind, head_kind, head_tied, 0, emb_kind, max_ctx, max_new, layer_fusion,
+            # (no partial-sum handoffs between packed GEMVs, no persistent kernel).
+            if persistent:
+                raise ValueError("a rotated (Hadamard) image runs one kernel per operation")
+        cfg = make_config(mc, weight_kind, head_kind, head_tied, 0, emb_kind, max_ctx, max_new, persistent,
                           packed_ops)
         if rot is not None:
             block, scale, signs = rot
@@ -150,13 +150,13 @@ class Decoder:
 
     @classmethod
     def synthetic(cls, mc, seed=0, weight_kind=L.KIND_TERNARY5, max_ctx=None, max_new=256,
-                  use_graph=True, layer_fusion=False, packed_ops=PACK_AUTO):
+                  use_graph=True, persistent=False, packed_ops=PACK_AUTO):
         """Fill every tensor on the device from the counter-based generator (same values as
         trixium_amd.synth.hashed_*): ternary token_embd rows (embedded by decoding the row), an
         untied ternary LM head unless the config ties them. A hybrid's DeltaNet beta|alpha Q8
         rows come from the host (seeded int8 values, fp16 scales U(0.01, 0.05))."""
         cfg = make_config(mc, weight_kind, weight_kind, mc.tie_embeddings, 1, weight_kind, max_ctx, max_new,
-                          layer_fusion, packed_ops)
+                          persistent, packed_ops)
         d = cls(mc, cfg, use_graph)
         try:
             ranges = np.array([SYNTH_SCALE[0], SYNTH_SCALE[1] - SYNTH_SCALE[0],
@@ -336,9 +336,9 @@ class Decoder:
         return v.value
 
     @property
-    def fused_layers(self):
-        """True when full-attention layers run as one kernel each."""
-        return bool(self.info(INFO_FUSED_LAYERS))
+    def persistent(self):
+        """True when each position runs as one persistent kernel."""
+        return bool(self.info(INFO_PERSISTENT))
 
     @property
     def stream(self):
