@@ -165,6 +165,7 @@ int trx_gemv_packed_parts_f32(const uint8_t* packed, int kind, int M, int K, con
 #define TRX_ROLE_FFN_GATE 11
 #define TRX_ROLE_FFN_UP 12
 #define TRX_ROLE_FFN_DOWN 13
+#define TRX_ROLE_ROPE_TAB 14   /* int16 Q14 [max_ctx][rope_dims]: cos half, then sin half */
 #define TRX_ROLE_TOK_EMB16 15
 #define TRX_ROLE_TOK_EMB16_EXP 16
 #define TRX_ROLE_ATTN_QKV 17
@@ -209,6 +210,11 @@ typedef struct {
   float hadamard_scale;        /* the rotation tensors' scale (a power of two) */
   int hadamard_widths[4];      /* the rotated input widths (0 = unused); signs per width as
                                   model tensors TRX_ROLE_HADAMARD, layer = index here */
+  int rope_table;              /* 1: RoPE cos/sin per position from the model tensor
+                                  TRX_ROLE_ROPE_TAB (the image's int16 Q14 rows [cos | sin] of
+                                  rope_dims values, max_ctx rows; model/bons.py:356-367, read as
+                                  model/mirror.py:478-483 does), which is how YaRN scaling
+                                  reaches the decoder; 0: angles pos * rope_freq[i] */
 } trx_model_config;
 
 #define TRX_PACK_QKV 1         /* attention q|k|v */

@@ -2,7 +2,10 @@
 
 The arithmetic is model/fastref.py's (HybridRef: fp32 activations, weights dequantised as
 (code - 1) * scale and held in fp16, which is exact for ternary; embedding rows from the int16
-BFP table; plain RoPE with float32 angles; NEOX pairs on the first rope_dims of a head). The
+BFP table; plain RoPE with float32 angles; NEOX pairs on the first rope_dims of a head). An
+image whose rope table is not plain RoPE (YaRN scaling, which exists only in that table) rotates
+with the table's Q14 cos/sin per position instead, as the firmware and model/mirror.py:478-483
+do; fastref ignores the table. The
 state semantics are model/golden.py:FloatModel's (K/V caches appended post-norm/post-RoPE (K)
 and raw (V), a (K-1)-deep conv window and a per-value-head fp32 recurrent matrix for every
 DeltaNet layer, `pos` advanced per forward), so the reference steps one token at a time like
@@ -38,6 +41,8 @@ class FloatRef:
         # fastref.py:62-63: theta**(-2i/n) evaluated in float32.
         self.rope_freq = np.array([f32(f32(h["rope_theta"]) ** f32(-2.0 * i / self.rope_n))
                                    for i in range(self.rope_n // 2)], dtype=f32)
+        from trixium_amd.bons import image_rope_table
+        self.rope_tab = image_rope_table(img)
         self.norm_attn = [self._f32(L.ROLE_ATTN_NORM, l) for l in range(self.n_layer)]
         self.norm_ffn = [self._f32(L.ROLE_FFN_NORM, l) for l in range(self.n_layer)]
         self.norm_q, self.norm_k, self.norm_ssm, self.ssm_a, self.ssm_dt, self.conv_w = {}, {}, {}, {}, {}, {}
@@ -142,9 +147,13 @@ class FloatRef:
             q, gate = qf.reshape(nh, hd), None
         q = self.rmsnorm(q, self.norm_q[l])
         k = self.rmsnorm(k, self.norm_k[l])
-        ang = (f32(pos) * self.rope_freq).astype(f32)
-        cos, sin = np.cos(ang), np.sin(ang)
         half = self.rope_n // 2
+        if getattr(self, "rope_tab", None) is not None:
+            row = self.rope_tab[pos].astype(f32) * f32(2.0**-14)
+            cos, sin = row[:half], row[half:]
+        else:
+            ang = (f32(pos) * self.rope_freq).astype(f32)
+            cos, sin = np.cos(ang), np.sin(ang)
 
         def rope(x):
             x = x.copy()

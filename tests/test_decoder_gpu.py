@@ -345,3 +345,31 @@ def test_synthetic_hybrid_decodes():
     a.reset()
     assert a.generate(prompt, 8) == b.generate(prompt, 8)
     assert np.array_equal(a.read_tensor(L.ROLE_SSM_BETA, 1), b.read_tensor(L.ROLE_SSM_BETA, 1))
+
+
+def test_yarn_rope_table_decodes_like_floatmodel(tmp_path):
+    """A YaRN-scaled model (its scaling lives only in the image's rope table) on the GPU: the
+    attention rotates with the table's Q14 rows. Every teacher-forced position within 2e-3 of the
+    oracle, the reference's golden.FloatModel logits (tests/golden/golden_yarn.npz) within 1e-2,
+    and FloatModel's 80 greedy tokens."""
+    import os
+    import sys
+    from trixium_amd.model import Decoder
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
+    from make_golden_yarn import SEED, yarn_config
+    z = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden_yarn.npz"))
+    cfg = yarn_config()
+    p = str(tmp_path / "yarn.img")
+    bons.write_image(cfg, synth.small_model_tensors(cfg, SEED, True), 1, p, trit5=True)
+    seq, n = [int(t) for t in z["seq"]], int(z["n_prompt"])
+    dec = Decoder.from_image(p, max_new=len(seq) - n)
+    assert dec.cfg.rope_table == 1
+    lg = _teacher_forced_logits(dec, seq, n)
+    ref = FloatRef(bons.BONSReader(p), kv_fp16=True)
+    want = [ref.forward(seq[:n])] + [ref.step(t) for t in seq[n:]]
+    errs = [_rel_err(g, w) for g, w in zip(lg, want)]
+    print("yarn: max rel err vs oracle", max(errs))
+    assert max(errs) <= 2e-3
+    for i, pos in enumerate(z["pos"]):
+        assert _rel_err(lg[pos - (n - 1)], z["floatmodel_logits"][i]) <= LOGIT_RTOL
+    assert dec.generate_fresh(seq[:n], len(seq) - n) == seq[n:]

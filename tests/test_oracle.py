@@ -8,7 +8,7 @@ import pytest
 
 from oracle import bitexact as bx
 from oracle.floatref import FloatRef
-from trixium_amd import bons, configs as C
+from trixium_amd import bons, configs as C, layout as L, synth
 
 
 def test_rne_shift_known_answers():
@@ -160,3 +160,46 @@ def test_shape_sample_steps_like_the_cpu_baseline():
     lg = s.step(1)
     assert lg.shape == (mc.vocab,) and np.isfinite(lg).all()
     s.step(2, want_logits=False)
+
+
+def _yarn_fixture(tmp_path):
+    import os
+    import sys
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
+    from make_golden_yarn import SEED, yarn_config
+    z = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden_yarn.npz"))
+    cfg = yarn_config()
+    p = str(tmp_path / "yarn.img")
+    bons.write_image(cfg, synth.small_model_tensors(cfg, SEED, True), 1, p, trit5=True)
+    return p, z
+
+
+def test_yarn_rope_table_follows_floatmodel(tmp_path):
+    """A YaRN-scaled model (factor 4 over an original context of 32) exists only in the image's
+    rope table. The writer's image equals the reference writer's byte for byte (rope table
+    included), and the oracle, rotating with the table's Q14 rows as the firmware and the mirror
+    do, follows the reference's golden.FloatModel (float64 YaRN tables) to 1e-4 at positions on
+    both sides of the original context, while fastref's plain RoPE is far from it: a table
+    without the ramp or without mscale would fail one of the two."""
+    import hashlib
+    p, z = _yarn_fixture(tmp_path)
+    assert hashlib.sha256(open(p, "rb").read()).hexdigest() == bytes(z["image_sha256"]).decode()
+    img = bons.BONSReader(p)
+    assert bons.image_rope_table(img) is not None
+    r = FloatRef(img)
+    seq, n = [int(t) for t in z["seq"]], int(z["n_prompt"])
+    lg = [r.forward(seq[:n])] + [r.step(t) for t in seq[n:]]
+    for i, pos in enumerate(z["pos"]):
+        got, want = lg[pos - (n - 1)], z["floatmodel_logits"][i]
+        assert np.abs(got - want).max() <= 1e-4 * np.abs(want).max(), pos
+        assert np.abs(z["fastref_logits"][i] - want).max() >= 0.1 * np.abs(want).max(), pos
+        assert int(np.argmax(got)) == int(np.argmax(want))
+
+
+def test_plain_rope_table_is_not_a_yarn_table(tiny_images):
+    """Every fixture image carries a rope table; with yarn_factor 1 it is plain RoPE, which the
+    loaders recognise (the oracle then computes the angles as fastref does)."""
+    for key in (("tiny-qwen3", True), ("tiny-hybrid", False)):
+        img = bons.BONSReader(tiny_images[key])
+        assert img.find(L.ROLE_ROPE_TAB, 0) is not None
+        assert bons.image_rope_table(img) is None

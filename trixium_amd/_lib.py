@@ -33,7 +33,7 @@ class ModelConfig(ctypes.Structure):
         (n, ctypes.c_int) for n in ("weight_kind", "head_kind", "head_tied", "emb_mode", "emb_kind",
                                     "max_new", "persistent", "packed_ops")] + [
         ("hadamard_block", ctypes.c_int), ("hadamard_scale", ctypes.c_float),
-        ("hadamard_widths", ctypes.c_int * 4)]
+        ("hadamard_widths", ctypes.c_int * 4), ("rope_table", ctypes.c_int)]
 
 
 _mcp = ctypes.POINTER(ModelConfig)

@@ -195,6 +195,31 @@ def rope_tables(cfg, positions):
     return np.cos(theta) * mscale, np.sin(theta) * mscale
 
 
+def rope_q14(cfg, n_pos):
+    """The image's rope table: one row per position, [cos | sin] of rope_tables in Q14 int16
+    (model/bons.py:356-367; Q14 holds YaRN's mscale > 1)."""
+    cos, sin = rope_tables(cfg, np.arange(n_pos))
+    tab = np.concatenate([cos, sin], axis=1)
+    return np.clip(np.round(tab * (1 << 14)), -32767, 32767).astype(np.int16)
+
+
+def image_rope_table(img):
+    """The image's Q14 rope table (int16 [max_ctx, rope_dims]) when it differs from plain RoPE
+    (theta^(-2i/n), no YaRN: what model/fastref.py computes), else None. A YaRN-scaled model
+    exists only in this table (the header has no YaRN fields); the firmware and the mirror read
+    it per position (model/mirror.py:478-483)."""
+    e = img.find(L.ROLE_ROPE_TAB, 0)
+    if e is None:
+        return None
+    _, t14 = img.entry_tensor(e)
+    t14 = np.asarray(t14, dtype=np.int16).reshape(e["rows"], e["cols"])
+    h = img.header
+    plain = type("PlainRope", (), dict(rope_dims=h["rope_dims"], head_dim=h["head_dim"],
+                                       rope_theta=float(h["rope_theta"]), yarn_factor=1.0,
+                                       yarn_orig_ctx=0))
+    return None if np.array_equal(t14, rope_q14(plain, e["rows"])) else t14
+
+
 def embed_bfp_rows(codes, scales):
     """Ternary embedding rows -> the int16 BFP table (mantissas (rows, cols) int16, exponents
     (rows,) int32), integer-exact: every group's (code-1)*m11 aligned to the row's smallest scale
@@ -258,11 +283,9 @@ def write_image(cfg, tensors, n_channels, path, tokenizer_sha256=b"", manifest_p
     derived rope table, .w16 companions, int16 embedding table, optional trit5 storage)."""
     tensors = list(tensors)
     if cfg.max_ctx and cfg.head_dim:
-        cos, sin = rope_tables(cfg, np.arange(cfg.max_ctx))
-        tab = np.concatenate([cos, sin], axis=1)
-        t14 = np.clip(np.round(tab * (1 << 14)), -32767, 32767).astype(np.int16)
+        t14 = rope_q14(cfg, cfg.max_ctx)
         tensors.append(TensorSpec("rope_tab", L.ROLE_ROPE_TAB, 0, L.KIND_NORM16, cfg.max_ctx,
-                                  tab.shape[1], values=t14, flags=L.FLAG_REPLICATED))
+                                  t14.shape[1], values=t14, flags=L.FLAG_REPLICATED))
     for spec in [t for t in tensors if t.kind == L.KIND_F32]:
         w = spec.values.astype(np.float64)
         e = L.norm16_exp(w)

@@ -6,7 +6,7 @@
 //   - the split's K and V rows are loaded into registers first (16-byte loads, HD/8 lanes per
 //     position), so one memory round trip overlaps the rest of the prologue;
 //   - q: RMS-normalised per head, rotated (NEOX pairs on the first rope_n dims, angle =
-//     pos * freq in fp32) and scaled by 1/sqrt(hd); the block holding `pos` does the same for
+//     pos * freq in fp32, or the cos/sin of the model's Q14 table row) and scaled by 1/sqrt(hd); the block holding `pos` does the same for
 //     the new k and appends k (post-RoPE) and v to the fp16 cache;
 //   - scores, softmax over the split, the unnormalised V sum; the split's (max, sum, output) go
 //     to the partials.
@@ -92,7 +92,12 @@ __device__ __forceinline__ void attn_split_body(const AttnParams& p, int bid, Wa
         for (int d = tid; d < HD; d += kAttnThreads) hv[REP + 1][d] = ld_vec<FUSED>(kraw + (size_t)p.n_kv * HD + d);
       for (int i = tid; i < half; i += kAttnThreads) {
         float sn, cs;
-        sincosf((float)pos * p.rope_freq[i], &sn, &cs);
+        if (p.rope_tab) {
+          cs = (float)p.rope_tab[(size_t)pos * p.rope_n + i] * (1.0f / 16384.0f);
+          sn = (float)p.rope_tab[(size_t)pos * p.rope_n + half + i] * (1.0f / 16384.0f);
+        } else {
+          sincosf((float)pos * p.rope_freq[i], &sn, &cs);
+        }
         cs_s[i] = cs;
         sn_s[i] = sn;
       }

@@ -2,7 +2,7 @@
 // of the T = pos + 1 cached positions, the split's partial (max, sum, output) per q head, and the
 // merge of a kv head's splits by the block that finishes last. The arithmetic is that of
 // model/fastref.py:216-241 for one position: q and k RMS-normalised per head, NEOX RoPE on the
-// first rope_n dims (angle = pos * freq in fp32), q scaled by 1/sqrt(hd), k (post-RoPE) and v
+// first rope_n dims (angle = pos * freq in fp32, or the model's Q14 cos/sin table row), q scaled by 1/sqrt(hd), k (post-RoPE) and v
 // appended to the fp16 cache and read back rounded, softmax over the positions, the output gate
 // of gated attention.
 //
@@ -115,7 +115,12 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fd_kernel(AttnParams p) {
   if (n > 0) {
     if (tid < half) {
       float sn, cs;
-      sincosf((float)pos * fr, &sn, &cs);
+      if (p.rope_tab) {
+        cs = (float)p.rope_tab[(size_t)pos * p.rope_n + tid] * (1.0f / 16384.0f);
+        sn = (float)p.rope_tab[(size_t)pos * p.rope_n + half + tid] * (1.0f / 16384.0f);
+      } else {
+        sincosf((float)pos * fr, &sn, &cs);
+      }
       cs_s[tid] = cs;
       sn_s[tid] = sn;
     }

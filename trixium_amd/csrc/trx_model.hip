@@ -168,6 +168,8 @@ static void plan_arena(Model& m, size_t& cur) {
   if (c.hadamard_block)
     for (int i = 0; i < 4; ++i)
       if (c.hadamard_widths[i]) plan_tensor(m, cur, TRX_ROLE_HADAMARD, i, TRX_KIND_F32, 1, c.hadamard_widths[i]);
+  if (c.rope_table && m.n_attn)
+    plan_tensor(m, cur, TRX_ROLE_ROPE_TAB, 0, TRX_KIND_NORM16, c.max_ctx, c.rope_dims ? c.rope_dims : c.head_dim);
 }
 
 static int dalloc(Model& m, void** p, size_t bytes);
@@ -467,6 +469,7 @@ static int run_step(Model& m, hipStream_t s) {
       ap.q_norm = PF(m, TRX_ROLE_ATTN_Q_NORM, l);
       ap.k_norm = PF(m, TRX_ROLE_ATTN_K_NORM, l);
       ap.rope_freq = m.rope_dev;
+      ap.rope_tab = m.cfg.rope_table ? (const int16_t*)P(m, TRX_ROLE_ROPE_TAB, 0) : nullptr;
       ap.pos = m.pos();
       const size_t per = (size_t)c.n_kv_head * c.max_ctx * hd;
       ap.kcache = m.kcache + (size_t)m.attn_index[l] * per;

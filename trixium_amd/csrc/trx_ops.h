@@ -29,6 +29,7 @@ struct AttnParams {
   const float* q_norm;
   const float* k_norm;
   const float* rope_freq;  // [rope_n/2]
+  const int16_t* rope_tab; // or [max_ctx][rope_n] Q14: cos half, then sin half (null: rope_freq)
   const int* pos;
   __half* kcache;          // [n_kv][max_ctx][hd]
   __half* vcache;

@@ -139,8 +139,16 @@ class Decoder:
             cfg.hadamard_block, cfg.hadamard_scale = block, scale
             for i, w in enumerate(signs):
                 cfg.hadamard_widths[i] = w
+        # A rope table that is not plain RoPE (YaRN scaling) is read per position on the device.
+        from .bons import image_rope_table
+        t14 = image_rope_table(img)
+        if t14 is not None:
+            if t14.shape[0] < cfg.max_ctx:
+                raise ValueError(f"the image's rope table holds {t14.shape[0]} positions, max_ctx is {cfg.max_ctx}")
+            cfg.rope_table = 1
         d = cls(mc, cfg, use_graph)
         d.n_channels = img.header["n_channels"]
+        d._rope_t14 = None if t14 is None else np.ascontiguousarray(t14[:cfg.max_ctx])
         try:
             d._load_image(img)
         except Exception:
@@ -222,6 +230,8 @@ class Decoder:
             for r in roles + _LAYER_MATRICES_FFN:
                 self.set_tensor(r, l, self._rows(img, img.find(r, l), wk))
         self.set_tensor(L.ROLE_OUT_NORM, 0, self._f32(img, L.ROLE_OUT_NORM, 0))
+        if getattr(self, "_rope_t14", None) is not None and mc.n_layer > mc.n_dn_layers:
+            self.set_tensor(L.ROLE_ROPE_TAB, 0, self._rope_t14)
         rot = image_rotation(img)
         if rot is not None:
             for i, (w, sg) in enumerate(rot[2].items()):
