@@ -263,7 +263,8 @@ int trx_model_sync(trx_model* m);
 int trx_model_generate(trx_model* m, const int32_t* prompt, int n_prompt, int n_new, int32_t* out,
                        int use_graph);
 #define TRX_READ_LOGITS 0      /* float32 [vocab] of the last forward that ran the head */
-#define TRX_READ_HIDDEN 1      /* float32 [n_embd]: residual stream after the last layer */
+#define TRX_READ_HIDDEN 1      /* float32 [n_embd]: the final normed hidden state of the last
+                                  forward, rmsnorm(residual, output norm) (fastref.py:244-258) */
 #define TRX_READ_POSITION 2    /* int32 */
 #define TRX_READ_TOKEN 3       /* int32: the token of the last forward */
 #define TRX_READ_OUT 4         /* int32 [max_new]: generated tokens */
@@ -271,7 +272,17 @@ int trx_model_generate(trx_model* m, const int32_t* prompt, int n_prompt, int n_
 #define TRX_READ_QKV 6         /* float32: q|k|v projection of the last attention layer run */
 #define TRX_READ_ATTN 7        /* float32 [n_head*head_dim]: its attention output */
 #define TRX_READ_ACT 8         /* float32 [ffn_dim]: the last layer's SwiGLU activation */
+#define TRX_READ_RESIDUAL 9    /* float32 [n_embd]: the residual stream after the last layer */
 int trx_model_read(trx_model* m, int what, void* host, size_t bytes);
+/* Teacher-forced scoring of a sequence from position 0 (model/fastref.py:263-273 score; resets
+ * the model): nll[i] = logsumexp(logits_i) - logits_i[tokens[i + 1]] for i < n - 1 (host float32,
+ * may be NULL), and the final normed hidden states hidden[n][n_embd] (host, may be NULL,
+ * fastref.py:244-258 hidden). Synchronous; every position runs the LM head. */
+int trx_model_score(trx_model* m, const int32_t* tokens, int n, float* nll, float* hidden);
+/* The LM head applied to n given hidden states (host float32 [n][n_embd] -> [n][vocab]):
+ * model/fastref.py:260-261 logits (the rotation of a rotated model included, no norm).
+ * Synchronous. */
+int trx_model_project_head(trx_model* m, const float* hidden, int n, float* logits);
 #define TRX_INFO_ARENA_BYTES 0
 #define TRX_INFO_DEVICE_BYTES 1
 #define TRX_INFO_STREAM 2

@@ -232,6 +232,21 @@ class FloatRef:
         hn = self.rmsnorm(x, self.out_norm)
         return self.proj(self.head_role, 0, hn)[:self.vocab]
 
+    def score(self, tokens):
+        """(nll [T-1], final normed hidden states [T, n_embd]) of a sequence teacher-forced from
+        position 0 after a reset (fastref.py:244-273: hidden = rmsnorm(residual, out_norm); the
+        log-sum-exp of every position's logits in float64)."""
+        self.reset()
+        nll, hid = [], []
+        for i, t in enumerate(tokens):
+            lg = self.step(int(t), want_logits=i + 1 < len(tokens))
+            hid.append(self.rmsnorm(self.last_hidden, self.out_norm))
+            if lg is not None:
+                l64 = lg.astype(np.float64)
+                m = l64.max()
+                nll.append(m + np.log(np.exp(l64 - m).sum()) - l64[int(tokens[i + 1])])
+        return np.array(nll, np.float64), np.stack(hid)
+
     def forward(self, tokens):
         """FloatModel.forward contract (golden.py:436-460): logits of the last position."""
         logits = None

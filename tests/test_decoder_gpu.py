@@ -373,3 +373,31 @@ def test_yarn_rope_table_decodes_like_floatmodel(tmp_path):
     for i, pos in enumerate(z["pos"]):
         assert _rel_err(lg[pos - (n - 1)], z["floatmodel_logits"][i]) <= LOGIT_RTOL
     assert dec.generate_fresh(seq[:n], len(seq) - n) == seq[n:]
+
+
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-hybrid"])
+def test_score_hidden_and_head_match_fastref(tiny_images, name):
+    """Decoder.score / hidden / logits(Hs) (model/fastref.py:244-273) on the GPU: the next-token
+    NLLs and the final normed hidden states against the reference's HybridRef.score
+    (tests/golden/golden_score.npz) and the oracle; hidden() after a forward is that position's
+    normed state; the LM head applied to the returned states gives the decode's own logits."""
+    import os
+    z = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden_score.npz"))
+    toks = [int(t) for t in z[f"{name}/tokens"]]
+    dec = _decoder(tiny_images[(name, True)])
+    nll, hid = dec.score(toks)
+    ref_nll, ref_hid = FloatRef(bons.BONSReader(tiny_images[(name, True)]), kv_fp16=True).score(toks)
+    print(name, "nll err vs fastref", np.abs(nll - z[f"{name}/nll"]).max(), "vs oracle", np.abs(nll - ref_nll).max())
+    assert np.abs(nll - ref_nll).max() <= 2e-3
+    assert np.abs(nll - z[f"{name}/nll"]).max() <= 2e-2
+    assert _rel_err(hid, ref_hid) <= 2e-3
+    hp = z[f"{name}/hidden_pos"]
+    assert _rel_err(hid[hp], z[f"{name}/hidden"]) <= LOGIT_RTOL
+    # hidden() of the last forward, and the head over given hidden states.
+    dec.reset()
+    lg = dec.forward(toks[:20])
+    assert np.allclose(dec.hidden(), hid[19], rtol=0, atol=1e-5 * np.abs(hid[19]).max())
+    proj = dec.logits(hid[[19, 5]])
+    assert proj.shape == (2, dec.vocab)
+    assert _rel_err(proj[0], lg) <= 1e-4
+    assert _rel_err(dec.logits(dec.hidden()[None])[0], lg) <= 1e-4

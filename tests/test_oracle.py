@@ -203,3 +203,18 @@ def test_plain_rope_table_is_not_a_yarn_table(tiny_images):
         img = bons.BONSReader(tiny_images[key])
         assert img.find(L.ROLE_ROPE_TAB, 0) is not None
         assert bons.image_rope_table(img) is None
+
+
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-hybrid"])
+def test_floatref_score_matches_fastref(tiny_images, name):
+    """The oracle's score (next-token NLLs) and final normed hidden states against the reference's
+    HybridRef.score on the same model and sequence (tests/golden/golden_score.npz)."""
+    import os
+    z = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden_score.npz"))
+    r = FloatRef(bons.BONSReader(tiny_images[(name, True)]))
+    nll, hid = r.score([int(t) for t in z[f"{name}/tokens"]])
+    assert nll.shape == z[f"{name}/nll"].shape
+    assert np.abs(nll - z[f"{name}/nll"]).max() <= 1e-4
+    want = z[f"{name}/hidden"]
+    got = hid[z[f"{name}/hidden_pos"]]
+    assert np.abs(got - want).max() <= 1e-4 * np.abs(want).max()

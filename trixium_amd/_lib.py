@@ -88,6 +88,8 @@ SIGNATURES = {
     "trx_model_sync": [_vp],
     "trx_model_generate": [_vp, _ip, _i, _i, _ip, _i],
     "trx_model_read": [_vp, _i, _vp, _sz],
+    "trx_model_score": [_vp, _ip, _i, _vp, _vp],
+    "trx_model_project_head": [_vp, _vp, _i, _vp],
     "trx_model_info": [_vp, _i, _i64p],
     "trx_model_tensor_ptr": [_vp, _i, _i, ctypes.POINTER(_vp), _i64p],
     "trx_model_packed_ptr": [_vp, _i, _i, ctypes.POINTER(_vp), ctypes.POINTER(_vp)],

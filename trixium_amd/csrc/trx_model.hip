@@ -85,6 +85,13 @@ struct Model {
   bool sampling = false;
   int smp_channels = 1;
   float* hidden = nullptr;                         // the residual after the last layer
+  // Scoring (trx_model_score): per position the normed hidden state and the next token's NLL.
+  bool scoring = false;
+  float* hid_rows = nullptr;                       // [max_ctx][n_embd]
+  float* nll = nullptr;                            // [max_ctx]
+  float* hid_last = nullptr;                       // [n_embd]: TRX_READ_HIDDEN
+  float* proj_x = nullptr;                         // [n_embd], [vocab]: trx_model_project_head
+  float* proj_y = nullptr;
   hipGraph_t graph = nullptr;
   hipGraphExec_t graph_exec = nullptr;
   size_t dev_bytes = 0;
@@ -627,6 +634,11 @@ static int run_step(Model& m, hipStream_t s) {
     if ((rc = launch_sample(sp, s))) return rc;
   }
   m.hidden = xc;
+  if (m.scoring) {
+    ScoreParams sp = {xc, PF(m, TRX_ROLE_OUT_NORM, 0), c.rms_eps, E, m.hid_rows, c.max_ctx, m.logits, c.vocab,
+                      m.pos(), m.head_from(), m.n_prompt(), m.prompt(), m.nll};
+    if ((rc = launch_score(sp, s))) return rc;
+  }
   return TRX_OK;
 }
 
@@ -712,6 +724,7 @@ TRX_API int trx_model_create(const trx_model_config* cfg, const float* rope_freq
   if ((rc = dalloc(m, (void**)&m.attn_out, (size_t)c.n_head * hd * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.act, (size_t)c.ffn_dim * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.logits, (size_t)c.vocab * 4))) return fail(rc);
+  if ((rc = dalloc(m, (void**)&m.hid_last, (size_t)c.n_embd * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.part_m, (size_t)c.n_head * splits * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.part_l, (size_t)c.n_head * splits * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.part_o, (size_t)c.n_head * splits * hd * 4))) return fail(rc);
@@ -944,6 +957,69 @@ TRX_API int trx_model_generate(trx_model* h, const int32_t* prompt, int n_prompt
   return check_err(m);
 }
 
+TRX_API int trx_model_score(trx_model* h, const int32_t* tokens, int n, float* nll, float* hidden) {
+  TRX_CHECK(h && tokens && n >= 1, TRX_E_INVALID, "trx_model_score: bad arguments");
+  Model& m = h->m;
+  const trx_model_config& c = m.cfg;
+  TRX_CHECK(n <= c.max_ctx, TRX_E_STATE, "trx_model_score: %d tokens exceed max_ctx %d", n, c.max_ctx);
+  int rc;
+  if (!m.nll) {
+    if ((rc = dalloc(m, (void**)&m.nll, (size_t)c.max_ctx * 4))) return rc;
+    if ((rc = dalloc(m, (void**)&m.hid_rows, (size_t)c.max_ctx * c.n_embd * 4))) return rc;
+  }
+  if ((rc = trx_model_reset(h))) return rc;
+  if ((rc = trx_model_set_prompt(h, tokens, n, 0))) return rc;
+  // Every position runs the head and the score launch; the captured graph has no score launch,
+  // so these positions run eagerly.
+  m.scoring = true;
+  rc = trx_model_step(h, n, 0);
+  m.scoring = false;
+  if (rc) return rc;
+  TRX_HIP(hipStreamSynchronize(m.stream));
+  if ((rc = check_err(m))) return rc;
+  if (nll && n > 1) TRX_HIP(hipMemcpy(nll, m.nll, (size_t)(n - 1) * 4, hipMemcpyDeviceToHost));
+  if (hidden) TRX_HIP(hipMemcpy(hidden, m.hid_rows, (size_t)n * c.n_embd * 4, hipMemcpyDeviceToHost));
+  return TRX_OK;
+}
+
+TRX_API int trx_model_project_head(trx_model* h, const float* hidden, int n, float* logits) {
+  TRX_CHECK(h && hidden && logits && n >= 0, TRX_E_INVALID, "trx_model_project_head: bad arguments");
+  Model& m = h->m;
+  const trx_model_config& c = m.cfg;
+  int rc;
+  if ((rc = check_loaded(m))) return rc;
+  if ((rc = ensure_packed(m))) return rc;
+  if (!m.proj_x) {
+    if ((rc = dalloc(m, (void**)&m.proj_x, (size_t)c.n_embd * 4))) return rc;
+    if ((rc = dalloc(m, (void**)&m.proj_y, (size_t)c.vocab * 4))) return rc;
+  }
+  const int head_role = c.head_tied ? TRX_ROLE_TOK_EMB : TRX_ROLE_LM_HEAD;
+  const int head_kind = c.head_tied ? c.emb_kind : c.head_kind;
+  for (int i = 0; i < n; ++i) {
+    TRX_HIP(hipMemcpyAsync(m.proj_x, hidden + (size_t)i * c.n_embd, (size_t)c.n_embd * 4, hipMemcpyHostToDevice,
+                           m.stream));
+    if (head_kind == TRX_KIND_F16) {
+      DenseParams dp = {};
+      dp.W = P(m, head_role, 0);
+      dp.kind = TRX_KIND_F16;
+      dp.M = c.vocab;
+      dp.K = c.n_embd;
+      dp.row_bytes = 2 * c.n_embd;
+      dp.x = m.proj_x;
+      dp.eps = c.rms_eps;
+      dp.y = m.proj_y;
+      if ((rc = launch_dense_gemv(dp, m.stream))) return rc;
+    } else if ((rc = projection(m, OP_HEAD, 0, P(m, head_role, 0), head_kind, c.vocab, c.n_embd, m.proj_x, nullptr,
+                                m.proj_y, TRX_EPI_STORE, nullptr, m.stream))) {
+      return rc;
+    }
+    TRX_HIP(hipMemcpyAsync(logits + (size_t)i * c.vocab, m.proj_y, (size_t)c.vocab * 4, hipMemcpyDeviceToHost,
+                           m.stream));
+  }
+  TRX_HIP(hipStreamSynchronize(m.stream));
+  return TRX_OK;
+}
+
 TRX_API int trx_model_read(trx_model* h, int what, void* host, size_t bytes) {
   TRX_CHECK(h && host, TRX_E_INVALID, "trx_model_read: null argument");
   Model& m = h->m;
@@ -953,7 +1029,8 @@ TRX_API int trx_model_read(trx_model* h, int what, void* host, size_t bytes) {
   size_t n = 0;
   switch (what) {
     case TRX_READ_LOGITS: src = m.logits; n = (size_t)c.vocab * 4; break;
-    case TRX_READ_HIDDEN: src = m.hidden; n = (size_t)c.n_embd * 4; break;
+    case TRX_READ_HIDDEN: src = m.hid_last; n = (size_t)c.n_embd * 4; break;
+    case TRX_READ_RESIDUAL: src = m.hidden; n = (size_t)c.n_embd * 4; break;
     case TRX_READ_POSITION: src = m.pos(); n = 4; break;
     case TRX_READ_TOKEN: src = m.cur_tok(); n = 4; break;
     case TRX_READ_OUT: src = m.out(); n = (size_t)c.max_new * 4; break;
@@ -967,6 +1044,17 @@ TRX_API int trx_model_read(trx_model* h, int what, void* host, size_t bytes) {
     default: TRX_CHECK(false, TRX_E_INVALID, "trx_model_read: unknown item %d", what);
   }
   TRX_CHECK(bytes <= n, TRX_E_INVALID, "trx_model_read: %zu bytes requested, %zu available", bytes, n);
+  if (what == TRX_READ_HIDDEN) {
+    // fastref's hidden state: the residual through the output RMSNorm (fastref.py:258).
+    ScoreParams sp = {};
+    sp.x = m.hidden;
+    sp.out_norm = PF(m, TRX_ROLE_OUT_NORM, 0);
+    sp.eps = c.rms_eps;
+    sp.n = c.n_embd;
+    sp.hid = m.hid_last;
+    sp.max_rows = 1;
+    if ((rc = launch_score(sp, m.stream))) return rc;
+  }
   TRX_HIP(hipStreamSynchronize(m.stream));
   if ((rc = check_err(m))) return rc;
   TRX_HIP(hipMemcpy(host, src, bytes, hipMemcpyDeviceToHost));

@@ -122,6 +122,28 @@ struct SampleParams {
   unsigned* done;            // blocks finished (zero between launches)
 };
 
+// The final normed hidden state and the sequence score of one position (model/fastref.py:244-273:
+// hidden = rmsnorm(x, out_norm); nll = logsumexp(logits) - logits[next token]). hidden goes to
+// hid + row * n (row = *pos when `pos` is set, else 0; rows past max_rows are skipped); nll[*pos]
+// is written when the position ran the head (*pos >= *head_from) and a next token was fed
+// (*pos + 1 < *n_fed). With logits null only the hidden state is written.
+struct ScoreParams {
+  const float* x;          // the residual after the last layer
+  const float* out_norm;
+  float eps;
+  int n;
+  float* hid;
+  int max_rows;
+  const float* logits;
+  int vocab;
+  const int* pos;
+  const int* head_from;
+  const int* n_fed;
+  const int* fed;          // the fed tokens by absolute position
+  float* nll;
+};
+int launch_score(const ScoreParams& p, hipStream_t s);
+
 int launch_embed(const EmbedParams& p, hipStream_t s);
 int launch_sample(const SampleParams& p, hipStream_t s);
 int launch_finalize(const int* pos, const int* n_prompt, unsigned long long* slot, int* out, int max_out,

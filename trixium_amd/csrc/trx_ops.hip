@@ -545,6 +545,44 @@ int launch_embed(const EmbedParams& p, hipStream_t s) {
   return TRX_OK;
 }
 
+// Score ------------------------------------------------------------------------------------------
+
+__global__ __launch_bounds__(1024) void score_kernel(ScoreParams p) {
+  __shared__ float red[16];
+  const int tid = threadIdx.x;
+  const int pos = p.pos ? *p.pos : 0;
+  // The normed hidden state (fastref.py:143-145 with the output norm, fastref.py:258).
+  float ss = 0.f;
+  for (int i = tid; i < p.n; i += 1024) ss += p.x[i] * p.x[i];
+  const float r = 1.0f / sqrtf(block_sum(ss, red) / (float)p.n + p.eps);
+  if (p.hid && pos < p.max_rows)
+    for (int i = tid; i < p.n; i += 1024) p.hid[(size_t)pos * p.n + i] = p.x[i] * r * p.out_norm[i];
+  if (!p.logits || pos < *p.head_from || pos + 1 >= *p.n_fed) return;
+  // log-sum-exp over the vocabulary, then the next token's negative log-likelihood
+  // (fastref.py:267-272).
+  float mx = -INFINITY;
+  for (int i = tid; i < p.vocab; i += 1024) mx = fmaxf(mx, p.logits[i]);
+  mx = wave_max(mx);
+  __syncthreads();
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  float m = red[0];
+  for (int i = 1; i < 16; ++i) m = fmaxf(m, red[i]);
+  __syncthreads();
+  float se = 0.f;
+  for (int i = tid; i < p.vocab; i += 1024) se += expf(p.logits[i] - m);
+  se = block_sum(se, red);
+  if (tid == 0) p.nll[pos] = (m + logf(se)) - p.logits[p.fed[pos + 1]];
+}
+
+int launch_score(const ScoreParams& p, hipStream_t s) {
+  TRX_CHECK(p.x && p.out_norm && p.n > 0 && (!p.logits || (p.nll && p.pos && p.head_from && p.n_fed && p.fed)),
+            TRX_E_INVALID, "score: bad arguments");
+  hipLaunchKernelGGL(score_kernel, dim3(1), dim3(1024), 0, s, p);
+  TRX_LAUNCHED();
+  return TRX_OK;
+}
+
 int launch_finalize(const int* pos, const int* n_prompt, unsigned long long* slot, int* out, int max_out,
                     hipStream_t s) {
   hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(64), 0, s, pos, n_prompt, slot, out, max_out);

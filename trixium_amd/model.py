@@ -23,7 +23,8 @@ from .hadamard import image_rotation
 
 f32 = np.float32
 
-READ_LOGITS, READ_HIDDEN, READ_POSITION, READ_TOKEN, READ_OUT, READ_SLOT, READ_QKV, READ_ATTN, READ_ACT = range(9)
+(READ_LOGITS, READ_HIDDEN, READ_POSITION, READ_TOKEN, READ_OUT, READ_SLOT, READ_QKV, READ_ATTN, READ_ACT,
+ READ_RESIDUAL) = range(10)
 INFO_ARENA_BYTES, INFO_DEVICE_BYTES, INFO_STREAM, INFO_WEIGHT_BYTES, INFO_PERSISTENT, INFO_PACKED_OPS = range(6)
 
 # Projections run by the packed GEMV (TRX_PACK_* bits; PACK_AUTO lets the library choose).
@@ -321,11 +322,42 @@ class Decoder:
         _lib.call("trx_model_read", self._h, what, arr.ctypes.data, arr.nbytes)
         return arr
 
-    def logits(self):
-        return self._read(READ_LOGITS, np.empty(self.vocab, dtype=f32))
+    def logits(self, Hs=None):
+        """Without arguments: the logits (vocab,) of the last forward that ran the LM head. With
+        hidden states Hs [T, n_embd]: the LM head applied to them on the GPU, [T, vocab]
+        (HybridRef.logits, model/fastref.py:260-261)."""
+        if Hs is None:
+            return self._read(READ_LOGITS, np.empty(self.vocab, dtype=f32))
+        h = np.ascontiguousarray(np.asarray(Hs, dtype=f32).reshape(-1, self.n_embd))
+        out = np.empty((h.shape[0], self.vocab), dtype=f32)
+        _lib.call("trx_model_project_head", self._h, h.ctypes.data, int(h.shape[0]), out.ctypes.data)
+        return out
 
-    def hidden(self):
-        return self._read(READ_HIDDEN, np.empty(self.n_embd, dtype=f32))
+    def hidden(self, tokens=None):
+        """Without arguments: the final normed hidden state (n_embd,) of the last forward. With
+        tokens: reset, run them teacher-forced from position 0 and return every position's final
+        normed hidden state [T, n_embd] (HybridRef.hidden, model/fastref.py:244-258)."""
+        if tokens is None:
+            return self._read(READ_HIDDEN, np.empty(self.n_embd, dtype=f32))
+        return self.score(tokens)[1]
+
+    def residual(self):
+        """The residual stream (n_embd,) after the last layer of the last forward (un-normed)."""
+        return self._read(READ_RESIDUAL, np.empty(self.n_embd, dtype=f32))
+
+    def score(self, tokens, chunk=256):
+        """(nll [T-1] of tokens[1:] given their prefix, final normed hidden states [T, n_embd]),
+        teacher-forced from position 0 after a reset (HybridRef.score, model/fastref.py:263-273).
+        The log-sum-exp over the vocabulary runs on the GPU in float32; `chunk` is accepted for
+        the reference's signature (the GPU scores one position at a time)."""
+        t = np.ascontiguousarray(np.asarray(tokens, dtype=np.int32).reshape(-1))
+        if t.size == 0:
+            raise ValueError("no tokens to score")
+        nll = np.empty(max(t.size - 1, 1), dtype=f32)
+        hid = np.empty((t.size, self.n_embd), dtype=f32)
+        _lib.call("trx_model_score", self._h, t.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), int(t.size),
+                  nll.ctypes.data, hid.ctypes.data)
+        return nll[:t.size - 1].astype(np.float64), hid
 
     def taps(self):
         """Intermediate vectors of the last forward: the last attention layer's q|k|v projection
