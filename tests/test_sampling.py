@@ -40,6 +40,42 @@ def test_penalty_temperature_and_top_p():
     assert picks == {7, 9, 3}
 
 
+def test_draw_against_closed_forms():
+    """The draw of smp_pick (firmware/infer.c:456-466) on cases whose answer is fixed without its
+    loop. x is the next xorshift32 state and u = (x >> 8) / 2^24 the uniform it yields.
+    * 32 equal candidates, top_p 1: the mass is 32 and the draw picks index floor(32 u) = x >> 27.
+    * 4 equal candidates, top_p 0.5: the cut (0.5 * 4 = 2) is reached at the second candidate
+      (acc >= cut), so two are kept, the draw is scaled by their mass 2 and picks x >> 31. Scaling
+      by the whole mass, cutting one candidate early or late, or a strict acc > cut would each
+      pick otherwise for some u in [0.25, 1).
+    * Two candidates d apart at temperature T, top_p 1: the second is picked iff
+      u * (1 + e^(-d/T)) >= 1."""
+    def states(pred, n=12):
+        out, s = [], 12345
+        while len(out) < n:
+            s = S.xorshift32(s)
+            if pred(S.xorshift32(s)):
+                out.append(s)
+        return out
+
+    eq32 = [(np.float32(0.5), 100 + i) for i in range(32)]
+    for s in states(lambda x: True, 40):
+        x = S.xorshift32(s)
+        t, r = S.pick(eq32, [], 0.7, 1.0, 1.0, s)
+        assert r == x and t == 100 + (x >> 27)
+    eq4 = [(np.float32(1.0), t) for t in (10, 20, 30, 40)]
+    for quarter in range(4):
+        for s in states(lambda x: x >> 30 == quarter, 5):
+            x = S.xorshift32(s)
+            assert S.pick(eq4, [], 1.0, 0.5, 1.0, s)[0] == (10, 20)[x >> 31], (quarter, s)
+    d, T = 1.0, 0.5
+    two = [(np.float32(2.0), 1), (np.float32(2.0 - d), 2)]
+    thr = 1.0 / (1.0 + np.exp(-d / T))
+    for s in states(lambda x: abs((x >> 8) / 2.0**24 - thr) > 1e-4, 30):
+        u = (S.xorshift32(s) >> 8) / 2.0**24
+        assert S.pick(two, [], T, 1.0, 1.0, s)[0] == (2 if u >= thr else 1)
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-hybrid"])
 def test_gpu_sampler_matches_the_oracle(tiny_images, golden, name):
