@@ -75,7 +75,8 @@ int trx_gemv_ternary_exact(const uint8_t* rows, int kind, int M, int K, const in
 /* Multi-row exact engine matvec (model/bitexact.py:121-125 matvec_ternary_rows): one pass over
  * the rows against n_rows (1..8) int8 vectors x8_rows[n_rows][K] (16-byte aligned,
  * n_rows * K <= 114688), y[n_rows][M]; row r equals trx_gemv_ternary_exact on x8_rows[r], and
- * *status is OR-ed the same way. */
+ * *status is OR-ed the same way. Up to 4 rows run the single-row kernel once per row (faster at
+ * that count); 5..8 rows share one pass over the weights. */
 int trx_gemv_ternary_exact_rows(const uint8_t* rows, int kind, int M, int K, const int8_t* x8_rows,
                                 int n_rows, int B, int R, int32_t* y, int32_t* status,
                                 trx_stream_t s);
