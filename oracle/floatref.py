@@ -326,3 +326,45 @@ class ShapeSample(FloatRef):
             self.k_cache[l] = list(kc)
             self.v_cache[l] = list(vc)
         self.pos = ctx
+
+
+class TensorRef(FloatRef):
+    """FloatRef's step over weights given as arrays instead of an image (full-attention models):
+    the headline shapes, whose weights the device generator fills in HBM and a test reads back.
+
+    weights: {(role, layer): float32 [rows, cols]} for every projection and the LM head (under
+    ROLE_LM_HEAD, or ROLE_TOK_EMB when tied); gains: {(role, layer): float32 vector} for the
+    RMSNorm gains (ATTN_NORM, FFN_NORM, ATTN_Q_NORM, ATTN_K_NORM per layer, OUT_NORM at 0);
+    embed_row(tok) -> float32 [n_embd], the token's embedding row. Numerics are FloatRef's with
+    the weights held in float32 (exact for ternary values times fp16 scales)."""
+
+    def __init__(self, mc, weights, gains, embed_row, kv_fp16=True):
+        self.n_layer, self.n_embd = mc.n_layer, mc.n_embd
+        self.n_head, self.n_kv, self.hd = mc.n_head, mc.n_kv_head, mc.head_dim
+        self.rope_n = mc.rope_dims or mc.head_dim
+        self.eps = f32(mc.rms_eps)
+        self.gated = False
+        self.hb, self.hwidths = 0, []
+        self.vocab = mc.vocab
+        self.dn = [False] * mc.n_layer
+        self.nk = self.hk = self.nv = self.hv = 0
+        self.K = 1
+        self.kv_fp16 = kv_fp16
+        self.rope_tab = None
+        self.rope_freq = np.array([f32(f32(mc.rope_theta) ** f32(-2.0 * i / self.rope_n))
+                                   for i in range(self.rope_n // 2)], dtype=f32)
+        self.w32 = weights
+        self.head_role = L.ROLE_LM_HEAD if (L.ROLE_LM_HEAD, 0) in weights else L.ROLE_TOK_EMB
+        self.norm_attn = [gains[(L.ROLE_ATTN_NORM, l)] for l in range(mc.n_layer)]
+        self.norm_ffn = [gains[(L.ROLE_FFN_NORM, l)] for l in range(mc.n_layer)]
+        self.norm_q = {l: gains[(L.ROLE_ATTN_Q_NORM, l)] for l in range(mc.n_layer)}
+        self.norm_k = {l: gains[(L.ROLE_ATTN_K_NORM, l)] for l in range(mc.n_layer)}
+        self.out_norm = gains[(L.ROLE_OUT_NORM, 0)]
+        self.embed_row = embed_row
+        self.reset()
+
+    def proj(self, role, l, x):
+        return (self.w32[(role, l)] @ np.asarray(x, dtype=f32)).astype(f32)
+
+    def embed(self, tok):
+        return np.asarray(self.embed_row(int(tok)), dtype=f32)

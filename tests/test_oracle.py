@@ -218,3 +218,36 @@ def test_floatref_score_matches_fastref(tiny_images, name):
     want = z[f"{name}/hidden"]
     got = hid[z[f"{name}/hidden_pos"]]
     assert np.abs(got - want).max() <= 1e-4 * np.abs(want).max()
+
+
+def test_tensor_ref_equals_floatref_on_an_image(tmp_path):
+    """TensorRef (the oracle over weights given as arrays, used at the headline shapes) steps like
+    FloatRef over the same model written as an image: the hashed tiny model, its embedding from
+    the ternary rows by the int16-table rule."""
+    from oracle.floatref import TensorRef
+    cfg = C.TINY.replace(name="tiny-hashed", n_layer=2, tie_embeddings=False, max_ctx=64)
+    specs = synth.hashed_model_tensors(cfg, 4)
+    p = str(tmp_path / "h.img")
+    bons.write_image(cfg, specs, 1, p, trit5=True)
+    a = FloatRef(bons.BONSReader(p), kv_fp16=True)
+    w, g = {}, {}
+    emb = None
+    for s in specs:
+        if L.is_ternary(s.kind):
+            v = (s.values.astype(np.float32).reshape(s.rows, -1, 128) - 1) * s.scales.astype(np.float32)[:, :, None]
+            w[(s.role, s.layer)] = v.reshape(s.rows, s.cols)
+            if s.role == L.ROLE_TOK_EMB:
+                emb = s
+        else:
+            g[(s.role, s.layer)] = s.values.reshape(-1).astype(np.float32)
+
+    def row(t):
+        m, e = bons.embed_bfp_rows(emb.values[t:t + 1], emb.scales[t:t + 1])
+        return m[0].astype(np.float32) * np.float32(np.exp2(int(e[0])))
+
+    b = TensorRef(cfg, w, g, row, kv_fp16=True)
+    prompt = synth.random_prompt(cfg, 6, 4)
+    for t in prompt:
+        la, lb = a.step(t), b.step(t)
+        assert np.abs(la - lb).max() <= 1e-5 * np.abs(la).max()
+    assert a.generate([1, 2, 3], 5) == b.generate([1, 2, 3], 5)

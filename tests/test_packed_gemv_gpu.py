@@ -216,3 +216,22 @@ def test_partial_sums_residual_to_normed_gemv(gpu, kind, E, K):
     xn = x64 / np.sqrt(np.mean(x64 ** 2) + 1e-6) * w
     W2 = _w64(c2, s2)
     assert np.max(np.abs(y - W2 @ xn) / (np.abs(W2) @ np.abs(xn))) < 1e-5
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("M,K,n", [(2048, 2048, 5), (257, 640, 3), (6144, 2048, 2), (2048, 6144, 2), (1, 128, 4)])
+def test_batched_matvec_equals_single_launches(gpu, kind, M, K, n):
+    """Many independent GEMVs in one dispatch (trx_gemv_packed_batched_f32): every y_i within
+    the float64 tolerance and bitwise equal to the single-matrix packed GEMV of the same W_i, x_i
+    (the same per-slice partial sums, added in slice order)."""
+    print(f"batched matvec kind={kind} M={M} K={K} n={n}", flush=True)
+    mats = [_rand(M, K, 1000 * i + K + M)[::-1] for i in range(n)]
+    xs = np.random.default_rng(K + n).normal(0, 1, (n, K)).astype(np.float32)
+    y = gpu.batched_matvec(mats, xs, kind)
+    for i, (sc, cd) in enumerate(mats):
+        W = _w64(cd, sc)
+        ref = W @ xs[i].astype(np.float64)
+        mag = np.abs(W) @ np.abs(xs[i].astype(np.float64))
+        assert np.max(np.abs(y[i] - ref) / np.maximum(mag, 1e-30)) < TOL
+        single = gpu.PackedMatrix(sc, cd, kind).matvec(xs[i])
+        assert np.array_equal(y[i], single), i

@@ -109,6 +109,30 @@ def pack_geometry(kind, M, K):
     return pb.value, wb.value
 
 
+def batched_matvec(mats, xs, kind=L.KIND_TERNARY5):
+    """y_i = W_i x_i for every (scales, codes) of `mats` (one shape) in one dispatch
+    (trx_gemv_packed_batched_f32): the packed copies back to back at a 256-byte multiple stride.
+    Returns float32 (n, M)."""
+    n = len(mats)
+    M, K = mats[0][1].shape
+    pb, _ = pack_geometry(kind, M, K)
+    stride = -(-pb // 256) * 256
+    packed = DeviceBuffer(stride * n)
+    for i, (sc, cd) in enumerate(mats):
+        assert cd.shape == (M, K)
+        rows = DeviceBuffer.from_array(_packets(sc, cd, kind))
+        call("trx_pack_ternary", rows.ptr, kind, M, K, 0, packed.ptr + i * stride, None)
+        synchronize()
+    wb = ctypes.c_size_t()
+    call("trx_pack_batched_geometry", kind, M, K, n, ctypes.byref(wb))
+    work = DeviceBuffer(wb.value)
+    xb = DeviceBuffer.from_array(np.ascontiguousarray(np.asarray(xs, dtype=np.float32).reshape(n, K)))
+    yb = DeviceBuffer(4 * n * M)
+    call("trx_gemv_packed_batched_f32", packed.ptr, stride, n, kind, M, K, xb.ptr, K, yb.ptr, M, work.ptr, None)
+    synchronize()
+    return yb.download(np.float32, n * M).reshape(n, M)
+
+
 class PackedMatrix:
     """A ternary matrix packed for the float GEMV (trx_pack_ternary) with its workspace."""
 

@@ -218,6 +218,19 @@ TRX_API int trx_gemv_packed_parts_f32(const uint8_t* packed, int kind, int M, in
                    nullptr, nullptr, nullptr, parts ? &ps : nullptr);
 }
 
+TRX_API int trx_pack_batched_geometry(int kind, int M, int K, int n_mat, size_t* workspace_bytes) {
+  TRX_CHECK(workspace_bytes, TRX_E_INVALID, "trx_pack_batched_geometry: null argument");
+  PackGeom g;
+  return tgemv_batched_geom(kind, M, K, n_mat, g, workspace_bytes);
+}
+
+TRX_API int trx_gemv_packed_batched_f32(const uint8_t* packed, size_t mat_stride, int n_mat, int kind, int M,
+                                        int K, const float* x, int x_stride, float* y, int y_stride,
+                                        void* workspace, trx_stream_t s) {
+  return tgemv_f32_batched(packed, mat_stride, n_mat, kind, M, K, x, x_stride, y, y_stride, (float*)workspace,
+                           (hipStream_t)s);
+}
+
 TRX_API int trx_gemv_packed_f32(const uint8_t* packed, int kind, int M, int K, const float* x,
                                 const float* norm_w, float eps, float* y, int epilogue,
                                 const float* resid, void* workspace, trx_stream_t s) {

@@ -261,6 +261,11 @@ struct TgParams {
   const float* rot_signs;  // a rotation of x in the prologue (RotSrc), or null
   int rot_B;
   float rot_scale;
+  // Several matrices in one launch (blockIdx.y = matrix): matrix i's packed copy at
+  // codes/scales + i * mat_bytes, its x at x + i * x_stride, its partial sums of slice s at
+  // part + s * part_sstride + i * part_mstride. One matrix: 0, 0, rows_p, 0.
+  uint32_t mat_bytes;
+  int x_stride, part_sstride, part_mstride;
 };
 
 template <bool T5>
@@ -281,7 +286,7 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   __shared__ int n_todo;
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int s = blockIdx.x % p.S, j = blockIdx.x / p.S;
+  const int s = blockIdx.x % p.S, j = blockIdx.x / p.S, mi = blockIdx.y;
   const int xmode = p.merge.o ? kXMerge : p.parts.in ? (p.parts.F ? kXSwiglu : kXResid) : kXPlain;
   // A gated-off launch does nothing but store the residual it was handed in partials. The gate
   // is read here and tested after the prologue's loads and the first weight loads are issued,
@@ -361,7 +366,7 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
       if (p.norm_w) wv = p.norm_w[cs];
     }
   } else if (tid < kSliceCols && cs < p.K) {
-    xv = p.x[cs];
+    xv = p.x[(size_t)mi * p.x_stride + cs];
     if (p.norm_w) wv = p.norm_w[cs];
   }
   // A rotated input: this thread's element of the rotation span holding the slice (the slice
@@ -380,8 +385,8 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   // 2. The first NB - 1 items of this lane (they do not depend on x).
   const int rg = lane >> 4, l16 = lane & 15, half = l16 >> 3;
   const int dw = tg_lane_dword(T5, l16), msk = tg_lane_mask(l16);
-  const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.codes, p.code_bytes);
-  const __amdgpu_buffer_rsrc_t rsc = make_rsrc(p.scales, p.scale_bytes);
+  const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.codes + (size_t)mi * p.mat_bytes, p.code_bytes);
+  const __amdgpu_buffer_rsrc_t rsc = make_rsrc(p.scales + (size_t)mi * p.mat_bytes, p.scale_bytes);
   // Item n of this lane is quad quad0 + n * qstep. The lane's offsets stay in fixed VGPRs and
   // the item's step goes in the scalar offset, so no VGPR that an in-flight access reads is
   // rewritten (that would cost a vmcnt wait per item). Only the VGPR offset is relied on for the
@@ -396,8 +401,10 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   // Partial sums: every lane stores every item (a fixed count of memory events per item keeps
   // the compiler's waits exact); the lanes that hold no row total store past the buffer (dropped
   // by the range check), and the items of a partial last tile land in padding rows.
-  const __amdgpu_buffer_rsrc_t rpart = make_rsrc(p.part, (uint32_t)((size_t)p.S * p.rows_p * 4));
-  const uint32_t po0 = (l16 & 9) == 0 ? ((uint32_t)s * p.rows_p + 4u * (uint32_t)quad0 + msk) * 4u : kOut;
+  const __amdgpu_buffer_rsrc_t rpart = make_rsrc(p.part, (uint32_t)((size_t)p.S * p.part_sstride * 4));
+  const uint32_t po0 = (l16 & 9) == 0 ? ((uint32_t)s * p.part_sstride + (uint32_t)mi * p.part_mstride +
+                                         4u * (uint32_t)quad0 + msk) * 4u
+                                      : kOut;
   const uint32_t pstep = (uint32_t)qstep * 16u;
   auto load_item = [&](TgItem<T5>& it, int n) {
     const int nn = min(n, p.tpb - 1);
@@ -654,7 +661,7 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   constexpr int kRedRows = 2, kRedChunk = 16;
   constexpr int kTilesPerPass = kTgThreads * kRedRows / kTileRows;
   static_assert(kTilesPerPass <= kMaxTilesPerBlock, "reduction pass");
-  const uint32_t step = (uint32_t)p.rows_p * 4u;
+  const uint32_t step = (uint32_t)p.part_sstride * 4u;
   for (int i0 = 0; i0 < nt; i0 += kTilesPerPass) {
     float yv[kRedRows];
     int prow[kRedRows];
@@ -730,6 +737,9 @@ struct RdParams {
   int S, rows_p, M, K, rpb;   // rpb: rows per block
   float eps;
   float* y;
+  // Rows of several matrices (mat_rows_p > 0): row r is row r % mat_rows_p of matrix
+  // r / mat_rows_p, stored at y[matrix * y_stride + row] when row < mat_M.
+  int mat_rows_p, mat_M, y_stride;
   unsigned long long* amax_slot;
   const int* gate_pos;
   const int* gate_from;
@@ -775,6 +785,11 @@ __global__ __launch_bounds__(kRdThreads) void tgemv_reduce_kernel(RdParams p) {
   for (int i = 0; i < kRdRowsMax; ++i) {
     if (!live[i]) continue;
     const float out = acc[i] * rs;
+    if (p.mat_rows_p) {
+      const int mt = row[i] / p.mat_rows_p, r = row[i] - mt * p.mat_rows_p;
+      if (r < p.mat_M) p.y[(size_t)mt * p.y_stride + r] = out;
+      continue;
+    }
     p.y[row[i]] = out;
     const unsigned long long kr =
         ((unsigned long long)ordered_bits(out) << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)row[i]);
@@ -813,6 +828,7 @@ int tgemv_reduce_f32(const float* part, const float* ss, int S, int rows_p, int 
   p.amax_slot = amax_slot;
   p.gate_pos = gate_pos;
   p.gate_from = gate_from;
+  p.mat_rows_p = p.mat_M = p.y_stride = 0;
   const int blocks = std::min(kRdBlocks, cdiv(M, kRdThreads));
   p.rpb = cdiv(M, blocks);
   TRX_CHECK(p.rpb <= kRdRowsMax * kRdThreads, TRX_E_INVALID, "partial-sum reduction: %d rows (at most %d)", M,
@@ -887,12 +903,93 @@ int tgemv_f32(const uint8_t* packed, int kind, int M, int K, const float* x, con
   p.rot_signs = rot ? rot->signs : nullptr;
   p.rot_B = rot ? rot->B : 0;
   p.rot_scale = rot ? rot->scale : 1.f;
+  p.mat_bytes = 0;
+  p.x_stride = 0;
+  p.part_sstride = g.rows_p;
+  p.part_mstride = 0;
   TRX_CHECK(!rot || (x && !merge && !p_in && rot->signs && rot->B >= 1 && rot->B <= kTgThreads &&
                      (rot->B & (rot->B - 1)) == 0 && K % std::max(rot->B, kSliceCols) == 0),
             TRX_E_INVALID, "packed GEMV: rotation of block %d over %d columns unsupported", rot ? rot->B : 0, K);
   const void* fn = kind == TRX_KIND_TERNARY5 ? tg_fn<true>() : tg_fn<false>();
   void* args[] = {(void*)&p};
   TRX_HIP(hipLaunchKernel(fn, dim3(g.S * g.bps), dim3(kTgThreads), args, 0, s));
+  return TRX_OK;
+}
+
+int tgemv_batched_geom(int kind, int M, int K, int n_mat, PackGeom& g, size_t* part_bytes) {
+  int rc = pack_geom(g, kind, M, K);
+  if (rc) return rc;
+  TRX_CHECK(n_mat >= 1 && n_mat <= 65535, TRX_E_INVALID, "batched GEMV: %d matrices (1..65535)", n_mat);
+  TRX_CHECK(g.n_tiles <= kMaxTilesPerBlock, TRX_E_INVALID, "batched GEMV: %d rows (at most %d)", M,
+            kMaxTilesPerBlock * kTileRows);
+  // One block per (slice, matrix) streams every row of its slice: one table per slice column.
+  g.bps = 1;
+  g.tpb = g.n_tiles;
+  g.rows_p = g.n_tiles * kTileRows;
+  const size_t pb = (size_t)g.S * n_mat * g.rows_p * 4;
+  TRX_CHECK(pb < (1ull << 32), TRX_E_INVALID, "batched GEMV: %zu bytes of partial sums exceed 4 GiB", pb);
+  if (part_bytes) *part_bytes = pb;
+  return TRX_OK;
+}
+
+int tgemv_f32_batched(const uint8_t* packed, size_t mat_stride, int n_mat, int kind, int M, int K, const float* x,
+                      int x_stride, float* y, int y_stride, float* part, hipStream_t s) {
+  PackGeom g;
+  size_t pb = 0;
+  int rc = tgemv_batched_geom(kind, M, K, n_mat, g, &pb);
+  if (rc) return rc;
+  TRX_CHECK(packed && x && y && part, TRX_E_INVALID, "batched GEMV: null argument");
+  TRX_CHECK(mat_stride % 256 == 0 && (n_mat == 1 || mat_stride >= g.bytes) && mat_stride < (1ull << 32),
+            TRX_E_INVALID, "batched GEMV: matrix stride %zu (a multiple of 256, at least %zu bytes)", mat_stride, g.bytes);
+  TRX_CHECK(x_stride >= K && y_stride >= M && ((uintptr_t)x & 15) == 0 && x_stride % 4 == 0, TRX_E_INVALID,
+            "batched GEMV: x stride %d, y stride %d (x 16-byte aligned)", x_stride, y_stride);
+  TgParams p = {};
+  p.codes = packed;
+  p.scales = packed + g.scale_off;
+  p.code_bytes = (uint32_t)g.code_bytes;
+  p.scale_bytes = (uint32_t)(g.bytes - g.scale_off);
+  p.K = K;
+  p.M = M;
+  p.M4 = g.M4;
+  p.Q = g.Q;
+  p.S = g.S;
+  p.D = g.D;
+  p.n_tiles = g.n_tiles;
+  p.bps = g.bps;
+  p.tpb = g.tpb;
+  p.rows_p = g.rows_p;
+  p.x = x;
+  p.eps = 0.f;
+  p.epi = TRX_EPI_STORE;
+  p.n_out = M;
+  p.part = part;
+  p.parts.out = part;
+  p.mat_bytes = (uint32_t)mat_stride;
+  p.x_stride = x_stride;
+  p.part_sstride = n_mat * g.rows_p;
+  p.part_mstride = g.rows_p;
+  const void* fn = kind == TRX_KIND_TERNARY5 ? tg_fn<true>() : tg_fn<false>();
+  void* args[] = {(void*)&p};
+  TRX_HIP(hipLaunchKernel(fn, dim3(g.S, n_mat), dim3(kTgThreads), args, 0, s));
+  // The S partial sums of every row of every matrix, reduced over the whole GPU.
+  RdParams r = {};
+  r.part = part;
+  r.S = g.S;
+  r.rows_p = n_mat * g.rows_p;
+  r.M = n_mat * g.rows_p;
+  r.K = K;
+  r.y = y;
+  r.mat_rows_p = g.rows_p;
+  r.mat_M = M;
+  r.y_stride = y_stride;
+  const int blocks = std::min(kRdBlocks, cdiv(r.M, kRdThreads));
+  r.rpb = cdiv(r.M, blocks);
+  if (r.rpb > kRdRowsMax * kRdThreads) {
+    // More rows than one pass of the grid holds: more blocks.
+    r.rpb = kRdRowsMax * kRdThreads;
+  }
+  hipLaunchKernelGGL(tgemv_reduce_kernel, dim3(cdiv(r.M, r.rpb)), dim3(kRdThreads), 0, s, r);
+  TRX_LAUNCHED();
   return TRX_OK;
 }
 
