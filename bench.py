@@ -21,7 +21,10 @@ Besides the JSON contract fields the line carries
                 the KV cache at the mean timed position) against the same 8 TB/s;
   cpu_baseline  the float oracle's decode step (the reference's numpy CPU path restated) on a
                 sample of the same shape: one layer and the LM head at context 2048, scaled to
-                36 layers.
+                36 layers;
+  matvec_microbench  the isolated ternary matvec at the Qwen3-1.7B layer shapes, trit5 and 2-bit,
+                over more than 512 MB of distinct matrix copies, at least 1000 matvecs per
+                shape: GB/s against 8 TB/s, with the exact integer group sums checked.
 """
 
 import argparse
@@ -65,6 +68,10 @@ def parse_args():
                          "choice for the weight kind, 0: none, 63: all)")
     ap.add_argument("--persistent", action="store_true",
                     help="run each position as one persistent kernel instead of one kernel per operation")
+    ap.add_argument("--no-microbench", action="store_true",
+                    help="skip the isolated matvec benchmark at the Qwen3-1.7B layer shapes")
+    ap.add_argument("--only-microbench", action="store_true",
+                    help="run only the isolated matvec benchmark and print its record")
     ap.add_argument("--only-kernel", action="store_true",
                     help="time only the dominant kernel (for hardware-counter runs)")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -129,6 +136,112 @@ def time_exact_rows(n, kind, reps=50):
                       "speedup": round(us_single / us_multi, 2), "bytes_per_launch": algo,
                       "achieved_GBs": round(algo / (us_multi * 1e-6) / 1e9, 1), "peak_GBs": 8000,
                       "status": int(st.download(np.int32)[0])}), flush=True)
+
+
+def matvec_microbench(reps=1000, rotate_bytes=512 << 20):
+    """The isolated ternary matvec at the Qwen3-1.7B layer shapes (2048x2048, 1024x2048,
+    6144x2048, 2048x6144), trit5 and 2-bit rows, fp16 group scales U(0.01, 0.05), P(0) = 0.4:
+    y = W x with fp32 x ~ N(0, 1), batch 1. The packed GEMV runs over distinct copies of the
+    matrix laid out back to back (at least `rotate_bytes` of them, more than the 256 MB Infinity
+    Cache, so every launch streams from HBM), many matvecs per dispatch
+    (trx_gemv_packed_batched_f32), at least `reps` matvecs timed with HIP events. Also timed:
+    one matvec per launch (the decoder's own launch, latency bound at these sizes), and the
+    engine's exact group sums on int8 x checked bit for bit against integer numpy."""
+    import ctypes
+    from trixium_amd import _lib, configs as C, layout as L
+    from trixium_amd.bons import encode_rows
+    from trixium_amd.bitexact import pack_geometry
+    e0, e1 = ctypes.c_void_p(), ctypes.c_void_p()
+    _lib.call("trx_event_create", ctypes.byref(e0))
+    _lib.call("trx_event_create", ctypes.byref(e1))
+
+    def timed(fn, n):
+        fn()
+        _lib.synchronize()
+        _lib.call("trx_event_record", e0, None)
+        for _ in range(n):
+            fn()
+        _lib.call("trx_event_record", e1, None)
+        _lib.synchronize()
+        ms = ctypes.c_float()
+        _lib.call("trx_event_elapsed_ms", e0, e1, ctypes.byref(ms))
+        return ms.value * 1e3
+
+    out = {}
+    for M, K in C.MICROBENCH_SHAPES:
+        r = np.random.default_rng(M * 7919 + K)
+        u = r.random((M, K))
+        codes = np.where(u < 0.3, 0, np.where(u < 0.7, 1, 2)).astype(np.uint8)
+        scales = r.uniform(0.01, 0.05, (M, K // 128)).astype(np.float16)
+        W64 = (codes.astype(np.float64) - 1).reshape(M, -1, 128) * scales.astype(np.float64)[:, :, None]
+        W64 = W64.reshape(M, K)
+        x8 = r.integers(-127, 128, K, dtype=np.int8)
+        gs_want = ((codes.astype(np.int64) - 1) * x8.astype(np.int64)).reshape(M, -1, 128).sum(axis=2)
+        for kind, kname in ((L.KIND_TERNARY5, "trit5"), (L.KIND_TERNARY, "2bit")):
+            rows = _lib.DeviceBuffer.from_array(encode_rows(kind, K, scales, codes))
+            pb, wb = pack_geometry(kind, M, K)
+            stride = -(-pb // 256) * 256
+            n = max(1, -(-rotate_bytes // stride))
+            packed = _lib.DeviceBuffer(stride * n)
+            _lib.call("trx_pack_ternary", rows.ptr, kind, M, K, 0, packed.ptr, None)
+            for i in range(1, n):
+                _lib.call("trx_memcpy_d2d", packed.ptr + i * stride, packed.ptr, pb, None)
+            xs = r.standard_normal((n, K)).astype(np.float32)
+            xb = _lib.DeviceBuffer.from_array(xs)
+            yb = _lib.DeviceBuffer(4 * n * M)
+            bw = ctypes.c_size_t()
+            _lib.call("trx_pack_batched_geometry", kind, M, K, n, ctypes.byref(bw))
+            part = _lib.DeviceBuffer(bw.value)
+            _lib.synchronize()
+
+            def batched():
+                _lib.call("trx_gemv_packed_batched_f32", packed.ptr, stride, n, kind, M, K, xb.ptr, K, yb.ptr, M,
+                          part.ptr, None)
+            n_launch = max(1, -(-reps // n))
+            us = timed(batched, n_launch)
+            # Correctness of the first and the last matrix of the dispatch (float64, 2e-6 of sum |w x|).
+            y = yb.download(np.float32, n * M).reshape(n, M)
+            err = 0.0
+            for i in (0, n - 1):
+                ref = W64 @ xs[i].astype(np.float64)
+                mag = np.abs(W64) @ np.abs(xs[i].astype(np.float64))
+                err = max(err, float(np.max(np.abs(y[i] - ref) / mag)))
+            row_b = L.row_bytes(K, kind)
+            algo = M * row_b + 4 * K + 4 * M            # weight rows (scales + codes), fp32 x and y
+            count = n * n_launch
+            gbs = algo * count / (us * 1e-6) / 1e9
+            # One matvec per launch (the decoder's form), over the copies in turn.
+            work = _lib.DeviceBuffer(wb)
+            work.zero()
+            ys = _lib.DeviceBuffer(4 * M)
+            idx = [0]
+
+            def single():
+                i = idx[0] % n
+                idx[0] += 1
+                _lib.call("trx_gemv_packed_f32", packed.ptr + i * stride, kind, M, K, xb.ptr + 4 * i * K, None,
+                          ctypes.c_float(1e-6), ys.ptr, 0, None, work.ptr, None)
+            us1 = timed(single, reps) / reps
+            # The engine's exact group sums on int8 x (the integer path), bit for bit.
+            xq = _lib.DeviceBuffer.from_array(x8)
+            gsb = _lib.DeviceBuffer(4 * M * (K // 128))
+            _lib.call("trx_gemv_ternary_groupsums", rows.ptr, kind, M, K, xq.ptr, gsb.ptr, None)
+            _lib.synchronize()
+            gs_ok = bool(np.array_equal(gsb.download(np.int32, M * (K // 128)).reshape(M, -1), gs_want))
+            out[f"{M}x{K}/{kname}"] = {
+                "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "us_per_matvec": round(us / count, 3),
+                "bytes_per_matvec": algo, "matvecs": count, "copies": n, "rotated_MB": round(n * stride / 2**20, 1),
+                "single_launch_us": round(us1, 3), "single_launch_GBs": round(algo / (us1 * 1e-6) / 1e9, 1),
+                "max_rel_err": float(f"{err:.2e}"), "groupsums_bitexact": gs_ok}
+            del packed, xb, yb, part, rows
+    _lib.call("trx_event_destroy", e0)
+    _lib.call("trx_event_destroy", e1)
+    tot_bytes = sum(v["bytes_per_matvec"] * v["matvecs"] for v in out.values())
+    tot_us = sum(v["us_per_matvec"] * v["matvecs"] for v in out.values())
+    agg = tot_bytes / (tot_us * 1e-6) / 1e9
+    return {"kernel": "packed table-lookup GEMV, many matvecs per dispatch (trx_gemv_packed_batched_f32), "
+                      "fp32 x and y", "aggregate_GBs": round(agg, 1), "aggregate_frac": round(agg / HBM_PEAK_GBS, 4),
+            "peak_GBs": HBM_PEAK_GBS, "shapes": out}
 
 
 def copy_calibration(nbytes):
@@ -255,6 +368,9 @@ def main():
     if a.exact_rows:
         time_exact_rows(a.exact_rows, L.KIND_TERNARY5 if a.kind == "trit5" else L.KIND_TERNARY)
         return
+    if a.only_microbench:
+        print(json.dumps({"matvec_microbench": matvec_microbench()}), flush=True)
+        return
     mc = {"8b": C.QWEN3_8B, "1.7b": C.QWEN3_1P7B, "27b": C.QWEN35_27B}[a.model]
     if a.prompt is None:
         a.prompt = {"8b": 2048, "1.7b": 512, "27b": 1024}[a.model]
@@ -369,6 +485,8 @@ def main():
         "cpu_baseline": None,
     }
     dec.close()
+    if not a.no_microbench:
+        rec["matvec_microbench"] = matvec_microbench()
     if not a.no_cpu_baseline:
         rec["cpu_baseline"] = cpu_baseline(mc, a.prompt)
     print(json.dumps(rec), flush=True)
