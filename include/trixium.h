@@ -116,6 +116,16 @@ int trx_gemv_packed_f32(const uint8_t* packed, int kind, int M, int K, const flo
                         const float* norm_w, float eps, float* y, int epilogue,
                         const float* resid, void* workspace, trx_stream_t s);
 
+/* trx_gemv_packed_f32 without a workspace argument, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. The workspace is a fixed 24 MiB device array of the library (one
+ * per GPU, held until the process ends), so the matrix's workspace (trx_pack_geometry) must fit
+ * in it: TRX_E_INVALID otherwise (the 151936 x 4096 LM head fits). Calls on one GPU share the
+ * array: calls that overlap on one GPU race. */
+int trx_gemv_packed_f32_noalloc(const uint8_t* packed, int kind, int M, int K, const float* x,
+                                const float* norm_w, float eps, float* y, int epilogue,
+                                const float* resid, trx_stream_t s);
+
 /* Many independent packed GEMVs in one dispatch (no counterpart in the reference, whose engine
  * runs one matvec op per submit, firmware/engine.c:111-238; for callers with many matrices and
  * vectors, such as the isolated matvec benchmark): y_i = W_i x_i, i < n_mat, matrix i's packed
