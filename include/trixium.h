@@ -81,6 +81,21 @@ int trx_gemv_ternary_exact_rows(const uint8_t* rows, int kind, int M, int K, con
                                 int n_rows, int B, int R, int32_t* y, int32_t* status,
                                 trx_stream_t s);
 
+/* The firmware's activation quantizer (model/mirror.py:45-51 _quantize_f_pow2, firmware/infer.c:144
+ * quantize_f_pow2): *e8 = frexp(max |x|) - 7 (0 for an all-zero x), x8[i] = clip(lroundf(x[i] *
+ * 2^-e8), -127, 127), lroundf evaluated in float32 as model/mirror.py:34-35 does. One block;
+ * K >= 1. */
+int trx_quantize_f_pow2(const float* x, int K, int8_t* x8, int* e8, trx_stream_t s);
+
+/* The projection through the engine, as the firmware runs it (model/mirror.py:663-678, the
+ * non-exact matvec_f; firmware/infer_float.c:350 infer_matvec_f): x quantized by
+ * trx_quantize_f_pow2, the exact engine matvec of trx_gemv_ternary_exact with the tensor's B and
+ * R, y[m] = (float)result[m] * 2^(e8 + R - B) (float32). `workspace` holds
+ * trx_gemv_quantized_geometry's bytes; *status is OR-ed as for trx_gemv_ternary_exact. */
+int trx_gemv_quantized_geometry(int M, int K, size_t* workspace_bytes);
+int trx_gemv_ternary_quantized(const uint8_t* rows, int kind, int M, int K, const float* x, int B, int R,
+                               float* y, void* workspace, int32_t* status, trx_stream_t s);
+
 /* Exact per-group sums gs[m*G + g] = sum (code-1)*x8 over group g (the engine's adder-tree
  * output, model/bitexact.py:110; debug form of engine op 0). */
 int trx_gemv_ternary_groupsums(const uint8_t* rows, int kind, int M, int K, const int8_t* x8,

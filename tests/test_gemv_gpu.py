@@ -187,3 +187,51 @@ def test_matvec_float_deterministic(gpu):
     a = gpu.matvec_float(scales, codes, x)
     b = gpu.matvec_float(scales, codes, x)
     assert np.array_equal(a, b)
+
+
+def test_quantizer_matches_the_reference_fixture():
+    """The GPU quantizer (trx_quantize_f_pow2) bit for bit against the reference's
+    _quantize_f_pow2 outputs (tests/golden/golden_quant.npz) and the oracle on random vectors of
+    the model widths."""
+    import os
+    from trixium_amd import bitexact
+    z = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden_quant.npz"))
+    for k in [k for k in z.files if k.startswith("q/") and k.endswith("/x")]:
+        n = k[2:-2]
+        q, e = bitexact.quantize_f_pow2(z[k])
+        assert np.array_equal(q, z[f"q/{n}/x8"]) and e == int(z[f"q/{n}/e8"]), n
+    r = np.random.default_rng(5)
+    for K in (128, 2048, 4096, 12288, 17408):
+        x = (r.standard_normal(K) * r.uniform(0.01, 50)).astype(np.float32)
+        q, e = bitexact.quantize_f_pow2(x)
+        wq, we = ob.quantize_f_pow2(x)
+        assert np.array_equal(q, wq) and e == we, K
+
+
+@pytest.mark.parametrize("kind", [L.KIND_TERNARY5, L.KIND_TERNARY])
+def test_engine_projection_matches_the_reference_fixture(kind):
+    """The projection through the engine (trx_gemv_ternary_quantized: quantize, exact matvec,
+    scale by 2^(e8 + R - B)) bit for bit against the reference's mirror path
+    (tests/golden/golden_quant.npz) and the oracle at the 8B widths."""
+    import os
+    import sys
+    from trixium_amd import bitexact
+    here = os.path.dirname(os.path.abspath(__file__))
+    z = np.load(os.path.join(here, "golden", "golden_quant.npz"))
+    sys.path.insert(0, os.path.join(here, "golden"))
+    from make_golden_quant import projections
+    for name, codes, scales, x in projections():
+        y = bitexact.matvec_quantized(scales, codes, x, int(z[f"p/{name}/B"]), int(z[f"p/{name}/R"]), kind=kind)
+        assert np.array_equal(y, z[f"p/{name}/y"]), name
+    r = np.random.default_rng(9)
+    for M, K in ((6144, 4096), (4096, 12288)):
+        u = r.random((M, K))
+        codes = np.where(u < 0.3, 0, np.where(u < 0.7, 1, 2)).astype(np.uint8)
+        scales = r.uniform(0.01, 0.05, (M, K // 128)).astype(np.float16)
+        x = r.standard_normal(K).astype(np.float32)
+        _, e16 = ob.fp16_decompose(scales)
+        B = ob.choose_scale_bias(e16)
+        R = ob.choose_result_shift(scales, B)
+        x8, e8 = ob.quantize_f_pow2(x)
+        want = ob.matvec_ternary(scales, codes, x8, B, R).astype(np.float32) * np.float32(2.0 ** (e8 + R - B))
+        assert np.array_equal(bitexact.matvec_quantized(scales, codes, x, B, R, kind=kind), want)

@@ -251,3 +251,26 @@ def test_tensor_ref_equals_floatref_on_an_image(tmp_path):
         la, lb = a.step(t), b.step(t)
         assert np.abs(la - lb).max() <= 1e-5 * np.abs(la).max()
     assert a.generate([1, 2, 3], 5) == b.generate([1, 2, 3], 5)
+
+
+def test_quantizer_and_engine_projection_match_the_reference():
+    """The oracle's quantize_f_pow2 and engine projection against the reference's
+    model/mirror.py:45-51 and :663-678 on edge-case vectors (tests/golden/golden_quant.npz): ties
+    away from zero, float32 lroundf (0.49999997 rounds to 1 there), a maximum at and just below a
+    power of two, extreme magnitudes, a mantissa rounding to 128 and clipped, all zeros."""
+    import os
+    z = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden_quant.npz"))
+    names = [k[2:-2] for k in z.files if k.startswith("q/") and k.endswith("/x")]
+    assert len(names) >= 10
+    for n in names:
+        q, e = bx.quantize_f_pow2(z[f"q/{n}/x"])
+        assert np.array_equal(q, z[f"q/{n}/x8"]) and e == int(z[f"q/{n}/e8"]), n
+    assert z["q/ties/x8"].tolist() == [100, 3, -3, 4, -1, 1, -127, 127]
+    import sys
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
+    from make_golden_quant import projections
+    for name, codes, scales, x in projections():
+        B, R = int(z[f"p/{name}/B"]), int(z[f"p/{name}/R"])
+        x8, e8 = bx.quantize_f_pow2(x)
+        y = bx.matvec_ternary(scales, codes, x8, B, R).astype(np.int32).astype(np.float32) * np.float32(2.0 ** (e8 + R - B))
+        assert np.array_equal(y, z[f"p/{name}/y"]), name

@@ -69,6 +69,9 @@ SIGNATURES = {
     "trx_gemv_ternary_exact": [_vp, _i, _i, _i, _vp, _i, _i, _vp, _vp, _vp],
     "trx_gemv_ternary_exact_rows": [_vp, _i, _i, _i, _vp, _i, _i, _i, _vp, _vp, _vp],
     "trx_gemv_ternary_groupsums": [_vp, _i, _i, _i, _vp, _vp, _vp],
+    "trx_quantize_f_pow2": [_vp, _i, _vp, _vp, _vp],
+    "trx_gemv_quantized_geometry": [_i, _i, ctypes.POINTER(_sz)],
+    "trx_gemv_ternary_quantized": [_vp, _i, _i, _i, _vp, _i, _i, _vp, _vp, _vp, _vp],
     "trx_gemv_ternary_f32": [_vp, _i, _i, _i, _vp, _vp, _f, _vp, _i, _vp, _vp],
     "trx_pack_geometry": [_i, _i, _i, ctypes.POINTER(_sz), ctypes.POINTER(_sz)],
     "trx_pack_ternary": [_vp, _i, _i, _i, _i, _vp, _vp],

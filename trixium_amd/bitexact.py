@@ -77,6 +77,38 @@ def matvec_ternary_rows(scales_f16, codes, x8_rows, B, R, kind=L.KIND_TERNARY5):
                            for i in range(0, x.shape[0], step)])
 
 
+def quantize_f_pow2(x):
+    """The firmware's activation quantizer on the GPU (model/mirror.py:45-51): (int8 [K], e8)."""
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32).reshape(-1))
+    xb = DeviceBuffer.from_array(x)
+    qb = DeviceBuffer(max(16, x.size))
+    eb = DeviceBuffer(4)
+    call("trx_quantize_f_pow2", xb.ptr, int(x.size), qb.ptr, eb.ptr, None)
+    synchronize()
+    return qb.download(np.int8, x.size), int(eb.download(np.int32)[0])
+
+
+def matvec_quantized(scales_f16, codes, x, B, R, kind=L.KIND_TERNARY5):
+    """The projection as the firmware runs it through the engine (model/mirror.py:663-678): x
+    quantized to int8 with a power-of-two exponent, the exact matvec, the int32 result scaled by
+    2^(e8 + R - B). float32 (M,). Asserts as matvec_ternary on overflow."""
+    M, K = codes.shape
+    rows = DeviceBuffer.from_array(_packets(scales_f16, codes, kind))
+    xb = DeviceBuffer.from_array(np.asarray(x, dtype=np.float32))
+    wb = ctypes.c_size_t()
+    call("trx_gemv_quantized_geometry", M, K, ctypes.byref(wb))
+    work = DeviceBuffer(wb.value)
+    yb = DeviceBuffer(4 * M)
+    st = DeviceBuffer(4)
+    st.zero()
+    call("trx_gemv_ternary_quantized", rows.ptr, kind, M, K, xb.ptr, int(B), int(R), yb.ptr, work.ptr, st.ptr, None)
+    synchronize()
+    status = int(st.download(np.int32)[0])
+    assert not (status & 1), "int48 accumulator overflow"
+    assert not (status & 2), "int32 result overflow"
+    return yb.download(np.float32, M)
+
+
 def group_sums(scales_f16, codes, x8, kind=L.KIND_TERNARY5):
     """Exact per-group sums (M, K/128) of (code - 1) * x8 on the GPU."""
     M, K = codes.shape
