@@ -109,6 +109,19 @@ int trx_gemv_ternary_f32(const uint8_t* rows, int kind, int M, int K, const floa
                          const float* norm_w, float eps, float* y, int epilogue,
                          const float* resid, trx_stream_t s);
 
+/* Multi-position float projection, the batched prefill's GEMM (the float counterpart of
+ * model/bitexact.py:121-125 matvec_ternary_rows, one weight pass for many rows): y[r] = W xhat_r
+ * for n rows x_r of K floats (xhat = x, or x / rms(x) * norm_w with norm_w != NULL), on the matrix
+ * cores. W's rows are decoded to fp16 weights exactly as fastref's fp16 weight cache holds them
+ * (model/fastref.py:104-116: (code - 1) * scale, or fp16(q * scale) for Q8) and xhat is split
+ * into fp16 hi and lo planes, so each product is fp32-accurate. kind: TRX_KIND_TERNARY,
+ * TRX_KIND_TERNARY5 or TRX_KIND_Q8. Epilogues: TRX_EPI_STORE y [n][M]; TRX_EPI_RESID y [n][M] +=;
+ * TRX_EPI_SWIGLU (rows [0,F) gate, [F,2F) up) y [n][M/2]. rows must be followed by 16 readable
+ * bytes; workspace holds 4*n*K bytes. */
+int trx_gemm_ternary_f32(const uint8_t* rows, int kind, int M, int K, const float* x, int n,
+                         const float* norm_w, float eps, float* y, int epilogue, void* workspace,
+                         trx_stream_t s);
+
 /* Packed float GEMV: the decoder's projection (the same arithmetic as trx_gemv_ternary_f32, with
  * x kept in fp32) over a GPU-native copy of the rows. The copy cuts K into 256-column slices
  * (two 128-groups) and stores, per slice, the rows' code bytes and fp16 scales slice-major in
@@ -253,6 +266,9 @@ typedef struct {
                                   rope_dims values, max_ctx rows; model/bons.py:356-367, read as
                                   model/mirror.py:478-483 does), which is how YaRN scaling
                                   reaches the decoder; 0: angles pos * rope_freq[i] */
+  int prefill_chunk;           /* trx_model_generate runs the prompt (all but its last token)
+                                  through trx_model_prefill in chunks of this many positions;
+                                  0: one position per forward, as the firmware's loop */
 } trx_model_config;
 
 #define TRX_PACK_QKV 1         /* attention q|k|v */
@@ -293,6 +309,14 @@ int trx_model_reset(trx_model* m);
 int trx_model_set_prompt(trx_model* m, const int32_t* tokens, int n, int head_from);
 /* Enqueue n forwards of one position each (eagerly, or as replays of one captured hipGraph). */
 int trx_model_step(trx_model* m, int n_steps, int use_graph);
+/* Batched prefill (model/bitexact.py:121-125 matvec_ternary_rows; firmware/infer.c:1956-1977
+ * forward_pair, which runs two prompt tokens per weight pass): the next n fed positions in
+ * chunks of up to `chunk` positions (<= 0: 1024), one weight pass per chunk. Every projection is
+ * a GEMM over the chunk on the matrix cores, attention is causal over the cache, the DeltaNet
+ * recurrence runs over the chunk's positions in order. The positions must precede head_from (no
+ * logits); afterwards the KV cache, the DeltaNet state and the position are those of n
+ * one-position forwards, and the next trx_model_step continues from there. */
+int trx_model_prefill(trx_model* m, int n, int chunk);
 /* Resolve the argmax of the last forward into the output buffer. */
 int trx_model_finalize(trx_model* m);
 int trx_model_sync(trx_model* m);

@@ -33,7 +33,7 @@ class ModelConfig(ctypes.Structure):
         (n, ctypes.c_int) for n in ("weight_kind", "head_kind", "head_tied", "emb_mode", "emb_kind",
                                     "max_new", "persistent", "packed_ops")] + [
         ("hadamard_block", ctypes.c_int), ("hadamard_scale", ctypes.c_float),
-        ("hadamard_widths", ctypes.c_int * 4), ("rope_table", ctypes.c_int)]
+        ("hadamard_widths", ctypes.c_int * 4), ("rope_table", ctypes.c_int), ("prefill_chunk", ctypes.c_int)]
 
 
 _mcp = ctypes.POINTER(ModelConfig)
@@ -90,6 +90,8 @@ SIGNATURES = {
     "trx_model_reset": [_vp],
     "trx_model_set_prompt": [_vp, _ip, _i, _i],
     "trx_model_step": [_vp, _i, _i],
+    "trx_model_prefill": [_vp, _i, _i],
+    "trx_gemm_ternary_f32": [_vp, _i, _i, _i, _vp, _i, _vp, ctypes.c_float, _vp, _i, _vp, _vp],
     "trx_model_finalize": [_vp],
     "trx_model_sync": [_vp],
     "trx_model_generate": [_vp, _ip, _i, _i, _ip, _i],

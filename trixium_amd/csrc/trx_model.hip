@@ -16,6 +16,7 @@
 #include "trx_ops.h"
 #include "trx_model.h"
 #include "trx_tgemv.h"
+#include "trx_prefill.h"
 
 namespace trx {
 
@@ -92,6 +93,12 @@ struct Model {
   float* hid_last = nullptr;                       // [n_embd]: TRX_READ_HIDDEN
   float* proj_x = nullptr;                         // [n_embd], [vocab]: trx_model_project_head
   float* proj_y = nullptr;
+  // Batched prefill (trx_model_prefill): buffers for chunks of up to pf_rows positions.
+  int pf_rows = 0;
+  float *pf_x = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_att = nullptr, *pf_act = nullptr;
+  float *pf_ba = nullptr, *pf_conv = nullptr, *pf_oraw = nullptr;
+  _Float16 *pf_h = nullptr, *pf_l = nullptr;
+  int host_n_fed = 0, host_head_from = 0;          // host copies of the control words
   hipGraph_t graph = nullptr;
   hipGraphExec_t graph_exec = nullptr;
   size_t dev_bytes = 0;
@@ -642,6 +649,189 @@ static int run_step(Model& m, hipStream_t s) {
   return TRX_OK;
 }
 
+// Batched prefill of positions p0 .. p0 + R - 1 --------------------------------------------------
+
+// The input planes of a projection of width K: RMSNorm (norm_w), and a rotated model's rotation of
+// that width unless `plain` (the DeltaNet beta/alpha take the unrotated input).
+static int pf_prep(Model& m, const float* x, int ldx, int K, int R, const float* norm_w, bool plain, hipStream_t s) {
+  PrepParams pp = {};
+  pp.x = x;
+  pp.ldx = ldx;
+  pp.K = K;
+  pp.R = R;
+  pp.norm_w = norm_w;
+  pp.eps = m.cfg.rms_eps;
+  pp.xh = m.pf_h;
+  pp.xl = m.pf_l;
+  if (m.cfg.hadamard_block && !plain) {
+    int wi = 0;
+    while (wi < 4 && m.cfg.hadamard_widths[wi] != K) ++wi;
+    TRX_CHECK(wi < 4, TRX_E_INVALID, "rotated model: no rotation for input width %d", K);
+    pp.signs = PF(m, TRX_ROLE_HADAMARD, wi);
+    pp.B = m.cfg.hadamard_block;
+    pp.scale = m.cfg.hadamard_scale;
+  }
+  return launch_prep(pp, s);
+}
+
+// One GEMM over the planes pf_prep left: W's rows (role, layer; the fused group starting there).
+static int pf_gemm(Model& m, int role, int l, int kind, int M, int K, int R, int epi, float* y, int ldy,
+                   hipStream_t s) {
+  const Tensor& t = T(m, role, l);
+  GemmParams g = {};
+  g.W = m.arena + t.off;
+  g.w_bytes = (uint32_t)std::min<size_t>(m.arena_bytes - t.off, 0xFFFFFFF0u);
+  g.kind = kind;
+  g.M = M;
+  g.K = K;
+  g.row_bytes = row_bytes_of(kind, K);
+  g.code_off = kind == TRX_KIND_Q8 ? kBeat * cdiv(K / 32, 16) : row_geom(kind, K).code_off;
+  g.xh = m.pf_h;
+  g.xl = m.pf_l;
+  g.R = R;
+  g.epi = epi;
+  g.y = y;
+  g.ldy = ldy;
+  return launch_gemm(g, s);
+}
+
+static int pf_alloc(Model& m, int R) {
+  if (R <= m.pf_rows) return TRX_OK;
+  const trx_model_config& c = m.cfg;
+  const int E = c.n_embd, F = c.ffn_dim, hd = c.head_dim;
+  const int qrows = c.n_head * hd * (c.attn_gated ? 2 : 1), kvrows = c.n_kv_head * hd;
+  const int nq = c.dn_num_k_heads * c.dn_k_head_dim, nvh = c.dn_num_v_heads * c.dn_v_head_dim;
+  const int C = 2 * nq + nvh;
+  const int kmax = std::max({E, F, c.n_head * hd, nvh});
+  const int io = std::max(m.n_attn ? qrows + 2 * kvrows : 0, m.n_dn ? C + nvh : 0);
+  const int att = std::max(c.n_head * hd, nvh);
+  // Earlier (smaller) buffers stay allocated until the model is destroyed.
+  int rc;
+  const size_t r = (size_t)R;
+  if ((rc = dalloc(m, (void**)&m.pf_x, r * E * 4))) return rc;
+  if ((rc = dalloc(m, (void**)&m.pf_h, r * kmax * 2))) return rc;
+  if ((rc = dalloc(m, (void**)&m.pf_l, r * kmax * 2))) return rc;
+  if ((rc = dalloc(m, (void**)&m.pf_qkv, r * io * 4))) return rc;
+  if ((rc = dalloc(m, (void**)&m.pf_att, r * att * 4))) return rc;
+  if ((rc = dalloc(m, (void**)&m.pf_act, r * F * 4))) return rc;
+  if (m.n_attn && (rc = dalloc(m, (void**)&m.pf_q, r * c.n_head * hd * 4))) return rc;
+  if (m.n_dn) {
+    if ((rc = dalloc(m, (void**)&m.pf_ba, r * 2 * c.dn_num_v_heads * 4))) return rc;
+    if ((rc = dalloc(m, (void**)&m.pf_conv, r * C * 4))) return rc;
+    if ((rc = dalloc(m, (void**)&m.pf_oraw, r * nvh * 4))) return rc;
+  }
+  m.pf_rows = R;
+  return TRX_OK;
+}
+
+static int run_prefill(Model& m, int p0, int R, hipStream_t s) {
+  const trx_model_config& c = m.cfg;
+  const int E = c.n_embd, hd = c.head_dim, F = c.ffn_dim, wk = c.weight_kind;
+  const int qrows = c.n_head * hd * (c.attn_gated ? 2 : 1), kvrows = c.n_kv_head * hd;
+  int rc;
+  EmbedParams ep = {};
+  ep.mode = c.emb_mode == 0 ? EMBED_TABLE : EMBED_TERNARY;
+  ep.n_embd = E;
+  ep.vocab = c.vocab;
+  if (c.emb_mode == 0) {
+    ep.mant = (const int16_t*)P(m, TRX_ROLE_TOK_EMB16, 0);
+    ep.exps = (const int32_t*)P(m, TRX_ROLE_TOK_EMB16_EXP, 0);
+  } else {
+    ep.rows = P(m, TRX_ROLE_TOK_EMB, 0);
+    ep.kind = c.emb_kind;
+    ep.row_bytes = row_bytes_of(c.emb_kind, E);
+    ep.code_off = row_geom(c.emb_kind, E).code_off;
+  }
+  if ((rc = launch_embed_rows(ep, m.prompt(), p0, R, m.pf_x, s))) return rc;
+
+  for (int l = 0; l < c.n_layer; ++l) {
+    if (m.is_dn(l)) {
+      const int nq = c.dn_num_k_heads * c.dn_k_head_dim, nvh = c.dn_num_v_heads * c.dn_v_head_dim;
+      const int C = 2 * nq + nvh, nv = c.dn_num_v_heads;
+      // beta|alpha (Q8) from the unrotated normed input, then qkv|z.
+      if ((rc = pf_prep(m, m.pf_x, E, E, R, PF(m, TRX_ROLE_ATTN_NORM, l), true, s))) return rc;
+      if ((rc = pf_gemm(m, TRX_ROLE_SSM_BETA, l, TRX_KIND_Q8, 2 * nv, E, R, GM_STORE, m.pf_ba, 2 * nv, s))) return rc;
+      if (c.hadamard_block && (rc = pf_prep(m, m.pf_x, E, E, R, PF(m, TRX_ROLE_ATTN_NORM, l), false, s))) return rc;
+      if ((rc = pf_gemm(m, TRX_ROLE_ATTN_QKV, l, wk, C + nvh, E, R, GM_STORE, m.pf_qkv, C + nvh, s))) return rc;
+      DnRowsParams dp = {};
+      dp.io = m.pf_qkv;
+      dp.ld_io = C + nvh;
+      dp.taps = PF(m, TRX_ROLE_SSM_CONV, l);
+      dp.conv_state = m.conv_state + (size_t)m.dn_index[l] * (c.dn_conv_kernel - 1) * C;
+      dp.conv_out = m.pf_conv;
+      dp.ba = m.pf_ba;
+      dp.A = PF(m, TRX_ROLE_SSM_A, l);
+      dp.dt = PF(m, TRX_ROLE_SSM_DT, l);
+      dp.norm_w = PF(m, TRX_ROLE_SSM_NORM, l);
+      dp.S = m.dn_state + (size_t)m.dn_index[l] * nvh * c.dn_k_head_dim;
+      dp.o_raw = m.pf_oraw;
+      dp.out = m.pf_att;
+      dp.R = R;
+      dp.C = C;
+      dp.Kc = c.dn_conv_kernel;
+      dp.nq = nq;
+      dp.nv = nv;
+      dp.nk = c.dn_num_k_heads;
+      dp.hk = c.dn_k_head_dim;
+      dp.hv = c.dn_v_head_dim;
+      dp.eps = c.rms_eps;
+      if ((rc = launch_dn_rows(dp, s))) return rc;
+      if ((rc = pf_prep(m, m.pf_att, nvh, nvh, R, nullptr, false, s))) return rc;
+      if ((rc = pf_gemm(m, TRX_ROLE_SSM_OUT, l, wk, E, nvh, R, GM_RESID, m.pf_x, E, s))) return rc;
+    } else {
+      const int M = qrows + 2 * kvrows;
+      if ((rc = pf_prep(m, m.pf_x, E, E, R, PF(m, TRX_ROLE_ATTN_NORM, l), false, s))) return rc;
+      if ((rc = pf_gemm(m, TRX_ROLE_ATTN_Q, l, wk, M, E, R, GM_STORE, m.pf_qkv, M, s))) return rc;
+      const size_t per = (size_t)c.n_kv_head * c.max_ctx * hd;
+      RopeKvParams rp = {};
+      rp.qkv = m.pf_qkv;
+      rp.ldq = M;
+      rp.q_norm = PF(m, TRX_ROLE_ATTN_Q_NORM, l);
+      rp.k_norm = PF(m, TRX_ROLE_ATTN_K_NORM, l);
+      rp.rope_freq = m.rope_dev;
+      rp.rope_tab = c.rope_table ? (const int16_t*)P(m, TRX_ROLE_ROPE_TAB, 0) : nullptr;
+      rp.p0 = p0;
+      rp.R = R;
+      rp.kcache = m.kcache + (size_t)m.attn_index[l] * per;
+      rp.vcache = m.vcache + (size_t)m.attn_index[l] * per;
+      rp.q_out = m.pf_q;
+      rp.n_head = c.n_head;
+      rp.n_kv = c.n_kv_head;
+      rp.hd = hd;
+      rp.rope_n = c.rope_dims ? c.rope_dims : hd;
+      rp.max_ctx = c.max_ctx;
+      rp.gated = c.attn_gated;
+      rp.eps = c.rms_eps;
+      if ((rc = launch_rope_kv(rp, s))) return rc;
+      AttnPrefillParams ap = {};
+      ap.q = m.pf_q;
+      ap.qkv = m.pf_qkv;
+      ap.ldq = M;
+      ap.kcache = rp.kcache;
+      ap.vcache = rp.vcache;
+      ap.out = m.pf_att;
+      ap.p0 = p0;
+      ap.R = R;
+      ap.n_head = c.n_head;
+      ap.n_kv = c.n_kv_head;
+      ap.hd = hd;
+      ap.max_ctx = c.max_ctx;
+      ap.gated = c.attn_gated;
+      if ((rc = launch_attn_prefill(ap, s))) return rc;
+      if ((rc = pf_prep(m, m.pf_att, c.n_head * hd, c.n_head * hd, R, nullptr, false, s))) return rc;
+      if ((rc = pf_gemm(m, TRX_ROLE_ATTN_OUT, l, wk, E, c.n_head * hd, R, GM_RESID, m.pf_x, E, s))) return rc;
+    }
+    if ((rc = pf_prep(m, m.pf_x, E, E, R, PF(m, TRX_ROLE_FFN_NORM, l), false, s))) return rc;
+    if ((rc = pf_gemm(m, TRX_ROLE_FFN_GATE, l, wk, 2 * F, E, R, GM_SWIGLU, m.pf_act, F, s))) return rc;
+    if ((rc = pf_prep(m, m.pf_act, F, F, R, nullptr, false, s))) return rc;
+    if ((rc = pf_gemm(m, TRX_ROLE_FFN_DOWN, l, wk, E, F, R, GM_RESID, m.pf_x, E, s))) return rc;
+  }
+  // The last position's residual is readable as the last forward's (TRX_READ_RESIDUAL), and the
+  // control words move on.
+  TRX_HIP(hipMemcpyAsync(m.hidden, m.pf_x + (size_t)(R - 1) * E, (size_t)E * 4, hipMemcpyDeviceToDevice, s));
+  return launch_prefill_ctl(m.pos(), m.cur_tok(), m.prompt(), p0 + R - 1, s);
+}
+
 }  // namespace trx
 
 using namespace trx;
@@ -851,6 +1041,8 @@ TRX_API int trx_model_reset(trx_model* h) {
   const trx_model_config& c = m.cfg;
   int init[8] = {-1, 0, 0, 0, 0, 0, 0, 0};
   m.host_pos = -1;
+  m.host_n_fed = 0;
+  m.host_head_from = 0;
   TRX_HIP(hipMemcpyAsync(m.ctl, init, sizeof init, hipMemcpyHostToDevice, m.stream));
   TRX_HIP(hipMemsetAsync(m.slot, 0, 8, m.stream));
   if (m.n_dn) {
@@ -883,6 +1075,8 @@ TRX_API int trx_model_set_prompt(trx_model* h, const int32_t* tokens, int n, int
   TRX_HIP(hipMemcpyAsync(m.ctl + 1, &n_fed, 4, hipMemcpyHostToDevice, m.stream));
   TRX_HIP(hipMemcpyAsync(m.ctl + 3, &hf, 4, hipMemcpyHostToDevice, m.stream));
   TRX_HIP(hipStreamSynchronize(m.stream));
+  m.host_n_fed = n_fed;
+  m.host_head_from = hf;
   return TRX_OK;
 }
 
@@ -912,6 +1106,29 @@ TRX_API int trx_model_step(trx_model* h, int n_steps, int use_graph) {
       return rc;
     }
   }
+  return TRX_OK;
+}
+
+TRX_API int trx_model_prefill(trx_model* h, int n, int chunk) {
+  TRX_CHECK(h && n >= 0, TRX_E_INVALID, "trx_model_prefill: bad arguments");
+  Model& m = h->m;
+  int rc;
+  if ((rc = check_loaded(m))) return rc;
+  const int first = m.host_pos + 1;
+  TRX_CHECK(first + n <= m.host_n_fed, TRX_E_STATE, "trx_model_prefill: positions %d..%d were not fed (%d fed)",
+            first, first + n - 1, m.host_n_fed);
+  TRX_CHECK(first + n <= m.host_head_from, TRX_E_STATE,
+            "trx_model_prefill: position %d computes logits (head_from %d); step it instead", first + n - 1,
+            m.host_head_from);
+  if (n == 0) return TRX_OK;
+  if (chunk <= 0) chunk = 1024;
+  chunk = std::min(chunk, n);
+  if ((rc = pf_alloc(m, chunk))) return rc;
+  for (int p0 = first; p0 < first + n; p0 += chunk) {
+    const int R = std::min(chunk, first + n - p0);
+    if ((rc = run_prefill(m, p0, R, m.stream))) return rc;
+  }
+  m.host_pos = first + n - 1;
   return TRX_OK;
 }
 
@@ -950,7 +1167,9 @@ TRX_API int trx_model_generate(trx_model* h, const int32_t* prompt, int n_prompt
   int rc;
   if ((rc = trx_model_reset(h))) return rc;
   if ((rc = trx_model_set_prompt(h, prompt, n_prompt, -1))) return rc;
-  if ((rc = trx_model_step(h, n_prompt + n_new - 1, use_graph))) return rc;
+  const int pre = m.cfg.prefill_chunk > 0 ? n_prompt - 1 : 0;
+  if (pre && (rc = trx_model_prefill(h, pre, m.cfg.prefill_chunk))) return rc;
+  if ((rc = trx_model_step(h, n_prompt - pre + n_new - 1, use_graph))) return rc;
   if ((rc = trx_model_finalize(h))) return rc;
   TRX_HIP(hipMemcpyAsync(out, m.out(), (size_t)n_new * 4, hipMemcpyDeviceToHost, m.stream));
   TRX_HIP(hipStreamSynchronize(m.stream));

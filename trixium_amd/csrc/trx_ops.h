@@ -145,6 +145,9 @@ struct ScoreParams {
 int launch_score(const ScoreParams& p, hipStream_t s);
 
 int launch_embed(const EmbedParams& p, hipStream_t s);
+// Prefill: the embeddings of the tokens fed at positions p0 .. p0 + R - 1 into X [R][n_embd]
+// (p's control-word fields are not used).
+int launch_embed_rows(const EmbedParams& p, const int* fed, int p0, int R, float* X, hipStream_t s);
 int launch_sample(const SampleParams& p, hipStream_t s);
 int launch_finalize(const int* pos, const int* n_prompt, unsigned long long* slot, int* out, int max_out,
                     hipStream_t s);

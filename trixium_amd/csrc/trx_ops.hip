@@ -37,36 +37,15 @@ __device__ __forceinline__ int wave_min_i(int v) {
   return v;
 }
 
-__global__ __launch_bounds__(kEmbedThreads) void embed_kernel(EmbedParams p) {
-  __shared__ int s_tok;
+// The embedding of token `tok` into x (n_embd floats); a whole block of kEmbedThreads.
+__device__ void embed_token(const EmbedParams& p, int tok, float* x) {
   __shared__ int s_red[kEmbedThreads / 64];
   __shared__ __align__(16) uint8_t s_row[kEmbedRowMax];
   const int tid = threadIdx.x;
-  if (tid == 0) {
-    // The control words are read together (one round trip), before the position is written.
-    const int pos0 = *p.pos, np = *p.n_prompt;
-    const unsigned long long key = *p.slot;
-    const int pos = pos0 + 1;
-    *p.pos = pos;
-    int tok;
-    if (pos < np) {
-      tok = p.prompt[pos];
-    } else {
-      tok = slot_token(key);
-      const int k = pos - np;
-      if (k < p.max_out) p.out[k] = tok;
-    }
-    if (tok < 0 || tok >= p.vocab) tok = 0;
-    *p.slot = 0ull;
-    *p.cur_tok = tok;
-    s_tok = tok;
-  }
-  __syncthreads();
-  const int tok = s_tok;
   if (p.mode == EMBED_TABLE) {
     const float sc = bfp_scale(p.exps[tok]);
     const int16_t* m = p.mant + (size_t)tok * p.n_embd;
-    for (int c = tid; c < p.n_embd; c += kEmbedThreads) p.x[c] = (float)m[c] * sc;
+    for (int c = tid; c < p.n_embd; c += kEmbedThreads) x[c] = (float)m[c] * sc;
     return;
   }
   // Ternary row: scales at the head of the row packet, codes after code_off. The whole packet
@@ -139,8 +118,41 @@ __global__ __launch_bounds__(kEmbedThreads) void embed_kernel(EmbedParams p) {
     const int sh = min(e16 - emin, 20) - k2;
     const long long v = (long long)(code_of(c) - 1) * m11;
     const long long w = sh >= 0 ? (v << sh) : (v >> (-sh));
-    p.x[c] = (float)(int16_t)(w & 0xFFFF) * scale;
+    x[c] = (float)(int16_t)(w & 0xFFFF) * scale;
   }
+}
+
+__global__ __launch_bounds__(kEmbedThreads) void embed_kernel(EmbedParams p) {
+  __shared__ int s_tok;
+  const int tid = threadIdx.x;
+  if (tid == 0) {
+    // The control words are read together (one round trip), before the position is written.
+    const int pos0 = *p.pos, np = *p.n_prompt;
+    const unsigned long long key = *p.slot;
+    const int pos = pos0 + 1;
+    *p.pos = pos;
+    int tok;
+    if (pos < np) {
+      tok = p.prompt[pos];
+    } else {
+      tok = slot_token(key);
+      const int k = pos - np;
+      if (k < p.max_out) p.out[k] = tok;
+    }
+    if (tok < 0 || tok >= p.vocab) tok = 0;
+    *p.slot = 0ull;
+    *p.cur_tok = tok;
+    s_tok = tok;
+  }
+  __syncthreads();
+  embed_token(p, s_tok, p.x);
+}
+
+// Prefill: the tokens fed at positions p0 .. p0 + gridDim.x - 1 into rows of X.
+__global__ __launch_bounds__(kEmbedThreads) void embed_rows_kernel(EmbedParams p, const int* fed, int p0, float* X) {
+  int tok = fed[p0 + blockIdx.x];
+  if (tok < 0 || tok >= p.vocab) tok = 0;
+  embed_token(p, tok, X + (size_t)blockIdx.x * p.n_embd);
 }
 
 // Resolve the last generated token (after the final step): out[pos + 1 - n_prompt].
@@ -531,6 +543,16 @@ int launch_rotate(const RotParams& p, hipStream_t s) {
   TRX_CHECK(p.B >= 64 && p.B <= 1024 && (p.B & (p.B - 1)) == 0 && p.K > 0 && p.K % p.B == 0 && p.x != p.y,
             TRX_E_INVALID, "rotation: block %d over %d columns unsupported", p.B, p.K);
   hipLaunchKernelGGL(rotate_kernel, dim3(p.K / p.B), dim3(p.B), 0, s, p);
+  TRX_LAUNCHED();
+  return TRX_OK;
+}
+
+int launch_embed_rows(const EmbedParams& p, const int* fed, int p0, int R, float* X, hipStream_t s) {
+  TRX_CHECK(p.n_embd % kGroup == 0 && p.n_embd / kGroup <= kMaxEmbedGroups && R >= 1, TRX_E_INVALID,
+            "embedding: n_embd %d unsupported", p.n_embd);
+  TRX_CHECK(p.mode == EMBED_TABLE || (p.row_bytes % 16 == 0 && p.row_bytes <= kEmbedRowMax), TRX_E_INVALID,
+            "embedding: row of %d bytes unsupported", p.row_bytes);
+  hipLaunchKernelGGL(embed_rows_kernel, dim3(R), dim3(kEmbedThreads), 0, s, p, fed, p0, X);
   TRX_LAUNCHED();
   return TRX_OK;
 }

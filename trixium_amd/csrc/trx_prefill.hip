@@ -1,0 +1,781 @@
+// Batched prefill kernels: R prompt positions per forward, one weight pass for all of them.
+//
+// The projections run on the matrix cores (v_mfma_f32_32x32x16_f16): a block decodes a 128-row x
+// 128-column tile of the stored ternary rows into LDS as fp16 weights and multiplies 64 positions
+// by it, x split into two fp16 planes (hi, lo) so the fp32 accumulation sees x to ~22 bits.
+// Attention, the RoPE/KV append and the Gated DeltaNet recurrence are the one-position rules of
+// the decode kernels applied to every position of the chunk (the recurrence in order).
+
+#include "trx_internal.h"
+#include "trx_prefill.h"
+
+#include <algorithm>
+
+namespace trx {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// GEMM ------------------------------------------------------------------------------------------
+
+constexpr int kGmThreads = 256;
+constexpr int kGmBR = 64;                  // positions per block
+constexpr int kGmBM = 128;                 // weight rows per block
+constexpr int kGmLd = kGroup + 8;          // LDS row stride in halves (272 bytes)
+
+__device__ __forceinline__ uint32_t pk_mul_h2(uint32_t a, uint32_t s2) {
+  typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+  const h2_t r = __builtin_bit_cast(h2_t, a) * __builtin_bit_cast(h2_t, s2);
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+__device__ __forceinline__ uint32_t half_bits(float v) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v);
+}
+
+// Weight row of LDS tile row i: plain tiles take M rows in order; a SwiGLU tile takes 64 gate rows
+// f0 .. f0 + 63 (LDS rows 0..63) and the matching up rows F + f0 .. (LDS rows 64..127).
+__device__ __forceinline__ int gm_wrow(int epi, int i, int M) {
+  if (epi == GM_SWIGLU) {
+    const int F = M / 2, f = blockIdx.x * (kGmBM / 2) + (i & 63);
+    return f < F ? (i < 64 ? f : F + f) : M;
+  }
+  return blockIdx.x * kGmBM + i;
+}
+
+template <int KIND>
+struct GmRaw {
+  uint4 c[KIND == TRX_KIND_Q8 ? 4 : 1];
+  uint32_t sc;
+};
+
+template <int KIND, int EPI>
+__global__ __launch_bounds__(kGmThreads, 2) void gemm_kernel(GemmParams p) {
+  __shared__ __align__(16) _Float16 ws[kGmBM * kGmLd];
+  __shared__ __align__(16) _Float16 xs[2][kGmBR * kGmLd];
+  __shared__ __align__(16) uint4 lut[2][256];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int r0 = blockIdx.y * kGmBR;
+  const int G = p.K / kGroup;
+
+  // Code byte -> (digit - 1) as fp16, two per dword. trit5: the even table starts a byte's five
+  // digits on a dword boundary (d0 d1 | d2 d3 | d4 0), the odd one a half later (0 d0 | d1 d2 | d3
+  // d4): two consecutive bytes fill five dwords. 2-bit: (c0 c1 | c2 c3).
+  {
+    const int b = tid;
+    if (KIND == TRX_KIND_TERNARY5) {
+      uint32_t h[5];
+      int v = b;
+#pragma unroll
+      for (int k = 0; k < 5; ++k) {
+        h[k] = half_bits((float)(v % 3 - 1));
+        v /= 3;
+      }
+      lut[0][b] = make_uint4(h[0] | h[1] << 16, h[2] | h[3] << 16, h[4], 0u);
+      lut[1][b] = make_uint4(h[0] << 16, h[1] | h[2] << 16, h[3] | h[4] << 16, 0u);
+    } else if (KIND == TRX_KIND_TERNARY) {
+      uint32_t h[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) h[k] = half_bits((float)(((b >> (2 * k)) & 3) - 1));
+      lut[0][b] = make_uint4(h[0] | h[1] << 16, h[2] | h[3] << 16, 0u, 0u);
+    }
+  }
+
+  // Staging roles: thread t decodes half (t >> 7) of the 128 codes of LDS row t & 127, and copies
+  // eight 16-byte pieces of the two x planes.
+  const int srow = tid & 127, shalf = tid >> 7;
+  const int wrow = gm_wrow(EPI, srow, p.M);
+  const bool wvalid = wrow < p.M;
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.W, p.w_bytes);
+  const uint32_t rbase = (uint32_t)(wvalid ? wrow : 0) * (uint32_t)p.row_bytes;
+  const __amdgpu_buffer_rsrc_t rxh = make_rsrc(p.xh, (uint32_t)((size_t)p.R * p.K * 2));
+  const __amdgpu_buffer_rsrc_t rxl = make_rsrc(p.xl, (uint32_t)((size_t)p.R * p.K * 2));
+
+  auto load_w = [&](GmRaw<KIND>& raw, int g) {
+    if (KIND == TRX_KIND_TERNARY5) {
+      const uint32_t o = (uint32_t)p.code_off + 26u * (uint32_t)g + (shalf ? 12u : 0u);
+      const auto a = __builtin_amdgcn_raw_buffer_load_b128(rw, rbase + (o & ~3u), 0, 0);
+      raw.c[0] = make_uint4(a[0], a[1], a[2], a[3]);
+      raw.sc = __builtin_amdgcn_raw_buffer_load_b16(rw, rbase + 2u * (uint32_t)g, 0, 0);
+    } else if (KIND == TRX_KIND_TERNARY) {
+      const uint32_t o = (uint32_t)p.code_off + 32u * (uint32_t)g + 16u * (uint32_t)shalf;
+      const auto a = __builtin_amdgcn_raw_buffer_load_b128(rw, rbase + o, 0, 0);
+      raw.c[0] = make_uint4(a[0], a[1], a[2], a[3]);
+      raw.sc = __builtin_amdgcn_raw_buffer_load_b16(rw, rbase + 2u * (uint32_t)g, 0, 0);
+    } else {
+      const uint32_t o = (uint32_t)p.code_off + 128u * (uint32_t)g + 64u * (uint32_t)shalf;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const auto a = __builtin_amdgcn_raw_buffer_load_b128(rw, rbase + o + 16u * k, 0, 0);
+        raw.c[k] = make_uint4(a[0], a[1], a[2], a[3]);
+      }
+      // The two 32-column group scales of this half (groups 4g + 2 shalf and the next).
+      raw.sc = __builtin_amdgcn_raw_buffer_load_b32(rw, rbase + 2u * (4u * (uint32_t)g + 2u * (uint32_t)shalf), 0, 0);
+    }
+  };
+  uint4 xr[8];
+  auto load_x = [&](int g) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int piece = tid + kGmThreads * q, row = piece >> 4, c16 = piece & 15;
+      const uint32_t off = ((uint32_t)(r0 + row) * (uint32_t)p.K + (uint32_t)(kGroup * g + 8 * c16)) * 2u;
+      const auto a = __builtin_amdgcn_raw_buffer_load_b128(rxh, off, 0, 0);
+      const auto b = __builtin_amdgcn_raw_buffer_load_b128(rxl, off, 0, 0);
+      xr[q] = make_uint4(a[0], a[1], a[2], a[3]);
+      xr[4 + q] = make_uint4(b[0], b[1], b[2], b[3]);
+    }
+  };
+  // Decoded weights of this thread's 64 codes: 32 dwords of fp16 pairs, times the scale.
+  auto stage_w = [&](const GmRaw<KIND>& raw, int g) {
+    uint32_t D[32];
+    if (!wvalid) {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) D[i] = 0u;
+    } else if (KIND == TRX_KIND_TERNARY5) {
+      const uint32_t o = (uint32_t)p.code_off + 26u * (uint32_t)g + (shalf ? 12u : 0u);
+      const uint32_t sh = o & 3u;
+      const uint32_t d0 = __builtin_amdgcn_alignbyte(raw.c[0].y, raw.c[0].x, sh);
+      const uint32_t d1 = __builtin_amdgcn_alignbyte(raw.c[0].z, raw.c[0].y, sh);
+      const uint32_t d2 = __builtin_amdgcn_alignbyte(raw.c[0].w, raw.c[0].z, sh);
+      const uint32_t d3 = __builtin_amdgcn_alignbyte(0u, raw.c[0].w, sh);
+      const uint32_t dw[4] = {d0, d1, d2, d3};
+      auto byte = [&](int j) { return (dw[j >> 2] >> (8 * (j & 3))) & 0xFFu; };
+      if (shalf == 0) {
+        // bytes 0..12: codes 0..64, of which 0..63 are this half's
+#pragma unroll
+        for (int i = 0; i < 6; ++i) {
+          const uint4 e = lut[0][byte(2 * i)], od = lut[1][byte(2 * i + 1)];
+          D[5 * i] = e.x;
+          D[5 * i + 1] = e.y;
+          D[5 * i + 2] = e.z | od.x;
+          D[5 * i + 3] = od.y;
+          D[5 * i + 4] = od.z;
+        }
+        const uint4 e = lut[0][byte(12)];
+        D[30] = e.x;
+        D[31] = e.y;
+      } else {
+        // bytes 12..25: codes 60..129; this half takes 64..127
+        const uint4 e0 = lut[0][byte(0)], o1 = lut[1][byte(1)];
+        D[0] = e0.z | o1.x;
+        D[1] = o1.y;
+        D[2] = o1.z;
+#pragma unroll
+        for (int i = 1; i < 6; ++i) {
+          const uint4 e = lut[0][byte(2 * i)], od = lut[1][byte(2 * i + 1)];
+          D[5 * i - 2] = e.x;
+          D[5 * i - 1] = e.y;
+          D[5 * i] = e.z | od.x;
+          D[5 * i + 1] = od.y;
+          D[5 * i + 2] = od.z;
+        }
+        const uint4 e = lut[0][byte(12)], od = lut[1][byte(13)];
+        D[28] = e.x;
+        D[29] = e.y;
+        D[30] = e.z | od.x;
+        D[31] = od.y;
+      }
+    } else if (KIND == TRX_KIND_TERNARY) {
+      const uint32_t dw[4] = {raw.c[0].x, raw.c[0].y, raw.c[0].z, raw.c[0].w};
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const uint4 e = lut[0][(dw[j >> 2] >> (8 * (j & 3))) & 0xFFu];
+        D[2 * j] = e.x;
+        D[2 * j + 1] = e.y;
+      }
+    } else {
+      // Q8: int8 -> fp16 exactly, times the 32-column group's scale in fp16 (fp16(q * s)).
+      const uint32_t dw[16] = {raw.c[0].x, raw.c[0].y, raw.c[0].z, raw.c[0].w, raw.c[1].x, raw.c[1].y,
+                               raw.c[1].z, raw.c[1].w, raw.c[2].x, raw.c[2].y, raw.c[2].z, raw.c[2].w,
+                               raw.c[3].x, raw.c[3].y, raw.c[3].z, raw.c[3].w};
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        auto q = [&](int b) { return half_bits((float)(int8_t)(uint8_t)(dw[j] >> (8 * b))); };
+        D[2 * j] = q(0) | q(1) << 16;
+        D[2 * j + 1] = q(2) | q(3) << 16;
+      }
+    }
+    if (wvalid) {
+      if (KIND == TRX_KIND_Q8) {
+        const uint32_t s0 = raw.sc & 0xFFFFu, s1 = raw.sc >> 16;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) D[i] = pk_mul_h2(D[i], i < 16 ? (s0 | s0 << 16) : (s1 | s1 << 16));
+      } else {
+        const uint32_t s2 = (raw.sc & 0xFFFFu) | (raw.sc << 16);
+#pragma unroll
+        for (int i = 0; i < 32; ++i) D[i] = pk_mul_h2(D[i], s2);
+      }
+    }
+    uint4* dst = (uint4*)(ws + srow * kGmLd + 64 * shalf);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dst[i] = make_uint4(D[4 * i], D[4 * i + 1], D[4 * i + 2], D[4 * i + 3]);
+  };
+  auto stage_x = [&]() {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int piece = tid + kGmThreads * q, row = piece >> 4, c16 = piece & 15;
+      *(uint4*)(xs[0] + row * kGmLd + 8 * c16) = xr[q];
+      *(uint4*)(xs[1] + row * kGmLd + 8 * c16) = xr[4 + q];
+    }
+  };
+
+  // Wave tiles: positions 32 wr .. + 31 of the block; weight columns ct0 and ct1 (32 each).
+  const int wr = w & 1, wm = w >> 1;
+  const int ct0 = EPI == GM_SWIGLU ? 32 * wm : 64 * wm;
+  const int ct1 = EPI == GM_SWIGLU ? 64 + 32 * wm : 64 * wm + 32;
+  const int li = lane & 31, lk = 8 * (lane >> 5);
+  f32x16_t acc0 = {}, acc1 = {};
+
+  GmRaw<KIND> raw;
+  load_w(raw, 0);
+  load_x(0);
+  for (int g = 0; g < G; ++g) {
+    __syncthreads();                      // the previous group's fragments are read
+    stage_w(raw, g);
+    stage_x();
+    __syncthreads();
+    if (g + 1 < G) {
+      load_w(raw, g + 1);
+      load_x(g + 1);
+    }
+#pragma unroll
+    for (int kk = 0; kk < kGroup / 16; ++kk) {
+      const int k = 16 * kk + lk;
+      const half8_t ah = *(const half8_t*)(xs[0] + (32 * wr + li) * kGmLd + k);
+      const half8_t al = *(const half8_t*)(xs[1] + (32 * wr + li) * kGmLd + k);
+      const half8_t b0 = *(const half8_t*)(ws + (ct0 + li) * kGmLd + k);
+      const half8_t b1 = *(const half8_t*)(ws + (ct1 + li) * kGmLd + k);
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b0, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b1, acc1, 0, 0, 0);
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b0, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b1, acc1, 0, 0, 0);
+    }
+  }
+
+  // Accumulator e of lane l holds D[i][j], i = 8 (e / 4) + 4 (l / 32) + e % 4, j = l % 32.
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int i = 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+    const int r = r0 + 32 * wr + i;
+    if (r >= p.R) continue;
+    float* yr = p.y + (size_t)r * p.ldy;
+    if (EPI == GM_SWIGLU) {
+      const int f = blockIdx.x * (kGmBM / 2) + 32 * wm + li;
+      if (f < p.M / 2) yr[f] = silu(acc0[e]) * acc1[e];
+    } else {
+      const int m0 = blockIdx.x * kGmBM + ct0 + li, m1 = blockIdx.x * kGmBM + ct1 + li;
+      if (EPI == GM_RESID) {
+        if (m0 < p.M) yr[m0] += acc0[e];
+        if (m1 < p.M) yr[m1] += acc1[e];
+      } else {
+        if (m0 < p.M) yr[m0] = acc0[e];
+        if (m1 < p.M) yr[m1] = acc1[e];
+      }
+    }
+  }
+}
+
+template <int KIND>
+static void gemm_dispatch(const GemmParams& p, dim3 grid, hipStream_t s) {
+  if (p.epi == GM_SWIGLU)
+    hipLaunchKernelGGL((gemm_kernel<KIND, GM_SWIGLU>), grid, dim3(kGmThreads), 0, s, p);
+  else if (p.epi == GM_RESID)
+    hipLaunchKernelGGL((gemm_kernel<KIND, GM_RESID>), grid, dim3(kGmThreads), 0, s, p);
+  else
+    hipLaunchKernelGGL((gemm_kernel<KIND, GM_STORE>), grid, dim3(kGmThreads), 0, s, p);
+}
+
+int launch_gemm(const GemmParams& p, hipStream_t s) {
+  TRX_CHECK(p.kind == TRX_KIND_TERNARY || p.kind == TRX_KIND_TERNARY5 || p.kind == TRX_KIND_Q8, TRX_E_INVALID,
+            "prefill GEMM: weight kind %d unsupported", p.kind);
+  TRX_CHECK(p.M >= 1 && p.K >= kGroup && p.K % kGroup == 0 && p.R >= 1, TRX_E_INVALID,
+            "prefill GEMM: M=%d K=%d R=%d", p.M, p.K, p.R);
+  TRX_CHECK(p.epi != GM_SWIGLU || p.M % 2 == 0, TRX_E_INVALID, "prefill GEMM: SwiGLU needs an even M");
+  TRX_CHECK((size_t)p.R * p.K * 2 < (1ull << 32) && (size_t)p.M * p.row_bytes < (1ull << 32) &&
+            (size_t)p.M * p.row_bytes + 16 <= p.w_bytes, TRX_E_INVALID, "prefill GEMM: operands too large");
+  const int nx = p.epi == GM_SWIGLU ? cdiv(p.M / 2, kGmBM / 2) : cdiv(p.M, kGmBM);
+  const dim3 grid(nx, cdiv(p.R, kGmBR));
+  if (p.kind == TRX_KIND_TERNARY5) gemm_dispatch<TRX_KIND_TERNARY5>(p, grid, s);
+  else if (p.kind == TRX_KIND_TERNARY) gemm_dispatch<TRX_KIND_TERNARY>(p, grid, s);
+  else gemm_dispatch<TRX_KIND_Q8>(p, grid, s);
+  TRX_LAUNCHED();
+  return TRX_OK;
+}
+
+// Input planes ---------------------------------------------------------------------------------
+
+__device__ __forceinline__ void store_hilo(const PrepParams& p, size_t i, float v) {
+  const _Float16 h = (_Float16)v;
+  p.xh[i] = h;
+  p.xl[i] = (_Float16)(v - (float)h);
+}
+
+// One block of 256 threads per position, no rotation.
+__global__ __launch_bounds__(256) void prep_kernel(PrepParams p) {
+  __shared__ float red[16];
+  const int r = blockIdx.x, t = threadIdx.x;
+  const float* x = p.x + (size_t)r * p.ldx;
+  float rs = 1.f;
+  if (p.norm_w) {
+    float ss = 0.f;
+    for (int c = t; c < p.K; c += 256) ss += x[c] * x[c];
+    rs = 1.0f / sqrtf(block_sum(ss, red) / (float)p.K + p.eps);
+  }
+  for (int c = t; c < p.K; c += 256) {
+    const float v = p.norm_w ? x[c] * rs * p.norm_w[c] : x[c];
+    store_hilo(p, (size_t)r * p.K + c, v);
+  }
+}
+
+// Rotated input: one block of B threads per (rotation block, position), as rotate_kernel does for
+// one vector (the whole row's sum of squares, the butterflies by shuffles then LDS).
+__global__ __launch_bounds__(1024) void prep_rot_kernel(PrepParams p) {
+  __shared__ float v[1024];
+  __shared__ float red[16];
+  const int t = threadIdx.x, B = blockDim.x, c = blockIdx.x * B + t, r = blockIdx.y;
+  const int lane = t & 63, w = t >> 6;
+  const float* x = p.x + (size_t)r * p.ldx;
+  float a = x[c] * p.signs[c];
+  if (p.norm_w) {
+    float ss = 0.f;
+    for (int i = t; i < p.K; i += B) ss += x[i] * x[i];
+    ss = wave_sum(ss);
+    if (lane == 0) red[w] = ss;
+    __syncthreads();
+    float tot = 0.f;
+    for (int k = 0; k < B / 64; ++k) tot += red[k];
+    a *= p.norm_w[c] / sqrtf(tot / (float)p.K + p.eps);
+  }
+  for (int h = 1; h < 64; h <<= 1) {
+    const float o = __shfl_xor(a, h, 64);
+    a = (lane & h) ? o - a : a + o;
+  }
+  for (int h = 64; h < B; h <<= 1) {
+    v[t] = a;
+    __syncthreads();
+    const float o = v[t ^ h];
+    __syncthreads();
+    a = (t & h) ? o - a : a + o;
+  }
+  store_hilo(p, (size_t)r * p.K + c, a * p.scale);
+}
+
+int launch_prep(const PrepParams& p, hipStream_t s) {
+  TRX_CHECK(p.R >= 1 && p.K >= 1 && p.ldx >= p.K, TRX_E_INVALID, "prefill input: R=%d K=%d", p.R, p.K);
+  if (p.signs) {
+    TRX_CHECK(p.B >= 64 && p.B <= 1024 && (p.B & (p.B - 1)) == 0 && p.K % p.B == 0, TRX_E_INVALID,
+              "prefill input: rotation block %d over %d columns unsupported", p.B, p.K);
+    hipLaunchKernelGGL(prep_rot_kernel, dim3(p.K / p.B, p.R), dim3(p.B), 0, s, p);
+  } else {
+    hipLaunchKernelGGL(prep_kernel, dim3(p.R), dim3(256), 0, s, p);
+  }
+  TRX_LAUNCHED();
+  return TRX_OK;
+}
+
+// RoPE and the KV append -----------------------------------------------------------------------
+
+// One wave per (position, head): q heads first, then kv heads. HD / 64 elements per lane.
+template <int HD>
+__global__ __launch_bounds__(64) void rope_kv_kernel(RopeKvParams p) {
+  constexpr int E = HD / 64;
+  __shared__ float nv_s[HD];
+  const int r = blockIdx.x, j = blockIdx.y, lane = threadIdx.x;
+  const int pos = p.p0 + r, half = p.rope_n / 2;
+  const int qstride = p.gated ? 2 * HD : HD;
+  const bool isq = j < p.n_head;
+  const int g = j - p.n_head;
+  const float* src = p.qkv + (size_t)r * p.ldq + (isq ? (size_t)j * qstride : (size_t)p.n_head * qstride + (size_t)g * HD);
+  const float* wn = isq ? p.q_norm : p.k_norm;
+  float v[E];
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    v[e] = src[lane + 64 * e];
+    ss += v[e] * v[e];
+  }
+  ss = wave_sum(ss);
+  const float rr = 1.0f / sqrtf(ss / (float)HD + p.eps);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    v[e] = v[e] * rr * wn[lane + 64 * e];
+    nv_s[lane + 64 * e] = v[e];
+  }
+  __syncthreads();
+  float o[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int d = lane + 64 * e;
+    o[e] = v[e];
+    if (d < 2 * half) {
+      const int i = d < half ? d : d - half;
+      float sn, cs;
+      if (p.rope_tab) {
+        cs = (float)p.rope_tab[(size_t)pos * p.rope_n + i] * (1.0f / 16384.0f);
+        sn = (float)p.rope_tab[(size_t)pos * p.rope_n + half + i] * (1.0f / 16384.0f);
+      } else {
+        sincosf((float)pos * p.rope_freq[i], &sn, &cs);
+      }
+      o[e] = d < half ? v[e] * cs - nv_s[d + half] * sn : nv_s[d - half] * sn + v[e] * cs;
+    }
+  }
+  if (isq) {
+    const float post = 1.0f / sqrtf((float)HD);
+    float* dst = p.q_out + ((size_t)r * p.n_head + j) * HD;
+#pragma unroll
+    for (int e = 0; e < E; ++e) dst[lane + 64 * e] = o[e] * post;
+  } else {
+    const size_t c = ((size_t)g * p.max_ctx + pos) * HD;
+    const float* vsrc = p.qkv + (size_t)r * p.ldq + (size_t)p.n_head * qstride + (size_t)p.n_kv * HD + (size_t)g * HD;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      p.kcache[c + lane + 64 * e] = __float2half(o[e]);
+      p.vcache[c + lane + 64 * e] = __float2half(vsrc[lane + 64 * e]);
+    }
+  }
+}
+
+int launch_rope_kv(const RopeKvParams& p, hipStream_t s) {
+  TRX_CHECK(p.R >= 1 && p.p0 >= 0 && p.p0 + p.R <= p.max_ctx && p.rope_n % 2 == 0 && p.rope_n <= p.hd,
+            TRX_E_INVALID, "prefill RoPE: positions %d..%d", p.p0, p.p0 + p.R);
+  const dim3 grid(p.R, p.n_head + p.n_kv);
+  if (p.hd == 64) hipLaunchKernelGGL(rope_kv_kernel<64>, grid, dim3(64), 0, s, p);
+  else if (p.hd == 128) hipLaunchKernelGGL(rope_kv_kernel<128>, grid, dim3(64), 0, s, p);
+  else if (p.hd == 256) hipLaunchKernelGGL(rope_kv_kernel<256>, grid, dim3(64), 0, s, p);
+  else TRX_CHECK(false, TRX_E_INVALID, "prefill RoPE: head_dim %d unsupported", p.hd);
+  TRX_LAUNCHED();
+  return TRX_OK;
+}
+
+// Causal attention ------------------------------------------------------------------------------
+//
+// Block (query tile, kv head): the rep q heads of the kv head at QT = 64 / rep positions, one
+// query row per 4 threads (row = position offset * rep + head offset). Key tiles of KT cache
+// positions in LDS as fp32; each thread scores KT/4 keys, the row's online softmax runs over its
+// four lanes (shuffles), and each thread accumulates HD/4 output dims.
+
+template <int HD, int KT>
+__global__ __launch_bounds__(256) void attn_prefill_kernel(AttnPrefillParams p) {
+  constexpr int KPT = KT / 4, DPT = HD / 4;
+  __shared__ __align__(16) float qs[64][HD];
+  __shared__ __align__(16) float ks[KT][HD + 4];
+  __shared__ __align__(16) float vs[KT][HD + 4];
+  __shared__ float ps[64][KT + 1];
+  const int tid = threadIdx.x, row = tid >> 2, tq = tid & 3;
+  const int rep = p.n_head / p.n_kv, QT = 64 / rep;
+  const int g = blockIdx.y, q0 = blockIdx.x * QT;        // chunk offset of the tile's first query
+  const int pq = row / rep, jh = row - pq * rep;
+  const bool rvalid = pq < QT && q0 + pq < p.R;
+  const int qpos = p.p0 + q0 + pq;                        // absolute position of this row
+  const int h = g * rep + jh;
+  const int last = p.p0 + min(p.R, q0 + QT) - 1;          // last key any row of the tile sees
+
+  for (int i = tid; i < 64 * HD / 4; i += 256) {
+    const int rr = i / (HD / 4), d4 = i - rr * (HD / 4);
+    const int pq_ = rr / rep, j_ = rr - pq_ * rep;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (pq_ < QT && q0 + pq_ < p.R)
+      v = *(const float4*)(p.q + ((size_t)(q0 + pq_) * p.n_head + g * rep + j_) * HD + 4 * d4);
+    *(float4*)&qs[rr][4 * d4] = v;
+  }
+  float acc[DPT];
+#pragma unroll
+  for (int d = 0; d < DPT; ++d) acc[d] = 0.f;
+  float m = -INFINITY, l = 0.f;
+  const __half* kc = p.kcache + (size_t)g * p.max_ctx * HD;
+  const __half* vc = p.vcache + (size_t)g * p.max_ctx * HD;
+
+  for (int t0 = 0; t0 <= last; t0 += KT) {
+    __syncthreads();                                      // previous tile's reads are done
+    for (int i = tid; i < KT * HD / 8; i += 256) {
+      const int t = i / (HD / 8), d8 = i - t * (HD / 8);
+      float kf[8], vf[8];
+      if (t0 + t <= last) {
+        const uint4 kr = *(const uint4*)(kc + (size_t)(t0 + t) * HD + 8 * d8);
+        const uint4 vr = *(const uint4*)(vc + (size_t)(t0 + t) * HD + 8 * d8);
+        const __half* kh = (const __half*)&kr;
+        const __half* vh = (const __half*)&vr;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          kf[k] = __half2float(kh[k]);
+          vf[k] = __half2float(vh[k]);
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) kf[k] = vf[k] = 0.f;
+      }
+      *(float4*)&ks[t][8 * d8] = make_float4(kf[0], kf[1], kf[2], kf[3]);
+      *(float4*)&ks[t][8 * d8 + 4] = make_float4(kf[4], kf[5], kf[6], kf[7]);
+      *(float4*)&vs[t][8 * d8] = make_float4(vf[0], vf[1], vf[2], vf[3]);
+      *(float4*)&vs[t][8 * d8 + 4] = make_float4(vf[4], vf[5], vf[6], vf[7]);
+    }
+    __syncthreads();
+    // Scores of keys t0 + tq * KPT .. + KPT - 1.
+    float sc[KPT];
+#pragma unroll
+    for (int k = 0; k < KPT; ++k) sc[k] = 0.f;
+    for (int d = 0; d < HD; d += 4) {
+      const float4 qv = *(const float4*)&qs[row][d];
+#pragma unroll
+      for (int k = 0; k < KPT; ++k) {
+        const float4 kv = *(const float4*)&ks[tq * KPT + k][d];
+        sc[k] += qv.x * kv.x + qv.y * kv.y + qv.z * kv.z + qv.w * kv.w;
+      }
+    }
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < KPT; ++k) {
+      if (t0 + tq * KPT + k > qpos) sc[k] = -INFINITY;
+      tmax = fmaxf(tmax, sc[k]);
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 1, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 2, 64));
+    const float mn = fmaxf(m, tmax);
+    // A tile past this row's position is all masked: nothing changes (mn stays m).
+    const float corr = mn == -INFINITY ? 1.f : __expf(m - mn);
+    float psum = 0.f;
+#pragma unroll
+    for (int k = 0; k < KPT; ++k) {
+      const float pk = sc[k] == -INFINITY ? 0.f : __expf(sc[k] - mn);
+      ps[row][tq * KPT + k] = pk;
+      psum += pk;
+    }
+    psum += __shfl_xor(psum, 1, 64);
+    psum += __shfl_xor(psum, 2, 64);
+    l = l * corr + psum;
+    m = mn;
+#pragma unroll
+    for (int d = 0; d < DPT; ++d) acc[d] *= corr;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int t = 0; t < KT; ++t) {
+      const float pt = ps[row][t];
+#pragma unroll
+      for (int d = 0; d < DPT; d += 4) {
+        const float4 vv = *(const float4*)&vs[t][tq * DPT + d];
+        acc[d] += pt * vv.x;
+        acc[d + 1] += pt * vv.y;
+        acc[d + 2] += pt * vv.z;
+        acc[d + 3] += pt * vv.w;
+      }
+    }
+  }
+  if (!rvalid) return;
+  const float inv = 1.0f / l;
+  float* dst = p.out + (size_t)(q0 + pq) * p.n_head * HD + (size_t)h * HD + tq * DPT;
+  const float* gate = p.qkv + (size_t)(q0 + pq) * p.ldq + (size_t)h * 2 * HD + HD + tq * DPT;
+#pragma unroll
+  for (int d = 0; d < DPT; ++d) {
+    float o = acc[d] * inv;
+    if (p.gated) o *= sigmoidf_(gate[d]);
+    dst[d] = o;
+  }
+}
+
+int launch_attn_prefill(const AttnPrefillParams& p, hipStream_t s) {
+  TRX_CHECK(p.n_kv >= 1 && p.n_head % p.n_kv == 0 && p.n_head / p.n_kv <= 64 && p.R >= 1 &&
+            p.p0 + p.R <= p.max_ctx, TRX_E_INVALID, "prefill attention: bad geometry");
+  const int rep = p.n_head / p.n_kv, QT = 64 / rep;
+  const dim3 grid(cdiv(p.R, QT), p.n_kv);
+  if (p.hd == 64) hipLaunchKernelGGL((attn_prefill_kernel<64, 32>), grid, dim3(256), 0, s, p);
+  else if (p.hd == 128) hipLaunchKernelGGL((attn_prefill_kernel<128, 32>), grid, dim3(256), 0, s, p);
+  else if (p.hd == 256) hipLaunchKernelGGL((attn_prefill_kernel<256, 16>), grid, dim3(256), 0, s, p);
+  else TRX_CHECK(false, TRX_E_INVALID, "prefill attention: head_dim %d unsupported", p.hd);
+  TRX_LAUNCHED();
+  return TRX_OK;
+}
+
+// Gated DeltaNet over R positions ---------------------------------------------------------------
+
+// Conv + SiLU (+ the L2 norm of q/k heads) of every position: one block per (head-sized channel
+// segment, position). in(rho, c) is the raw projection of chunk row rho, or for rho < 0 the
+// state's row Kc - 1 + rho (oldest first).
+__global__ void dn_conv_rows_kernel(DnRowsParams p) {
+  __shared__ float red[8];
+  const int seg = blockIdx.x, r = blockIdx.y, t = threadIdx.x;
+  const int c = seg * p.hk + t;
+  float acc = 0.f;
+  for (int i = 0; i < p.Kc; ++i) {
+    const int rho = r - (p.Kc - 1) + i;
+    const float x = rho >= 0 ? p.io[(size_t)rho * p.ld_io + c] : p.conv_state[(size_t)(p.Kc - 1 + rho) * p.C + c];
+    acc += p.taps[c * p.Kc + i] * x;
+  }
+  float y = silu(acc);
+  if (c < 2 * p.nq) {
+    const float ss = wave_sum(y * y);
+    if ((t & 63) == 0) red[t >> 6] = ss;
+    __syncthreads();
+    float tot = 0.f;
+    for (int i = 0; i < (blockDim.x + 63) / 64; ++i) tot += red[i];
+    y = y / fmaxf(sqrtf(tot), p.eps);
+  }
+  p.conv_out[(size_t)r * p.C + c] = y;
+}
+
+// The window after the chunk: the last Kc - 1 raw rows (older state rows when R < Kc - 1).
+__global__ void dn_conv_tail_kernel(DnRowsParams p) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= p.C) return;
+  float keep[8];
+  for (int i = 0; i < p.Kc - 1; ++i) {
+    const int rho = p.R - (p.Kc - 1) + i;
+    keep[i] = rho >= 0 ? p.io[(size_t)rho * p.ld_io + c] : p.conv_state[(size_t)(p.Kc - 1 + rho) * p.C + c];
+  }
+  for (int i = 0; i < p.Kc - 1; ++i) p.conv_state[(size_t)i * p.C + c] = keep[i];
+}
+
+// The recurrence of one value head over the chunk, kRB state rows per block: a row's HK columns
+// over HK/4 lanes (a float4 each), row sums by shuffles. The position's k, q, v, beta and alpha
+// are loaded one position ahead. The per-position arithmetic is dn_recur_fixed_kernel's.
+constexpr int kRB = 32;
+template <int HK>
+__global__ __launch_bounds__(256) void dn_scan_kernel(DnRowsParams p) {
+  constexpr int LPR = HK / 4, RPW = 64 / LPR, RPP = 4 * RPW, NIT = kRB / RPP;
+  static_assert(NIT >= 1 && kRB % RPP == 0, "rows per block");
+  const int h = blockIdx.x, rb = blockIdx.y, t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const int sub = lane / LPR, c4 = lane % LPR;
+  const int nk = p.nk, kh = h % nk, hv = p.hv;
+  float4* S = (float4*)(p.S + (size_t)h * hv * HK);
+  float4 sv[NIT];
+  int jr[NIT];
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    jr[it] = rb * kRB + (it * 4 + w) * RPW + sub;
+    sv[it] = S[jr[it] * LPR + c4];
+  }
+  const float Ah = p.A[h], dth = p.dt[h];
+  const float qs = 1.0f / sqrtf((float)HK);
+  auto ld = [&](int r, float4& k4, float4& q4, float* vj, float& bb, float& aa) {
+    const float* cr = p.conv_out + (size_t)r * p.C;
+    k4 = *(const float4*)(cr + p.nq + kh * HK + 4 * c4);
+    q4 = *(const float4*)(cr + kh * HK + 4 * c4);
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) vj[it] = cr[2 * p.nq + h * hv + jr[it]];
+    bb = p.ba[(size_t)r * 2 * p.nv + h];
+    aa = p.ba[(size_t)r * 2 * p.nv + p.nv + h];
+  };
+  float4 k4, q4;
+  float vj[NIT], bb, aa;
+  ld(0, k4, q4, vj, bb, aa);
+  for (int r = 0; r < p.R; ++r) {
+    const float4 ck = k4, cq = q4;
+    float cv[NIT];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) cv[it] = vj[it];
+    const float cb = bb, ca = aa;
+    if (r + 1 < p.R) ld(r + 1, k4, q4, vj, bb, aa);
+    const float a = ca + dth;
+    const float sp = a > 20.f ? a : log1pf(expf(a));
+    const float decay = expf(sp * Ah);
+    const float beta = sigmoidf_(cb);
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      float4 s4 = make_float4(sv[it].x * decay, sv[it].y * decay, sv[it].z * decay, sv[it].w * decay);
+      float dot = (s4.x * ck.x + s4.y * ck.y) + (s4.z * ck.z + s4.w * ck.w);
+#pragma unroll
+      for (int o = LPR >> 1; o >= 1; o >>= 1) dot += __shfl_xor(dot, o, 64);
+      const float delta = (cv[it] - dot) * beta;
+      s4 = make_float4(s4.x + delta * ck.x, s4.y + delta * ck.y, s4.z + delta * ck.z, s4.w + delta * ck.w);
+      sv[it] = s4;
+      float oq = (s4.x * cq.x + s4.y * cq.y) + (s4.z * cq.z + s4.w * cq.w);
+#pragma unroll
+      for (int o = LPR >> 1; o >= 1; o >>= 1) oq += __shfl_xor(oq, o, 64);
+      if (c4 == 0) p.o_raw[(size_t)r * p.nv * hv + (size_t)h * hv + jr[it]] = oq * qs;
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) S[jr[it] * LPR + c4] = sv[it];
+}
+
+// Gated RMSNorm of every (position, value head), into the grouped output order.
+__global__ void dn_gnorm_rows_kernel(DnRowsParams p) {
+  __shared__ float red[16];
+  const int h = blockIdx.x, r = blockIdx.y, t = threadIdx.x, hv = p.hv;
+  const float* o = p.o_raw + (size_t)r * p.nv * hv + (size_t)h * hv;
+  float ss = 0.f;
+  for (int i = t; i < hv; i += blockDim.x) ss += o[i] * o[i];
+  ss = block_sum(ss, red);
+  const float rr = 1.0f / sqrtf(ss / (float)hv + p.eps);
+  const int gpos = (h % p.nk) * (p.nv / p.nk) + h / p.nk;
+  const float* z = p.io + (size_t)r * p.ld_io + p.C + (size_t)h * hv;
+  for (int i = t; i < hv; i += blockDim.x)
+    p.out[(size_t)r * p.nv * hv + (size_t)gpos * hv + i] = o[i] * rr * p.norm_w[i] * silu(z[i]);
+}
+
+int launch_dn_rows(const DnRowsParams& p, hipStream_t s) {
+  TRX_CHECK(p.R >= 1 && p.hk <= 256 && p.C % p.hk == 0 && p.Kc >= 1 && p.Kc <= 9 && p.nv % p.nk == 0 &&
+            (p.hk == 64 || p.hk == 128) && p.hv % kRB == 0 && p.hv <= 1024, TRX_E_INVALID,
+            "prefill DeltaNet: unsupported geometry hk=%d hv=%d Kc=%d", p.hk, p.hv, p.Kc);
+  hipLaunchKernelGGL(dn_conv_rows_kernel, dim3(p.C / p.hk, p.R), dim3(p.hk), 0, s, p);
+  TRX_LAUNCHED();
+  if (p.Kc > 1) {
+    hipLaunchKernelGGL(dn_conv_tail_kernel, dim3(cdiv(p.C, 256)), dim3(256), 0, s, p);
+    TRX_LAUNCHED();
+  }
+  const dim3 sg(p.nv, p.hv / kRB);
+  if (p.hk == 128) hipLaunchKernelGGL(dn_scan_kernel<128>, sg, dim3(256), 0, s, p);
+  else hipLaunchKernelGGL(dn_scan_kernel<64>, sg, dim3(256), 0, s, p);
+  TRX_LAUNCHED();
+  hipLaunchKernelGGL(dn_gnorm_rows_kernel, dim3(p.nv, p.R), dim3(std::min(256, p.hv)), 0, s, p);
+  TRX_LAUNCHED();
+  return TRX_OK;
+}
+
+__global__ void prefill_ctl_kernel(int* ctl_pos, int* cur_tok, const int* fed, int p_last) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) {
+    *ctl_pos = p_last;
+    *cur_tok = fed[p_last];
+  }
+}
+
+int launch_prefill_ctl(int* ctl_pos, int* cur_tok, const int* fed, int p_last, hipStream_t s) {
+  hipLaunchKernelGGL(prefill_ctl_kernel, dim3(1), dim3(64), 0, s, ctl_pos, cur_tok, fed, p_last);
+  TRX_LAUNCHED();
+  return TRX_OK;
+}
+
+}  // namespace trx
+
+using namespace trx;
+
+#define TRX_API extern "C" __attribute__((visibility("default")))
+
+TRX_API int trx_gemm_ternary_f32(const uint8_t* rows, int kind, int M, int K, const float* x, int n,
+                                 const float* norm_w, float eps, float* y, int epilogue, void* workspace,
+                                 trx_stream_t s) {
+  TRX_CHECK(rows && x && y && workspace && n >= 1, TRX_E_INVALID, "trx_gemm_ternary_f32: bad arguments");
+  TRX_CHECK(epilogue == TRX_EPI_STORE || epilogue == TRX_EPI_RESID || epilogue == TRX_EPI_SWIGLU, TRX_E_INVALID,
+            "trx_gemm_ternary_f32: unknown epilogue %d", epilogue);
+  TRX_CHECK(K >= kGroup && K % kGroup == 0 && M >= 1, TRX_E_INVALID, "trx_gemm_ternary_f32: M=%d K=%d", M, K);
+  const int row_bytes = kind == TRX_KIND_Q8 ? kBeat * cdiv(K / 32, 16) + K : row_geom(kind, K).row_bytes;
+  const int code_off = kind == TRX_KIND_Q8 ? kBeat * cdiv(K / 32, 16) : row_geom(kind, K).code_off;
+  _Float16* xh = (_Float16*)workspace;
+  _Float16* xl = xh + (size_t)n * K;
+  PrepParams pp = {};
+  pp.x = x;
+  pp.ldx = K;
+  pp.K = K;
+  pp.R = n;
+  pp.norm_w = norm_w;
+  pp.eps = eps;
+  pp.xh = xh;
+  pp.xl = xl;
+  int rc;
+  if ((rc = launch_prep(pp, (hipStream_t)s))) return rc;
+  GemmParams g = {};
+  g.W = rows;
+  g.w_bytes = (uint32_t)std::min<size_t>((size_t)M * row_bytes + 16, 0xFFFFFFF0u);
+  g.kind = kind;
+  g.M = M;
+  g.K = K;
+  g.row_bytes = row_bytes;
+  g.code_off = code_off;
+  g.xh = xh;
+  g.xl = xl;
+  g.R = n;
+  g.epi = epilogue == TRX_EPI_STORE ? GM_STORE : epilogue == TRX_EPI_RESID ? GM_RESID : GM_SWIGLU;
+  g.y = y;
+  g.ldy = epilogue == TRX_EPI_SWIGLU ? M / 2 : M;
+  return launch_gemm(g, (hipStream_t)s);
+}

@@ -54,7 +54,7 @@ def layer_type_bits(layer_types, n_layer):
 
 
 def make_config(mc, weight_kind, head_kind, head_tied, emb_mode, emb_kind, max_ctx=None, max_new=256,
-                persistent=False, packed_ops=PACK_AUTO):
+                persistent=False, packed_ops=PACK_AUTO, prefill_chunk=0):
     """trx_model_config from a ModelConfig (or a BONS header turned into one)."""
     c = _lib.ModelConfig()
     for name in ("n_layer", "n_embd", "n_head", "n_kv_head", "head_dim", "ffn_dim", "vocab",
@@ -70,6 +70,7 @@ def make_config(mc, weight_kind, head_kind, head_tied, emb_mode, emb_kind, max_c
     c.emb_mode, c.emb_kind, c.max_new = emb_mode, emb_kind, int(max_new)
     c.persistent = int(persistent)
     c.packed_ops = int(packed_ops)
+    c.prefill_chunk = int(prefill_chunk)
     return c
 
 
@@ -102,8 +103,10 @@ class Decoder:
     # Construction ------------------------------------------------------------------------------
     @classmethod
     def from_image(cls, img, max_ctx=None, max_new=256, use_graph=True, persistent=False,
-                   packed_ops=PACK_AUTO):
-        """Load a BONS image (path or BONSReader) into HBM."""
+                   packed_ops=PACK_AUTO, prefill_chunk=0):
+        """Load a BONS image (path or BONSReader) into HBM. prefill_chunk > 0: forward() and
+        generate() run all but the last fed token through the batched prefill, that many
+        positions per weight pass (0: one position per forward, as the firmware's loop)."""
         from .bons import BONSReader
         if isinstance(img, str):
             img = BONSReader(img)
@@ -134,7 +137,7 @@ class Decoder:
             if persistent:
                 raise ValueError("a rotated (Hadamard) image runs one kernel per operation")
         cfg = make_config(mc, weight_kind, head_kind, head_tied, 0, emb_kind, max_ctx, max_new, persistent,
-                          packed_ops)
+                          packed_ops, prefill_chunk)
         if rot is not None:
             block, scale, signs = rot
             cfg.hadamard_block, cfg.hadamard_scale = block, scale
@@ -159,13 +162,13 @@ class Decoder:
 
     @classmethod
     def synthetic(cls, mc, seed=0, weight_kind=L.KIND_TERNARY5, max_ctx=None, max_new=256,
-                  use_graph=True, persistent=False, packed_ops=PACK_AUTO):
+                  use_graph=True, persistent=False, packed_ops=PACK_AUTO, prefill_chunk=0):
         """Fill every tensor on the device from the counter-based generator (same values as
         trixium_amd.synth.hashed_*): ternary token_embd rows (embedded by decoding the row), an
         untied ternary LM head unless the config ties them. A hybrid's DeltaNet beta|alpha Q8
         rows come from the host (seeded int8 values, fp16 scales U(0.01, 0.05))."""
         cfg = make_config(mc, weight_kind, weight_kind, mc.tie_embeddings, 1, weight_kind, max_ctx, max_new,
-                          persistent, packed_ops)
+                          persistent, packed_ops, prefill_chunk)
         d = cls(mc, cfg, use_graph)
         try:
             ranges = np.array([SYNTH_SCALE[0], SYNTH_SCALE[1] - SYNTH_SCALE[0],
@@ -279,11 +282,26 @@ class Decoder:
         g = self.use_graph if use_graph is None else use_graph
         _lib.call("trx_model_step", self._h, int(n_steps), int(bool(g)))
 
+    def prefill(self, n, chunk=0):
+        """Enqueue the batched prefill of the next n fed positions, `chunk` positions per weight
+        pass (0: the config's prefill_chunk, else 1024); they must precede the first position
+        that computes logits. The state afterwards is that of n one-position forwards."""
+        c = int(chunk or self.cfg.prefill_chunk or 1024)
+        _lib.call("trx_model_prefill", self._h, int(n), c)
+
+    def _run_fed(self, n, extra, use_graph):
+        # n fed tokens, then `extra` more positions: all but the last fed one through the batched
+        # prefill when the config asks for it.
+        pre = n - 1 if self.cfg.prefill_chunk > 0 else 0
+        if pre:
+            self.prefill(pre)
+        self.step(n - pre + extra, use_graph)
+
     def forward(self, tokens, use_graph=None):
         """Feed `tokens` after the current position; logits (vocab,) of the last one
         (FloatModel.forward, golden.py:436-460)."""
         n = self.feed(tokens)
-        self.step(n, use_graph)
+        self._run_fed(n, 0, use_graph)
         return self.logits()
 
     def generate(self, tokens, n, use_graph=None):
@@ -294,7 +312,7 @@ class Decoder:
         if n > self.cfg.max_new:
             raise ValueError(f"{n} tokens requested, the output buffer holds {self.cfg.max_new}")
         n_fed = self.feed(tokens)
-        self.step(n_fed + n - 1, use_graph)
+        self._run_fed(n_fed, n - 1, use_graph)
         self.finalize()
         return [int(v) for v in self.outputs()[:n]]
 
