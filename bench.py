@@ -9,8 +9,9 @@ counter-based generator, stored as 5-trit packed rows (2-bit with --kind 2bit).
 
 A step is one decode token: one forward of the whole model at the next position (embedding, 36
 layers, LM head, on-device argmax), replayed from the captured hipGraph. The prompt is prefilled
-one position per forward before the clock starts, then `--warmup` tokens are decoded untimed and
-`--steps` tokens timed (defaults 16 + 240 = 256 decode tokens at positions 2048..2303).
+before the clock starts (the batched prefill: `--prefill-chunk` positions per weight pass, the
+last prompt position as a step), then `--warmup` tokens are decoded untimed and `--steps` tokens
+timed (defaults 16 + 240 = 256 decode tokens at positions 2048..2303).
 
 Besides the JSON contract fields the line carries
   roofline      the dominant kernel (the fused FFN gate|up GEMV with RMSNorm prologue and SwiGLU
@@ -22,6 +23,9 @@ Besides the JSON contract fields the line carries
   cpu_baseline  the float oracle's decode step (the reference's numpy CPU path restated) on a
                 sample of the same shape: one layer and the LM head at context 2048, scaled to
                 36 layers;
+  prefill       time to first token of the prompt through the batched prefill, against the same
+                prompt one position per forward (the firmware's loop), and whether both give the
+                same first token;
   matvec_microbench  the isolated ternary matvec at the Qwen3-1.7B layer shapes, trit5 and 2-bit,
                 over more than 512 MB of distinct matrix copies, at least 1000 matvecs per
                 shape: GB/s against 8 TB/s, with the exact integer group sums checked.
@@ -77,6 +81,10 @@ def parse_args():
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="run a plain device copy of this many bytes, 10 times, and exit (the "
                          "reference kernel that calibrates the FETCH_SIZE/WRITE_SIZE counters)")
+    ap.add_argument("--prefill-chunk", type=int, default=2048,
+                    help="prompt positions per batched prefill forward (0: one position per forward)")
+    ap.add_argument("--no-ttft-compare", action="store_true",
+                    help="skip timing the one-position-per-forward prompt for comparison")
     ap.add_argument("--exact-rows", type=int, default=0, metavar="N",
                     help="time the engine matvec at the 8B gate|up shape on N int8 rows in one "
                          "weight pass (trx_gemv_ternary_exact_rows) against N single-row calls, "
@@ -393,9 +401,45 @@ def main():
     if a.sampling:
         t, p_, r = (float(v) for v in a.sampling.split(","))
         dec.set_sampling(t, p_, r, seed=a.seed + 1)
+    # Time to first token: the prompt's first a.prompt - 1 positions through the batched prefill
+    # (a.prefill_chunk positions per weight pass), then the last prompt position, whose forward
+    # computes the logits and the first generated token. For comparison, the same prompt one
+    # position per forward (the firmware's loop); both give the same first token.
+    prefill = None
+    if a.prefill_chunk > 0:
+        ttft = []
+        for _ in range(2):
+            dec.reset()
+            dec.feed(prompt)
+            dec.synchronize()
+            t0 = time.perf_counter()
+            dec.prefill(a.prompt - 1, a.prefill_chunk)
+            dec.step(1)
+            dec.synchronize()
+            ttft.append(time.perf_counter() - t0)
+        dec.finalize()
+        first = int(dec.outputs()[0])
+        prefill = {"prompt_tokens": a.prompt, "chunk": a.prefill_chunk, "ttft_ms": round(min(ttft) * 1e3, 2),
+                   "prompt_tok_s": round(a.prompt / min(ttft), 1)}
+        if not a.no_ttft_compare:
+            dec.reset()
+            dec.feed(prompt)
+            dec.synchronize()
+            t0 = time.perf_counter()
+            dec.step(a.prompt)
+            dec.synchronize()
+            t1 = time.perf_counter() - t0
+            dec.finalize()
+            prefill.update({"ttft_ms_one_position_per_forward": round(t1 * 1e3, 2),
+                            "speedup": round(t1 / min(ttft), 2),
+                            "first_token_match": int(dec.outputs()[0]) == first})
     dec.reset()
     dec.feed(prompt)
-    dec.step(a.prompt)                           # prefill, one position per forward
+    if a.prefill_chunk > 0:
+        dec.prefill(a.prompt - 1, a.prefill_chunk)
+        dec.step(1)
+    else:
+        dec.step(a.prompt)                       # one position per forward
     dec.synchronize()
     dec.step(a.warmup)
     dec.synchronize()
@@ -440,7 +484,7 @@ def main():
                        "packed_ops": dec.packed_ops},
             "token_roofline": {"bytes_per_token": int(tok_bytes), "tok_s": round(HBM_PEAK_GBS * 1e9 / tok_bytes, 1),
                                "frac": round(tok_s / (HBM_PEAK_GBS * 1e9 / tok_bytes), 4)},
-            "roofline": None, "cpu_baseline": None}), flush=True)
+            "roofline": None, "cpu_baseline": None, "prefill": prefill}), flush=True)
         dec.close()
         return
 
@@ -483,6 +527,7 @@ def main():
         "token_roofline": {"bytes_per_token": int(tok_bytes), "tok_s": round(roof_tok_s, 1),
                            "frac": round(tok_s / roof_tok_s, 4)},
         "cpu_baseline": None,
+        "prefill": prefill,
     }
     dec.close()
     if not a.no_microbench:
