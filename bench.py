@@ -85,6 +85,12 @@ def parse_args():
                     help="prompt positions per batched prefill forward (0: one position per forward)")
     ap.add_argument("--no-ttft-compare", action="store_true",
                     help="skip timing the one-position-per-forward prompt for comparison")
+    ap.add_argument("--only-prefill", action="store_true",
+                    help="time only the batched prefill of the prompt (twice) and print its record "
+                         "(for kernel traces)")
+    ap.add_argument("--trace-decode", type=int, default=0, metavar="N",
+                    help="prefill the prompt, then run N decode positions and exit (for kernel traces "
+                         "and hardware counters; with --no-graph every kernel launches eagerly)")
     ap.add_argument("--exact-rows", type=int, default=0, metavar="N",
                     help="time the engine matvec at the 8B gate|up shape on N int8 rows in one "
                          "weight pass (trx_gemv_ternary_exact_rows) against N single-row calls, "
@@ -389,6 +395,27 @@ def main():
         us, algo, n_launch, _ = time_dominant_kernel(dec, mc, a.kernel_reps)
         print(json.dumps({"kernel_us": round(us, 3), "bytes_per_launch": algo, "launches": n_launch,
                           "achieved_GBs": round(algo / (us * 1e-6) / 1e9, 1)}), flush=True)
+        dec.close()
+        return
+    if a.only_prefill or a.trace_decode:
+        dec = Decoder.synthetic(mc, a.seed, weight_kind=kind, max_ctx=mc.max_ctx, max_new=a.trace_decode + 8,
+                                use_graph=not a.no_graph, packed_ops=a.packed_ops)
+        prompt = np.random.default_rng(a.seed).integers(0, mc.vocab, a.prompt).astype(np.int32)
+        chunk = a.prefill_chunk or 2048
+        for rep in range(2 if a.only_prefill else 1):
+            dec.reset()
+            dec.feed(prompt)
+            dec.synchronize()
+            t0 = time.perf_counter()
+            dec.prefill(a.prompt - 1, chunk)
+            dec.step(1)
+            dec.synchronize()
+            print(json.dumps({"prefill_rep": rep, "prompt_tokens": a.prompt, "chunk": chunk,
+                              "ttft_ms": round((time.perf_counter() - t0) * 1e3, 2)}), flush=True)
+        if a.trace_decode:
+            dec.step(a.trace_decode)
+            dec.synchronize()
+            print(json.dumps({"decode_positions": a.trace_decode}), flush=True)
         dec.close()
         return
     n_dec = a.warmup + a.steps
