@@ -157,8 +157,9 @@ def matvec_microbench(reps=1000, rotate_bytes=512 << 20):
     6144x2048, 2048x6144), trit5 and 2-bit rows, fp16 group scales U(0.01, 0.05), P(0) = 0.4:
     y = W x with fp32 x ~ N(0, 1), batch 1. The packed GEMV runs over distinct copies of the
     matrix laid out back to back (at least `rotate_bytes` of them, more than the 256 MB Infinity
-    Cache, so every launch streams from HBM), many matvecs per dispatch
-    (trx_gemv_packed_batched_f32), at least `reps` matvecs timed with HIP events. Also timed:
+    Cache, so every launch streams from HBM), one dispatch of at least `reps` matvecs that cycles
+    over the copies, each with its own x (trx_gemv_packed_batched_f32), two dispatches timed with
+    HIP events. Also timed:
     one matvec per launch (the decoder's own launch, latency bound at these sizes), and the
     engine's exact group sums on int8 x checked bit for bit against integer numpy."""
     import ctypes
@@ -200,29 +201,32 @@ def matvec_microbench(reps=1000, rotate_bytes=512 << 20):
             _lib.call("trx_pack_ternary", rows.ptr, kind, M, K, 0, packed.ptr, None)
             for i in range(1, n):
                 _lib.call("trx_memcpy_d2d", packed.ptr + i * stride, packed.ptr, pb, None)
-            xs = r.standard_normal((n, K)).astype(np.float32)
+            # One dispatch of at least `reps` matvecs cycling over the n copies (each copy is read
+            # again only after every other one: more than 512 MB apart), each with its own x.
+            nm = n * -(-reps // n)
+            xs = r.standard_normal((nm, K)).astype(np.float32)
             xb = _lib.DeviceBuffer.from_array(xs)
-            yb = _lib.DeviceBuffer(4 * n * M)
+            yb = _lib.DeviceBuffer(4 * nm * M)
             bw = ctypes.c_size_t()
-            _lib.call("trx_pack_batched_geometry", kind, M, K, n, ctypes.byref(bw))
+            _lib.call("trx_pack_batched_geometry", kind, M, K, nm, ctypes.byref(bw))
             part = _lib.DeviceBuffer(bw.value)
             _lib.synchronize()
 
             def batched():
-                _lib.call("trx_gemv_packed_batched_f32", packed.ptr, stride, n, kind, M, K, xb.ptr, K, yb.ptr, M,
+                _lib.call("trx_gemv_packed_batched_f32", packed.ptr, stride, nm, n, kind, M, K, xb.ptr, K, yb.ptr, M,
                           part.ptr, None)
-            n_launch = max(1, -(-reps // n))
+            n_launch = 2
             us = timed(batched, n_launch)
-            # Correctness of the first and the last matrix of the dispatch (float64, 2e-6 of sum |w x|).
-            y = yb.download(np.float32, n * M).reshape(n, M)
+            # Correctness of the first and the last matvec of the dispatch (float64, 2e-6 of sum |w x|).
+            y = yb.download(np.float32, nm * M).reshape(nm, M)
             err = 0.0
-            for i in (0, n - 1):
+            for i in (0, nm - 1):
                 ref = W64 @ xs[i].astype(np.float64)
                 mag = np.abs(W64) @ np.abs(xs[i].astype(np.float64))
                 err = max(err, float(np.max(np.abs(y[i] - ref) / mag)))
             row_b = L.row_bytes(K, kind)
             algo = M * row_b + 4 * K + 4 * M            # weight rows (scales + codes), fp32 x and y
-            count = n * n_launch
+            count = nm * n_launch
             gbs = algo * count / (us * 1e-6) / 1e9
             # One matvec per launch (the decoder's form), over the copies in turn.
             work = _lib.DeviceBuffer(wb)

@@ -156,14 +156,15 @@ int trx_gemv_packed_f32_noalloc(const uint8_t* packed, int kind, int M, int K, c
 
 /* Many independent packed GEMVs in one dispatch (no counterpart in the reference, whose engine
  * runs one matvec op per submit, firmware/engine.c:111-238; for callers with many matrices and
- * vectors, such as the isolated matvec benchmark): y_i = W_i x_i, i < n_mat, matrix i's packed
- * copy (trx_pack_ternary) at packed + i * mat_stride (a multiple of 256, at least
- * trx_pack_geometry's packed bytes), x_i at x + i * x_stride (x 16-byte aligned, x_stride a
- * multiple of 4 and >= K), y_i at y + i * y_stride. M <= 16384. `workspace` holds
- * trx_pack_batched_geometry's bytes of split-K partial sums (no zeroing needed). */
+ * vectors, such as the isolated matvec benchmark): y_i = W_i x_i, i < n_mat (<= 65535), matrix
+ * i's packed copy (trx_pack_ternary) at packed + (i % n_copies) * mat_stride (a multiple of 256,
+ * at least trx_pack_geometry's packed bytes; 1 <= n_copies <= n_mat), x_i at x + i * x_stride
+ * (x 16-byte aligned, x_stride a multiple of 4 and >= K), y_i at y + i * y_stride. M <= 16384.
+ * `workspace` holds trx_pack_batched_geometry's bytes of split-K partial sums (no zeroing
+ * needed). */
 int trx_pack_batched_geometry(int kind, int M, int K, int n_mat, size_t* workspace_bytes);
-int trx_gemv_packed_batched_f32(const uint8_t* packed, size_t mat_stride, int n_mat, int kind, int M,
-                                int K, const float* x, int x_stride, float* y, int y_stride,
+int trx_gemv_packed_batched_f32(const uint8_t* packed, size_t mat_stride, int n_mat, int n_copies, int kind,
+                                int M, int K, const float* x, int x_stride, float* y, int y_stride,
                                 void* workspace, trx_stream_t s);
 
 /* Split-K partial sums handed from one packed GEMV to the next, as the decoder chains its

@@ -79,7 +79,7 @@ SIGNATURES = {
     "trx_gemv_packed_f32_noalloc": [_vp, _i, _i, _i, _vp, _vp, _f, _vp, _i, _vp, _vp],
     "trx_pack_partials_geometry": [_i, _i, _i, _ip, _ip, _ip],
     "trx_pack_batched_geometry": [_i, _i, _i, _i, ctypes.POINTER(_sz)],
-    "trx_gemv_packed_batched_f32": [_vp, _sz, _i, _i, _i, _i, _vp, _i, _vp, _i, _vp, _vp],
+    "trx_gemv_packed_batched_f32": [_vp, _sz, _i, _i, _i, _i, _i, _vp, _i, _vp, _i, _vp, _vp],
     "trx_gemv_packed_parts_f32": [_vp, _i, _i, _i, _vp, _vp, _f, _vp, _i, _vp, _vp, _vp, _vp],
     "trx_gemv_set_variant": [_i],
     "trx_model_create": [_mcp, _fp, ctypes.POINTER(_vp)],

@@ -160,7 +160,7 @@ def batched_matvec(mats, xs, kind=L.KIND_TERNARY5):
     work = DeviceBuffer(wb.value)
     xb = DeviceBuffer.from_array(np.ascontiguousarray(np.asarray(xs, dtype=np.float32).reshape(n, K)))
     yb = DeviceBuffer(4 * n * M)
-    call("trx_gemv_packed_batched_f32", packed.ptr, stride, n, kind, M, K, xb.ptr, K, yb.ptr, M, work.ptr, None)
+    call("trx_gemv_packed_batched_f32", packed.ptr, stride, n, n, kind, M, K, xb.ptr, K, yb.ptr, M, work.ptr, None)
     synchronize()
     return yb.download(np.float32, n * M).reshape(n, M)
 

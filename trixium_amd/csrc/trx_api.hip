@@ -224,11 +224,11 @@ TRX_API int trx_pack_batched_geometry(int kind, int M, int K, int n_mat, size_t*
   return tgemv_batched_geom(kind, M, K, n_mat, g, workspace_bytes);
 }
 
-TRX_API int trx_gemv_packed_batched_f32(const uint8_t* packed, size_t mat_stride, int n_mat, int kind, int M,
-                                        int K, const float* x, int x_stride, float* y, int y_stride,
+TRX_API int trx_gemv_packed_batched_f32(const uint8_t* packed, size_t mat_stride, int n_mat, int n_copies, int kind,
+                                        int M, int K, const float* x, int x_stride, float* y, int y_stride,
                                         void* workspace, trx_stream_t s) {
-  return tgemv_f32_batched(packed, mat_stride, n_mat, kind, M, K, x, x_stride, y, y_stride, (float*)workspace,
-                           (hipStream_t)s);
+  return tgemv_f32_batched(packed, mat_stride, n_mat, n_copies, kind, M, K, x, x_stride, y, y_stride,
+                           (float*)workspace, (hipStream_t)s);
 }
 
 TRX_API int trx_gemv_packed_f32(const uint8_t* packed, int kind, int M, int K, const float* x,

@@ -123,12 +123,12 @@ struct RotSrc {
 };
 
 // Many independent GEMVs in one launch: y_i = W_i x_i for i < n_mat, matrix i's packed copy at
-// packed + i * mat_stride, x_i at x + i * x_stride, y_i at y + i * y_stride. One block per (slice,
-// matrix) streams every row of its slice (one table per slice column); `part` holds
-// tgemv_batched_geom's part_bytes of split-K partial sums, reduced by a second launch.
+// packed + (i % n_copies) * mat_stride, x_i at x + i * x_stride, y_i at y + i * y_stride. One
+// block per (slice, matrix) streams every row of its slice (one table per slice column); `part`
+// holds tgemv_batched_geom's part_bytes of split-K partial sums, reduced by a second launch.
 int tgemv_batched_geom(int kind, int M, int K, int n_mat, PackGeom& g, size_t* part_bytes);
-int tgemv_f32_batched(const uint8_t* packed, size_t mat_stride, int n_mat, int kind, int M, int K, const float* x,
-                      int x_stride, float* y, int y_stride, float* part, hipStream_t s);
+int tgemv_f32_batched(const uint8_t* packed, size_t mat_stride, int n_mat, int n_copies, int kind, int M, int K,
+                      const float* x, int x_stride, float* y, int y_stride, float* part, hipStream_t s);
 
 int tgemv_f32(const uint8_t* packed, int kind, int M, int K, const float* x, const float* norm_w,
               float eps, float* y, int epi, const float* resid, unsigned long long* amax_slot,

@@ -266,6 +266,7 @@ struct TgParams {
   // part + s * part_sstride + i * part_mstride. One matrix: 0, 0, rows_p, 0.
   uint32_t mat_bytes;
   int x_stride, part_sstride, part_mstride;
+  int mat_copies;          // > 0: matrix i reads the packed copy i % mat_copies
 };
 
 template <bool T5>
@@ -385,8 +386,9 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   // 2. The first NB - 1 items of this lane (they do not depend on x).
   const int rg = lane >> 4, l16 = lane & 15, half = l16 >> 3;
   const int dw = tg_lane_dword(T5, l16), msk = tg_lane_mask(l16);
-  const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.codes + (size_t)mi * p.mat_bytes, p.code_bytes);
-  const __amdgpu_buffer_rsrc_t rsc = make_rsrc(p.scales + (size_t)mi * p.mat_bytes, p.scale_bytes);
+  const size_t mcopy = (size_t)(p.mat_copies > 0 ? mi % p.mat_copies : mi);
+  const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.codes + mcopy * p.mat_bytes, p.code_bytes);
+  const __amdgpu_buffer_rsrc_t rsc = make_rsrc(p.scales + mcopy * p.mat_bytes, p.scale_bytes);
   // Item n of this lane is quad quad0 + n * qstep. The lane's offsets stay in fixed VGPRs and
   // the item's step goes in the scalar offset, so no VGPR that an in-flight access reads is
   // rewritten (that would cost a vmcnt wait per item). Only the VGPR offset is relied on for the
@@ -932,14 +934,15 @@ int tgemv_batched_geom(int kind, int M, int K, int n_mat, PackGeom& g, size_t* p
   return TRX_OK;
 }
 
-int tgemv_f32_batched(const uint8_t* packed, size_t mat_stride, int n_mat, int kind, int M, int K, const float* x,
-                      int x_stride, float* y, int y_stride, float* part, hipStream_t s) {
+int tgemv_f32_batched(const uint8_t* packed, size_t mat_stride, int n_mat, int n_copies, int kind, int M, int K,
+                      const float* x, int x_stride, float* y, int y_stride, float* part, hipStream_t s) {
   PackGeom g;
   size_t pb = 0;
   int rc = tgemv_batched_geom(kind, M, K, n_mat, g, &pb);
   if (rc) return rc;
-  TRX_CHECK(packed && x && y && part, TRX_E_INVALID, "batched GEMV: null argument");
-  TRX_CHECK(mat_stride % 256 == 0 && (n_mat == 1 || mat_stride >= g.bytes) && mat_stride < (1ull << 32),
+  TRX_CHECK(packed && x && y && part && n_copies >= 1 && n_copies <= n_mat, TRX_E_INVALID,
+            "batched GEMV: null argument or %d copies for %d matrices", n_copies, n_mat);
+  TRX_CHECK(mat_stride % 256 == 0 && (n_copies == 1 || mat_stride >= g.bytes) && mat_stride < (1ull << 32),
             TRX_E_INVALID, "batched GEMV: matrix stride %zu (a multiple of 256, at least %zu bytes)", mat_stride, g.bytes);
   TRX_CHECK(x_stride >= K && y_stride >= M && ((uintptr_t)x & 15) == 0 && x_stride % 4 == 0, TRX_E_INVALID,
             "batched GEMV: x stride %d, y stride %d (x 16-byte aligned)", x_stride, y_stride);
@@ -968,6 +971,7 @@ int tgemv_f32_batched(const uint8_t* packed, size_t mat_stride, int n_mat, int k
   p.x_stride = x_stride;
   p.part_sstride = n_mat * g.rows_p;
   p.part_mstride = g.rows_p;
+  p.mat_copies = n_copies;
   const void* fn = kind == TRX_KIND_TERNARY5 ? tg_fn<true>() : tg_fn<false>();
   void* args[] = {(void*)&p};
   TRX_HIP(hipLaunchKernel(fn, dim3(g.S, n_mat), dim3(kTgThreads), args, 0, s));
