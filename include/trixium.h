@@ -242,8 +242,12 @@ typedef struct {
   int weight_kind;             /* kind of every layer matrix: TRX_KIND_TERNARY5 or _TERNARY */
   int head_kind;               /* untied LM head: a ternary kind or TRX_KIND_F16 */
   int head_tied;               /* the LM head is the ternary token embedding */
-  int emb_mode;                /* 0: int16 BFP lookup table; 1: ternary token_embd rows */
-  int emb_kind;                /* kind of token_embd rows (emb_mode 1 or a tied head) */
+  int emb_mode;                /* 0: int16 BFP lookup table; 1: ternary token_embd rows (the
+                                  table's integer rule evaluated on the row); 2: rotated
+                                  ternary token_embd rows restored to the plain basis in
+                                  integers (model/bons.py:262-295 restored_row_exact; needs the
+                                  n_embd width among the rotated widths) */
+  int emb_kind;                /* kind of token_embd rows (emb_mode 1 or 2, or a tied head) */
   int max_new;                 /* capacity of the generated-token buffer */
   int persistent;              /* 1: each position runs as one persistent kernel (reserved) */
   int packed_ops;              /* projections run by the packed GEMV (trx_gemv_packed_f32) over

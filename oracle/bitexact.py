@@ -112,3 +112,34 @@ def quantize_f_pow2(x):
     e8 = int(np.frexp(np.float32(amax))[1]) - 7
     q = lroundf(x * np.float32(np.exp2(-e8)))
     return np.clip(q, -127, 127).astype(np.int8), e8
+
+
+def restored_row_exact(scales_f16, codes, signs, hblock):
+    """A rotated embedding row restored to the plain basis in integers (model/bons.py:262-295,
+    the firmware's embed_row_restore for images without the int16 table):
+      v = (code - 1) * m11 aligned to the row's smallest fp16 exponent (int64);
+      y = s * (H v) per block of hblock columns (natural-order Walsh-Hadamard butterflies);
+      the absmax mantissa normalised into [2^14, 2^15) by a round-half-to-even right shift (or a
+      left shift), clipped to +-32767; exponent = e16min - floor(log2(hblock) / 2) + shift.
+    -> (int16 row, int exponent)."""
+    m11, e16 = fp16_decompose(np.asarray(scales_f16).reshape(-1))
+    e16min = int(e16.min())
+    q = np.asarray(codes).astype(np.int64).reshape(len(m11), -1) - 1
+    v = (q * (m11.astype(np.int64) << (e16 - e16min).astype(np.int64))[:, None]).reshape(-1)
+    n = v.size
+    h = 1
+    while h < hblock:
+        v = v.reshape(n // (2 * h), 2, h)
+        v = np.stack([v[:, 0] + v[:, 1], v[:, 0] - v[:, 1]], axis=1).reshape(-1)
+        h *= 2
+    y = v * np.asarray(signs).astype(np.int64)
+    fexp = -((int(hblock).bit_length() - 1) // 2)
+    amax = int(np.abs(y).max())
+    if amax == 0:
+        return np.zeros(n, dtype=np.int16), 0
+    r = amax.bit_length() - 15
+    if r > 0:
+        mant = np.where(y < 0, -rne_shift(np.abs(y), r), rne_shift(np.abs(y), r))
+    else:
+        mant = y << -r
+    return np.clip(mant, -32767, 32767).astype(np.int16), e16min + fexp + r

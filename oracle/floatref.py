@@ -58,9 +58,22 @@ class FloatRef:
         self.out_norm = self._f32(L.ROLE_OUT_NORM, 0)
         self.head_role = L.ROLE_LM_HEAD if img.find(L.ROLE_LM_HEAD, 0) else L.ROLE_TOK_EMB
         e16 = img.find(L.ROLE_TOK_EMB16, 0)
-        _, self.emb_mant = img.entry_tensor(e16)
-        _, ex = img.entry_tensor(img.find(L.ROLE_TOK_EMB16_EXP, 0))
-        self.emb_exp = np.asarray(ex).reshape(-1)
+        if e16 is not None:
+            _, self.emb_mant = img.entry_tensor(e16)
+            _, ex = img.entry_tensor(img.find(L.ROLE_TOK_EMB16_EXP, 0))
+            self.emb_exp = np.asarray(ex).reshape(-1)
+            self.emb_restore = None
+        else:
+            # No int16 table: each row of the rotated token_embd is restored to the plain basis
+            # in integers (fastref.py:173-177, bons.py:262-295); the signs are row 0 of each
+            # rotation block of the n_embd width (R[0] = +1).
+            assert self.hb, "an image without the int16 table must be rotated"
+            wi = self.hwidths.index(self.n_embd)
+            signs = np.concatenate([
+                np.asarray(img.entry_tensor(img.find(L.ROLE_HADAMARD, L.hadamard_layer(wi, b)))[1])[0]
+                .astype(np.int64) - 1 for b in range(self.n_embd // self.hb)])
+            sc, codes = img.entry_tensor(img.find(L.ROLE_TOK_EMB, 0))
+            self.emb_restore = (np.asarray(sc), np.asarray(codes), signs)
         self.reset()
 
     # Tensors (fastref.py:86-125) -----------------------------------------------------------
@@ -133,6 +146,11 @@ class FloatRef:
         self.dn_state = {l: np.zeros((self.nv, self.hv, self.hk), f32) for l in range(self.n_layer) if self.dn[l]}
 
     def embed(self, tok):
+        if getattr(self, "emb_restore", None) is not None:
+            from .bitexact import restored_row_exact
+            sc, codes, signs = self.emb_restore
+            m, e = restored_row_exact(sc[tok], codes[tok], signs, self.hb)
+            return (m.astype(f32) * f32(np.exp2(e))).astype(f32)
         return (self.emb_mant[tok].astype(f32) * f32(np.exp2(int(self.emb_exp[tok])))).astype(f32)
 
     def attention(self, l, hn, pos):

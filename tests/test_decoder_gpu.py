@@ -401,3 +401,37 @@ def test_score_hidden_and_head_match_fastref(tiny_images, name):
     assert proj.shape == (2, dec.vocab)
     assert _rel_err(proj[0], lg) <= 1e-4
     assert _rel_err(dec.logits(dec.hidden()[None])[0], lg) <= 1e-4
+
+
+@pytest.mark.parametrize("case", ["qwen3_rot128", "qwen35_rot256"])
+def test_rotated_image_without_the_int16_table(tmp_path, case):
+    """A rotated image converted without the int16 embedding table (`--no-emb16`): every token's
+    row is restored to the plain basis in integers on the GPU (the firmware's embed_row_restore,
+    model/bons.py:262-295). Logits at every prompt position within 2e-3 of the oracle's (which
+    restores the rows with its own restatement), within 1e-2 of the same model with the table
+    (whose rows differ by at most one LSB), the same tokens; eager, graph and the batched prefill
+    agree."""
+    import synth_gguf
+    from trixium_amd import convert
+    c = next(x for x in synth_gguf.ROT_CASES if x["id"] == case)
+    g, p, p16 = str(tmp_path / "m.gguf"), str(tmp_path / "m.bons"), str(tmp_path / "m16.bons")
+    synth_gguf.build(g, c["cfg"], c["seed"], c["arch"], hadamard=c["hadamard"])
+    convert.convert(g, 1, p, trit5=c["trit5"], emb16=False, log=lambda *a: None)
+    convert.convert(g, 1, p16, trit5=c["trit5"], log=lambda *a: None)
+    img = bons.BONSReader(p)
+    assert img.find(L.ROLE_TOK_EMB16, 0) is None
+    prompt = synth.random_prompt(c["cfg"], 8, c["seed"])
+    dec = _decoder(p)
+    assert dec.cfg.emb_mode == 2
+    ref = FloatRef(img, kv_fp16=True)
+    d16 = _decoder(p16)
+    got = [dec.forward(prompt[:1])] + [dec.forward([t]) for t in prompt[1:]]
+    want = [ref.forward(prompt[:1])] + [ref.step(t) for t in prompt[1:]]
+    w16 = [d16.forward(prompt[:1])] + [d16.forward([t]) for t in prompt[1:]]
+    for gl, o, t16 in zip(got, want, w16):
+        assert _rel_err(gl, o) <= 2e-3
+        assert _rel_err(gl, t16) <= 1e-2
+    dec.reset()
+    toks = dec.generate(prompt, 6)
+    assert toks == _decoder(p, use_graph=False).generate(prompt, 6)
+    assert toks == _decoder(p, prefill_chunk=3).generate(prompt, 6)

@@ -274,3 +274,36 @@ def test_quantizer_and_engine_projection_match_the_reference():
         x8, e8 = bx.quantize_f_pow2(x)
         y = bx.matvec_ternary(scales, codes, x8, B, R).astype(np.int32).astype(np.float32) * np.float32(2.0 ** (e8 + R - B))
         assert np.array_equal(y, z[f"p/{name}/y"]), name
+
+
+def test_restored_row_exact_pinned():
+    """The integer restore of a rotated embedding row (oracle restatement of model/bons.py:262-295)
+    against an explicit Sylvester-matrix product in int64 (the value to within half an LSB of the
+    result, so the butterfly order, the signs, the alignment to the smallest exponent and the
+    normalisation are all fixed), and against the float restore that writes the int16 table rows
+    (trixium_amd/hadamard.py:restored_bfp_rows, whose tables are byte-identical to the reference
+    converter's) within one LSB; a zero row gives zeros and exponent 0."""
+    from oracle import bitexact as ob
+    from trixium_amd import hadamard as H
+    r = np.random.default_rng(1)
+    for hb, E in ((64, 256), (128, 512), (256, 1024), (1024, 2048)):
+        i = np.arange(hb)
+        Hm = np.where(np.bitwise_count((i[:, None] & i[None, :]).astype(np.uint64)) % 2 == 1, -1, 1).astype(np.int64)
+        for t in range(6):
+            codes = r.integers(0, 3, E).astype(np.uint8)
+            sc = (r.uniform(0.001, 0.06, E // 128) * (2.0 ** r.integers(-6, 3, E // 128))).astype(np.float16)
+            signs = np.where(r.random(E) < 0.5, -1, 1)
+            m, e = ob.restored_row_exact(sc, codes, signs, hb)
+            m11, e16 = ob.fp16_decompose(sc)
+            emin = e16.min()
+            v = ((codes.astype(np.int64).reshape(-1, 128) - 1) * (m11 * (2 ** (e16 - emin)))[:, None]).reshape(-1)
+            y = np.concatenate([Hm @ v[b:b + hb] for b in range(0, E, hb)]) * signs
+            want = y.astype(np.float64) * 2.0 ** (emin - (hb.bit_length() - 1) // 2)
+            got = m.astype(np.float64) * 2.0 ** e
+            assert 2 ** 14 <= np.abs(m.astype(np.int64)).max() <= 32767        # absmax in [2^14, 2^15)
+            assert np.all(np.abs(got - want) <= 2.0 ** e * 0.5), (hb, t)
+            mf, ef = H.restored_bfp_rows(sc[None], codes[None], signs, hb)
+            gf = mf[0].astype(np.float64) * 2.0 ** ef[0]
+            assert np.all(np.abs(gf - got) <= 2.0 ** max(e, int(ef[0])) * 1.0001), (hb, t)
+    m, e = ob.restored_row_exact(np.full(2, 0.5, np.float16), np.ones(256, np.uint8), np.ones(256, np.int64), 64)
+    assert e == 0 and not m.any()

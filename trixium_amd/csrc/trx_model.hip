@@ -177,7 +177,7 @@ static void plan_arena(Model& m, size_t& cur) {
     plan_tensor(m, cur, TRX_ROLE_TOK_EMB16, 0, TRX_KIND_NORM16, c.vocab, E);
     plan_tensor(m, cur, TRX_ROLE_TOK_EMB16_EXP, 0, TRX_KIND_F32, 1, c.vocab);  // int32 exponents
   }
-  if (c.emb_mode == 1 || c.head_tied) plan_tensor(m, cur, TRX_ROLE_TOK_EMB, 0, c.emb_kind, c.vocab, E);
+  if (c.emb_mode != 0 || c.head_tied) plan_tensor(m, cur, TRX_ROLE_TOK_EMB, 0, c.emb_kind, c.vocab, E);
   if (!c.head_tied) plan_tensor(m, cur, TRX_ROLE_LM_HEAD, 0, c.head_kind, c.vocab, E);
   if (c.hadamard_block)
     for (int i = 0; i < 4; ++i)
@@ -402,9 +402,15 @@ static int run_step(Model& m, hipStream_t s) {
   int rc;
   // Embedding of this position's token.
   EmbedParams ep = {};
-  ep.mode = c.emb_mode == 0 ? EMBED_TABLE : EMBED_TERNARY;
+  ep.mode = c.emb_mode == 0 ? EMBED_TABLE : c.emb_mode == 1 ? EMBED_TERNARY : EMBED_RESTORE;
   ep.n_embd = E;
   ep.vocab = c.vocab;
+  if (c.emb_mode == 2) {
+    int wi = 0;
+    while (wi < 4 && c.hadamard_widths[wi] != E) ++wi;
+    ep.signs = PF(m, TRX_ROLE_HADAMARD, wi);
+    ep.hblock = c.hadamard_block;
+  }
   if (c.emb_mode == 0) {
     ep.mant = (const int16_t*)P(m, TRX_ROLE_TOK_EMB16, 0);
     ep.exps = (const int32_t*)P(m, TRX_ROLE_TOK_EMB16_EXP, 0);
@@ -730,9 +736,15 @@ static int run_prefill(Model& m, int p0, int R, hipStream_t s) {
   const int qrows = c.n_head * hd * (c.attn_gated ? 2 : 1), kvrows = c.n_kv_head * hd;
   int rc;
   EmbedParams ep = {};
-  ep.mode = c.emb_mode == 0 ? EMBED_TABLE : EMBED_TERNARY;
+  ep.mode = c.emb_mode == 0 ? EMBED_TABLE : c.emb_mode == 1 ? EMBED_TERNARY : EMBED_RESTORE;
   ep.n_embd = E;
   ep.vocab = c.vocab;
+  if (c.emb_mode == 2) {
+    int wi = 0;
+    while (wi < 4 && c.hadamard_widths[wi] != E) ++wi;
+    ep.signs = PF(m, TRX_ROLE_HADAMARD, wi);
+    ep.hblock = c.hadamard_block;
+  }
   if (c.emb_mode == 0) {
     ep.mant = (const int16_t*)P(m, TRX_ROLE_TOK_EMB16, 0);
     ep.exps = (const int32_t*)P(m, TRX_ROLE_TOK_EMB16_EXP, 0);
@@ -853,6 +865,13 @@ TRX_API int trx_model_create(const trx_model_config* cfg, const float* rope_freq
   TRX_CHECK(c.weight_kind == TRX_KIND_TERNARY || c.weight_kind == TRX_KIND_TERNARY5, TRX_E_INVALID,
             "trx_model_create: weight_kind must be ternary");
   TRX_CHECK(c.persistent == 0, TRX_E_INVALID, "trx_model_create: persistent %d is not supported", c.persistent);
+  TRX_CHECK(c.emb_mode >= 0 && c.emb_mode <= 2, TRX_E_INVALID, "trx_model_create: emb_mode %d", c.emb_mode);
+  if (c.emb_mode == 2) {
+    bool has = false;
+    for (int i = 0; i < 4; ++i) has = has || (c.hadamard_block && c.hadamard_widths[i] == c.n_embd);
+    TRX_CHECK(has && c.n_embd <= 8192 && (c.emb_kind == TRX_KIND_TERNARY || c.emb_kind == TRX_KIND_TERNARY5),
+              TRX_E_INVALID, "trx_model_create: the embedding restore needs a rotated n_embd width (<= 8192) and ternary rows");
+  }
   if (c.hadamard_block) {
     const int B = c.hadamard_block;
     TRX_CHECK(B >= 64 && B <= 1024 && (B & (B - 1)) == 0 && c.hadamard_scale > 0.f, TRX_E_INVALID,

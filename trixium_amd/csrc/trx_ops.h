@@ -5,7 +5,7 @@
 
 namespace trx {
 
-enum { EMBED_TABLE = 0, EMBED_TERNARY = 1 };
+enum { EMBED_TABLE = 0, EMBED_TERNARY = 1, EMBED_RESTORE = 2 };
 
 struct EmbedParams {
   int mode;
@@ -22,6 +22,8 @@ struct EmbedParams {
   int max_out;
   int* cur_tok;            // the token embedded this step
   float* x;                // [n_embd]
+  const float* signs;      // restore mode: the n_embd width's rotation signs (+-1)
+  int hblock;              // restore mode: the rotation block
 };
 
 struct AttnParams {

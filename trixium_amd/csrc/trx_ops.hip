@@ -37,6 +37,18 @@ __device__ __forceinline__ int wave_min_i(int v) {
   return v;
 }
 
+// Restore mode (model/bons.py:262-295 restored_row_exact, the firmware's embed_row_restore):
+// the rotated ternary row in integers, v = (code - 1) * m11 << (e16 - e16min); the natural-order
+// Walsh-Hadamard butterflies per block of hblock columns (int64 in LDS); y = sign * v; the absmax
+// normalised into [2^14, 2^15) with a round-half-even right shift; exponent e16min - floor(log2
+// hblock / 2) + shift.
+constexpr int kRestoreMax = 8192;
+
+__device__ __forceinline__ long long rne_shift_ll(long long mag, int r) {
+  const long long q = mag >> r, rem = mag & ((1ll << r) - 1), half = 1ll << (r - 1);
+  return q + ((rem > half || (rem == half && (q & 1))) ? 1 : 0);
+}
+
 // The embedding of token `tok` into x (n_embd floats); a whole block of kEmbedThreads.
 __device__ void embed_token(const EmbedParams& p, int tok, float* x) {
   __shared__ int s_red[kEmbedThreads / 64];
@@ -108,6 +120,53 @@ __device__ void embed_token(const EmbedParams& p, int tok, float* x) {
   __syncthreads();
   amax = s_lred[0];
   for (int i = 1; i < kEmbedThreads / 64; ++i) amax = s_lred[i] > amax ? s_lred[i] : amax;
+  if (p.mode == EMBED_RESTORE) {
+    __shared__ long long s_v[kRestoreMax];
+    for (int c = tid; c < p.n_embd; c += kEmbedThreads) {
+      int m11, e16;
+      fp16_split(sc[c >> 7], m11, e16);
+      s_v[c] = (long long)(code_of(c) - 1) * (long long)m11 * (1ll << (e16 - emin));
+    }
+    for (int h = 1; h < p.hblock; h <<= 1) {
+      __syncthreads();
+      for (int i2 = tid; i2 < p.n_embd / 2; i2 += kEmbedThreads) {
+        const int i = (i2 / h) * 2 * h + (i2 % h);
+        const long long a = s_v[i], b = s_v[i + h];
+        s_v[i] = a + b;
+        s_v[i + h] = a - b;
+      }
+    }
+    __syncthreads();
+    long long ym = 0;
+    for (int c = tid; c < p.n_embd; c += kEmbedThreads) {
+      const long long y = p.signs[c] < 0.f ? -s_v[c] : s_v[c];
+      s_v[c] = y;
+      const long long a = y < 0 ? -y : y;
+      ym = a > ym ? a : ym;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const long long other = __shfl_xor(ym, o, 64);
+      ym = other > ym ? other : ym;
+    }
+    __syncthreads();
+    if ((tid & 63) == 0) s_lred[tid >> 6] = ym;
+    __syncthreads();
+    ym = s_lred[0];
+    for (int i = 1; i < kEmbedThreads / 64; ++i) ym = s_lred[i] > ym ? s_lred[i] : ym;
+    int lg = 0;
+    while ((1 << (lg + 1)) <= p.hblock) ++lg;
+    const int bits = ym ? 64 - __clzll(ym) : 0;
+    const int r = bits - 15;
+    const float sc2 = ym ? bfp_scale(emin - lg / 2 + r) : 0.f;
+    for (int c = tid; c < p.n_embd; c += kEmbedThreads) {
+      const long long y = s_v[c], a = y < 0 ? -y : y;
+      long long mag = r > 0 ? rne_shift_ll(a, r) : (a << (-r));
+      mag = mag > 32767 ? 32767 : mag;
+      x[c] = (float)(y < 0 ? -mag : mag) * sc2;
+    }
+    return;
+  }
   int bl = 0;
   while (bl < 63 && (amax >> bl) != 0) ++bl;
   const int k2 = bl - 15;
@@ -552,6 +611,9 @@ int launch_embed_rows(const EmbedParams& p, const int* fed, int p0, int R, float
             "embedding: n_embd %d unsupported", p.n_embd);
   TRX_CHECK(p.mode == EMBED_TABLE || (p.row_bytes % 16 == 0 && p.row_bytes <= kEmbedRowMax), TRX_E_INVALID,
             "embedding: row of %d bytes unsupported", p.row_bytes);
+  TRX_CHECK(p.mode != EMBED_RESTORE || (p.signs && p.hblock >= 1 && p.n_embd % p.hblock == 0 &&
+                                        p.n_embd <= kRestoreMax), TRX_E_INVALID,
+            "embedding: restore of %d columns in blocks of %d unsupported", p.n_embd, p.hblock);
   hipLaunchKernelGGL(embed_rows_kernel, dim3(R), dim3(kEmbedThreads), 0, s, p, fed, p0, X);
   TRX_LAUNCHED();
   return TRX_OK;
@@ -562,6 +624,9 @@ int launch_embed(const EmbedParams& p, hipStream_t s) {
             "embedding: n_embd %d unsupported", p.n_embd);
   TRX_CHECK(p.mode == EMBED_TABLE || (p.row_bytes % 16 == 0 && p.row_bytes <= kEmbedRowMax), TRX_E_INVALID,
             "embedding: row of %d bytes unsupported", p.row_bytes);
+  TRX_CHECK(p.mode != EMBED_RESTORE || (p.signs && p.hblock >= 1 && p.n_embd % p.hblock == 0 &&
+                                        p.n_embd <= kRestoreMax), TRX_E_INVALID,
+            "embedding: restore of %d columns in blocks of %d unsupported", p.n_embd, p.hblock);
   hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(kEmbedThreads), 0, s, p);
   TRX_LAUNCHED();
   return TRX_OK;

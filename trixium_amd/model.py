@@ -120,8 +120,15 @@ class Decoder:
         weight_kind = kinds.pop()
         head = img.find(L.ROLE_LM_HEAD, 0)
         emb = img.find(L.ROLE_TOK_EMB, 0)
+        rot = image_rotation(img)
+        emb_mode = 0
         if img.find(L.ROLE_TOK_EMB16, 0) is None:
-            raise ValueError("the image has no int16 embedding table (token_embd.bfp16)")
+            # Without the int16 table, a rotated image's rows are restored to the plain basis in
+            # integers per token (the firmware's embed_row_restore, model/bons.py:262-295).
+            if rot is None or emb is None or not L.is_ternary(emb["kind"]) or mc.n_embd not in rot[2]:
+                raise ValueError("the image has no int16 embedding table (token_embd.bfp16) and no "
+                                 "rotated ternary token_embd to restore")
+            emb_mode = 2
         head_tied = head is None
         if head_tied:
             if emb is None or not L.is_ternary(emb["kind"]):
@@ -130,13 +137,12 @@ class Decoder:
         else:
             head_kind = L.KIND_F16 if head["kind"] == L.KIND_F32 else head["kind"]
             emb_kind = emb["kind"] if emb is not None and L.is_ternary(emb["kind"]) else weight_kind
-        rot = image_rotation(img)
         if rot is not None:
             # A rotated model: one kernel per operation, every projection's input rotated first
             # (no partial-sum handoffs between packed GEMVs, no persistent kernel).
             if persistent:
                 raise ValueError("a rotated (Hadamard) image runs one kernel per operation")
-        cfg = make_config(mc, weight_kind, head_kind, head_tied, 0, emb_kind, max_ctx, max_new, persistent,
+        cfg = make_config(mc, weight_kind, head_kind, head_tied, emb_mode, emb_kind, max_ctx, max_new, persistent,
                           packed_ops, prefill_chunk)
         if rot is not None:
             block, scale, signs = rot
@@ -240,13 +246,14 @@ class Decoder:
         if rot is not None:
             for i, (w, sg) in enumerate(rot[2].items()):
                 self.set_tensor(L.ROLE_HADAMARD, i, sg.astype(f32))
-        _, mant = img.entry_tensor(img.find(L.ROLE_TOK_EMB16, 0))
-        _, ex = img.entry_tensor(img.find(L.ROLE_TOK_EMB16_EXP, 0))
-        self.set_tensor(L.ROLE_TOK_EMB16, 0, np.asarray(mant, dtype=np.int16))
-        self.set_tensor(L.ROLE_TOK_EMB16_EXP, 0, np.asarray(ex).reshape(-1)[:cfg.vocab].astype(np.int32))
-        if cfg.head_tied:
+        if cfg.emb_mode == 0:
+            _, mant = img.entry_tensor(img.find(L.ROLE_TOK_EMB16, 0))
+            _, ex = img.entry_tensor(img.find(L.ROLE_TOK_EMB16_EXP, 0))
+            self.set_tensor(L.ROLE_TOK_EMB16, 0, np.asarray(mant, dtype=np.int16))
+            self.set_tensor(L.ROLE_TOK_EMB16_EXP, 0, np.asarray(ex).reshape(-1)[:cfg.vocab].astype(np.int32))
+        if cfg.head_tied or cfg.emb_mode != 0:
             self.set_tensor(L.ROLE_TOK_EMB, 0, self._rows(img, img.find(L.ROLE_TOK_EMB, 0), cfg.emb_kind))
-        else:
+        if not cfg.head_tied:
             head = img.find(L.ROLE_LM_HEAD, 0)
             if cfg.head_kind == L.KIND_F16:
                 w = np.asarray(img.entry_tensor(img.find(L.ROLE_LM_HEAD, 0, L.KIND_F32))[1], dtype=f32)
