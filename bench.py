@@ -349,8 +349,43 @@ def traffic_from_profile(kind, mode):
     return None
 
 
+def blas_info():
+    """numpy's BLAS library and version, as numpy reports them."""
+    try:
+        cfg = np.show_config(mode="dicts")
+        b = cfg.get("Build Dependencies", {}).get("blas", {})
+        return f"{b.get('name', '?')} {b.get('version', '')}".strip()
+    except Exception:
+        return "unknown"
+
+
+def tiny_cpu_decode(seed=0, n_prompt=16, n_new=64):
+    """The tiny random Qwen3 model (hidden 256, 4 layers, vocab 2048, seed 0): the float oracle's
+    full greedy decode of 64 tokens after a 16-token prompt, timed on the host, and the GPU
+    decoder's tokens for the same model and prompt."""
+    import tempfile
+    from oracle.floatref import FloatRef
+    from trixium_amd import bons, configs as C, synth
+    from trixium_amd.model import Decoder
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "tiny.img")
+        bons.write_image(C.TINY, synth.small_model_tensors(C.TINY, seed, True), 1, path, trit5=True)
+        prompt = synth.random_prompt(C.TINY, n_prompt, seed)
+        ref = FloatRef(bons.BONSReader(path), kv_fp16=True)
+        t0 = time.perf_counter()
+        cpu = ref.generate(prompt, n_new)
+        dt = time.perf_counter() - t0
+        dec = Decoder.from_image(path, max_new=n_new)
+        gpu = dec.generate_fresh(prompt, n_new)
+        dec.close()
+    return {"config": "tiny qwen3 (256 wide, 4 layers, vocab 2048), seed 0", "prompt_tokens": n_prompt,
+            "new_tokens": n_new, "seconds": round(dt, 3), "tok_s": round(n_new / dt, 2),
+            "tokens_equal_gpu": cpu == gpu}
+
+
 def cpu_baseline(mc, ctx):
-    """The oracle's decode step on one layer + the LM head of the shape, scaled to all layers."""
+    """The oracle's decode step on one layer + the LM head of the shape, scaled to all layers;
+    and the tiny model's full greedy decode."""
     from oracle.floatref import ShapeSample
     cores = len(os.sched_getaffinity(0))
     threads = int(os.environ.get("OMP_NUM_THREADS", cores))
@@ -363,7 +398,10 @@ def cpu_baseline(mc, ctx):
     s.step(3, want_logits=True)
     t_head = max(time.perf_counter() - t0 - t_layer, 0.0)
     per_tok = mc.n_layer * t_layer + t_head
+    tiny = tiny_cpu_decode()
     return {"value": round(1.0 / per_tok, 6), "unit": "tok/s", "cores": min(cores, threads),
+            "blas": blas_info(), "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
+            "tiny_decode": tiny,
             "kind": "port",
             "sample": (f"float oracle decode step (numpy, fp16 weight cache) on 1 of {mc.n_layer} "
                        f"layers + the {mc.vocab}x{mc.n_embd} LM head at context {ctx}: "

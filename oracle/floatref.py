@@ -126,7 +126,8 @@ class FloatRef:
 
     @staticmethod
     def sigmoid(x):
-        return (f32(1.0) / (f32(1.0) + np.exp(-x))).astype(f32)
+        with np.errstate(over="ignore"):       # exp(-x) = inf for x << 0 gives the exact 0
+            return (f32(1.0) / (f32(1.0) + np.exp(-x))).astype(f32)
 
     @staticmethod
     def silu(x):
@@ -347,8 +348,9 @@ class ShapeSample(FloatRef):
 
 
 class TensorRef(FloatRef):
-    """FloatRef's step over weights given as arrays instead of an image (full-attention models):
-    the headline shapes, whose weights the device generator fills in HBM and a test reads back.
+    """FloatRef's step over weights given as arrays instead of an image: the headline shapes (and
+    the hybrid's layer pattern), whose weights the device generator fills in HBM and a test reads
+    back.
 
     weights: {(role, layer): float32 [rows, cols]} for every projection and the LM head (under
     ROLE_LM_HEAD, or ROLE_TOK_EMB when tied); gains: {(role, layer): float32 vector} for the
@@ -356,17 +358,29 @@ class TensorRef(FloatRef):
     embed_row(tok) -> float32 [n_embd], the token's embedding row. Numerics are FloatRef's with
     the weights held in float32 (exact for ternary values times fp16 scales)."""
 
-    def __init__(self, mc, weights, gains, embed_row, kv_fp16=True):
+    def __init__(self, mc, weights, gains, embed_row, kv_fp16=True, dn_tensors=None):
         self.n_layer, self.n_embd = mc.n_layer, mc.n_embd
         self.n_head, self.n_kv, self.hd = mc.n_head, mc.n_kv_head, mc.head_dim
         self.rope_n = mc.rope_dims or mc.head_dim
         self.eps = f32(mc.rms_eps)
-        self.gated = False
+        self.gated = bool(mc.attn_gated)
         self.hb, self.hwidths = 0, []
         self.vocab = mc.vocab
-        self.dn = [False] * mc.n_layer
-        self.nk = self.hk = self.nv = self.hv = 0
-        self.K = 1
+        self.dn = [mc.layer_type(l) == "deltanet" for l in range(mc.n_layer)]
+        self.nk, self.hk = mc.dn_num_k_heads, mc.dn_k_head_dim
+        self.nv, self.hv = mc.dn_num_v_heads, mc.dn_v_head_dim
+        self.K = max(mc.dn_conv_kernel, 1)
+        # Gated DeltaNet layers: dn_tensors {(role, layer): float32} of SSM_CONV [C, K], SSM_A,
+        # SSM_DT, SSM_NORM; their projections (ATTN_QKV, ATTN_ZGATE, SSM_BETA, SSM_ALPHA,
+        # SSM_OUT) are in `weights`.
+        dn_tensors = dn_tensors or {}
+        self.norm_ssm, self.ssm_a, self.ssm_dt, self.conv_w = {}, {}, {}, {}
+        for l in range(mc.n_layer):
+            if self.dn[l]:
+                self.norm_ssm[l] = dn_tensors[(L.ROLE_SSM_NORM, l)]
+                self.ssm_a[l] = dn_tensors[(L.ROLE_SSM_A, l)]
+                self.ssm_dt[l] = dn_tensors[(L.ROLE_SSM_DT, l)]
+                self.conv_w[l] = dn_tensors[(L.ROLE_SSM_CONV, l)].reshape(-1, self.K)
         self.kv_fp16 = kv_fp16
         self.rope_tab = None
         self.rope_freq = np.array([f32(f32(mc.rope_theta) ** f32(-2.0 * i / self.rope_n))
@@ -375,8 +389,8 @@ class TensorRef(FloatRef):
         self.head_role = L.ROLE_LM_HEAD if (L.ROLE_LM_HEAD, 0) in weights else L.ROLE_TOK_EMB
         self.norm_attn = [gains[(L.ROLE_ATTN_NORM, l)] for l in range(mc.n_layer)]
         self.norm_ffn = [gains[(L.ROLE_FFN_NORM, l)] for l in range(mc.n_layer)]
-        self.norm_q = {l: gains[(L.ROLE_ATTN_Q_NORM, l)] for l in range(mc.n_layer)}
-        self.norm_k = {l: gains[(L.ROLE_ATTN_K_NORM, l)] for l in range(mc.n_layer)}
+        self.norm_q = {l: gains[(L.ROLE_ATTN_Q_NORM, l)] for l in range(mc.n_layer) if not self.dn[l]}
+        self.norm_k = {l: gains[(L.ROLE_ATTN_K_NORM, l)] for l in range(mc.n_layer) if not self.dn[l]}
         self.out_norm = gains[(L.ROLE_OUT_NORM, 0)]
         self.embed_row = embed_row
         self.reset()

@@ -2,7 +2,9 @@
 
 Two layers at the full Qwen3-8B width (4096 wide, FFN 12288, 32 q / 8 kv heads of 128, the
 untied 151936-row ternary LM head) and at the full Qwen3-1.7B width (2048 wide, FFN 6144, the
-tied 151936-row ternary embedding as the head), with every weight from the device generator.
+tied 151936-row ternary embedding as the head), with every weight from the device generator; and
+one Gated DeltaNet plus one gated attention layer at the full Qwen3.5-27B width with its
+248320-row head.
 The oracle runs on the weights read back from HBM (a sample of rows of every tensor checked
 against the host hash first): every prompt position's logits within 2e-3 and the first 64 greedy
 tokens identical. At full depth (36 and 28 layers) the checks are size-independent properties:
@@ -83,6 +85,95 @@ def _oracle(dec, mc, seed):
         return mant[0].astype(np.float32) * np.float32(np.exp2(int(ex[0])))
 
     return TensorRef(mc, weights, gains, embed_row, kv_fp16=True)
+
+
+def _oracle_hybrid(dec, mc, seed):
+    """TensorRef over a hybrid's weights in HBM: ternary rows checked against the host hash, the
+    Q8 beta/alpha rows and the DeltaNet float tensors read back (fp16(q * scale) as fastref caches
+    Q8 weights)."""
+    rng = np.random.default_rng(seed)
+    E, hd, F, V = mc.n_embd, mc.head_dim, mc.ffn_dim, mc.vocab
+    nq, nvh = mc.dn_num_k_heads * mc.dn_k_head_dim, mc.dn_num_v_heads * mc.dn_v_head_dim
+    C_ = 2 * nq + nvh
+    qrows = mc.n_head * hd * (2 if mc.attn_gated else 1)
+    weights, gains, dn = {}, {}, {}
+    for l in range(mc.n_layer):
+        if mc.layer_type(l) == "deltanet":
+            shapes = {L.ROLE_ATTN_QKV: (C_, E), L.ROLE_ATTN_ZGATE: (nvh, E), L.ROLE_SSM_OUT: (E, nvh)}
+            for role in (L.ROLE_SSM_BETA, L.ROLE_SSM_ALPHA):
+                raw = np.asarray(dec.read_tensor(role, l)).reshape(-1)
+                rb = L.row_bytes(E, L.KIND_Q8)
+                sc, q = bons.decode_rows(L.KIND_Q8, E, raw[:mc.dn_num_v_heads * rb].reshape(mc.dn_num_v_heads, rb))
+                w = (q.astype(np.float16).reshape(q.shape[0], -1, 32) * sc[:, :, None]).astype(np.float16)
+                weights[(role, l)] = w.reshape(q.shape[0], E).astype(np.float32)
+            for role, n in ((L.ROLE_SSM_CONV, C_ * mc.dn_conv_kernel), (L.ROLE_SSM_A, mc.dn_num_v_heads),
+                            (L.ROLE_SSM_DT, mc.dn_num_v_heads), (L.ROLE_SSM_NORM, mc.dn_v_head_dim)):
+                dn[(role, l)] = dec.read_tensor(role, l).view(np.float32)[:n].copy()
+            norm_roles = ((L.ROLE_ATTN_NORM, E), (L.ROLE_FFN_NORM, E))
+        else:
+            shapes = {L.ROLE_ATTN_Q: (qrows, E), L.ROLE_ATTN_K: (mc.n_kv_head * hd, E),
+                      L.ROLE_ATTN_V: (mc.n_kv_head * hd, E), L.ROLE_ATTN_OUT: (E, mc.n_head * hd)}
+            norm_roles = ((L.ROLE_ATTN_NORM, E), (L.ROLE_FFN_NORM, E), (L.ROLE_ATTN_Q_NORM, hd),
+                          (L.ROLE_ATTN_K_NORM, hd))
+        shapes.update({L.ROLE_FFN_GATE: (F, E), L.ROLE_FFN_UP: (F, E), L.ROLE_FFN_DOWN: (E, F)})
+        for role, (r, c) in shapes.items():
+            w, raw = _dequant(dec.read_tensor(role, l), r, c)
+            _check_rows(raw, r, c, seed, role, l, rng)
+            weights[(role, l)] = w
+        for role, n in norm_roles:
+            gains[(role, l)] = dec.read_tensor(role, l).view(np.float32)[:n].copy()
+    gains[(L.ROLE_OUT_NORM, 0)] = dec.read_tensor(L.ROLE_OUT_NORM, 0).view(np.float32)[:E].copy()
+    emb_raw = np.asarray(dec.read_tensor(L.ROLE_TOK_EMB, 0)).reshape(-1)
+    rb = L.row_bytes(E, TRIT5)
+    emb_raw = emb_raw[:V * rb].reshape(V, rb)
+    _check_rows(emb_raw, V, E, seed, L.ROLE_TOK_EMB, 0, rng)
+    w, raw = _dequant(dec.read_tensor(L.ROLE_LM_HEAD, 0), V, E)
+    _check_rows(raw, V, E, seed, L.ROLE_LM_HEAD, 0, rng)
+    weights[(L.ROLE_LM_HEAD, 0)] = w
+
+    def embed_row(tok):
+        sc, codes = bons.decode_rows(TRIT5, E, emb_raw[tok:tok + 1])
+        mant, ex = bons.embed_bfp_rows(codes, sc)
+        return mant[0].astype(np.float32) * np.float32(np.exp2(int(ex[0])))
+
+    return TensorRef(mc, weights, gains, embed_row, kv_fp16=True, dn_tensors=dn)
+
+
+@pytest.mark.timeout(1200)
+def test_full_width_27b_hybrid_matches_the_oracle():
+    """One Gated DeltaNet layer and one gated attention layer at the full Qwen3.5-27B width (5120
+    wide; 48 v / 16 k DeltaNet heads of 128; 24 q / 4 kv heads of 256, 64 RoPE dims; FFN 17408)
+    with the full 248320-row ternary head: the logits at the last 8 positions of a 64-token prompt
+    (the DeltaNet state and conv window carried over 64 positions) within 2e-3 of the oracle, then
+    16 greedy tokens identical to the oracle's; the batched prefill of the same prompt gives the
+    same last-position logits within 2e-3."""
+    from trixium_amd.model import Decoder
+    mc = C.QWEN35_27B.replace(name="qwen3.5-27b-shape-2l", n_layer=2, layer_types=("deltanet", "attn"),
+                              max_ctx=128)
+    seed = 27
+    dec = Decoder.synthetic(mc, seed, weight_kind=TRIT5, max_new=16)
+    print("27b: reading the weights back", flush=True)
+    ref = _oracle_hybrid(dec, mc, seed)
+    prompt = synth.random_prompt(mc, 64, seed)
+    errs, want = [], None
+    for i, t in enumerate(prompt):
+        got = dec.forward([t])
+        want = ref.step(t, want_logits=i >= len(prompt) - 8)
+        if want is not None:
+            errs.append(_rel_err(got, want))
+    print(f"27b: last 8 prompt positions max rel err {max(errs):.2e}", flush=True)
+    assert max(errs) <= 2e-3
+    ids, lg = [], want
+    for i in range(16):
+        ids.append(int(np.argmax(lg)))
+        if i + 1 < 16:
+            lg = ref.step(ids[-1])
+    got = dec.generate_fresh(prompt, 16)
+    assert got == ids
+    dec.close()
+    pre = Decoder.synthetic(mc, seed, weight_kind=TRIT5, max_new=16, prefill_chunk=32)
+    assert _rel_err(pre.forward(prompt), want) <= 2e-3
+    assert pre.generate_fresh(prompt, 16) == ids
 
 
 @pytest.mark.timeout(900)
