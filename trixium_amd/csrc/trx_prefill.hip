@@ -573,10 +573,164 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnPrefillParams p) 
   }
 }
 
+// The same causal attention on the matrix cores, for head dims 64 and 128. A wave takes 32
+// score columns (PW = 32 / rep positions x rep heads of one kv head; rep 6 leaves 2 columns
+// idle) and a block four waves; every key tile of 32 cache positions is staged in LDS once per
+// block (K row-major, V transposed), as fp16, which is how the cache holds them.
+//   S^T = K Q^T   (v_mfma_f32_32x32x16_f16, keys x columns): q enters as two fp16 planes,
+//                 q = hi + lo, so each score is the fp32 dot product to ~2^-22 relative;
+//   online softmax per column in registers (a lane holds one column: 16 of its 32 keys, the
+//                 other 16 in lane l ^ 32);
+//   O^T += V^T P^T: the probabilities, again as hi + lo fp16 planes, feed the B operand straight
+//                 from the score registers; the K slot order of A (V^T, read from LDS) follows
+//                 the score layout (lane half h holds keys 4h..4h+3 and 8+4h..8+4h+3 of each 16).
+// Numerics as attn_prefill_kernel's to fp32 rounding (softmax in fp32, __expf).
+template <int HD>
+__global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(AttnPrefillParams p) {
+  constexpr int NC = HD / 16, NDT = HD / 32;       // q chunks of 16 dims; 32-dim output tiles
+  constexpr int KS = HD + 8, VS = 32 + 8;           // LDS row strides (halfs)
+  __shared__ __align__(16) _Float16 ks[32 * KS];
+  __shared__ __align__(16) _Float16 vt[HD * VS];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, j = lane & 31;
+  const int rep = p.n_head / p.n_kv, PW = 32 / rep, g = blockIdx.y;
+  const int q0 = blockIdx.x * 4 * PW;                              // chunk offset of the block
+  const int pq = j / rep, jh = j - pq * rep;
+  const int qrow = q0 + w * PW + pq;                               // chunk row of this column
+  const bool cvalid = pq < PW && qrow < p.R;
+  const int qpos = cvalid ? p.p0 + qrow : -1;                      // -1: every key masked
+  const int head = g * rep + jh;
+  const int wave_last = p.p0 + min(p.R, q0 + (w + 1) * PW) - 1;
+  const int block_last = p.p0 + min(p.R, q0 + 4 * PW) - 1;
+
+  // This column's q as fp16 hi/lo planes in the B-operand layout (dims 16c + 8h .. + 7).
+  half8_t qh[NC], ql[NC];
+  {
+    const float* qr = p.q + ((size_t)(cvalid ? qrow : 0) * p.n_head + head) * HD + 8 * h;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const float4 a = cvalid ? *(const float4*)(qr + 16 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 b = cvalid ? *(const float4*)(qr + 16 * c + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const _Float16 hi = (_Float16)v[k];
+        qh[c][k] = hi;
+        ql[c][k] = (_Float16)(v[k] - (float)hi);
+      }
+    }
+  }
+  f32x16_t o[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
+  float m = -INFINITY, l = 0.f;
+  const __half* kc = p.kcache + (size_t)g * p.max_ctx * HD;
+  const __half* vc = p.vcache + (size_t)g * p.max_ctx * HD;
+  // Staging: thread t moves 16 bytes (8 dims) of key row t / (HD / 8) per pass; rows past the
+  // block's last query are zeros (their V would otherwise meet probability 0 as garbage).
+  constexpr int SEG = HD / 8, PASS = 256 / SEG, NPASS = 32 / PASS;
+  const int srow = tid / SEG, sd = (tid % SEG) * 8;
+
+  for (int t0 = 0; t0 <= block_last; t0 += 32) {
+    uint4 kr[NPASS], vr[NPASS];
+#pragma unroll
+    for (int ps = 0; ps < NPASS; ++ps) {
+      const int kp = t0 + ps * PASS + srow;
+      const bool ok = kp <= block_last;
+      kr[ps] = ok ? *(const uint4*)(kc + (size_t)kp * HD + sd) : make_uint4(0, 0, 0, 0);
+      vr[ps] = ok ? *(const uint4*)(vc + (size_t)kp * HD + sd) : make_uint4(0, 0, 0, 0);
+    }
+    __syncthreads();                                  // the previous tile's reads are done
+#pragma unroll
+    for (int ps = 0; ps < NPASS; ++ps) {
+      const int r = ps * PASS + srow;
+      *(uint4*)(ks + r * KS + sd) = kr[ps];
+      const _Float16* vh = (const _Float16*)&vr[ps];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) vt[(sd + k) * VS + r] = vh[k];
+    }
+    __syncthreads();
+    if (t0 > wave_last) continue;                     // every key past this wave's queries
+
+    f32x16_t s;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s[e] = 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const half8_t a = *(const half8_t*)(ks + j * KS + 16 * c + 8 * h);
+      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qh[c], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, ql[c], s, 0, 0, 0);
+    }
+    // Causal mask and the column's running max over its keys.
+    float mx = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int kp = t0 + 8 * (e >> 2) + 4 * h + (e & 3);
+      if (kp > qpos) s[e] = -INFINITY;
+      mx = fmaxf(mx, s[e]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mn = fmaxf(m, mx);
+    const float corr = mn == -INFINITY ? 1.f : __expf(m - mn);
+    float ps_ = 0.f;
+    half8_t ph[2], pl[2];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float pe = s[e] == -INFINITY ? 0.f : __expf(s[e] - mn);
+      ps_ += pe;
+      const _Float16 hi = (_Float16)pe;
+      ph[e >> 3][e & 7] = hi;
+      pl[e >> 3][e & 7] = (_Float16)(pe - (float)hi);
+    }
+    ps_ += __shfl_xor(ps_, 32, 64);
+    l = l * corr + ps_;
+    m = mn;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[dt][e] *= corr;
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh) {
+        // V^T rows dt * 32 + j, keys 16 kh + 4h .. + 3 and 16 kh + 8 + 4h .. + 3.
+        const _Float16* vr0 = vt + (dt * 32 + j) * VS + 16 * kh + 4 * h;
+        const uint2 lo4 = *(const uint2*)vr0, hi4 = *(const uint2*)(vr0 + 8);
+        const uint4 av = make_uint4(lo4.x, lo4.y, hi4.x, hi4.y);
+        const half8_t a = __builtin_bit_cast(half8_t, av);
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, ph[kh], o[dt], 0, 0, 0);
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pl[kh], o[dt], 0, 0, 0);
+      }
+    }
+  }
+  if (!cvalid) return;
+  const float inv = 1.0f / l;
+  float* dst = p.out + (size_t)qrow * p.n_head * HD + (size_t)head * HD;
+  const float* gate = p.qkv + (size_t)qrow * p.ldq + (size_t)head * 2 * HD + HD;
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+    for (int a4 = 0; a4 < 4; ++a4) {
+      const int d0 = dt * 32 + 8 * a4 + 4 * h;
+      float4 v = make_float4(o[dt][4 * a4] * inv, o[dt][4 * a4 + 1] * inv, o[dt][4 * a4 + 2] * inv, o[dt][4 * a4 + 3] * inv);
+      if (p.gated) {
+        const float4 gv = *(const float4*)(gate + d0);
+        v = make_float4(v.x * sigmoidf_(gv.x), v.y * sigmoidf_(gv.y), v.z * sigmoidf_(gv.z), v.w * sigmoidf_(gv.w));
+      }
+      *(float4*)(dst + d0) = v;
+    }
+}
+
 int launch_attn_prefill(const AttnPrefillParams& p, hipStream_t s) {
   TRX_CHECK(p.n_kv >= 1 && p.n_head % p.n_kv == 0 && p.n_head / p.n_kv <= 64 && p.R >= 1 &&
             p.p0 + p.R <= p.max_ctx, TRX_E_INVALID, "prefill attention: bad geometry");
   const int rep = p.n_head / p.n_kv, QT = 64 / rep;
+  if ((p.hd == 64 || p.hd == 128) && rep <= 32) {
+    const dim3 mgrid(cdiv(p.R, 4 * (32 / rep)), p.n_kv);
+    if (p.hd == 64) hipLaunchKernelGGL((attn_prefill_mfma_kernel<64>), mgrid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((attn_prefill_mfma_kernel<128>), mgrid, dim3(256), 0, s, p);
+    TRX_LAUNCHED();
+    return TRX_OK;
+  }
   const dim3 grid(cdiv(p.R, QT), p.n_kv);
   if (p.hd == 64) hipLaunchKernelGGL((attn_prefill_kernel<64, 32>), grid, dim3(256), 0, s, p);
   else if (p.hd == 128) hipLaunchKernelGGL((attn_prefill_kernel<128, 32>), grid, dim3(256), 0, s, p);
