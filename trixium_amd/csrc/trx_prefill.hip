@@ -1,6 +1,6 @@
 // Batched prefill kernels: R prompt positions per forward, one weight pass for all of them.
 //
-// The projections run on the matrix cores (v_mfma_f32_32x32x16_f16): a block decodes a 128-row x
+// The projections run on the matrix cores (v_mfma_f32_32x32x16_f16): a block decodes a 256-row x
 // 128-column tile of the stored ternary rows into LDS as fp16 weights and multiplies 64 positions
 // by it, x split into two fp16 planes (hi, lo) so the fp32 accumulation sees x to ~22 bits.
 // Attention, the RoPE/KV append and the Gated DeltaNet recurrence are the one-position rules of
@@ -20,7 +20,7 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 constexpr int kGmThreads = 256;
 constexpr int kGmBR = 64;                  // positions per block
-constexpr int kGmBM = 128;                 // weight rows per block
+constexpr int kGmBM = 256;                 // weight rows per block
 constexpr int kGmLd = kGroup + 8;          // LDS row stride in halves (272 bytes)
 
 __device__ __forceinline__ uint32_t pk_mul_h2(uint32_t a, uint32_t s2) {
@@ -33,12 +33,12 @@ __device__ __forceinline__ uint32_t half_bits(float v) {
   return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v);
 }
 
-// Weight row of LDS tile row i: plain tiles take M rows in order; a SwiGLU tile takes 64 gate rows
-// f0 .. f0 + 63 (LDS rows 0..63) and the matching up rows F + f0 .. (LDS rows 64..127).
+// Weight row of LDS tile row i: plain tiles take M rows in order; a SwiGLU tile takes 128 gate
+// rows f0 .. f0 + 127 (LDS rows 0..127) and the matching up rows F + f0 .. (LDS rows 128..255).
 __device__ __forceinline__ int gm_wrow(int epi, int i, int M) {
   if (epi == GM_SWIGLU) {
-    const int F = M / 2, f = blockIdx.x * (kGmBM / 2) + (i & 63);
-    return f < F ? (i < 64 ? f : F + f) : M;
+    const int F = M / 2, f = blockIdx.x * (kGmBM / 2) + (i % (kGmBM / 2));
+    return f < F ? (i < kGmBM / 2 ? f : F + f) : M;
   }
   return blockIdx.x * kGmBM + i;
 }
@@ -50,7 +50,7 @@ struct GmRaw {
 };
 
 template <int KIND, int EPI>
-__global__ __launch_bounds__(kGmThreads, 2) void gemm_kernel(GemmParams p) {
+__global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
   __shared__ __align__(16) _Float16 ws[kGmBM * kGmLd];
   __shared__ __align__(16) _Float16 xs[2][kGmBR * kGmLd];
   __shared__ __align__(16) uint4 lut[2][256];
@@ -81,9 +81,9 @@ __global__ __launch_bounds__(kGmThreads, 2) void gemm_kernel(GemmParams p) {
     }
   }
 
-  // Staging roles: thread t decodes half (t >> 7) of the 128 codes of LDS row t & 127, and copies
+  // Staging roles: thread t decodes the 128 codes of LDS row t (two halves of 64), and copies
   // eight 16-byte pieces of the two x planes.
-  const int srow = tid & 127, shalf = tid >> 7;
+  const int srow = tid;
   const int wrow = gm_wrow(EPI, srow, p.M);
   const bool wvalid = wrow < p.M;
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.W, p.w_bytes);
@@ -91,7 +91,7 @@ __global__ __launch_bounds__(kGmThreads, 2) void gemm_kernel(GemmParams p) {
   const __amdgpu_buffer_rsrc_t rxh = make_rsrc(p.xh, (uint32_t)((size_t)p.R * p.K * 2));
   const __amdgpu_buffer_rsrc_t rxl = make_rsrc(p.xl, (uint32_t)((size_t)p.R * p.K * 2));
 
-  auto load_w = [&](GmRaw<KIND>& raw, int g) {
+  auto load_w = [&](GmRaw<KIND>& raw, int g, int shalf) {
     if (KIND == TRX_KIND_TERNARY5) {
       const uint32_t o = (uint32_t)p.code_off + 26u * (uint32_t)g + (shalf ? 12u : 0u);
       const auto a = __builtin_amdgcn_raw_buffer_load_b128(rw, rbase + (o & ~3u), 0, 0);
@@ -126,7 +126,7 @@ __global__ __launch_bounds__(kGmThreads, 2) void gemm_kernel(GemmParams p) {
     }
   };
   // Decoded weights of this thread's 64 codes: 32 dwords of fp16 pairs, times the scale.
-  auto stage_w = [&](const GmRaw<KIND>& raw, int g) {
+  auto stage_w = [&](const GmRaw<KIND>& raw, int g, int shalf) {
     uint32_t D[32];
     if (!wvalid) {
 #pragma unroll
@@ -219,23 +219,29 @@ __global__ __launch_bounds__(kGmThreads, 2) void gemm_kernel(GemmParams p) {
     }
   };
 
-  // Wave tiles: positions 32 wr .. + 31 of the block; weight columns ct0 and ct1 (32 each).
+  // Wave tiles: positions 32 wr .. + 31 of the block; four weight column tiles of 32 (SwiGLU: two
+  // gate tiles and the two up tiles of the same features).
   const int wr = w & 1, wm = w >> 1;
-  const int ct0 = EPI == GM_SWIGLU ? 32 * wm : 64 * wm;
-  const int ct1 = EPI == GM_SWIGLU ? 64 + 32 * wm : 64 * wm + 32;
+  int ct[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+    ct[t] = EPI == GM_SWIGLU ? (t >> 1) * (kGmBM / 2) + 64 * wm + 32 * (t & 1) : 128 * wm + 32 * t;
   const int li = lane & 31, lk = 8 * (lane >> 5);
-  f32x16_t acc0 = {}, acc1 = {};
+  f32x16_t acc[4] = {};
 
-  GmRaw<KIND> raw;
-  load_w(raw, 0);
+  GmRaw<KIND> raw[2];
+  load_w(raw[0], 0, 0);
+  load_w(raw[1], 0, 1);
   load_x(0);
   for (int g = 0; g < G; ++g) {
     __syncthreads();                      // the previous group's fragments are read
-    stage_w(raw, g);
+    stage_w(raw[0], g, 0);
+    stage_w(raw[1], g, 1);
     stage_x();
     __syncthreads();
     if (g + 1 < G) {
-      load_w(raw, g + 1);
+      load_w(raw[0], g + 1, 0);
+      load_w(raw[1], g + 1, 1);
       load_x(g + 1);
     }
 #pragma unroll
@@ -243,12 +249,13 @@ __global__ __launch_bounds__(kGmThreads, 2) void gemm_kernel(GemmParams p) {
       const int k = 16 * kk + lk;
       const half8_t ah = *(const half8_t*)(xs[0] + (32 * wr + li) * kGmLd + k);
       const half8_t al = *(const half8_t*)(xs[1] + (32 * wr + li) * kGmLd + k);
-      const half8_t b0 = *(const half8_t*)(ws + (ct0 + li) * kGmLd + k);
-      const half8_t b1 = *(const half8_t*)(ws + (ct1 + li) * kGmLd + k);
-      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b0, acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b1, acc1, 0, 0, 0);
-      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b0, acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b1, acc1, 0, 0, 0);
+      half8_t b[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) b[t] = *(const half8_t*)(ws + (ct[t] + li) * kGmLd + k);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b[t], acc[t], 0, 0, 0);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b[t], acc[t], 0, 0, 0);
     }
   }
 
@@ -260,16 +267,19 @@ __global__ __launch_bounds__(kGmThreads, 2) void gemm_kernel(GemmParams p) {
     if (r >= p.R) continue;
     float* yr = p.y + (size_t)r * p.ldy;
     if (EPI == GM_SWIGLU) {
-      const int f = blockIdx.x * (kGmBM / 2) + 32 * wm + li;
-      if (f < p.M / 2) yr[f] = silu(acc0[e]) * acc1[e];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int f = blockIdx.x * (kGmBM / 2) + ct[t] + li;
+        if (f < p.M / 2) yr[f] = silu(acc[t][e]) * acc[t + 2][e];
+      }
     } else {
-      const int m0 = blockIdx.x * kGmBM + ct0 + li, m1 = blockIdx.x * kGmBM + ct1 + li;
-      if (EPI == GM_RESID) {
-        if (m0 < p.M) yr[m0] += acc0[e];
-        if (m1 < p.M) yr[m1] += acc1[e];
-      } else {
-        if (m0 < p.M) yr[m0] = acc0[e];
-        if (m1 < p.M) yr[m1] = acc1[e];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int m = blockIdx.x * kGmBM + ct[t] + li;
+        if (m < p.M) {
+          if (EPI == GM_RESID) yr[m] += acc[t][e];
+          else yr[m] = acc[t][e];
+        }
       }
     }
   }
