@@ -734,10 +734,11 @@ int launch_attn_prefill(const AttnPrefillParams& p, hipStream_t s) {
   TRX_CHECK(p.n_kv >= 1 && p.n_head % p.n_kv == 0 && p.n_head / p.n_kv <= 64 && p.R >= 1 &&
             p.p0 + p.R <= p.max_ctx, TRX_E_INVALID, "prefill attention: bad geometry");
   const int rep = p.n_head / p.n_kv, QT = 64 / rep;
-  if ((p.hd == 64 || p.hd == 128) && rep <= 32) {
+  if ((p.hd == 64 || p.hd == 128 || p.hd == 256) && rep <= 32) {
     const dim3 mgrid(cdiv(p.R, 4 * (32 / rep)), p.n_kv);
     if (p.hd == 64) hipLaunchKernelGGL((attn_prefill_mfma_kernel<64>), mgrid, dim3(256), 0, s, p);
-    else hipLaunchKernelGGL((attn_prefill_mfma_kernel<128>), mgrid, dim3(256), 0, s, p);
+    else if (p.hd == 128) hipLaunchKernelGGL((attn_prefill_mfma_kernel<128>), mgrid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((attn_prefill_mfma_kernel<256>), mgrid, dim3(256), 0, s, p);
     TRX_LAUNCHED();
     return TRX_OK;
   }
