@@ -201,11 +201,12 @@ def matvec_microbench(reps=1000, rotate_bytes=512 << 20):
             _lib.call("trx_pack_ternary", rows.ptr, kind, M, K, 0, packed.ptr, None)
             for i in range(1, n):
                 _lib.call("trx_memcpy_d2d", packed.ptr + i * stride, packed.ptr, pb, None)
-            # One dispatch of at least `reps` matvecs cycling over the n copies (each copy is read
-            # again only after every other one: more than 512 MB apart), each with its own x.
+            # One dispatch of at least `reps` matvecs y = W x cycling over the n copies (each copy
+            # is read again only after every other one: more than 512 MB apart), one x for all
+            # of them (x_stride 0: a block reuses its slice's table over several matrices).
             nm = n * -(-reps // n)
-            xs = r.standard_normal((nm, K)).astype(np.float32)
-            xb = _lib.DeviceBuffer.from_array(xs)
+            x = r.standard_normal(K).astype(np.float32)
+            xb = _lib.DeviceBuffer.from_array(x)
             yb = _lib.DeviceBuffer(4 * nm * M)
             bw = ctypes.c_size_t()
             _lib.call("trx_pack_batched_geometry", kind, M, K, nm, ctypes.byref(bw))
@@ -213,16 +214,16 @@ def matvec_microbench(reps=1000, rotate_bytes=512 << 20):
             _lib.synchronize()
 
             def batched():
-                _lib.call("trx_gemv_packed_batched_f32", packed.ptr, stride, nm, n, kind, M, K, xb.ptr, K, yb.ptr, M,
+                _lib.call("trx_gemv_packed_batched_f32", packed.ptr, stride, nm, n, kind, M, K, xb.ptr, 0, yb.ptr, M,
                           part.ptr, None)
             n_launch = 2
             us = timed(batched, n_launch)
             # Correctness of the first and the last matvec of the dispatch (float64, 2e-6 of sum |w x|).
             y = yb.download(np.float32, nm * M).reshape(nm, M)
             err = 0.0
+            ref = W64 @ x.astype(np.float64)
+            mag = np.abs(W64) @ np.abs(x.astype(np.float64))
             for i in (0, nm - 1):
-                ref = W64 @ xs[i].astype(np.float64)
-                mag = np.abs(W64) @ np.abs(xs[i].astype(np.float64))
                 err = max(err, float(np.max(np.abs(y[i] - ref) / mag)))
             row_b = L.row_bytes(K, kind)
             algo = M * row_b + 4 * K + 4 * M            # weight rows (scales + codes), fp32 x and y
@@ -237,7 +238,7 @@ def matvec_microbench(reps=1000, rotate_bytes=512 << 20):
             def single():
                 i = idx[0] % n
                 idx[0] += 1
-                _lib.call("trx_gemv_packed_f32", packed.ptr + i * stride, kind, M, K, xb.ptr + 4 * i * K, None,
+                _lib.call("trx_gemv_packed_f32", packed.ptr + i * stride, kind, M, K, xb.ptr, None,
                           ctypes.c_float(1e-6), ys.ptr, 0, None, work.ptr, None)
             us1 = timed(single, reps) / reps
             # The engine's exact group sums on int8 x (the integer path), bit for bit.
@@ -257,8 +258,9 @@ def matvec_microbench(reps=1000, rotate_bytes=512 << 20):
     tot_bytes = sum(v["bytes_per_matvec"] * v["matvecs"] for v in out.values())
     tot_us = sum(v["us_per_matvec"] * v["matvecs"] for v in out.values())
     agg = tot_bytes / (tot_us * 1e-6) / 1e9
-    return {"kernel": "packed table-lookup GEMV, many matvecs per dispatch (trx_gemv_packed_batched_f32), "
-                      "fp32 x and y", "aggregate_GBs": round(agg, 1), "aggregate_frac": round(agg / HBM_PEAK_GBS, 4),
+    return {"kernel": "packed table-lookup GEMV, many matvecs y = W x per dispatch over rotating copies of W "
+                      "(trx_gemv_packed_batched_f32, one x: each block reuses its slice's table over several "
+                      "matrices), fp32 x and y", "aggregate_GBs": round(agg, 1), "aggregate_frac": round(agg / HBM_PEAK_GBS, 4),
             "peak_GBs": HBM_PEAK_GBS, "shapes": out}
 
 

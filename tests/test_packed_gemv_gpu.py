@@ -235,3 +235,25 @@ def test_batched_matvec_equals_single_launches(gpu, kind, M, K, n):
         assert np.max(np.abs(y[i] - ref) / np.maximum(mag, 1e-30)) < TOL
         single = gpu.PackedMatrix(sc, cd, kind).matvec(xs[i])
         assert np.array_equal(y[i], single), i
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("M,K,n_mat,copies", [(257, 2048, 300, 5), (2048, 2048, 96, 3), (128, 256, 2, 2), (640, 640, 1, 1)])
+def test_batched_matvec_with_one_x(gpu, kind, M, K, n_mat, copies):
+    """One x for every matrix (x_stride 0): a block reuses its table over several matrices (4 per
+    block at 300 matrices of 8 slices on 256 compute units), cycling over the copies; every y_i
+    bitwise equal to the single-matrix packed GEMV of its copy and within the float64 tolerance."""
+    print(f"batched matvec, one x: kind={kind} M={M} K={K} n_mat={n_mat} copies={copies}", flush=True)
+    mats = [_rand(M, K, 77 * i + K + M)[::-1] for i in range(copies)]
+    x = np.random.default_rng(K + n_mat).normal(0, 1, K).astype(np.float32)
+    y = gpu.batched_matvec(mats, x, kind, n_mat=n_mat)
+    singles = []
+    for sc, cd in mats:
+        W = _w64(cd, sc)
+        ref = W @ x.astype(np.float64)
+        mag = np.abs(W) @ np.abs(x.astype(np.float64))
+        single = gpu.PackedMatrix(sc, cd, kind).matvec(x)
+        assert np.max(np.abs(single - ref) / np.maximum(mag, 1e-30)) < TOL
+        singles.append(single)
+    for i in range(n_mat):
+        assert np.array_equal(y[i], singles[i % copies]), i

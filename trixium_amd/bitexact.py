@@ -141,12 +141,14 @@ def pack_geometry(kind, M, K):
     return pb.value, wb.value
 
 
-def batched_matvec(mats, xs, kind=L.KIND_TERNARY5):
-    """y_i = W_i x_i for every (scales, codes) of `mats` (one shape) in one dispatch
+def batched_matvec(mats, xs, kind=L.KIND_TERNARY5, n_mat=None):
+    """y_i = W_(i % len(mats)) x_i for i < n_mat (default len(mats)) in one dispatch
     (trx_gemv_packed_batched_f32): the packed copies back to back at a 256-byte multiple stride.
-    Returns float32 (n, M)."""
+    xs: (n_mat, K), or one (K,) vector for every matrix (x_stride 0). Returns float32 (n_mat, M)."""
     n = len(mats)
+    n_mat = n if n_mat is None else int(n_mat)
     M, K = mats[0][1].shape
+    shared = np.ndim(xs) == 1
     pb, _ = pack_geometry(kind, M, K)
     stride = -(-pb // 256) * 256
     packed = DeviceBuffer(stride * n)
@@ -156,13 +158,14 @@ def batched_matvec(mats, xs, kind=L.KIND_TERNARY5):
         call("trx_pack_ternary", rows.ptr, kind, M, K, 0, packed.ptr + i * stride, None)
         synchronize()
     wb = ctypes.c_size_t()
-    call("trx_pack_batched_geometry", kind, M, K, n, ctypes.byref(wb))
+    call("trx_pack_batched_geometry", kind, M, K, n_mat, ctypes.byref(wb))
     work = DeviceBuffer(wb.value)
-    xb = DeviceBuffer.from_array(np.ascontiguousarray(np.asarray(xs, dtype=np.float32).reshape(n, K)))
-    yb = DeviceBuffer(4 * n * M)
-    call("trx_gemv_packed_batched_f32", packed.ptr, stride, n, n, kind, M, K, xb.ptr, K, yb.ptr, M, work.ptr, None)
+    xb = DeviceBuffer.from_array(np.ascontiguousarray(np.asarray(xs, dtype=np.float32).reshape(-1 if shared else n_mat, K)))
+    yb = DeviceBuffer(4 * n_mat * M)
+    call("trx_gemv_packed_batched_f32", packed.ptr, stride, n_mat, n, kind, M, K, xb.ptr, 0 if shared else K, yb.ptr, M,
+         work.ptr, None)
     synchronize()
-    return yb.download(np.float32, n * M).reshape(n, M)
+    return yb.download(np.float32, n_mat * M).reshape(n_mat, M)
 
 
 class PackedMatrix:

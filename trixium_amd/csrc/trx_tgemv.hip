@@ -267,6 +267,9 @@ struct TgParams {
   uint32_t mat_bytes;
   int x_stride, part_sstride, part_mstride;
   int mat_copies;          // > 0: matrix i reads the packed copy i % mat_copies
+  // Several matrices per block (MULTI kernels): block y takes matrices y * mat_per_block .. (up to
+  // n_mat - 1), all with the same x (x_stride 0), so one table serves all of them.
+  int mat_per_block, n_mat;
 };
 
 template <bool T5>
@@ -275,7 +278,7 @@ struct TgItem {
   uint32_t sc;        // the two fp16 group scales of this lane's row
 };
 
-template <bool T5, int NB>
+template <bool T5, int NB, bool MULTI>
 __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgParams p) {
   constexpr int NLO = T5 ? 9 : 16;     // values of the low digits (trit5: 2 digits; 2-bit: 2 codes)
   constexpr int NHI = T5 ? 29 : 16;    // values of the rest (b / 9 <= 28; b >> 4)
@@ -287,7 +290,10 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   __shared__ int n_todo;
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int s = blockIdx.x % p.S, j = blockIdx.x / p.S, mi = blockIdx.y;
+  const int s = blockIdx.x % p.S, j = blockIdx.x / p.S;
+  const int mi = MULTI ? blockIdx.y * p.mat_per_block : blockIdx.y;
+  // Items of this block: tpb tiles of each of its matrices (one matrix unless MULTI).
+  const int n_items = MULTI ? p.tpb * min(p.mat_per_block, p.n_mat - mi) : p.tpb;
   const int xmode = p.merge.o ? kXMerge : p.parts.in ? (p.parts.F ? kXSwiglu : kXResid) : kXPlain;
   // A gated-off launch does nothing but store the residual it was handed in partials. The gate
   // is read here and tested after the prologue's loads and the first weight loads are issued,
@@ -386,9 +392,11 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   // 2. The first NB - 1 items of this lane (they do not depend on x).
   const int rg = lane >> 4, l16 = lane & 15, half = l16 >> 3;
   const int dw = tg_lane_dword(T5, l16), msk = tg_lane_mask(l16);
-  const size_t mcopy = (size_t)(p.mat_copies > 0 ? mi % p.mat_copies : mi);
-  const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.codes + mcopy * p.mat_bytes, p.code_bytes);
-  const __amdgpu_buffer_rsrc_t rsc = make_rsrc(p.scales + mcopy * p.mat_bytes, p.scale_bytes);
+  const size_t mcopy = MULTI ? 0 : (size_t)(p.mat_copies > 0 ? mi % p.mat_copies : mi);
+  // MULTI: the descriptors span every copy, an item's copy goes in its scalar offset.
+  const uint32_t span = MULTI ? (uint32_t)(p.mat_copies - 1) * p.mat_bytes : 0u;
+  const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.codes + mcopy * p.mat_bytes, p.code_bytes + span);
+  const __amdgpu_buffer_rsrc_t rsc = make_rsrc(p.scales + mcopy * p.mat_bytes, p.scale_bytes + span);
   // Item n of this lane is quad quad0 + n * qstep. The lane's offsets stay in fixed VGPRs and
   // the item's step goes in the scalar offset, so no VGPR that an in-flight access reads is
   // rewritten (that would cost a vmcnt wait per item). Only the VGPR offset is relied on for the
@@ -404,14 +412,33 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   // the compiler's waits exact); the lanes that hold no row total store past the buffer (dropped
   // by the range check), and the items of a partial last tile land in padding rows.
   const __amdgpu_buffer_rsrc_t rpart = make_rsrc(p.part, (uint32_t)((size_t)p.S * p.part_sstride * 4));
-  const uint32_t po0 = (l16 & 9) == 0 ? ((uint32_t)s * p.part_sstride + (uint32_t)mi * p.part_mstride +
+  const uint32_t po0 = (l16 & 9) == 0 ? ((uint32_t)s * p.part_sstride + (uint32_t)(MULTI ? 0 : mi) * p.part_mstride +
                                          4u * (uint32_t)quad0 + msk) * 4u
                                       : kOut;
   const uint32_t pstep = (uint32_t)qstep * 16u;
+  // Scalar offsets of item n: its tile's step, and (MULTI) its matrix copy and partial-sum block.
+  // MULTI items run tile by tile through the block's matrices; the matrix of item n is
+  // floor((n + 0.5) / tpb) in float (exact: n < 2^16 and tpb <= 96 keep the quotient at least
+  // 0.5 / 96 from an integer, far above the float error), its copy one step from the block's first.
+  const float inv_tpb = 1.0f / (float)p.tpb;
+  const int copy0 = MULTI ? mi % p.mat_copies : 0;
+  auto item_offsets = [&](int n, int& cso, int& sso, int& pso) {
+    if (MULTI) {
+      const int m = (int)(((float)n + 0.5f) * inv_tpb), t = n - m * p.tpb;
+      int copy = copy0 + m;
+      while (copy >= p.mat_copies) copy -= p.mat_copies;
+      cso = t * (int)cstep + copy * (int)p.mat_bytes;
+      sso = t * (int)sstep + copy * (int)p.mat_bytes;
+      pso = t * (int)pstep + (mi + m) * p.part_mstride * 4;
+    } else {
+      cso = n * (int)cstep;
+      sso = n * (int)sstep;
+      pso = n * (int)pstep;
+    }
+  };
   auto load_item = [&](TgItem<T5>& it, int n) {
-    const int nn = min(n, p.tpb - 1);
-    const int cso = nn * (int)cstep;
-    const int sso = nn * (int)sstep;
+    int cso, sso, pso;
+    item_offsets(min(n, n_items - 1), cso, sso, pso);
     const auto a = __builtin_amdgcn_raw_buffer_load_b128(rc, co0, cso, 0);
     it.c = make_uint4(a[0], a[1], a[2], a[3]);
     it.sc = __builtin_amdgcn_raw_buffer_load_b32(rsc, so0, sso, 0);
@@ -605,12 +632,14 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
     float v = a[0] * __half2float(__ushort_as_half((unsigned short)(it.sc >> sshift)));
     v += dpp_f<kDppRowRor8>(v);                      // the other group (lane l16 ^ 8)
     // Agent-scope store (sc1): the tile's reducing block may run on another XCD.
-    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), rpart, po0, n * (int)pstep, kCpolSc1);
+    int cso, sso, pso;
+    item_offsets(n, cso, sso, pso);
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), rpart, po0, pso, kCpolSc1);
   };
   // Whole groups of NB items (a loop with one exit keeps the compiler's vmcnt waits exact: item
   // n waits only for itself), then the remaining < NB items, already in flight.
   int n = 0;
-  const int ngroups = p.tpb / NB;
+  const int ngroups = n_items / NB;
   for (int gi = 0; gi < ngroups; ++gi) {
 #pragma unroll
     for (int ph = 0; ph < NB; ++ph) {
@@ -620,7 +649,7 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
       ++n;
     }
   }
-  const int rem = p.tpb - n;
+  const int rem = n_items - n;
 #pragma unroll
   for (int ph = 0; ph < NB - 1; ++ph) {
     if (ph < rem) compute(buf[ph], n + ph);
@@ -843,9 +872,9 @@ int tgemv_reduce_f32(const float* part, const float* ss, int S, int rows_p, int 
 int tgemv_partial_slices_max() { return kSwiPartMax; }
 int tgemv_resid_slices_max() { return kResPartMax; }
 
-template <bool T5>
+template <bool T5, bool MULTI = false>
 static const void* tg_fn() {
-  return (const void*)tgemv_kernel<T5, 4>;
+  return (const void*)tgemv_kernel<T5, 4, MULTI>;
 }
 
 int tgemv_f32(const uint8_t* packed, int kind, int M, int K, const float* x, const float* norm_w,
@@ -944,8 +973,12 @@ int tgemv_f32_batched(const uint8_t* packed, size_t mat_stride, int n_mat, int n
             "batched GEMV: null argument or %d copies for %d matrices", n_copies, n_mat);
   TRX_CHECK(mat_stride % 256 == 0 && (n_copies == 1 || mat_stride >= g.bytes) && mat_stride < (1ull << 32),
             TRX_E_INVALID, "batched GEMV: matrix stride %zu (a multiple of 256, at least %zu bytes)", mat_stride, g.bytes);
-  TRX_CHECK(x_stride >= K && y_stride >= M && ((uintptr_t)x & 15) == 0 && x_stride % 4 == 0, TRX_E_INVALID,
-            "batched GEMV: x stride %d, y stride %d (x 16-byte aligned)", x_stride, y_stride);
+  TRX_CHECK((x_stride == 0 || x_stride >= K) && y_stride >= M && ((uintptr_t)x & 15) == 0 && x_stride % 4 == 0,
+            TRX_E_INVALID, "batched GEMV: x stride %d, y stride %d (x 16-byte aligned)", x_stride, y_stride);
+  // One x for every matrix: a block takes several matrices with one table (their items in turn).
+  const bool multi = x_stride == 0 && n_mat > 1;
+  TRX_CHECK(!multi || ((size_t)(n_copies - 1) * mat_stride + g.bytes < (1ull << 31) && pb < (1ull << 31)),
+            TRX_E_INVALID, "batched GEMV with one x: %d copies of %zu bytes exceed 2 GiB", n_copies, mat_stride);
   TgParams p = {};
   p.codes = packed;
   p.scales = packed + g.scale_off;
@@ -972,9 +1005,20 @@ int tgemv_f32_batched(const uint8_t* packed, size_t mat_stride, int n_mat, int n
   p.part_sstride = n_mat * g.rows_p;
   p.part_mstride = g.rows_p;
   p.mat_copies = n_copies;
+  p.n_mat = n_mat;
+  int ny = n_mat;
   const void* fn = kind == TRX_KIND_TERNARY5 ? tg_fn<true>() : tg_fn<false>();
+  if (multi) {
+    // Matrices per block: as many as leave two blocks per compute unit in the grid, at most 16
+    // (measured best of 2 and 8 blocks per compute unit).
+    const int cus = cu_count();
+    if (cus <= 0) return TRX_E_HIP;
+    p.mat_per_block = std::max(1, std::min(16, g.S * n_mat / (2 * cus)));
+    ny = cdiv(n_mat, p.mat_per_block);
+    fn = kind == TRX_KIND_TERNARY5 ? tg_fn<true, true>() : tg_fn<false, true>();
+  }
   void* args[] = {(void*)&p};
-  TRX_HIP(hipLaunchKernel(fn, dim3(g.S, n_mat), dim3(kTgThreads), args, 0, s));
+  TRX_HIP(hipLaunchKernel(fn, dim3(g.S, ny), dim3(kTgThreads), args, 0, s));
   // The S partial sums of every row of every matrix, reduced over the whole GPU.
   RdParams r = {};
   r.part = part;
