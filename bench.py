@@ -157,9 +157,9 @@ def matvec_microbench(reps=1000, rotate_bytes=512 << 20):
     6144x2048, 2048x6144), trit5 and 2-bit rows, fp16 group scales U(0.01, 0.05), P(0) = 0.4:
     y = W x with fp32 x ~ N(0, 1), batch 1. The packed GEMV runs over distinct copies of the
     matrix laid out back to back (at least `rotate_bytes` of them, more than the 256 MB Infinity
-    Cache, so every launch streams from HBM), one dispatch of at least `reps` matvecs that cycles
-    over the copies, each with its own x (trx_gemv_packed_batched_f32), two dispatches timed with
-    HIP events. Also timed:
+    Cache, so every launch streams from HBM), one matvec per copy in each dispatch, one x for
+    all (trx_gemv_packed_batched_f32 with x_stride 0), at least two dispatches and `reps`
+    matvecs timed with HIP events. Also timed:
     one matvec per launch (the decoder's own launch, latency bound at these sizes), and the
     engine's exact group sums on int8 x checked bit for bit against integer numpy."""
     import ctypes
@@ -201,10 +201,10 @@ def matvec_microbench(reps=1000, rotate_bytes=512 << 20):
             _lib.call("trx_pack_ternary", rows.ptr, kind, M, K, 0, packed.ptr, None)
             for i in range(1, n):
                 _lib.call("trx_memcpy_d2d", packed.ptr + i * stride, packed.ptr, pb, None)
-            # One dispatch of at least `reps` matvecs y = W x cycling over the n copies (each copy
-            # is read again only after every other one: more than 512 MB apart), one x for all
-            # of them (x_stride 0: a block reuses its slice's table over several matrices).
-            nm = n * -(-reps // n)
+            # Dispatches of n matvecs y = W x, one per copy (no two blocks read one copy, and a
+            # copy is read again only a dispatch later, 512 MB on), at least `reps` in all, one x
+            # for all of them (x_stride 0: a block reuses its slice's table over several matrices).
+            nm = n
             x = r.standard_normal(K).astype(np.float32)
             xb = _lib.DeviceBuffer.from_array(x)
             yb = _lib.DeviceBuffer(4 * nm * M)
@@ -216,7 +216,7 @@ def matvec_microbench(reps=1000, rotate_bytes=512 << 20):
             def batched():
                 _lib.call("trx_gemv_packed_batched_f32", packed.ptr, stride, nm, n, kind, M, K, xb.ptr, 0, yb.ptr, M,
                           part.ptr, None)
-            n_launch = 2
+            n_launch = max(2, -(-reps // n))
             us = timed(batched, n_launch)
             # Correctness of the first and the last matvec of the dispatch (float64, 2e-6 of sum |w x|).
             y = yb.download(np.float32, nm * M).reshape(nm, M)
