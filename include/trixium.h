@@ -160,8 +160,9 @@ int trx_gemv_packed_f32_noalloc(const uint8_t* packed, int kind, int M, int K, c
  * i's packed copy (trx_pack_ternary) at packed + (i % n_copies) * mat_stride (a multiple of 256,
  * at least trx_pack_geometry's packed bytes; 1 <= n_copies <= n_mat), x_i at x + i * x_stride
  * (x 16-byte aligned, x_stride a multiple of 4 and >= K, or 0: one x for every matrix, whose
- * table a block then reuses over several matrices; the copies must then span under 2 GiB),
- * y_i at y + i * y_stride. M <= 16384.
+ * tables a block then reuses over several matrices, two K-slices per block; the copies must then
+ * span under 2 GiB, and a row's slices are summed in pairs: within rounding of, not bit for bit
+ * equal to, trx_gemv_packed_f32), y_i at y + i * y_stride. M <= 16384.
  * `workspace` holds trx_pack_batched_geometry's bytes of split-K partial sums (no zeroing
  * needed). */
 int trx_pack_batched_geometry(int kind, int M, int K, int n_mat, size_t* workspace_bytes);

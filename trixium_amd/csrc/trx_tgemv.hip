@@ -268,9 +268,7 @@ struct TgParams {
   uint32_t mat_bytes;
   int x_stride, part_sstride, part_mstride;
   int mat_copies;          // > 0: matrix i reads the packed copy i % mat_copies
-  // Several matrices per block (MULTI kernels): block y of ny takes matrices floor(y n_mat / ny)
-  // up to the next block's first, all with the same x (x_stride 0), so one table serves them.
-  int n_mat;
+  int n_mat;               // matrices of a batched launch with one x (the slice-pair kernel)
 };
 
 template <bool T5>
@@ -279,10 +277,74 @@ struct TgItem {
   uint32_t sc;        // the two fp16 group scales of this lane's row
 };
 
-template <bool T5, int NB, bool MULTI>
-__global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgParams p) {
+// The slice's lookup table from its 256 x values: T[b][c] = sum over the digits (codes) k of
+// byte b of (digit - 1) * x at table position c's k-th column, at tab[b * kTabCols + c]. T = hi(b)
+// + lo(b): lo from the low digits (trit5: b % 9; 2-bit: b & 15), hi from the rest (b / 9; b >> 4).
+// A thread owns one column: its x values and its lo sums in registers, then whole runs of entries
+// sharing one hi (waves take different hi values).
+template <bool T5>
+__device__ __forceinline__ void tg_build_table(float* tab, const float* xs, int tid) {
   constexpr int NLO = T5 ? 9 : 16;     // values of the low digits (trit5: 2 digits; 2-bit: 2 codes)
   constexpr int NHI = T5 ? 29 : 16;    // values of the rest (b / 9 <= 28; b >> 4)
+  const int c = tid & (kTabCols - 1);
+  int g, byte;
+  tg_position(T5, c, g, byte);
+  float u[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
+  if (g >= 0) {
+#pragma unroll
+    for (int k = 0; k < (T5 ? 5 : 4); ++k) {
+      const int cc = (T5 ? 5 : 4) * byte + k;
+      if (cc < kGroup) u[k] = xs[kGroup * g + cc];
+    }
+  }
+  float lo[NLO];
+#pragma unroll
+  for (int e = 0; e < NLO; ++e) {
+    const int d0 = T5 ? e % 3 : (e & 3), d1 = T5 ? e / 3 : (e >> 2);
+    lo[e] = (float)(d0 - 1) * u[0] + (float)(d1 - 1) * u[1];
+  }
+  for (int h = tid >> 6; h < NHI; h += kTgThreads / kTabCols) {
+    float hv;
+    if (T5) {
+      const int h1 = h / 3, h2 = h1 / 3;
+      hv = (float)(h - 3 * h1 - 1) * u[2] + (float)(h1 - 3 * h2 - 1) * u[3] + (float)(h2 % 3 - 1) * u[4];
+    } else {
+      hv = (float)((h & 3) - 1) * u[2] + (float)((h >> 2) - 1) * u[3];
+    }
+    float* col = tab + h * NLO * kTabCols + c;
+#pragma unroll
+    for (int e = 0; e < NLO; ++e)
+      if (h * NLO + e < 256) col[e * kTabCols] = lo[e] + hv;
+  }
+}
+
+// One item's row sums: lane l16 of a row group looks up its four code dwords (16 bytes of four
+// rows) in the table at tb (address = v_perm of the code byte and the lane's column: b * 256 +
+// col * 4, plus what sel's third byte takes from lw), then the row group's partial sums meet by
+// DPP; lane l16 ends with its group's sum of row mask(l16), times its fp16 group scale.
+__device__ __forceinline__ float tg_item_sum(const uint4 c, uint32_t scales, uint32_t sshift, const uint32_t* lw,
+                                             const uint32_t* sel, const char* tb) {
+  float a[4];
+  const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float t4[4];
+#pragma unroll
+    for (int jq = 0; jq < 4; ++jq) {
+      const uint32_t addr = __builtin_amdgcn_perm(cw[k], lw[jq], sel[jq]);
+      t4[jq] = *(const float*)(tb + addr);
+    }
+    a[k] = (t4[0] + t4[1]) + (t4[2] + t4[3]);
+  }
+  a[0] += dpp_f<kDppRowHalfMirror>(a[2]);
+  a[1] += dpp_f<kDppRowHalfMirror>(a[3]);
+  a[0] += dpp_f<kDppQuadXor2>(a[1]);
+  a[0] += dpp_f<kDppQuadXor1>(a[0]);
+  return a[0] * __half2float(__ushort_as_half((unsigned short)(scales >> sshift)));
+}
+
+template <bool T5, int NB>
+__global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgParams p) {
   __shared__ __align__(16) float tab[256 * kTabCols];
   __shared__ float xs[kSliceCols];
   __shared__ float red[16];
@@ -292,11 +354,8 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int s = blockIdx.x % p.S, j = blockIdx.x / p.S;
-  // MULTI: the matrices are spread evenly over the grid's y blocks (floor(y n_mat / ny) on).
-  const int mi = MULTI ? (int)(((long long)blockIdx.y * p.n_mat) / gridDim.y) : blockIdx.y;
-  const int mend = MULTI ? (int)(((long long)(blockIdx.y + 1) * p.n_mat) / gridDim.y) : mi + 1;
-  // Items of this block: tpb tiles of each of its matrices (one matrix unless MULTI).
-  const int n_items = p.tpb * (mend - mi);
+  const int mi = blockIdx.y;               // the matrix (batched launches)
+  const int n_items = p.tpb;               // row tiles of this block
   const int xmode = p.merge.o ? kXMerge : p.parts.in ? (p.parts.F ? kXSwiglu : kXResid) : kXPlain;
   // A gated-off launch does nothing but store the residual it was handed in partials. The gate
   // is read here and tested after the prologue's loads and the first weight loads are issued,
@@ -395,11 +454,9 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   // 2. The first NB - 1 items of this lane (they do not depend on x).
   const int rg = lane >> 4, l16 = lane & 15, half = l16 >> 3;
   const int dw = tg_lane_dword(T5, l16), msk = tg_lane_mask(l16);
-  const size_t mcopy = MULTI ? 0 : (size_t)(p.mat_copies > 0 ? mi % p.mat_copies : mi);
-  // MULTI: the descriptors span every copy, an item's copy goes in its scalar offset.
-  const uint32_t span = MULTI ? (uint32_t)(p.mat_copies - 1) * p.mat_bytes : 0u;
-  const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.codes + mcopy * p.mat_bytes, p.code_bytes + span);
-  const __amdgpu_buffer_rsrc_t rsc = make_rsrc(p.scales + mcopy * p.mat_bytes, p.scale_bytes + span);
+  const size_t mcopy = p.mat_copies > 0 ? mi % p.mat_copies : mi;
+  const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.codes + mcopy * p.mat_bytes, p.code_bytes);
+  const __amdgpu_buffer_rsrc_t rsc = make_rsrc(p.scales + mcopy * p.mat_bytes, p.scale_bytes);
   // Item n of this lane is quad quad0 + n * qstep. The lane's offsets stay in fixed VGPRs and
   // the item's step goes in the scalar offset, so no VGPR that an in-flight access reads is
   // rewritten (that would cost a vmcnt wait per item). Only the VGPR offset is relied on for the
@@ -415,38 +472,19 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   // the compiler's waits exact); the lanes that hold no row total store past the buffer (dropped
   // by the range check), and the items of a partial last tile land in padding rows.
   const __amdgpu_buffer_rsrc_t rpart = make_rsrc(p.part, (uint32_t)((size_t)p.S * p.part_sstride * 4));
-  const uint32_t po0 = (l16 & 9) == 0 ? ((uint32_t)s * p.part_sstride + (uint32_t)(MULTI ? 0 : mi) * p.part_mstride +
+  const uint32_t po0 = (l16 & 9) == 0 ? ((uint32_t)s * p.part_sstride + (uint32_t)mi * p.part_mstride +
                                          4u * (uint32_t)quad0 + msk) * 4u
                                       : kOut;
   const uint32_t pstep = (uint32_t)qstep * 16u;
-  // Offsets of the items, in scalar registers: item n is tile n of the block (loads past the
-  // block's last item re-read it). MULTI items run tile by tile through the block's matrices: a
-  // load cursor holds the next item's tile lt of matrix lm, read from copy lc. An item's
-  // partial-sum offset rides with it in the ring.
-  int ln = 0, lt = 0, lm = 0, lc = MULTI ? mi % p.mat_copies : 0;
+  // Item n is tile n of the block (loads past the block's last item re-read it); its offsets
+  // are scalar, and its partial-sum offset rides with it in the ring. (Non-temporal weight loads
+  // measured 0.6% slower in the decode.)
   auto load_next = [&](TgItem<T5>& it, int& pso, int n) {
-    int cso, sso;
-    if (MULTI) {
-      cso = lt * (int)cstep + lc * (int)p.mat_bytes;
-      sso = lt * (int)sstep + lc * (int)p.mat_bytes;
-      pso = lt * (int)pstep + (mi + lm) * p.part_mstride * 4;
-      const int adv = ln < n_items - 1 ? 1 : 0;
-      const int wrap = adv && lt + 1 == p.tpb ? 1 : 0;
-      ln += adv;
-      lt = wrap ? 0 : lt + adv;
-      lm += wrap;
-      lc = wrap && lc + 1 == p.mat_copies ? 0 : lc + wrap;
-    } else {
-      const int m = min(n, n_items - 1);
-      cso = m * (int)cstep;
-      sso = m * (int)sstep;
-      pso = m * (int)pstep;
-    }
-    // MULTI: non-temporal weight loads, so the caches keep the partial sums the reduction reads
-    // next (measured 5% faster there; in the decoder's launches 0.6% slower).
-    const auto a = __builtin_amdgcn_raw_buffer_load_b128(rc, co0, cso, MULTI ? kCpolNt : 0);
+    const int m = min(n, n_items - 1);
+    pso = m * (int)pstep;
+    const auto a = __builtin_amdgcn_raw_buffer_load_b128(rc, co0, m * (int)cstep, 0);
     it.c = make_uint4(a[0], a[1], a[2], a[3]);
-    it.sc = __builtin_amdgcn_raw_buffer_load_b32(rsc, so0, sso, MULTI ? kCpolNt : 0);
+    it.sc = __builtin_amdgcn_raw_buffer_load_b32(rsc, so0, m * (int)sstep, 0);
   };
   TgItem<T5> buf[NB];
   int rp[NB];
@@ -576,41 +614,7 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   if (p.norm_w && tid == 0)
     __hip_atomic_store(p.ss_out + j * p.S + s, (red[0] + red[1]) + (red[2] + red[3]), __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
-  {
-    // T[b][c] = hi(b) + lo(b): lo from the low digits (trit5: b % 9; 2-bit: b & 15), hi from the
-    // rest (b / 9; b >> 4). A thread owns one column: its x values and its lo sums in registers,
-    // then whole runs of entries sharing one hi (waves take different hi values).
-    const int c = tid & (kTabCols - 1);
-    int g, byte;
-    tg_position(T5, c, g, byte);
-    float u[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
-    if (g >= 0) {
-#pragma unroll
-      for (int k = 0; k < (T5 ? 5 : 4); ++k) {
-        const int cc = (T5 ? 5 : 4) * byte + k;
-        if (cc < kGroup) u[k] = xs[kGroup * g + cc];
-      }
-    }
-    float lo[NLO];
-#pragma unroll
-    for (int e = 0; e < NLO; ++e) {
-      const int d0 = T5 ? e % 3 : (e & 3), d1 = T5 ? e / 3 : (e >> 2);
-      lo[e] = (float)(d0 - 1) * u[0] + (float)(d1 - 1) * u[1];
-    }
-    for (int h = tid >> 6; h < NHI; h += kTgThreads / kTabCols) {
-      float hv;
-      if (T5) {
-        const int h1 = h / 3, h2 = h1 / 3;
-        hv = (float)(h - 3 * h1 - 1) * u[2] + (float)(h1 - 3 * h2 - 1) * u[3] + (float)(h2 % 3 - 1) * u[4];
-      } else {
-        hv = (float)((h & 3) - 1) * u[2] + (float)((h >> 2) - 1) * u[3];
-      }
-      float* col = tab + h * NLO * kTabCols + c;
-#pragma unroll
-      for (int e = 0; e < NLO; ++e)
-        if (h * NLO + e < 256) col[e * kTabCols] = lo[e] + hv;
-    }
-  }
+  tg_build_table<T5>(tab, xs, tid);
   __syncthreads();
 
   // 4. The items: four rows x one dword per lane; sixteen lanes per row group.
@@ -626,29 +630,12 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   const char* tb = (const char*)tab;
   const uint32_t sshift = 16u * (uint32_t)half;       // this lane's group scale in the dword
   auto compute = [&](const TgItem<T5>& it, int pso) {
-    float a[4];
-    const uint32_t cw[4] = {it.c.x, it.c.y, it.c.z, it.c.w};
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      float t4[4];
-#pragma unroll
-      for (int jq = 0; jq < 4; ++jq) {
-        const uint32_t addr = __builtin_amdgcn_perm(cw[k], lw[jq], sel[jq]);  // b * 256 + col * 4
-        t4[jq] = *(const float*)(tb + addr);
-      }
-      a[k] = (t4[0] + t4[1]) + (t4[2] + t4[3]);
-    }
-    a[0] += dpp_f<kDppRowHalfMirror>(a[2]);
-    a[1] += dpp_f<kDppRowHalfMirror>(a[3]);
-    a[0] += dpp_f<kDppQuadXor2>(a[1]);
-    a[0] += dpp_f<kDppQuadXor1>(a[0]);
-    float v = a[0] * __half2float(__ushort_as_half((unsigned short)(it.sc >> sshift)));
+    float v = tg_item_sum(it.c, it.sc, sshift, lw, sel, tb);
     v += dpp_f<kDppRowRor8>(v);                      // the other group (lane l16 ^ 8)
-    // MULTI partial sums are for a later launch: plain write-back stores (the kernel boundary
-    // makes them visible). Otherwise agent-scope stores (sc1): the tile's reducing block may run
-    // on another XCD. (One store either way: a branch between two kinds of store would leave the
-    // compiler's vmcnt counts short, and every item would wait for the next item's loads.)
-    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), rpart, po0, pso, MULTI ? 0 : kCpolSc1);
+    // Agent-scope store (sc1): the tile's reducing block may run on another XCD. (One kind of
+    // store: a branch between two kinds would leave the compiler's vmcnt counts short, and every
+    // item would also wait for the next item's loads.)
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), rpart, po0, pso, kCpolSc1);
   };
   // Whole groups of NB items (a loop with one exit keeps the compiler's vmcnt waits exact: item
   // n waits only for itself), then the remaining < NB items, already in flight.
@@ -797,6 +784,135 @@ struct RdParams {
   const int* gate_from;
 };
 
+// Batched matvecs with one x for every matrix (x_stride 0): block (q, y) builds the tables of
+// slices 2q and 2q + 1 once, then streams those two slices of its share of the (matrix, tile)
+// items (a contiguous run of the n_mat * tpb of them, y-th of ny), summing each row's two slices
+// before it stores the partial sum: half the partial sums of one slice per block (their traffic
+// to memory costs the batched launch more than their bytes). The two tables sit at LDS addresses
+// 0 and 64 KB, so a code byte's lookup address is still one v_perm: the second table's selector
+// takes a third address byte (1) from the lane's column word. The partial sums, [S2][n_mat]
+// [rows_p] for S2 = ceil(S/2) slice pairs, are for a later launch (plain stores). A missing
+// second slice (odd S) re-reads the first and adds nothing.
+template <bool T5, int NB>
+__global__ __launch_bounds__(kTgThreads, 1) void tgemv_pair_kernel(TgParams p) {
+  constexpr int kTab = 256 * kTabCols;          // floats per table
+  __shared__ __align__(16) float tab[2 * kTab];
+  __shared__ float xs[2 * kSliceCols];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int s = 2 * blockIdx.x;                 // the block's first slice
+  const bool two = s + 1 < p.S;
+  // The block's items: a contiguous share of the n_mat * tpb (matrix, tile) items.
+  const long long tot = (long long)p.n_mat * p.tpb;
+  const int i0 = (int)((blockIdx.y * tot) / gridDim.y), i1 = (int)(((blockIdx.y + 1) * tot) / gridDim.y);
+  const int n_items = i1 - i0, mi = i0 / p.tpb;
+
+  // 1. The two slices' 512 x values, loaded before the weight stream (vmcnt completes in order).
+  const int cx = s * kSliceCols + tid;
+  const float xv = tid < 2 * kSliceCols && cx < p.K ? p.x[cx] : 0.f;
+
+  // 2. The first NB - 1 items (they do not depend on x). The next item to load is tile lt of
+  //    matrix mi + lm (tiles run through each matrix in turn from the block's first item), read
+  //    from copy lc; its second slice lies one slice of codes (scales) further. The offsets stay
+  //    in scalar registers.
+  const int rg = lane >> 4, l16 = lane & 15, half = l16 >> 3;
+  const int dw = tg_lane_dword(T5, l16), msk = tg_lane_mask(l16);
+  const uint32_t span = (uint32_t)(p.mat_copies - 1) * p.mat_bytes;
+  const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.codes, p.code_bytes + span);
+  const __amdgpu_buffer_rsrc_t rsc = make_rsrc(p.scales, p.scale_bytes + span);
+  const int quad0 = w * 4 + rg;                 // one block per slice pair covers every tile
+  const uint32_t co0 = (((uint32_t)s * p.Q + (uint32_t)quad0) * p.D + dw) * 16u;
+  const uint32_t cstep = (uint32_t)kTileQuads * p.D * 16u;
+  const uint32_t so0 = ((uint32_t)s * p.M4 + 4u * (uint32_t)quad0 + msk) * 4u;
+  const uint32_t sstep = (uint32_t)kTileQuads * 16u;
+  const int c2 = two ? (int)(p.Q * p.D * 16u) : 0, s2 = two ? (int)(p.M4 * 4u) : 0;
+  constexpr uint32_t kOut = 0x40000000u;
+  const int S2 = (p.S + 1) / 2;
+  const __amdgpu_buffer_rsrc_t rpart = make_rsrc(p.part, (uint32_t)((size_t)S2 * p.part_sstride * 4));
+  const uint32_t po0 = (l16 & 9) == 0 ? ((uint32_t)blockIdx.x * p.part_sstride + 4u * (uint32_t)quad0 + msk) * 4u : kOut;
+  const uint32_t pstep = (uint32_t)kTileQuads * 16u;
+  struct Item {
+    uint4 c0, c1;        // the dwords of four rows in the two slices
+    uint32_t s0, s1;     // their fp16 group-scale pairs
+  };
+  int ln = 0, lt = i0 - mi * p.tpb, lm = 0, lc = mi % p.mat_copies;
+  auto load_next = [&](Item& it, int& pso) {
+    const int cso = lt * (int)cstep + lc * (int)p.mat_bytes;
+    const int sso = lt * (int)sstep + lc * (int)p.mat_bytes;
+    pso = lt * (int)pstep + (mi + lm) * p.part_mstride * 4;
+    const auto a = __builtin_amdgcn_raw_buffer_load_b128(rc, co0, cso, kCpolNt);
+    const auto b = __builtin_amdgcn_raw_buffer_load_b128(rc, co0, cso + c2, kCpolNt);
+    it.c0 = make_uint4(a[0], a[1], a[2], a[3]);
+    it.c1 = make_uint4(b[0], b[1], b[2], b[3]);
+    it.s0 = __builtin_amdgcn_raw_buffer_load_b32(rsc, so0, sso, kCpolNt);
+    it.s1 = __builtin_amdgcn_raw_buffer_load_b32(rsc, so0, sso + s2, kCpolNt);
+    const int adv = ln < n_items - 1 ? 1 : 0;   // past the last item: re-read it
+    const int wrap = adv && lt + 1 == p.tpb ? 1 : 0;
+    ln += adv;
+    lt = wrap ? 0 : lt + adv;
+    lm += wrap;
+    lc = wrap && lc + 1 == p.mat_copies ? 0 : lc + wrap;
+  };
+  Item buf[NB];
+  int rp[NB];
+  // Each prefetch is followed by a store that the range check drops, as each item's loads are
+  // followed by its partial-sum store in the loop (so the loop's vmcnt waits stay exact).
+#pragma unroll
+  for (int b = 0; b < NB - 1; ++b) {
+    load_next(buf[b], rp[b]);
+    __builtin_amdgcn_raw_buffer_store_b32(0u, rpart, 0xfffffff0u, 0, 0);
+  }
+
+  // 3. The two tables.
+  if (tid < 2 * kSliceCols) xs[tid] = xv;
+  __syncthreads();
+  tg_build_table<T5>(tab, xs, tid);
+  tg_build_table<T5>(tab + kTab, xs + kSliceCols, tid);
+  __syncthreads();
+
+  // 4. The items (as in the single-slice kernel, once per slice).
+  uint32_t lw[4], sel0[4], sel1[4];
+#pragma unroll
+  for (int jq = 0; jq < 4; ++jq) {
+    const int jj = (jq + rg + 2 * half) & 3;
+    lw[jq] = (uint32_t)(4 * l16 + jj) * 4u | 0x10000u;      // third byte: the second table
+    sel0[jq] = 0x0c0c0400u | ((uint32_t)jj << 8);            // address bytes: col*4, b, 0, 0
+    sel1[jq] = 0x0c020400u | ((uint32_t)jj << 8);            // col*4, b, 1, 0
+  }
+  const char* tb = (const char*)tab;
+  const uint32_t sshift = 16u * (uint32_t)half;
+  auto compute = [&](const Item& it, int pso) {
+    float v0 = tg_item_sum(it.c0, it.s0, sshift, lw, sel0, tb);
+    float v1 = tg_item_sum(it.c1, it.s1, sshift, lw, sel1, tb);
+    v0 += dpp_f<kDppRowRor8>(v0);               // the slice's other group (lane l16 ^ 8)
+    v1 += dpp_f<kDppRowRor8>(v1);
+    const float v = two ? v0 + v1 : v0;
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), rpart, po0, pso, 0);
+  };
+  // The first group of NB items peeled off the loop (exact vmcnt waits in the loop), then the
+  // remaining < NB items, already in flight.
+  int n = 0;
+  const int ngroups = n_items / NB;
+  auto group = [&]() {
+#pragma unroll
+    for (int ph = 0; ph < NB; ++ph) {
+      load_next(buf[(ph + NB - 1) % NB], rp[(ph + NB - 1) % NB]);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(buf[ph], rp[ph]);
+      ++n;
+    }
+  };
+  if (ngroups > 0) {
+    group();
+    for (int gi = 1; gi < ngroups; ++gi) group();
+  }
+  const int rem = n_items - n;
+#pragma unroll
+  for (int ph = 0; ph < NB - 1; ++ph) {
+    if (ph < rem) compute(buf[ph], rp[ph]);
+  }
+}
+
 __global__ __launch_bounds__(kRdThreads) void tgemv_reduce_kernel(RdParams p) {
   __shared__ unsigned long long kmax[kRdThreads / 64];
   // The gate is read with the partials (a gated-off launch drops them) rather than before them.
@@ -893,9 +1009,9 @@ int tgemv_reduce_f32(const float* part, const float* ss, int S, int rows_p, int 
 int tgemv_partial_slices_max() { return kSwiPartMax; }
 int tgemv_resid_slices_max() { return kResPartMax; }
 
-template <bool T5, bool MULTI = false>
+template <bool T5>
 static const void* tg_fn() {
-  return (const void*)tgemv_kernel<T5, 4, MULTI>;
+  return (const void*)tgemv_kernel<T5, 4>;
 }
 
 int tgemv_f32(const uint8_t* packed, int kind, int M, int K, const float* x, const float* norm_w,
@@ -1027,25 +1143,26 @@ int tgemv_f32_batched(const uint8_t* packed, size_t mat_stride, int n_mat, int n
   p.part_mstride = g.rows_p;
   p.mat_copies = n_copies;
   p.n_mat = n_mat;
-  int ny = n_mat;
+  int nx = g.S, ny = n_mat;
   const void* fn = kind == TRX_KIND_TERNARY5 ? tg_fn<true>() : tg_fn<false>();
   if (multi) {
-    // Matrices spread evenly over ny groups, ny a multiple of cus / gcd(S, cus) so the grid's
-    // S * ny blocks fill whole rounds of the GPU: two rounds (measured 3% better than one, and
-    // than at most 16 matrices per block with a partial last round).
+    // Blocks of slice pairs; the (matrix, tile) items spread evenly over ny groups, ny =
+    // cus / gcd(S2, cus) so the grid's S2 * ny blocks fill whole rounds of the GPU (one round
+    // when S2 divides the CU count; measured best of one to four rounds).
     const int cus = cu_count();
     if (cus <= 0) return TRX_E_HIP;
-    int a = g.S, b = cus;
+    nx = (g.S + 1) / 2;
+    int a = nx, b = cus;
     while (b) { const int t = a % b; a = b; b = t; }
-    ny = std::max(1, std::min(n_mat, 2 * (cus / a)));
-    fn = kind == TRX_KIND_TERNARY5 ? tg_fn<true, true>() : tg_fn<false, true>();
+    ny = std::max(1, std::min(n_mat * g.tpb, cus / a));
+    fn = kind == TRX_KIND_TERNARY5 ? (const void*)tgemv_pair_kernel<true, 4> : (const void*)tgemv_pair_kernel<false, 4>;
   }
   void* args[] = {(void*)&p};
-  TRX_HIP(hipLaunchKernel(fn, dim3(g.S, ny), dim3(kTgThreads), args, 0, s));
+  TRX_HIP(hipLaunchKernel(fn, dim3(nx, ny), dim3(kTgThreads), args, 0, s));
   // The S partial sums of every row of every matrix, reduced over the whole GPU.
   RdParams r = {};
   r.part = part;
-  r.S = g.S;
+  r.S = nx;                      // slices, or slice pairs
   r.rows_p = n_mat * g.rows_p;
   r.M = n_mat * g.rows_p;
   r.K = K;
