@@ -94,6 +94,10 @@ __device__ __forceinline__ float wave_max(float v) {
 // the row's sum (or maximum).
 constexpr int kDppQuadXor1 = 0xB1, kDppQuadXor2 = 0x4E, kDppRowHalfMirror = 0x141, kDppRowMirror = 0x140;
 
+// Matrix-core operand and accumulator types (v_mfma_f32_32x32x16_f16).
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
 template <int CTRL>
 __device__ __forceinline__ int dpp_i(int v) {
   return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);

@@ -13,9 +13,6 @@
 
 namespace trx {
 
-typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-
 // GEMM ------------------------------------------------------------------------------------------
 
 constexpr int kGmThreads = 256;
