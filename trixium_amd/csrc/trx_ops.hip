@@ -691,10 +691,11 @@ int attention_max_chunk(int head_dim) {
 }
 
 int attention_splits(int n_kv, int head_dim, int max_ctx) {
-  // Enough blocks to cover the CUs, and at most the register-held positions per block.
+  // Enough blocks to cover the CUs, but at most 32 (the splits the o projection's prologue
+  // merges, saving a merge launch) unless the register-held positions per block need more.
   int cap = head_dim == 64 ? attn_max_chunk<64>() : head_dim == 128 ? attn_max_chunk<128>()
                                                                       : attn_max_chunk<256>();
-  int s = min(cdiv(256, n_kv > 0 ? n_kv : 1), 64);
+  int s = min(cdiv(256, n_kv > 0 ? n_kv : 1), 32);
   if (cdiv(max_ctx, s) > cap) s = cdiv(max_ctx, cap);
   return s > 64 ? -1 : s;
 }
