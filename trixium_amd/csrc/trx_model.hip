@@ -75,6 +75,8 @@ struct Model {
   int o_S = 0, o_rows_p = 0;
   float* down_part = nullptr;
   int down_S = 0, down_rows_p = 0;
+  float* dn_out_part = nullptr;                    // DeltaNet out projection -> the FFN's gate|up
+  int dn_out_S = 0, dn_out_rows_p = 0;
   float* head_part = nullptr;                      // LM head: partial sums reduced by many blocks
   float* head_ss = nullptr;
   int head_S = 0, head_rows_p = 0;
@@ -264,6 +266,8 @@ static int plan_packed(Model& m) {
     if ((rc = part_buf(E, c.n_head * hd, &m.o_part, &m.o_S, &m.o_rows_p, nullptr, wk))) return rc;
   if ((ops & TRX_PACK_DOWN) && cdiv(F, kSliceCols) <= tgemv_resid_slices_max())
     if ((rc = part_buf(E, F, &m.down_part, &m.down_S, &m.down_rows_p, nullptr, wk))) return rc;
+  if ((ops & TRX_PACK_DN) && (ops & TRX_PACK_GATE_UP) && m.n_dn > 0 && cdiv(nvh, kSliceCols) <= tgemv_resid_slices_max())
+    if ((rc = part_buf(E, nvh, &m.dn_out_part, &m.dn_out_S, &m.dn_out_rows_p, nullptr, wk))) return rc;
   for (auto& e : list)
     if (e.first.first == OP_HEAD &&
         (rc = part_buf(c.vocab, E, &m.head_part, &m.head_S, &m.head_rows_p, &m.head_ss, e.second.kind)))
@@ -341,7 +345,12 @@ static int projection(Model& m, int op, int l, const uint8_t* rows, int kind, in
 
 // Gated DeltaNet layer: [qkv|z] GEMV and the beta/alpha Q8 GEMV (both with the attention
 // RMSNorm), conv, recurrence with the gated norm, then the out projection with the residual.
-int dn_layer_launch(Model& m, int l, hipStream_t s) {
+// With the packed [qkv|z] and out GEMVs (pz, pdo): [qkv|z] reads x = xin, or xres + the partial
+// sums pp (its prologue stores that x to xres for the Q8 GEMV); the out projection adds into
+// m.x from xres, or (hand) stores its partial sums to dn_out_part. Otherwise x is m.x.
+int dn_layer_launch(Model& m, int l, hipStream_t s, const PackedMat* pz = nullptr, const PackedMat* pdo = nullptr,
+                    const float* xin = nullptr, const PartialSums* pp = nullptr, const float* xres = nullptr,
+                    bool hand = false) {
   const trx_model_config& c = m.cfg;
   const int E = c.n_embd;
   const int nq = c.dn_num_k_heads * c.dn_k_head_dim, nvh = c.dn_num_v_heads * c.dn_v_head_dim;
@@ -350,8 +359,14 @@ int dn_layer_launch(Model& m, int l, hipStream_t s) {
   int rc;
   float* io = m.dn_io;                  // [C + nvh] projections
   float* conv_out = m.dn_io + C + nvh;  // [C]
-  if ((rc = projection(m, OP_DN_QKVZ, l, P(m, TRX_ROLE_ATTN_QKV, l), c.weight_kind, C + nvh, E, m.x,
-                        PF(m, TRX_ROLE_ATTN_NORM, l), io, TRX_EPI_STORE, nullptr, s))) return rc;
+  const float* x = pz ? xres : m.x;
+  if (pz) {
+    if ((rc = tgemv_f32(pz->buf, c.weight_kind, C + nvh, E, xin, PF(m, TRX_ROLE_ATTN_NORM, l), c.rms_eps, io,
+                        TRX_EPI_STORE, nullptr, nullptr, m.pack_work, s, nullptr, nullptr, nullptr, pp))) return rc;
+  } else if ((rc = projection(m, OP_DN_QKVZ, l, P(m, TRX_ROLE_ATTN_QKV, l), c.weight_kind, C + nvh, E, m.x,
+                               PF(m, TRX_ROLE_ATTN_NORM, l), io, TRX_EPI_STORE, nullptr, s))) {
+    return rc;
+  }
   DenseParams dp = {};
   dp.W = P(m, TRX_ROLE_SSM_BETA, l);
   dp.kind = TRX_KIND_Q8;
@@ -359,7 +374,7 @@ int dn_layer_launch(Model& m, int l, hipStream_t s) {
   dp.K = E;
   dp.row_bytes = kBeat * cdiv(E / 32, 16) + E;
   dp.code_off = kBeat * cdiv(E / 32, 16);
-  dp.x = m.x;
+  dp.x = x;
   dp.norm_w = PF(m, TRX_ROLE_ATTN_NORM, l);
   dp.eps = c.rms_eps;
   dp.y = m.dn_ba;
@@ -390,6 +405,15 @@ int dn_layer_launch(Model& m, int l, hipStream_t s) {
   rp.hv = c.dn_v_head_dim;
   rp.eps = c.rms_eps;
   if ((rc = launch_dn_recur(rp, s))) return rc;
+  if (pdo && hand) {
+    PartialSums out = {};
+    out.out = m.dn_out_part;
+    return tgemv_f32(pdo->buf, c.weight_kind, E, nvh, m.dn_out, nullptr, c.rms_eps, nullptr, TRX_EPI_STORE, nullptr,
+                     nullptr, m.pack_work, s, nullptr, nullptr, nullptr, &out);
+  }
+  if (pdo)
+    return tgemv_f32(pdo->buf, c.weight_kind, E, nvh, m.dn_out, nullptr, c.rms_eps, m.x, TRX_EPI_RESID, xres, nullptr,
+                     m.pack_work, s);
   return projection(m, OP_DN_OUT, l, P(m, TRX_ROLE_SSM_OUT, l), c.weight_kind, E, nvh, m.dn_out, nullptr,
                     m.x, TRX_EPI_RESID, m.x, s);
 }
@@ -465,12 +489,28 @@ static int run_step(Model& m, hipStream_t s) {
   // Whether the residual after layer l goes to a packed GEMV that takes the producer's S slices.
   auto next_packed = [&](int l, int S) {
     if (S > tgemv_resid_slices_max()) return false;
-    if (l + 1 < c.n_layer) return !m.is_dn(l + 1) && packed(OP_QKV, l + 1) != nullptr;
+    if (l + 1 < c.n_layer) return packed(m.is_dn(l + 1) ? OP_DN_QKVZ : OP_QKV, l + 1) != nullptr;
     return packed(OP_HEAD, 0) != nullptr;
   };
 
   for (int l = 0; l < c.n_layer; ++l) {
-    if (m.is_dn(l)) {
+    if (m.is_dn(l) && packed(OP_DN_QKVZ, l) && packed(OP_DN_OUT, l)) {
+      // Gated DeltaNet mixer on the packed GEMVs: [qkv|z] takes the residual (or the previous
+      // down's partial sums added to it), and the out projection hands its partial sums to the
+      // FFN's gate|up when that is packed too.
+      const float* xin;
+      const PartialSums* pp = take(xin);
+      const PackedMat* pdo = packed(OP_DN_OUT, l);
+      const bool hand = m.dn_out_part && packed(OP_GATE_UP, l);
+      if ((rc = dn_layer_launch(m, l, s, packed(OP_DN_QKVZ, l), pdo, xin, pp, xc, hand))) return rc;
+      if (hand) {
+        pend.in = m.dn_out_part;
+        pend.S = m.dn_out_S;
+        pend.rows_p = m.dn_out_rows_p;
+      } else {
+        xc = m.x;
+      }
+    } else if (m.is_dn(l)) {
       if ((rc = dn_layer_launch(m, l, s))) return rc;
     } else {
       // q|k|v with the attention RMSNorm fused in the prologue.

@@ -229,7 +229,7 @@ constexpr int kCpolSc1 = 16;          // buffer cache policy: device (agent) sco
 constexpr int kCpolNt = 2;            // buffer cache policy: non-temporal (streaming)
 constexpr int kMergeMax = 32;          // attention splits the merging prologue takes
 constexpr int kSwiPartMax = 32;        // gate|up slices the SwiGLU prologue takes
-constexpr int kResPartMax = 64;        // producer slices the residual prologue takes
+constexpr int kResPartMax = 80;        // producer slices the residual prologue takes (68: 17408-wide down)
 // Partial-sum prologues load 16 bytes per thread and slice: the SwiGLU one a packed row quad
 // (128 per slice, so 8 slices per pass of the block), the residual one 4 columns (64 per slice,
 // 16 slices per pass).
