@@ -8,31 +8,50 @@
 
 #include "trx_internal.h"
 #include "trx_ops.h"
+#include "trx_dense_dev.h"
 
 namespace trx {
 
-// One block per head-sized segment of the qkv channels (q heads, then k heads, then v heads).
-__global__ void dn_conv_kernel(DnConvParams p) {
-  extern __shared__ float red[];
-  const int seg = blockIdx.x, t = threadIdx.x;
-  const int c = seg * p.hk + t;
-  const float x = p.qkv[c];
-  float acc = 0.f;
-  for (int i = 0; i < p.Kc - 1; ++i) acc += p.taps[c * p.Kc + i] * p.state[(size_t)i * p.C + c];
-  acc += p.taps[c * p.Kc + p.Kc - 1] * x;
-  for (int i = 0; i + 1 < p.Kc - 1; ++i) p.state[(size_t)i * p.C + c] = p.state[(size_t)(i + 1) * p.C + c];
-  if (p.Kc > 1) p.state[(size_t)(p.Kc - 2) * p.C + c] = x;
-  float y = silu(acc);
-  if (c < 2 * p.nq) {
+// Conv of one head-sized segment of the qkv channels (q heads, then k heads, then v heads): thread
+// t < hk takes channel seg * hk + t; every thread of the block (blockDim >= hk, a multiple of 64)
+// calls this, the ones past hk only for the L2 norm's barrier.
+__device__ __forceinline__ void dn_conv_seg(const DnConvParams& p, int seg, int t, float* red) {
+  const bool on = t < p.hk;
+  const int c = seg * p.hk + (on ? t : 0);
+  float y = 0.f;
+  if (on) {
+    const float x = p.qkv[c];
+    float acc = 0.f;
+    for (int i = 0; i < p.Kc - 1; ++i) acc += p.taps[c * p.Kc + i] * p.state[(size_t)i * p.C + c];
+    acc += p.taps[c * p.Kc + p.Kc - 1] * x;
+    for (int i = 0; i + 1 < p.Kc - 1; ++i) p.state[(size_t)i * p.C + c] = p.state[(size_t)(i + 1) * p.C + c];
+    if (p.Kc > 1) p.state[(size_t)(p.Kc - 2) * p.C + c] = x;
+    y = silu(acc);
+  }
+  if (seg * p.hk < 2 * p.nq) {
     // L2 norm over the key/query head (x / max(|x|, eps), fastref.py:146-148).
     float ss = wave_sum(y * y);
     if ((t & 63) == 0) red[t >> 6] = ss;
     __syncthreads();
     float tot = 0.f;
-    for (int i = 0; i < (blockDim.x + 63) / 64; ++i) tot += red[i];
+    for (int i = 0; i < (int)(blockDim.x + 63) / 64; ++i) tot += red[i];
     y = y / fmaxf(sqrtf(tot), p.eps);
   }
-  p.out[c] = y;
+  if (on) p.out[c] = y;
+}
+
+// One block per head-sized segment of the qkv channels.
+__global__ void dn_conv_kernel(DnConvParams p) {
+  extern __shared__ float red[];
+  dn_conv_seg(p, blockIdx.x, threadIdx.x, red);
+}
+
+// The conv segments and the beta/alpha rows in one launch (both read only the [qkv|z] GEMV's
+// output and the residual): blocks below n_seg take a conv segment, the rest a Q8 row each.
+__global__ __launch_bounds__(256) void dn_conv_q8_kernel(DnConvParams cp, DenseParams dp, int n_seg) {
+  __shared__ float red[2][4];
+  if ((int)blockIdx.x < n_seg) dn_conv_seg(cp, blockIdx.x, threadIdx.x, red[0]);
+  else q8_row_dot(dp, blockIdx.x - n_seg, threadIdx.x, red);
 }
 
 // One block per value head; threads split the head's rows (hv) and columns (hk).
@@ -152,6 +171,17 @@ __global__ __launch_bounds__(NW * 64) void dn_recur_fixed_kernel(DnRecurParams p
 int launch_dn_conv(const DnConvParams& p, hipStream_t s) {
   TRX_CHECK(p.hk <= 256 && p.C % p.hk == 0, TRX_E_INVALID, "deltanet conv: head dim %d", p.hk);
   hipLaunchKernelGGL(dn_conv_kernel, dim3(p.C / p.hk), dim3(p.hk), 8 * sizeof(float), s, p);
+  TRX_LAUNCHED();
+  return TRX_OK;
+}
+
+int launch_dn_conv_q8(const DnConvParams& cp, const DenseParams& dp, hipStream_t s) {
+  TRX_CHECK(cp.hk <= 256 && cp.C % cp.hk == 0 && dp.kind == TRX_KIND_Q8 && !dp.amax_slot && !dp.gate_pos &&
+            dp.K % 32 == 0 && dp.code_off % 16 == 0 && dp.row_bytes % 16 == 0 &&
+            ((uintptr_t)dp.W | (uintptr_t)dp.x | (uintptr_t)dp.norm_w) % 16 == 0,
+            TRX_E_INVALID, "deltanet conv + beta/alpha: unsupported geometry");
+  const int n_seg = cp.C / cp.hk;
+  hipLaunchKernelGGL(dn_conv_q8_kernel, dim3(n_seg + dp.M), dim3(256), 0, s, cp, dp, n_seg);
   TRX_LAUNCHED();
   return TRX_OK;
 }

@@ -378,7 +378,6 @@ int dn_layer_launch(Model& m, int l, hipStream_t s, const PackedMat* pz = nullpt
   dp.norm_w = PF(m, TRX_ROLE_ATTN_NORM, l);
   dp.eps = c.rms_eps;
   dp.y = m.dn_ba;
-  if ((rc = launch_dense_gemv(dp, s))) return rc;
   DnConvParams cp = {};
   cp.qkv = io;
   cp.taps = PF(m, TRX_ROLE_SSM_CONV, l);
@@ -389,7 +388,14 @@ int dn_layer_launch(Model& m, int l, hipStream_t s, const PackedMat* pz = nullpt
   cp.nq = nq;
   cp.hk = c.dn_k_head_dim;
   cp.eps = c.rms_eps;
-  if ((rc = launch_dn_conv(cp, s))) return rc;
+  // One launch for both when the combined kernel takes them (aligned Q8 rows), else two.
+  const bool fused = c.dn_k_head_dim <= 256 && C % c.dn_k_head_dim == 0 && E % 32 == 0 && dp.code_off % 16 == 0 &&
+                     dp.row_bytes % 16 == 0 && ((uintptr_t)dp.W | (uintptr_t)dp.x | (uintptr_t)dp.norm_w) % 16 == 0;
+  if (fused) {
+    if ((rc = launch_dn_conv_q8(cp, dp, s))) return rc;
+  } else if ((rc = launch_dense_gemv(dp, s)) || (rc = launch_dn_conv(cp, s))) {
+    return rc;
+  }
   DnRecurParams rp = {};
   rp.conv = conv_out;
   rp.z = io + C;

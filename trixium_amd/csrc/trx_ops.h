@@ -103,6 +103,9 @@ struct RotParams {
 
 int launch_rotate(const RotParams& p, hipStream_t s);
 int launch_dn_conv(const DnConvParams& p, hipStream_t s);
+// The conv and a Q8 GEMV (the beta/alpha rows) in one launch; TRX_E_INVALID for a geometry or
+// layout the combined kernel does not take.
+int launch_dn_conv_q8(const DnConvParams& cp, const DenseParams& dp, hipStream_t s);
 int launch_dn_recur(const DnRecurParams& p, hipStream_t s);
 // Sampling of the next token (firmware/infer.c:385-488): the candidates are the maxima of 32 row
 // ranges of every channel's vocabulary shard; a repetition penalty over the last `window` tokens,
