@@ -16,7 +16,7 @@ namespace trx {
 // GEMM ------------------------------------------------------------------------------------------
 
 constexpr int kGmThreads = 256;
-constexpr int kGmBR = 64;                  // positions per block
+constexpr int kGmBR = 128;                 // positions per block
 constexpr int kGmBM = 256;                 // weight rows per block
 constexpr int kGmLd = kGroup + 8;          // LDS row stride in halves (272 bytes)
 
@@ -110,16 +110,17 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
       raw.sc = __builtin_amdgcn_raw_buffer_load_b32(rw, rbase + 2u * (4u * (uint32_t)g + 2u * (uint32_t)shalf), 0, 0);
     }
   };
-  uint4 xr[8];
+  constexpr int XQ = kGmBR * 16 / kGmThreads;      // 16-byte x pieces per thread and plane
+  uint4 xr[2 * XQ];
   auto load_x = [&](int g) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < XQ; ++q) {
       const int piece = tid + kGmThreads * q, row = piece >> 4, c16 = piece & 15;
       const uint32_t off = ((uint32_t)(r0 + row) * (uint32_t)p.K + (uint32_t)(kGroup * g + 8 * c16)) * 2u;
       const auto a = __builtin_amdgcn_raw_buffer_load_b128(rxh, off, 0, 0);
       const auto b = __builtin_amdgcn_raw_buffer_load_b128(rxl, off, 0, 0);
       xr[q] = make_uint4(a[0], a[1], a[2], a[3]);
-      xr[4 + q] = make_uint4(b[0], b[1], b[2], b[3]);
+      xr[XQ + q] = make_uint4(b[0], b[1], b[2], b[3]);
     }
   };
   // Decoded weights of this thread's 64 codes: 32 dwords of fp16 pairs, times the scale.
@@ -209,22 +210,23 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
   };
   auto stage_x = [&]() {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < XQ; ++q) {
       const int piece = tid + kGmThreads * q, row = piece >> 4, c16 = piece & 15;
       *(uint4*)(xs[0] + row * kGmLd + 8 * c16) = xr[q];
-      *(uint4*)(xs[1] + row * kGmLd + 8 * c16) = xr[4 + q];
+      *(uint4*)(xs[1] + row * kGmLd + 8 * c16) = xr[XQ + q];
     }
   };
 
-  // Wave tiles: positions 32 wr .. + 31 of the block; four weight column tiles of 32 (SwiGLU: two
-  // gate tiles and the two up tiles of the same features).
+  // Wave tiles: positions 64 wr .. + 63 of the block (two tiles of 32); four weight column tiles
+  // of 32 (SwiGLU: two gate tiles and the two up tiles of the same features). Per 16-column step a
+  // wave reads 4 A and 4 B fragments for 16 MFMAs.
   const int wr = w & 1, wm = w >> 1;
   int ct[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t)
     ct[t] = EPI == GM_SWIGLU ? (t >> 1) * (kGmBM / 2) + 64 * wm + 32 * (t & 1) : 128 * wm + 32 * t;
   const int li = lane & 31, lk = 8 * (lane >> 5);
-  f32x16_t acc[4] = {};
+  f32x16_t acc[2][4] = {};
 
   GmRaw<KIND> raw[2];
   load_w(raw[0], 0, 0);
@@ -244,38 +246,47 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
 #pragma unroll
     for (int kk = 0; kk < kGroup / 16; ++kk) {
       const int k = 16 * kk + lk;
-      const half8_t ah = *(const half8_t*)(xs[0] + (32 * wr + li) * kGmLd + k);
-      const half8_t al = *(const half8_t*)(xs[1] + (32 * wr + li) * kGmLd + k);
-      half8_t b[4];
+      half8_t ah[2], al[2], b[4];
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        ah[a] = *(const half8_t*)(xs[0] + (64 * wr + 32 * a + li) * kGmLd + k);
+        al[a] = *(const half8_t*)(xs[1] + (64 * wr + 32 * a + li) * kGmLd + k);
+      }
 #pragma unroll
       for (int t = 0; t < 4; ++t) b[t] = *(const half8_t*)(ws + (ct[t] + li) * kGmLd + k);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b[t], acc[t], 0, 0, 0);
+      for (int a = 0; a < 2; ++a)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b[t], acc[t], 0, 0, 0);
+        for (int t = 0; t < 4; ++t) acc[a][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[a], b[t], acc[a][t], 0, 0, 0);
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[a][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[a], b[t], acc[a][t], 0, 0, 0);
     }
   }
 
   // Accumulator e of lane l holds D[i][j], i = 8 (e / 4) + 4 (l / 32) + e % 4, j = l % 32.
 #pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
   for (int e = 0; e < 16; ++e) {
     const int i = 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-    const int r = r0 + 32 * wr + i;
+    const int r = r0 + 64 * wr + 32 * a + i;
     if (r >= p.R) continue;
     float* yr = p.y + (size_t)r * p.ldy;
     if (EPI == GM_SWIGLU) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const int f = blockIdx.x * (kGmBM / 2) + ct[t] + li;
-        if (f < p.M / 2) yr[f] = silu(acc[t][e]) * acc[t + 2][e];
+        if (f < p.M / 2) yr[f] = silu(acc[a][t][e]) * acc[a][t + 2][e];
       }
     } else {
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int m = blockIdx.x * kGmBM + ct[t] + li;
         if (m < p.M) {
-          if (EPI == GM_RESID) yr[m] += acc[t][e];
-          else yr[m] = acc[t][e];
+          if (EPI == GM_RESID) yr[m] += acc[a][t][e];
+          else yr[m] = acc[a][t][e];
         }
       }
     }
