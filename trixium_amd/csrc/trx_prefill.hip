@@ -18,7 +18,7 @@ namespace trx {
 constexpr int kGmThreads = 256;
 constexpr int kGmBR = 128;                 // positions per block
 constexpr int kGmBM = 256;                 // weight rows per block
-constexpr int kGmLd = kGroup + 8;          // LDS row stride in halves (272 bytes)
+constexpr int kGmLd = kGroup / 2 + 8;      // LDS row stride in halves (144 bytes): half a group per step
 
 __device__ __forceinline__ uint32_t pk_mul_h2(uint32_t a, uint32_t s2) {
   typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
@@ -48,8 +48,10 @@ struct GmRaw {
 
 template <int KIND, int EPI>
 __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
-  __shared__ __align__(16) _Float16 ws[kGmBM * kGmLd];
-  __shared__ __align__(16) _Float16 xs[2][kGmBR * kGmLd];
+  // Two buffers of each: a step (64 columns, half a group) is staged into one while the matrix
+  // cores read the other.
+  __shared__ __align__(16) _Float16 ws[2][kGmBM * kGmLd];
+  __shared__ __align__(16) _Float16 xs[2][2][kGmBR * kGmLd];
   __shared__ __align__(16) uint4 lut[2][256];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int r0 = blockIdx.y * kGmBR;
@@ -110,13 +112,13 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
       raw.sc = __builtin_amdgcn_raw_buffer_load_b32(rw, rbase + 2u * (4u * (uint32_t)g + 2u * (uint32_t)shalf), 0, 0);
     }
   };
-  constexpr int XQ = kGmBR * 16 / kGmThreads;      // 16-byte x pieces per thread and plane
-  uint4 xr[2 * XQ];
-  auto load_x = [&](int g) {
+  constexpr int XQ = kGmBR * 8 / kGmThreads;       // 16-byte x pieces per thread, plane and step
+  // x of step st (columns 64 st .. + 63): thread t moves pieces t + 256 q (row piece / 8, 8 columns).
+  auto load_x = [&](uint4* xr, int st) {
 #pragma unroll
     for (int q = 0; q < XQ; ++q) {
-      const int piece = tid + kGmThreads * q, row = piece >> 4, c16 = piece & 15;
-      const uint32_t off = ((uint32_t)(r0 + row) * (uint32_t)p.K + (uint32_t)(kGroup * g + 8 * c16)) * 2u;
+      const int piece = tid + kGmThreads * q, row = piece >> 3, c8 = piece & 7;
+      const uint32_t off = ((uint32_t)(r0 + row) * (uint32_t)p.K + (uint32_t)(64 * st + 8 * c8)) * 2u;
       const auto a = __builtin_amdgcn_raw_buffer_load_b128(rxh, off, 0, 0);
       const auto b = __builtin_amdgcn_raw_buffer_load_b128(rxl, off, 0, 0);
       xr[q] = make_uint4(a[0], a[1], a[2], a[3]);
@@ -124,7 +126,7 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
     }
   };
   // Decoded weights of this thread's 64 codes: 32 dwords of fp16 pairs, times the scale.
-  auto stage_w = [&](const GmRaw<KIND>& raw, int g, int shalf) {
+  auto stage_w = [&](const GmRaw<KIND>& raw, int g, int shalf, int buf) {
     uint32_t D[32];
     if (!wvalid) {
 #pragma unroll
@@ -204,16 +206,16 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
         for (int i = 0; i < 32; ++i) D[i] = pk_mul_h2(D[i], s2);
       }
     }
-    uint4* dst = (uint4*)(ws + srow * kGmLd + 64 * shalf);
+    uint4* dst = (uint4*)(ws[buf] + srow * kGmLd);
 #pragma unroll
     for (int i = 0; i < 8; ++i) dst[i] = make_uint4(D[4 * i], D[4 * i + 1], D[4 * i + 2], D[4 * i + 3]);
   };
-  auto stage_x = [&]() {
+  auto stage_x = [&](const uint4* xr, int buf) {
 #pragma unroll
     for (int q = 0; q < XQ; ++q) {
-      const int piece = tid + kGmThreads * q, row = piece >> 4, c16 = piece & 15;
-      *(uint4*)(xs[0] + row * kGmLd + 8 * c16) = xr[q];
-      *(uint4*)(xs[1] + row * kGmLd + 8 * c16) = xr[XQ + q];
+      const int piece = tid + kGmThreads * q, row = piece >> 3, c8 = piece & 7;
+      *(uint4*)(xs[buf][0] + row * kGmLd + 8 * c8) = xr[q];
+      *(uint4*)(xs[buf][1] + row * kGmLd + 8 * c8) = xr[XQ + q];
     }
   };
 
@@ -228,32 +230,33 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
   const int li = lane & 31, lk = 8 * (lane >> 5);
   f32x16_t acc[2][4] = {};
 
+  // Steps of 64 columns (st = 2g + half): step st + 1 is staged into the other buffers while the
+  // matrix cores take step st, and step st + 3 is loaded into the registers step st + 1 freed (two
+  // steps of latency cover). The loop is unrolled by two, so a step's registers and buffers are
+  // fixed per half.
+  const int NS = 2 * G;
   GmRaw<KIND> raw[2];
-  load_w(raw[0], 0, 0);
-  load_w(raw[1], 0, 1);
-  load_x(0);
-  for (int g = 0; g < G; ++g) {
-    __syncthreads();                      // the previous group's fragments are read
-    stage_w(raw[0], g, 0);
-    stage_w(raw[1], g, 1);
-    stage_x();
-    __syncthreads();
-    if (g + 1 < G) {
-      load_w(raw[0], g + 1, 0);
-      load_w(raw[1], g + 1, 1);
-      load_x(g + 1);
-    }
+  uint4 xr[2][2 * XQ];
+  auto load_step = [&](int st, int slot) {
+    load_w(raw[slot], st >> 1, st & 1);
+    load_x(xr[slot], st);
+  };
+  auto stage_step = [&](int st, int slot) {
+    stage_w(raw[slot], st >> 1, st & 1, slot);
+    stage_x(xr[slot], slot);
+  };
+  auto compute = [&](int buf) {
 #pragma unroll
-    for (int kk = 0; kk < kGroup / 16; ++kk) {
+    for (int kk = 0; kk < kGroup / 32; ++kk) {
       const int k = 16 * kk + lk;
       half8_t ah[2], al[2], b[4];
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
-        ah[a] = *(const half8_t*)(xs[0] + (64 * wr + 32 * a + li) * kGmLd + k);
-        al[a] = *(const half8_t*)(xs[1] + (64 * wr + 32 * a + li) * kGmLd + k);
+        ah[a] = *(const half8_t*)(xs[buf][0] + (64 * wr + 32 * a + li) * kGmLd + k);
+        al[a] = *(const half8_t*)(xs[buf][1] + (64 * wr + 32 * a + li) * kGmLd + k);
       }
 #pragma unroll
-      for (int t = 0; t < 4; ++t) b[t] = *(const half8_t*)(ws + (ct[t] + li) * kGmLd + k);
+      for (int t = 0; t < 4; ++t) b[t] = *(const half8_t*)(ws[buf] + (ct[t] + li) * kGmLd + k);
 #pragma unroll
       for (int a = 0; a < 2; ++a)
 #pragma unroll
@@ -263,6 +266,23 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) acc[a][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[a], b[t], acc[a][t], 0, 0, 0);
     }
+  };
+  load_step(0, 0);
+  load_step(1, 1);                        // NS >= 2: K is a multiple of 128
+  __syncthreads();                        // the code tables are written
+  stage_step(0, 0);
+  if (NS > 2) load_step(2, 0);
+  __syncthreads();
+  for (int st = 0; st < NS; st += 2) {
+    compute(0);
+    if (st + 1 < NS) stage_step(st + 1, 1);
+    if (st + 3 < NS) load_step(st + 3, 1);
+    __syncthreads();
+    if (st + 1 >= NS) break;
+    compute(1);
+    if (st + 2 < NS) stage_step(st + 2, 0);
+    if (st + 4 < NS) load_step(st + 4, 0);
+    __syncthreads();
   }
 
   // Accumulator e of lane l holds D[i][j], i = 8 (e / 4) + 4 (l / 32) + e % 4, j = l % 32.
