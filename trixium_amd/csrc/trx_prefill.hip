@@ -16,7 +16,6 @@ namespace trx {
 // GEMM ------------------------------------------------------------------------------------------
 
 constexpr int kGmThreads = 256;
-constexpr int kGmBR = 128;                 // positions per block
 constexpr int kGmBM = 256;                 // weight rows per block
 constexpr int kGmLd = kGroup / 2 + 8;      // LDS row stride in halves (144 bytes): half a group per step
 
@@ -46,15 +45,18 @@ struct GmRaw {
   uint32_t sc;
 };
 
-template <int KIND, int EPI>
+// NA: position tiles of 32 per wave (2: 128 positions per block; 1: 64, for grids that would
+// otherwise leave part of a round of blocks idle).
+template <int KIND, int EPI, int NA>
 __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
+  constexpr int BR = 64 * NA;
   // Two buffers of each: a step (64 columns, half a group) is staged into one while the matrix
   // cores read the other.
   __shared__ __align__(16) _Float16 ws[2][kGmBM * kGmLd];
-  __shared__ __align__(16) _Float16 xs[2][2][kGmBR * kGmLd];
+  __shared__ __align__(16) _Float16 xs[2][2][BR * kGmLd];
   __shared__ __align__(16) uint4 lut[2][256];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int r0 = blockIdx.y * kGmBR;
+  const int r0 = blockIdx.y * BR;
   const int G = p.K / kGroup;
 
   // Code byte -> (digit - 1) as fp16, two per dword. trit5: the even table starts a byte's five
@@ -112,7 +114,7 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
       raw.sc = __builtin_amdgcn_raw_buffer_load_b32(rw, rbase + 2u * (4u * (uint32_t)g + 2u * (uint32_t)shalf), 0, 0);
     }
   };
-  constexpr int XQ = kGmBR * 8 / kGmThreads;       // 16-byte x pieces per thread, plane and step
+  constexpr int XQ = BR * 8 / kGmThreads;          // 16-byte x pieces per thread, plane and step
   // x of step st (columns 64 st .. + 63): thread t moves pieces t + 256 q (row piece / 8, 8 columns).
   auto load_x = [&](uint4* xr, int st) {
 #pragma unroll
@@ -228,7 +230,7 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
   for (int t = 0; t < 4; ++t)
     ct[t] = EPI == GM_SWIGLU ? (t >> 1) * (kGmBM / 2) + 64 * wm + 32 * (t & 1) : 128 * wm + 32 * t;
   const int li = lane & 31, lk = 8 * (lane >> 5);
-  f32x16_t acc[2][4] = {};
+  f32x16_t acc[NA][4] = {};
 
   // Steps of 64 columns (st = 2g + half): step st + 1 is staged into the other buffers while the
   // matrix cores take step st, and step st + 3 is loaded into the registers step st + 1 freed (two
@@ -249,20 +251,20 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
 #pragma unroll
     for (int kk = 0; kk < kGroup / 32; ++kk) {
       const int k = 16 * kk + lk;
-      half8_t ah[2], al[2], b[4];
+      half8_t ah[NA], al[NA], b[4];
 #pragma unroll
-      for (int a = 0; a < 2; ++a) {
-        ah[a] = *(const half8_t*)(xs[buf][0] + (64 * wr + 32 * a + li) * kGmLd + k);
-        al[a] = *(const half8_t*)(xs[buf][1] + (64 * wr + 32 * a + li) * kGmLd + k);
+      for (int a = 0; a < NA; ++a) {
+        ah[a] = *(const half8_t*)(xs[buf][0] + (32 * NA * wr + 32 * a + li) * kGmLd + k);
+        al[a] = *(const half8_t*)(xs[buf][1] + (32 * NA * wr + 32 * a + li) * kGmLd + k);
       }
 #pragma unroll
       for (int t = 0; t < 4; ++t) b[t] = *(const half8_t*)(ws[buf] + (ct[t] + li) * kGmLd + k);
 #pragma unroll
-      for (int a = 0; a < 2; ++a)
+      for (int a = 0; a < NA; ++a)
 #pragma unroll
         for (int t = 0; t < 4; ++t) acc[a][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[a], b[t], acc[a][t], 0, 0, 0);
 #pragma unroll
-      for (int a = 0; a < 2; ++a)
+      for (int a = 0; a < NA; ++a)
 #pragma unroll
         for (int t = 0; t < 4; ++t) acc[a][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[a], b[t], acc[a][t], 0, 0, 0);
     }
@@ -287,11 +289,11 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
 
   // Accumulator e of lane l holds D[i][j], i = 8 (e / 4) + 4 (l / 32) + e % 4, j = l % 32.
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int a = 0; a < NA; ++a)
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
     const int i = 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-    const int r = r0 + 64 * wr + 32 * a + i;
+    const int r = r0 + 32 * NA * wr + 32 * a + i;
     if (r >= p.R) continue;
     float* yr = p.y + (size_t)r * p.ldy;
     if (EPI == GM_SWIGLU) {
@@ -313,15 +315,18 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
   }
 }
 
-template <int KIND>
+template <int KIND, int NA>
 static void gemm_dispatch(const GemmParams& p, dim3 grid, hipStream_t s) {
   if (p.epi == GM_SWIGLU)
-    hipLaunchKernelGGL((gemm_kernel<KIND, GM_SWIGLU>), grid, dim3(kGmThreads), 0, s, p);
+    hipLaunchKernelGGL((gemm_kernel<KIND, GM_SWIGLU, NA>), grid, dim3(kGmThreads), 0, s, p);
   else if (p.epi == GM_RESID)
-    hipLaunchKernelGGL((gemm_kernel<KIND, GM_RESID>), grid, dim3(kGmThreads), 0, s, p);
+    hipLaunchKernelGGL((gemm_kernel<KIND, GM_RESID, NA>), grid, dim3(kGmThreads), 0, s, p);
   else
-    hipLaunchKernelGGL((gemm_kernel<KIND, GM_STORE>), grid, dim3(kGmThreads), 0, s, p);
+    hipLaunchKernelGGL((gemm_kernel<KIND, GM_STORE, NA>), grid, dim3(kGmThreads), 0, s, p);
 }
+
+// Rounds of one block per CU that a grid of n blocks fills: the fraction of busy block slots.
+static double round_fill(int n, int cus) { return (double)n / ((double)cdiv(n, cus) * cus); }
 
 int launch_gemm(const GemmParams& p, hipStream_t s) {
   TRX_CHECK(p.kind == TRX_KIND_TERNARY || p.kind == TRX_KIND_TERNARY5 || p.kind == TRX_KIND_Q8, TRX_E_INVALID,
@@ -332,10 +337,22 @@ int launch_gemm(const GemmParams& p, hipStream_t s) {
   TRX_CHECK((size_t)p.R * p.K * 2 < (1ull << 32) && (size_t)p.M * p.row_bytes < (1ull << 32) &&
             (size_t)p.M * p.row_bytes + 16 <= p.w_bytes, TRX_E_INVALID, "prefill GEMM: operands too large");
   const int nx = p.epi == GM_SWIGLU ? cdiv(p.M / 2, kGmBM / 2) : cdiv(p.M, kGmBM);
-  const dim3 grid(nx, cdiv(p.R, kGmBR));
-  if (p.kind == TRX_KIND_TERNARY5) gemm_dispatch<TRX_KIND_TERNARY5>(p, grid, s);
-  else if (p.kind == TRX_KIND_TERNARY) gemm_dispatch<TRX_KIND_TERNARY>(p, grid, s);
-  else gemm_dispatch<TRX_KIND_Q8>(p, grid, s);
+  // 128 positions per block, or 64 when that fills the rounds of blocks better (by a fifth).
+  int cus = 0, dev = 0;
+  TRX_HIP(hipGetDevice(&dev));
+  TRX_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  const bool small = round_fill(nx * cdiv(p.R, 64), cus) > 1.2 * round_fill(nx * cdiv(p.R, 128), cus);
+  const dim3 grid(nx, cdiv(p.R, small ? 64 : 128));
+  if (p.kind == TRX_KIND_TERNARY5) {
+    if (small) gemm_dispatch<TRX_KIND_TERNARY5, 1>(p, grid, s);
+    else gemm_dispatch<TRX_KIND_TERNARY5, 2>(p, grid, s);
+  } else if (p.kind == TRX_KIND_TERNARY) {
+    if (small) gemm_dispatch<TRX_KIND_TERNARY, 1>(p, grid, s);
+    else gemm_dispatch<TRX_KIND_TERNARY, 2>(p, grid, s);
+  } else {
+    if (small) gemm_dispatch<TRX_KIND_Q8, 1>(p, grid, s);
+    else gemm_dispatch<TRX_KIND_Q8, 2>(p, grid, s);
+  }
   TRX_LAUNCHED();
   return TRX_OK;
 }
