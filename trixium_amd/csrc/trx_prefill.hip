@@ -1,8 +1,9 @@
 // Batched prefill kernels: R prompt positions per forward, one weight pass for all of them.
 //
-// The projections run on the matrix cores (v_mfma_f32_32x32x16_f16): a block decodes a 256-row x
-// 128-column tile of the stored ternary rows into LDS as fp16 weights and multiplies 64 positions
-// by it, x split into two fp16 planes (hi, lo) so the fp32 accumulation sees x to ~22 bits.
+// The projections run on the matrix cores (v_mfma_f32_32x32x16_f16): a block decodes 256 stored
+// ternary rows into LDS as fp16 weights, 64 columns at a time, and multiplies 128 (or 64)
+// positions by them, x split into two fp16 planes (hi, lo) so the fp32 accumulation sees x to
+// ~22 bits.
 // Attention, the RoPE/KV append and the Gated DeltaNet recurrence are the one-position rules of
 // the decode kernels applied to every position of the chunk (the recurrence in order).
 
