@@ -56,9 +56,24 @@ __device__ void embed_token(const EmbedParams& p, int tok, float* x) {
   __shared__ __align__(16) uint8_t s_row[kEmbedRowMax];
   const int tid = threadIdx.x;
   if (p.mode == EMBED_TABLE) {
+    // Every load of a chunk is issued before its stores (x could alias the table as far as the
+    // compiler knows, so a plain loop would wait out each load in turn).
+    constexpr int U = 4;
     const float sc = bfp_scale(p.exps[tok]);
     const int16_t* m = p.mant + (size_t)tok * p.n_embd;
-    for (int c = tid; c < p.n_embd; c += kEmbedThreads) x[c] = (float)m[c] * sc;
+    for (int c0 = 0; c0 < p.n_embd; c0 += U * kEmbedThreads) {
+      int16_t v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = c0 + u * kEmbedThreads + tid;
+        v[u] = c < p.n_embd ? m[c] : (int16_t)0;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = c0 + u * kEmbedThreads + tid;
+        if (c < p.n_embd) x[c] = (float)v[u] * sc;
+      }
+    }
     return;
   }
   // Ternary row: scales at the head of the row packet, codes after code_off. The whole packet
