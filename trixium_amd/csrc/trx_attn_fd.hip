@@ -36,7 +36,10 @@ __device__ __forceinline__ float group_sum(float v) {
 
 // ROR8: the RoPE partner lane is li ^ 8 (rope_n = 128), a DPP row_ror:8; otherwise a shuffle. A
 // template parameter, so the choice is not a branch around every element.
-template <int REP, int HD, bool ROR8>
+// QP: q, k and v arrive as the q|k|v GEMV's K-slice partial sums (p.qkv_part, [S][rows_p], with
+// its RMSNorm's slice sums of x^2 in p.qkv_ss), summed here: y = r * sum_s part[s], r =
+// 1/sqrt(sum(ss) / K + eps), the slices added in order as the GEMV's own tile reduction does.
+template <int REP, int HD, bool ROR8, bool QP>
 __global__ __launch_bounds__(kAttnThreads) void attn_fd_kernel(AttnParams p) {
   constexpr int LPP = HD / 8;                         // lanes per position
   constexpr int PPW = 64 / LPP;                       // groups per wave
@@ -66,19 +69,46 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fd_kernel(AttnParams p) {
   constexpr int NST = REP + 4, STV = NST * HD / 4;                 // rows, float4s staged
   constexpr int SPT = (STV + kAttnThreads - 1) / kAttnThreads;     // float4s per thread
   __shared__ __align__(16) float stg[NST][HD];
+  // With QP the position is read first: a scalar load, which the memory barrier below would
+  // otherwise turn into a vector load queued behind the partial sums.
+  const int pos_qp = QP ? *p.pos : 0;
   float4 sv[SPT];
+  constexpr int NPS = QP ? kQkvPartMax : 1;
+  float4 pv[SPT][NPS];
+  float ssv[NPS];
 #pragma unroll
   for (int k = 0; k < SPT; ++k) {
     const int e = min(tid + k * kAttnThreads, STV - 1);            // past the end: a repeat
     const int row = 4 * e / HD, d = 4 * e - row * HD;
-    const float* src = row < REP ? p.qkv + (size_t)(g * REP + row) * qstride + d
-                       : row == REP ? kraw + d
-                       : row == REP + 1 ? kraw + (size_t)p.n_kv * HD + d
-                       : row == REP + 2 ? p.q_norm + d : p.k_norm + d;
-    sv[k] = *(const float4*)src;
+    if (QP) {
+      // Every partial of the q/k/v rows (a norm-gain row reads row 0's and drops them); past S a
+      // repeat of the last slice that gets no weight.
+      const size_t qi = row < REP ? (size_t)(g * REP + row) * qstride + d
+                        : row == REP ? (size_t)p.n_head * qstride + (size_t)g * HD + d
+                        : row == REP + 1 ? (size_t)p.n_head * qstride + (size_t)(p.n_kv + g) * HD + d : (size_t)d;
+#pragma unroll
+      for (int q = 0; q < NPS; ++q)
+        pv[k][q] = *(const float4*)(p.qkv_part + (size_t)min(q, p.qkv_S - 1) * p.qkv_rows_p + qi);
+      sv[k] = *(const float4*)(row == REP + 3 ? p.k_norm + d : p.q_norm + (row == REP + 2 ? d : 0));
+    } else {
+      const float* src = row < REP ? p.qkv + (size_t)(g * REP + row) * qstride + d
+                         : row == REP ? kraw + d
+                         : row == REP + 1 ? kraw + (size_t)p.n_kv * HD + d
+                         : row == REP + 2 ? p.q_norm + d : p.k_norm + d;
+      sv[k] = *(const float4*)src;
+    }
+  }
+  if (QP) {
+#pragma unroll
+    for (int q = 0; q < NPS; ++q)     // vector loads: counted with the partials, not the position
+      ssv[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                   make_rsrc(p.qkv_ss, (uint32_t)p.qkv_S * 4u), (uint32_t)min(q, p.qkv_S - 1) * 4u, 0, 0));
+    // Keeps these loads ahead of the position's and the K/V rows' (the scheduler would otherwise
+    // issue them after the K/V stream, and the scalar ones after its waits).
+    asm volatile("" ::: "memory");
   }
 
-  const int pos = *p.pos, T = pos + 1;
+  const int pos = QP ? pos_qp : *p.pos, T = pos + 1;
   const int chunk = (T + S - 1) / S;
   const int p0 = sp * chunk, p1 = min(T, p0 + chunk), n = max(0, p1 - p0);
   const bool owner = n > 0 && pos >= p0 && pos < p1;
@@ -106,10 +136,25 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fd_kernel(AttnParams p) {
   }
 
   // The staged inputs into LDS (the loads are waited for here, after the K/V loads went out).
+  float rs = 1.f;
+  if (QP) {
+    float t = 0.f;
+#pragma unroll
+    for (int q = 0; q < NPS; ++q) t += q < p.qkv_S ? ssv[q] : 0.f;
+    rs = rsqrtf(t / (float)p.qkv_K + p.eps);
+  }
 #pragma unroll
   for (int k = 0; k < SPT; ++k) {
     const int e = min(tid + k * kAttnThreads, STV - 1);
-    *(float4*)(&stg[0][0] + 4 * e) = sv[k];
+    float4 v = sv[k];
+    if (QP && 4 * e / HD < REP + 2) {
+      float4 a = pv[k][0];
+#pragma unroll
+      for (int q = 1; q < NPS; ++q)
+        if (q < p.qkv_S) { a.x += pv[k][q].x; a.y += pv[k][q].y; a.z += pv[k][q].z; a.w += pv[k][q].w; }
+      v = make_float4(a.x * rs, a.y * rs, a.z * rs, a.w * rs);
+    }
+    *(float4*)(&stg[0][0] + 4 * e) = v;
   }
   float q[REP][8], kn[8], vn[8], qw[8], kw[8];
   if (n > 0) {
@@ -327,19 +372,19 @@ bool attention_fd_supported(int rep, int hd, int rope_n, int n_split) {
   return rope_ok && rep_ok && (hd == 64 || hd == 128 || hd == 256) && n_split <= kFdMaxSplits;
 }
 
-template <int REP>
-static int launch_fd_rep(const AttnParams& p, hipStream_t s) {
+template <int REP, bool QP>
+static int launch_fd_qp(const AttnParams& p, hipStream_t s) {
   const dim3 grid(p.n_kv * p.n_split), block(kAttnThreads);
   const bool ror8 = p.rope_n == 128;       // partner lane li ^ (rope_n / 16) = li ^ 8
   switch (p.hd) {
-    case 64: hipLaunchKernelGGL((attn_fd_kernel<REP, 64, false>), grid, block, 0, s, p); break;
+    case 64: hipLaunchKernelGGL((attn_fd_kernel<REP, 64, false, QP>), grid, block, 0, s, p); break;
     case 128:
-      if (ror8) hipLaunchKernelGGL((attn_fd_kernel<REP, 128, true>), grid, block, 0, s, p);
-      else hipLaunchKernelGGL((attn_fd_kernel<REP, 128, false>), grid, block, 0, s, p);
+      if (ror8) hipLaunchKernelGGL((attn_fd_kernel<REP, 128, true, QP>), grid, block, 0, s, p);
+      else hipLaunchKernelGGL((attn_fd_kernel<REP, 128, false, QP>), grid, block, 0, s, p);
       break;
     case 256:
-      if (ror8) hipLaunchKernelGGL((attn_fd_kernel<REP, 256, true>), grid, block, 0, s, p);
-      else hipLaunchKernelGGL((attn_fd_kernel<REP, 256, false>), grid, block, 0, s, p);
+      if (ror8) hipLaunchKernelGGL((attn_fd_kernel<REP, 256, true, QP>), grid, block, 0, s, p);
+      else hipLaunchKernelGGL((attn_fd_kernel<REP, 256, false, QP>), grid, block, 0, s, p);
       break;
     default: TRX_CHECK(false, TRX_E_INVALID, "attention: head_dim %d unsupported", p.hd);
   }
@@ -347,9 +392,18 @@ static int launch_fd_rep(const AttnParams& p, hipStream_t s) {
   return TRX_OK;
 }
 
+template <int REP>
+static int launch_fd_rep(const AttnParams& p, hipStream_t s) {
+  return p.qkv_part ? launch_fd_qp<REP, true>(p, s) : launch_fd_qp<REP, false>(p, s);
+}
+
 int launch_attention_fd(const AttnParams& p, hipStream_t s) {
   TRX_CHECK(attention_fd_supported(p.n_rep, p.hd, p.rope_n, p.n_split), TRX_E_INVALID,
             "attention: rep %d hd %d rope %d splits %d unsupported", p.n_rep, p.hd, p.rope_n, p.n_split);
+  TRX_CHECK(!p.qkv_part || (p.qkv_ss && !p.gated && p.qkv_S >= 1 && p.qkv_S <= kQkvPartMax &&
+                            p.qkv_rows_p % 4 == 0 && p.qkv_K > 0 &&
+                            p.qkv_rows_p >= (p.n_head + 2 * p.n_kv) * p.hd),
+            TRX_E_INVALID, "attention: unsupported q|k|v partial sums (S %d, rows %d)", p.qkv_S, p.qkv_rows_p);
   const int cap = attention_max_chunk(p.hd);
   TRX_CHECK(p.n_split >= 1 && (p.max_ctx + p.n_split - 1) / p.n_split <= cap, TRX_E_INVALID,
             "attention: %d splits for context %d", p.n_split, p.max_ctx);

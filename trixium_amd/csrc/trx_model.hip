@@ -73,6 +73,8 @@ struct Model {
   int ffn_S = 0, ffn_rows_p = 0;
   float* o_part = nullptr;
   int o_S = 0, o_rows_p = 0;
+  float *qkv_part = nullptr, *qkv_ss = nullptr;    // q|k|v partial sums, summed by the attention
+  int qkv_S = 0, qkv_rows_p = 0;
   float* down_part = nullptr;
   int down_S = 0, down_rows_p = 0;
   float* dn_out_part = nullptr;                    // DeltaNet out projection -> the FFN's gate|up
@@ -264,6 +266,9 @@ static int plan_packed(Model& m) {
   if ((ops & TRX_PACK_O) && (ops & TRX_PACK_GATE_UP) && m.n_attn > 0 &&
       cdiv(c.n_head * hd, kSliceCols) <= tgemv_resid_slices_max())
     if ((rc = part_buf(E, c.n_head * hd, &m.o_part, &m.o_S, &m.o_rows_p, nullptr, wk))) return rc;
+  if ((ops & TRX_PACK_QKV) && m.n_attn > 0 && !c.attn_gated && cdiv(E, kSliceCols) <= kQkvPartMax)
+    if ((rc = part_buf(c.n_head * hd + 2 * c.n_kv_head * hd, E, &m.qkv_part, &m.qkv_S, &m.qkv_rows_p, &m.qkv_ss,
+                       wk))) return rc;
   if ((ops & TRX_PACK_DOWN) && cdiv(F, kSliceCols) <= tgemv_resid_slices_max())
     if ((rc = part_buf(E, F, &m.down_part, &m.down_S, &m.down_rows_p, nullptr, wk))) return rc;
   if ((ops & TRX_PACK_DN) && (ops & TRX_PACK_GATE_UP) && m.n_dn > 0 && cdiv(nvh, kSliceCols) <= tgemv_resid_slices_max())
@@ -519,12 +524,22 @@ static int run_step(Model& m, hipStream_t s) {
     } else if (m.is_dn(l)) {
       if ((rc = dn_layer_launch(m, l, s))) return rc;
     } else {
-      // q|k|v with the attention RMSNorm fused in the prologue.
+      // q|k|v with the attention RMSNorm fused in the prologue; its partial sums go to the
+      // one-launch attention when that kernel takes them (non-gated), else it reduces them.
+      const int rope_n = c.rope_dims ? c.rope_dims : hd;
+      const bool fd_ok = attention_fd_supported(c.n_head / c.n_kv_head, hd, rope_n, m.n_split);
+      const bool qkv_hand = fd_ok && m.qkv_part && m.qkv_rows_p % 4 == 0 && packed(OP_QKV, l);
       if (const PackedMat* pq = packed(OP_QKV, l)) {
         const float* xin;
         const PartialSums* pp = take(xin);
+        PartialSums qp = pp ? *pp : PartialSums{};
+        if (qkv_hand) {
+          qp.out = m.qkv_part;
+          qp.out_ss = m.qkv_ss;
+        }
         if ((rc = tgemv_f32(pq->buf, wk, qrows + 2 * kvrows, E, xin, PF(m, TRX_ROLE_ATTN_NORM, l), c.rms_eps,
-                            m.qkv, TRX_EPI_STORE, nullptr, nullptr, m.pack_work, s, nullptr, nullptr, nullptr, pp)))
+                            qkv_hand ? nullptr : m.qkv, TRX_EPI_STORE, nullptr, nullptr, m.pack_work, s, nullptr,
+                            nullptr, nullptr, pp || qkv_hand ? &qp : nullptr)))
           return rc;
       } else if ((rc = projection(m, OP_QKV, l, P(m, TRX_ROLE_ATTN_Q, l), wk, qrows + 2 * kvrows, E, xc,
                                    PF(m, TRX_ROLE_ATTN_NORM, l), m.qkv, TRX_EPI_STORE, nullptr, s))) {
@@ -553,6 +568,13 @@ static int run_step(Model& m, hipStream_t s) {
       ap.n_split = m.n_split;
       ap.gated = c.attn_gated;
       ap.eps = c.rms_eps;
+      if (qkv_hand) {
+        ap.qkv_part = m.qkv_part;
+        ap.qkv_ss = m.qkv_ss;
+        ap.qkv_S = m.qkv_S;
+        ap.qkv_rows_p = m.qkv_rows_p;
+        ap.qkv_K = E;
+      }
       // One-launch attention; with a packed o projection the splits are merged in that GEMV's
       // prologue (each of its blocks merges the heads of its column slice).
       const bool fd = attention_fd_supported(ap.n_rep, hd, ap.rope_n, ap.n_split);

@@ -43,8 +43,14 @@ struct AttnParams {
   float eps;
   unsigned* done;          // [n_kv][kDoneStride] split counters of the one-launch kernel (zero
                            // between launches), one per 128-byte line
+  // One-launch kernel, non-gated: when set, q|k|v come as the packed GEMV's partial sums
+  // ([qkv_S][qkv_rows_p], slice sums of x^2 in qkv_ss, K = qkv_K) instead of qkv.
+  const float* qkv_part;
+  const float* qkv_ss;
+  int qkv_S, qkv_rows_p, qkv_K;
 };
 constexpr int kDoneStride = 32;
+constexpr int kQkvPartMax = 16;    // q|k|v K-slices the attention sums (4096 columns)
 
 struct DenseParams {
   const uint8_t* W;
