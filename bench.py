@@ -70,8 +70,6 @@ def parse_args():
     ap.add_argument("--packed-ops", type=int, default=-1,
                     help="projections on the packed GEMV, as TRX_PACK_* bits (-1: the library's "
                          "choice for the weight kind, 0: none, 63: all)")
-    ap.add_argument("--persistent", action="store_true",
-                    help="run each position as one persistent kernel instead of one kernel per operation")
     ap.add_argument("--no-microbench", action="store_true",
                     help="skip the isolated matvec benchmark at the Qwen3-1.7B layer shapes")
     ap.add_argument("--only-microbench", action="store_true",
@@ -472,7 +470,7 @@ def main():
         sys.exit(f"prompt {a.prompt} + {n_dec} decode tokens exceed the context {mc.max_ctx}")
     graph = not a.no_graph
     dec = Decoder.synthetic(mc, a.seed, weight_kind=kind, max_ctx=mc.max_ctx, max_new=n_dec + 8,
-                            use_graph=graph, persistent=a.persistent, packed_ops=a.packed_ops)
+                            use_graph=graph, packed_ops=a.packed_ops)
     prompt = np.random.default_rng(a.seed).integers(0, mc.vocab, a.prompt).astype(np.int32)
     if a.sampling:
         t, p_, r = (float(v) for v in a.sampling.split(","))
@@ -594,7 +592,7 @@ def main():
                    "n_kv_head": mc.n_kv_head, "head_dim": mc.head_dim, "ffn_dim": mc.ffn_dim,
                    "vocab": mc.vocab, "max_ctx": mc.max_ctx, "prompt_tokens": a.prompt,
                    "decode_tokens": n_dec, "weights": a.kind, "hipgraph": graph,
-                   "persistent": dec.persistent, "packed_ops": dec.packed_ops},
+                   "packed_ops": dec.packed_ops},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profile(a.kind, gu_mode),

@@ -116,8 +116,10 @@ int trx_gemv_ternary_f32(const uint8_t* rows, int kind, int M, int K, const floa
  * (model/fastref.py:104-116: (code - 1) * scale, or fp16(q * scale) for Q8) and xhat is split
  * into fp16 hi and lo planes, so each product is fp32-accurate. kind: TRX_KIND_TERNARY,
  * TRX_KIND_TERNARY5 or TRX_KIND_Q8. Epilogues: TRX_EPI_STORE y [n][M]; TRX_EPI_RESID y [n][M] +=;
- * TRX_EPI_SWIGLU (rows [0,F) gate, [F,2F) up) y [n][M/2]. rows must be followed by 16 readable
- * bytes; workspace holds 4*n*K bytes. */
+ * TRX_EPI_SWIGLU (rows [0,F) gate, [F,2F) up) y [n][M/2]. A row of xhat at or above 2^14 in
+ * magnitude is scaled by a power of two for the planes and back in the result (exact), so large
+ * inputs stay finite. rows must be followed by 16 readable bytes; workspace holds 4*n*(K+1)
+ * bytes. */
 int trx_gemm_ternary_f32(const uint8_t* rows, int kind, int M, int K, const float* x, int n,
                          const float* norm_w, float eps, float* y, int epilogue, void* workspace,
                          trx_stream_t s);
@@ -252,7 +254,6 @@ typedef struct {
                                   n_embd width among the rotated widths) */
   int emb_kind;                /* kind of token_embd rows (emb_mode 1 or 2, or a tied head) */
   int max_new;                 /* capacity of the generated-token buffer */
-  int persistent;              /* 1: each position runs as one persistent kernel (reserved) */
   int packed_ops;              /* projections run by the packed GEMV (trx_gemv_packed_f32) over
                                   a packed copy of their rows, as TRX_PACK_* bits; the others run
                                   trx_gemv_ternary_f32's kernel. TRX_PACK_AUTO: the library's
@@ -357,8 +358,10 @@ int trx_model_project_head(trx_model* m, const float* hidden, int n, float* logi
 #define TRX_INFO_DEVICE_BYTES 1
 #define TRX_INFO_STREAM 2
 #define TRX_INFO_WEIGHT_BYTES 3
-#define TRX_INFO_PERSISTENT 4     /* 1 when each position runs as one persistent kernel */
 #define TRX_INFO_PACKED_OPS 5     /* TRX_PACK_* bits in effect */
+#define TRX_INFO_ATTN_SPLITS 6    /* decode attention: blocks (position splits) per kv head */
+#define TRX_INFO_ATTN_PASS 7      /* decode attention: positions one pass of a split block covers
+                                     (a split of c positions takes ceil(c / this) passes) */
 int trx_model_info(trx_model* m, int what, int64_t* value);
 /* Device address and size of one resident tensor (for benchmarks and tests). */
 int trx_model_tensor_ptr(trx_model* m, int role, int layer, void** ptr, int64_t* bytes);

@@ -285,6 +285,130 @@ class FloatRef:
                 logits = self.step(nxt)
         return out
 
+    # Whole-sequence forward (fastref.py:244-258: every projection of a layer over all positions
+    # at once, causal attention over the sequence) --------------------------------------------
+    def proj_many(self, role, l, X):
+        """Rows X [T, cols] -> [T, rows]: fastref's X @ W.T (fastref.py:119-125)."""
+        W = self.weight(role, l)
+        X = np.asarray(X, dtype=f32)
+        if self.hb and role not in (L.ROLE_SSM_BETA, L.ROLE_SSM_ALPHA):
+            X = np.stack([self.rotate(x, W.shape[1]) for x in X])
+        return (X @ W.astype(f32).T).astype(f32)
+
+    def _rope_rows(self, positions):
+        half = self.rope_n // 2
+        if getattr(self, "rope_tab", None) is not None:
+            rows = self.rope_tab[positions].astype(f32) * f32(2.0**-14)
+            return rows[:, :half], rows[:, half:]
+        ang = (positions.astype(f32)[:, None] * self.rope_freq[None, :]).astype(f32)
+        return np.cos(ang), np.sin(ang)
+
+    def attention_many(self, l, Hn, pos0):
+        """Positions pos0 .. pos0 + T - 1 of one attention layer, each attending to the cached
+        positions and to the sequence's positions up to itself (fastref.py:216-241)."""
+        T = Hn.shape[0]
+        hd, nh, nkv = self.hd, self.n_head, self.n_kv
+        qf = self.proj_many(L.ROLE_ATTN_Q, l, Hn)
+        k = self.proj_many(L.ROLE_ATTN_K, l, Hn).reshape(T, nkv, hd)
+        v = self.proj_many(L.ROLE_ATTN_V, l, Hn).reshape(T, nkv, hd)
+        if self.gated:
+            qf = qf.reshape(T, nh, 2 * hd)
+            q, gate = qf[:, :, :hd], qf[:, :, hd:]
+        else:
+            q, gate = qf.reshape(T, nh, hd), None
+        q = self.rmsnorm(q, self.norm_q[l])
+        k = self.rmsnorm(k, self.norm_k[l])
+        half = self.rope_n // 2
+        cos, sin = self._rope_rows(pos0 + np.arange(T))
+        cos, sin = cos[:, None, :], sin[:, None, :]
+
+        def rope(x):
+            x = x.copy()
+            x0, x1 = x[:, :, :half].copy(), x[:, :, half:self.rope_n].copy()
+            x[:, :, :half] = x0 * cos - x1 * sin
+            x[:, :, half:self.rope_n] = x0 * sin + x1 * cos
+            return x
+
+        q, k = rope(q), rope(k)
+        q = (q * f32(1.0 / np.sqrt(hd))).astype(f32)
+        if self.kv_fp16:
+            k, v = k.astype(np.float16).astype(f32), v.astype(np.float16).astype(f32)
+        P = len(self.k_cache[l])
+        self.k_cache[l].extend(list(k))
+        self.v_cache[l].extend(list(v))
+        Kc = np.stack(self.k_cache[l])             # [P + T, nkv, hd]
+        Vc = np.stack(self.v_cache[l])
+        rep = nh // nkv
+        # Query i (position pos0 + i) sees cache rows 0 .. P + i.
+        future = np.arange(P + T)[None, :] > (P + np.arange(T))[:, None]
+        out = np.empty((T, nh, hd), f32)
+        for h in range(nh):
+            s = (q[:, h] @ Kc[:, h // rep].T).astype(f32)
+            s[future] = -np.inf
+            s = s - s.max(axis=1, keepdims=True)
+            p = np.exp(s)
+            p = (p / p.sum(axis=1, keepdims=True)).astype(f32)
+            out[:, h] = (p @ Vc[:, h // rep]).astype(f32)
+        if gate is not None:
+            out = (out * self.sigmoid(gate)).astype(f32)
+        return self.proj_many(L.ROLE_ATTN_OUT, l, out.reshape(T, -1))
+
+    def deltanet_many(self, l, Hn):
+        """The gated delta rule over T positions (fastref.py:182-214): projections and the conv
+        over the whole sequence, the recurrence position by position."""
+        T = Hn.shape[0]
+        nq = self.nk * self.hk
+        qkv = self.proj_many(L.ROLE_ATTN_QKV, l, Hn)
+        z = self.proj_many(L.ROLE_ATTN_ZGATE, l, Hn)
+        beta = self.sigmoid(self.proj_many(L.ROLE_SSM_BETA, l, Hn))
+        alpha = self.proj_many(L.ROLE_SSM_ALPHA, l, Hn)
+        decay = np.exp((self.softplus(alpha + self.ssm_dt[l]) * self.ssm_a[l]).astype(f32))
+        w = self.conv_w[l]
+        win = np.concatenate([self.conv_state[l], qkv], axis=0)                # [K - 1 + T, C]
+        conv = sum(win[i:i + T] * w[:, i] for i in range(self.K)).astype(f32)
+        self.conv_state[l] = win[T:].copy()
+        conv = self.silu(conv)
+        kh = np.arange(self.nv) % self.nk
+        rep = self.nv // self.nk
+        gpos = kh * rep + np.arange(self.nv) // self.nk
+        M = self.dn_state[l]
+        og = np.empty((T, self.nv * self.hv), f32)
+        for t in range(T):
+            q = self.l2norm(conv[t, :nq].reshape(self.nk, self.hk))
+            k = self.l2norm(conv[t, nq:2 * nq].reshape(self.nk, self.hk))
+            v = conv[t, 2 * nq:].reshape(self.nv, self.hv)
+            qt, kt = q[kh], k[kh]
+            M *= decay[t][:, None, None]
+            delta = (v - np.einsum("hjk,hk->hj", M, kt)) * beta[t][:, None]
+            M += delta[:, :, None] * kt[:, None, :]
+            o = (np.einsum("hjk,hk->hj", M, qt) * f32(1.0 / np.sqrt(self.hk))).astype(f32)
+            gz = self.rmsnorm(o, self.norm_ssm[l]) * self.silu(z[t].reshape(self.nv, self.hv))
+            row = np.empty_like(gz)
+            row[gpos] = gz
+            og[t] = row.reshape(-1)
+        return self.proj_many(L.ROLE_SSM_OUT, l, og)
+
+    def prefill(self, tokens, want_logits=False):
+        """Run `tokens` at the next len(tokens) positions as one teacher-forced sequence
+        (fastref.py:244-258's whole-sequence form; the caches, conv windows and recurrent states
+        end as after that many step() calls). Returns the last position's logits when asked."""
+        X = np.stack([self.embed(int(t)) for t in tokens]).astype(f32)
+        pos0 = self.pos
+        for l in range(self.n_layer):
+            hn = self.rmsnorm(X, self.norm_attn[l])
+            y = self.deltanet_many(l, hn) if self.dn[l] else self.attention_many(l, hn, pos0)
+            X = (X + y).astype(f32)
+            hn = self.rmsnorm(X, self.norm_ffn[l])
+            g = self.proj_many(L.ROLE_FFN_GATE, l, hn)
+            u = self.proj_many(L.ROLE_FFN_UP, l, hn)
+            X = (X + self.proj_many(L.ROLE_FFN_DOWN, l, (self.silu(g) * u).astype(f32))).astype(f32)
+        self.pos += len(tokens)
+        self.last_hidden = X[-1]
+        if not want_logits:
+            return None
+        hn = self.rmsnorm(X[-1], self.out_norm)
+        return self.proj(self.head_role, 0, hn)[:self.vocab]
+
 
 class ShapeSample(FloatRef):
     """FloatRef's decode step on random weights of a full-attention shape, built without an
@@ -397,6 +521,9 @@ class TensorRef(FloatRef):
 
     def proj(self, role, l, x):
         return (self.w32[(role, l)] @ np.asarray(x, dtype=f32)).astype(f32)
+
+    def proj_many(self, role, l, X):
+        return (np.asarray(X, dtype=f32) @ self.w32[(role, l)].T).astype(f32)
 
     def embed(self, tok):
         return np.asarray(self.embed_row(int(tok)), dtype=f32)

@@ -143,6 +143,48 @@ def test_floatref_matches_fastref_fixture(tiny_images, golden, golden_arrays, na
             assert np.abs(lg - ref[j]).max() <= 1e-4 * np.abs(ref[j]).max()
 
 
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-hybrid", "tiny-ternemb"])
+def test_sequence_forward_matches_fastref_fixture(tiny_images, golden, golden_arrays, name):
+    """The oracle's whole-sequence forward (FloatRef.prefill, the long-context tests' prompt pass)
+    against the reference's teacher-forced HybridRef logits: at every stored position p the first
+    p tokens run as two sequences (the second attending to the first's cache) and token p as a
+    step, within 1e-4 of the fixture; and the state after a sequence equals the state after the
+    same tokens stepped one by one (caches, conv windows, recurrent matrices, each within rounding)."""
+    r = FloatRef(bons.BONSReader(tiny_images[(name, True)]))
+    seq = golden[f"prompt/{name}"] + golden[f"fastref_tokens/{name}"]
+    pos = golden_arrays[f"fastref_logits_pos/{name}"].tolist()
+    ref = golden_arrays[f"fastref_logits/{name}"]
+    for j, p in enumerate(pos):
+        r.reset()
+        a = p // 2
+        if a:
+            r.prefill(seq[:a])
+        if p > a:
+            r.prefill(seq[a:p])
+        lg = r.step(seq[p])
+        assert np.abs(lg - ref[j]).max() <= 1e-4 * np.abs(ref[j]).max(), p
+        r.reset()
+        lg = r.prefill(seq[:p + 1], want_logits=True)
+        assert np.abs(lg - ref[j]).max() <= 1e-4 * np.abs(ref[j]).max(), p
+    n = len(seq)
+    a = FloatRef(bons.BONSReader(tiny_images[(name, True)]), kv_fp16=True)
+    b = FloatRef(bons.BONSReader(tiny_images[(name, True)]), kv_fp16=True)
+    a.prefill(seq)
+    for t in seq:
+        b.step(t, want_logits=False)
+    assert a.pos == b.pos == n
+    # fp16 values: a few fp16 steps apart at most where the fp32 sums round differently (a cache
+    # row at the wrong position or out of order would be O(1) off).
+    for l in a.k_cache:
+        for ca, cb in ((a.k_cache[l], b.k_cache[l]), (a.v_cache[l], b.v_cache[l])):
+            x, y = np.stack(ca), np.stack(cb)
+            assert np.abs(x - y).max() <= 1e-3 * np.abs(y).max()
+    for l in a.dn_state:
+        assert np.abs(a.conv_state[l] - b.conv_state[l]).max() <= 1e-5
+        assert np.abs(a.dn_state[l] - b.dn_state[l]).max() <= 1e-5 * max(1.0, np.abs(b.dn_state[l]).max())
+    assert np.array_equal([int(np.argmax(a.step(t))) for t in (5, 9)], [int(np.argmax(b.step(t))) for t in (5, 9)])
+
+
 def test_floatref_mirror_loop_contract(tiny_images, golden):
     """The hybrid mirror (exact) and the oracle agree; 2-bit and trit5 images give one model."""
     a = FloatRef(bons.BONSReader(tiny_images[("tiny-hybrid", True)]))
@@ -251,6 +293,11 @@ def test_tensor_ref_equals_floatref_on_an_image(tmp_path):
         la, lb = a.step(t), b.step(t)
         assert np.abs(la - lb).max() <= 1e-5 * np.abs(la).max()
     assert a.generate([1, 2, 3], 5) == b.generate([1, 2, 3], 5)
+    # The whole-sequence forward over the arrays (TensorRef.proj_many) equals FloatRef's.
+    a.reset()
+    b.reset()
+    la, lb = a.prefill(prompt, want_logits=True), b.prefill(prompt, want_logits=True)
+    assert np.abs(la - lb).max() <= 1e-5 * np.abs(la).max()
 
 
 def test_quantizer_and_engine_projection_match_the_reference():

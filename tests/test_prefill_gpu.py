@@ -53,7 +53,7 @@ def _gemm(rows, kind, M, K, x, norm_w, eps, epi, y0=None):
     gb = _lib.DeviceBuffer.from_array(norm_w) if norm_w is not None else None
     cols = M // 2 if epi == _lib.EPI_SWIGLU else M
     yb = _lib.DeviceBuffer.from_array(y0) if y0 is not None else _lib.DeviceBuffer(4 * n * cols)
-    wb = _lib.DeviceBuffer(4 * n * K)
+    wb = _lib.DeviceBuffer(4 * n * (K + 1))
     _lib.call("trx_gemm_ternary_f32", rb.ptr, kind, M, K, xb.ptr, n, gb.ptr if gb else None, ctypes.c_float(eps),
               yb.ptr, epi, wb.ptr, None)
     _lib.call("trx_stream_sync", None)
@@ -87,6 +87,43 @@ def test_gemm_matches_float64(kname, epi, M, K, n, norm):
         bound = 2e-5 * mag + 1e-6 * (np.abs(y0) if y0 is not None else 0) + 1e-7
     err = np.abs(got - want)
     print(kname, epi, M, K, n, "max err / bound", float(np.max(err / bound)))
+    assert np.all(err <= bound)
+
+
+@pytest.mark.parametrize("epi", [_lib.EPI_STORE, _lib.EPI_SWIGLU])
+@pytest.mark.parametrize("norm", [False, True])
+def test_gemm_large_inputs_stay_finite(epi, norm):
+    """Rows with values past fp16's range (1e5, 3e9; with the RMSNorm prologue, gains of 1e6):
+    the planes of such a row are scaled by a power of two and the result scaled back, so the
+    GEMM equals float64 within the same bound as for small inputs, and no output is inf or NaN
+    (an unscaled fp16 plane would turn a 1e5 input into inf - inf = NaN for every output)."""
+    kind, M, K, n = L.KIND_TERNARY5, 256, 512, 6
+    rng = np.random.default_rng(17 + epi + 2 * norm)
+    rows, W = _matrix(kind, M, K, rng)
+    x = rng.standard_normal((n, K)).astype(np.float32)
+    x[1, 7] = 1.0e5
+    x[3, :] *= 3.0e9
+    x[4, 100] = -65520.0
+    g = rng.uniform(0.8, 1.2, K).astype(np.float32) if norm else None
+    if norm:
+        g[5] = 1.0e6
+    eps = 1e-6
+    xd = x.astype(np.float64)
+    if norm:
+        xd = xd / np.sqrt(np.mean(xd * xd, axis=1, keepdims=True) + eps) * g.astype(np.float64)
+    ref, mag = xd @ W.T, np.abs(xd) @ np.abs(W).T
+    got = _gemm(rows, kind, M, K, x, g, eps, epi).astype(np.float64)
+    assert np.isfinite(got).all()
+    if epi == _lib.EPI_SWIGLU:
+        F = M // 2
+        gt, up = ref[:, :F], ref[:, F:]
+        with np.errstate(over="ignore"):
+            want = gt / (1 + np.exp(-gt)) * up
+        bound = 2e-5 * (mag[:, :F] * np.abs(up) + np.abs(gt) * mag[:, F:]) + 1e-7
+    else:
+        want, bound = ref, 2e-5 * mag + 1e-7
+    err = np.abs(got - want)
+    print("large inputs", epi, norm, "max err / bound", float(np.max(err / bound)))
     assert np.all(err <= bound)
 
 
@@ -166,6 +203,31 @@ def test_prefill_refuses_positions_that_compute_logits(tiny_images, golden):
     dec.prefill(len(prompt) - 1)
     dec.step(1)
     assert np.isfinite(dec.logits()).all()
+
+
+def test_prefill_buffers_do_not_grow_with_every_prompt(tiny_images):
+    """A session whose prompts keep growing: the prefill buffers grow in powers of two and the
+    smaller ones are freed, so the device bytes stay within the buffers of twice the longest
+    chunk, and the logits stay those of a fresh decoder."""
+    from trixium_amd.model import INFO_DEVICE_BYTES
+    path = tiny_images[("tiny-qwen3", True)]
+    dec = _decoder(path, prefill_chunk=1024, max_ctx=128)
+    base = dec.info(INFO_DEVICE_BYTES)
+    sizes = []
+    for n in range(2, 120, 7):
+        dec.reset()
+        dec.forward(list(range(1, n + 1)))
+        sizes.append(dec.info(INFO_DEVICE_BYTES) - base)
+    # tiny-qwen3: at most 128 rows of 256-wide activations, FFN 768, q|k|v 512 (a few MB).
+    per_row = 4 * 256 + 2 * 2 * 768 + 4 + 4 * 512 + 4 * 256 + 4 * 768 + 4 * 256
+    assert max(sizes) <= 128 * per_row, sizes
+    assert sizes[-1] == max(sizes)
+    ref = _decoder(path, prefill_chunk=1024, max_ctx=128)
+    lg = ref.forward(list(range(1, 114)))
+    dec.reset()
+    assert _rel_err(dec.forward(list(range(1, 114))), lg) <= 1e-6
+    dec.close()
+    ref.close()
 
 
 def test_prefill_yarn_image(tmp_path):

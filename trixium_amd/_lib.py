@@ -31,7 +31,7 @@ class ModelConfig(ctypes.Structure):
                                     "dn_v_head_dim", "dn_conv_kernel")] + [
         ("layer_types", ctypes.c_uint64 * 2)] + [
         (n, ctypes.c_int) for n in ("weight_kind", "head_kind", "head_tied", "emb_mode", "emb_kind",
-                                    "max_new", "persistent", "packed_ops")] + [
+                                    "max_new", "packed_ops")] + [
         ("hadamard_block", ctypes.c_int), ("hadamard_scale", ctypes.c_float),
         ("hadamard_widths", ctypes.c_int * 4), ("rope_table", ctypes.c_int), ("prefill_chunk", ctypes.c_int)]
 

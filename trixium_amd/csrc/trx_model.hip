@@ -102,6 +102,7 @@ struct Model {
   float *pf_x = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_att = nullptr, *pf_act = nullptr;
   float *pf_ba = nullptr, *pf_conv = nullptr, *pf_oraw = nullptr;
   _Float16 *pf_h = nullptr, *pf_l = nullptr;
+  float* pf_xs = nullptr;                          // [pf_rows] row scales of the input planes
   int host_n_fed = 0, host_head_from = 0;          // host copies of the control words
   hipGraph_t graph = nullptr;
   hipGraphExec_t graph_exec = nullptr;
@@ -737,6 +738,7 @@ static int pf_prep(Model& m, const float* x, int ldx, int K, int R, const float*
   pp.eps = m.cfg.rms_eps;
   pp.xh = m.pf_h;
   pp.xl = m.pf_l;
+  pp.xs = m.pf_xs;
   if (m.cfg.hadamard_block && !plain) {
     int wi = 0;
     while (wi < 4 && m.cfg.hadamard_widths[wi] != K) ++wi;
@@ -762,6 +764,7 @@ static int pf_gemm(Model& m, int role, int l, int kind, int M, int K, int R, int
   g.code_off = kind == TRX_KIND_Q8 ? kBeat * cdiv(K / 32, 16) : row_geom(kind, K).code_off;
   g.xh = m.pf_h;
   g.xl = m.pf_l;
+  g.xs = m.pf_xs;
   g.R = R;
   g.epi = epi;
   g.y = y;
@@ -769,6 +772,19 @@ static int pf_gemm(Model& m, int role, int l, int kind, int M, int K, int R, int
   return launch_gemm(g, s);
 }
 
+// Frees one of the model's device allocations (the stream must be idle for it).
+static int dfree(Model& m, void* p, size_t bytes) {
+  if (!p) return TRX_OK;
+  auto it = std::find(m.allocs.begin(), m.allocs.end(), p);
+  if (it != m.allocs.end()) m.allocs.erase(it);
+  m.dev_bytes -= bytes;
+  TRX_HIP(hipFree(p));
+  return TRX_OK;
+}
+
+// Prefill buffers for chunks of up to R positions. Capacities grow in powers of two (at least
+// 64 rows); the smaller buffers are freed when they grow, so prompts of growing length hold
+// at most twice the largest chunk.
 static int pf_alloc(Model& m, int R) {
   if (R <= m.pf_rows) return TRX_OK;
   const trx_model_config& c = m.cfg;
@@ -779,22 +795,33 @@ static int pf_alloc(Model& m, int R) {
   const int kmax = std::max({E, F, c.n_head * hd, nvh});
   const int io = std::max(m.n_attn ? qrows + 2 * kvrows : 0, m.n_dn ? C + nvh : 0);
   const int att = std::max(c.n_head * hd, nvh);
-  // Earlier (smaller) buffers stay allocated until the model is destroyed.
+  // (buffer, bytes per row) of every prefill buffer.
+  const std::vector<std::pair<void**, size_t>> bufs = {
+      {(void**)&m.pf_x, (size_t)E * 4},
+      {(void**)&m.pf_h, (size_t)kmax * 2},
+      {(void**)&m.pf_l, (size_t)kmax * 2},
+      {(void**)&m.pf_xs, 4},
+      {(void**)&m.pf_qkv, (size_t)io * 4},
+      {(void**)&m.pf_att, (size_t)att * 4},
+      {(void**)&m.pf_act, (size_t)F * 4},
+      {(void**)&m.pf_q, m.n_attn ? (size_t)c.n_head * hd * 4 : 0},
+      {(void**)&m.pf_ba, m.n_dn ? (size_t)2 * c.dn_num_v_heads * 4 : 0},
+      {(void**)&m.pf_conv, m.n_dn ? (size_t)C * 4 : 0},
+      {(void**)&m.pf_oraw, m.n_dn ? (size_t)nvh * 4 : 0}};
   int rc;
-  const size_t r = (size_t)R;
-  if ((rc = dalloc(m, (void**)&m.pf_x, r * E * 4))) return rc;
-  if ((rc = dalloc(m, (void**)&m.pf_h, r * kmax * 2))) return rc;
-  if ((rc = dalloc(m, (void**)&m.pf_l, r * kmax * 2))) return rc;
-  if ((rc = dalloc(m, (void**)&m.pf_qkv, r * io * 4))) return rc;
-  if ((rc = dalloc(m, (void**)&m.pf_att, r * att * 4))) return rc;
-  if ((rc = dalloc(m, (void**)&m.pf_act, r * F * 4))) return rc;
-  if (m.n_attn && (rc = dalloc(m, (void**)&m.pf_q, r * c.n_head * hd * 4))) return rc;
-  if (m.n_dn) {
-    if ((rc = dalloc(m, (void**)&m.pf_ba, r * 2 * c.dn_num_v_heads * 4))) return rc;
-    if ((rc = dalloc(m, (void**)&m.pf_conv, r * C * 4))) return rc;
-    if ((rc = dalloc(m, (void**)&m.pf_oraw, r * nvh * 4))) return rc;
+  if (m.pf_rows > 0) {
+    TRX_HIP(hipStreamSynchronize(m.stream));
+    for (auto& b : bufs) {
+      if ((rc = dfree(m, *b.first, b.second * (size_t)m.pf_rows))) return rc;
+      *b.first = nullptr;
+    }
+    m.pf_rows = 0;
   }
-  m.pf_rows = R;
+  int cap = 64;
+  while (cap < R) cap *= 2;
+  for (auto& b : bufs)
+    if (b.second && (rc = dalloc(m, b.first, b.second * (size_t)cap))) return rc;
+  m.pf_rows = cap;
   return TRX_OK;
 }
 
@@ -932,7 +959,6 @@ TRX_API int trx_model_create(const trx_model_config* cfg, const float* rope_freq
             "trx_model_create: unsupported geometry");
   TRX_CHECK(c.weight_kind == TRX_KIND_TERNARY || c.weight_kind == TRX_KIND_TERNARY5, TRX_E_INVALID,
             "trx_model_create: weight_kind must be ternary");
-  TRX_CHECK(c.persistent == 0, TRX_E_INVALID, "trx_model_create: persistent %d is not supported", c.persistent);
   TRX_CHECK(c.emb_mode >= 0 && c.emb_mode <= 2, TRX_E_INVALID, "trx_model_create: emb_mode %d", c.emb_mode);
   if (c.emb_mode == 2) {
     bool has = false;
@@ -1374,7 +1400,8 @@ TRX_API int trx_model_info(trx_model* h, int what, int64_t* value) {
     case TRX_INFO_ARENA_BYTES: *value = (int64_t)m.arena_bytes; break;
     case TRX_INFO_DEVICE_BYTES: *value = (int64_t)m.dev_bytes; break;
     case TRX_INFO_STREAM: *value = (int64_t)(intptr_t)m.stream; break;
-    case TRX_INFO_PERSISTENT: *value = 0; break;
+    case TRX_INFO_ATTN_SPLITS: *value = m.n_split; break;
+    case TRX_INFO_ATTN_PASS: *value = attention_pass_positions(m.cfg.head_dim); break;
     case TRX_INFO_PACKED_OPS: *value = m.packed_ops; break;
     case TRX_INFO_WEIGHT_BYTES: {
       int64_t s = 0;

@@ -172,6 +172,7 @@ int launch_attention_fd(const AttnParams& p, hipStream_t s);
 int launch_attention_merge(const AttnParams& p, hipStream_t s);
 int attention_splits(int n_kv, int head_dim, int max_ctx);   // -1: the context is too long
 int attention_max_chunk(int head_dim);                          // positions one split can hold
+int attention_pass_positions(int head_dim);                     // positions one pass of a split block covers
 int launch_dense_gemv(const DenseParams& p, hipStream_t s);
 int launch_synth_ternary(const SynthParams& p, hipStream_t s);
 int launch_synth_f32(float* out, long long n, uint32_t seed, uint32_t tensor_id, float lo, float span,

@@ -11,8 +11,10 @@ namespace trx {
 // W is read as stored (BONS row packets, M rows of row_bytes) and decoded per 128-column group
 // into LDS as fp16 weights (code - 1) * scale (2-bit, trit5) or fp16(q * scale) (Q8), which are
 // exactly fastref's fp16 weight cache (model/fastref.py:104-116). X comes as two fp16 planes,
-// xh = fp16(x) and xl = fp16(x - xh), so that each product of the fp32 accumulation sees x to
-// ~22 bits (the result is within float32 rounding of the fp32 product).
+// xh = fp16(x') and xl = fp16(x' - xh) of x' = x / xs[r], so that each product of the fp32
+// accumulation sees x to ~22 bits (the result is within float32 rounding of the fp32 product);
+// xs[r] is a power of two that keeps row r's planes finite (1 for rows below 2^14), multiplied
+// back in the epilogue.
 enum { GM_STORE = 0, GM_RESID = 1, GM_SWIGLU = 2 };
 struct GemmParams {
   const uint8_t* W;        // row packets
@@ -21,6 +23,7 @@ struct GemmParams {
   int M, K, row_bytes, code_off;
   const _Float16* xh;      // [R][K]
   const _Float16* xl;      // [R][K]
+  const float* xs;         // [R] row scales (powers of two)
   int R;
   int epi;
   float* y;                // GM_STORE: y[r*ldy + m] = acc; GM_RESID: y[r*ldy + m] += acc;
@@ -30,7 +33,9 @@ int launch_gemm(const GemmParams& p, hipStream_t s);
 
 // The GEMM's input planes from fp32 rows: v = x (no norm), or x / rms(x) * norm_w (RMSNorm,
 // model/fastref.py:143-144), or a PrismML rotation of that (signs != null: per block of B
-// columns v' = scale * H (signs * v), H the +-1 Sylvester matrix); xh = fp16(v), xl = fp16(v - xh).
+// columns v' = scale * H (signs * v), H the +-1 Sylvester matrix); xh = fp16(v / xs), xl =
+// fp16(v / xs - xh), with xs[r] the power of two that brings row r below 2^14 (1 for most rows:
+// fp16 holds values up to 65504, and a row past that would give inf and NaN products).
 struct PrepParams {
   const float* x;
   int ldx, K, R;
@@ -41,6 +46,7 @@ struct PrepParams {
   float scale;
   _Float16* xh;            // [R][K]
   _Float16* xl;
+  float* xs;               // [R]
 };
 int launch_prep(const PrepParams& p, hipStream_t s);
 

@@ -297,19 +297,20 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
     const int r = r0 + 32 * NA * wr + 32 * a + i;
     if (r >= p.R) continue;
     float* yr = p.y + (size_t)r * p.ldy;
+    const float up = p.xs[r];              // the row's plane scale (a power of two: exact)
     if (EPI == GM_SWIGLU) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const int f = blockIdx.x * (kGmBM / 2) + ct[t] + li;
-        if (f < p.M / 2) yr[f] = silu(acc[a][t][e]) * acc[a][t + 2][e];
+        if (f < p.M / 2) yr[f] = silu(acc[a][t][e] * up) * (acc[a][t + 2][e] * up);
       }
     } else {
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int m = blockIdx.x * kGmBM + ct[t] + li;
         if (m < p.M) {
-          if (EPI == GM_RESID) yr[m] += acc[a][t][e];
-          else yr[m] = acc[a][t][e];
+          if (EPI == GM_RESID) yr[m] += acc[a][t][e] * up;
+          else yr[m] = acc[a][t][e] * up;
         }
       }
     }
@@ -366,6 +367,29 @@ __device__ __forceinline__ void store_hilo(const PrepParams& p, size_t i, float 
   p.xl[i] = (_Float16)(v - (float)h);
 }
 
+// The power of two 2^e (e >= 0) that brings a row whose values are bounded by `bound` below 2^14
+// (fp16 planes stay finite and the low plane keeps its bits), and its inverse.
+__device__ __forceinline__ void row_scale(float bound, float& down, float& up) {
+  down = up = 1.f;
+  if (bound >= 16384.f && bound <= 3.0e38f) {
+    int k;
+    frexpf(bound, &k);                 // bound < 2^k
+    down = ldexpf(1.f, 14 - k);
+    up = ldexpf(1.f, k - 14);
+  }
+}
+
+__device__ __forceinline__ float block_max(float v, float* red) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+  v = wave_max(v);
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float t = red[0];
+  for (int i = 1; i < nw; ++i) t = fmaxf(t, red[i]);
+  return t;
+}
+
 // One block of 256 threads per position, no rotation.
 __global__ __launch_bounds__(256) void prep_kernel(PrepParams p) {
   __shared__ float red[16];
@@ -377,9 +401,14 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepParams p) {
     for (int c = t; c < p.K; c += 256) ss += x[c] * x[c];
     rs = 1.0f / sqrtf(block_sum(ss, red) / (float)p.K + p.eps);
   }
+  float am = 0.f;
+  for (int c = t; c < p.K; c += 256) am = fmaxf(am, fabsf(p.norm_w ? x[c] * rs * p.norm_w[c] : x[c]));
+  float down, up;
+  row_scale(block_max(am, red), down, up);
+  if (t == 0) p.xs[r] = up;
   for (int c = t; c < p.K; c += 256) {
     const float v = p.norm_w ? x[c] * rs * p.norm_w[c] : x[c];
-    store_hilo(p, (size_t)r * p.K + c, v);
+    store_hilo(p, (size_t)r * p.K + c, v * down);
   }
 }
 
@@ -390,18 +419,37 @@ __global__ __launch_bounds__(1024) void prep_rot_kernel(PrepParams p) {
   __shared__ float red[16];
   const int t = threadIdx.x, B = blockDim.x, c = blockIdx.x * B + t, r = blockIdx.y;
   const int lane = t & 63, w = t >> 6;
+  __shared__ float mred[16];
   const float* x = p.x + (size_t)r * p.ldx;
   float a = x[c] * p.signs[c];
-  if (p.norm_w) {
-    float ss = 0.f;
-    for (int i = t; i < p.K; i += B) ss += x[i] * x[i];
-    ss = wave_sum(ss);
-    if (lane == 0) red[w] = ss;
-    __syncthreads();
-    float tot = 0.f;
-    for (int k = 0; k < B / 64; ++k) tot += red[k];
-    a *= p.norm_w[c] / sqrtf(tot / (float)p.K + p.eps);
+  // The whole row's sum of squares (RMSNorm) and maximum of |x * gain|: every output of a
+  // rotation block is bounded by scale * B times that maximum (times 1/rms), which sets the row's
+  // scale for every block alike.
+  float ss = 0.f, am = 0.f;
+  for (int i = t; i < p.K; i += B) {
+    ss += x[i] * x[i];
+    am = fmaxf(am, fabsf(p.norm_w ? x[i] * p.norm_w[i] : x[i]));
   }
+  ss = wave_sum(ss);
+  am = wave_max(am);
+  if (lane == 0) {
+    red[w] = ss;
+    mred[w] = am;
+  }
+  __syncthreads();
+  float tot = 0.f, amax = 0.f;
+  for (int k = 0; k < B / 64; ++k) {
+    tot += red[k];
+    amax = fmaxf(amax, mred[k]);
+  }
+  float rsn = 1.f;
+  if (p.norm_w) {
+    rsn = 1.0f / sqrtf(tot / (float)p.K + p.eps);
+    a *= p.norm_w[c] * rsn;
+  }
+  float down, up;
+  row_scale(fabsf(p.scale) * (float)B * amax * rsn, down, up);
+  if (blockIdx.x == 0 && t == 0) p.xs[r] = up;
   for (int h = 1; h < 64; h <<= 1) {
     const float o = __shfl_xor(a, h, 64);
     a = (lane & h) ? o - a : a + o;
@@ -413,11 +461,11 @@ __global__ __launch_bounds__(1024) void prep_rot_kernel(PrepParams p) {
     __syncthreads();
     a = (t & h) ? o - a : a + o;
   }
-  store_hilo(p, (size_t)r * p.K + c, a * p.scale);
+  store_hilo(p, (size_t)r * p.K + c, a * p.scale * down);
 }
 
 int launch_prep(const PrepParams& p, hipStream_t s) {
-  TRX_CHECK(p.R >= 1 && p.K >= 1 && p.ldx >= p.K, TRX_E_INVALID, "prefill input: R=%d K=%d", p.R, p.K);
+  TRX_CHECK(p.R >= 1 && p.K >= 1 && p.ldx >= p.K && p.xs, TRX_E_INVALID, "prefill input: R=%d K=%d", p.R, p.K);
   if (p.signs) {
     TRX_CHECK(p.B >= 64 && p.B <= 1024 && (p.B & (p.B - 1)) == 0 && p.K % p.B == 0, TRX_E_INVALID,
               "prefill input: rotation block %d over %d columns unsupported", p.B, p.K);
@@ -963,6 +1011,7 @@ TRX_API int trx_gemm_ternary_f32(const uint8_t* rows, int kind, int M, int K, co
   const int code_off = kind == TRX_KIND_Q8 ? kBeat * cdiv(K / 32, 16) : row_geom(kind, K).code_off;
   _Float16* xh = (_Float16*)workspace;
   _Float16* xl = xh + (size_t)n * K;
+  float* xs = (float*)(xl + (size_t)n * K);
   PrepParams pp = {};
   pp.x = x;
   pp.ldx = K;
@@ -972,6 +1021,7 @@ TRX_API int trx_gemm_ternary_f32(const uint8_t* rows, int kind, int M, int K, co
   pp.eps = eps;
   pp.xh = xh;
   pp.xl = xl;
+  pp.xs = xs;
   int rc;
   if ((rc = launch_prep(pp, (hipStream_t)s))) return rc;
   GemmParams g = {};
@@ -984,6 +1034,7 @@ TRX_API int trx_gemm_ternary_f32(const uint8_t* rows, int kind, int M, int K, co
   g.code_off = code_off;
   g.xh = xh;
   g.xl = xl;
+  g.xs = xs;
   g.R = n;
   g.epi = epilogue == TRX_EPI_STORE ? GM_STORE : epilogue == TRX_EPI_RESID ? GM_RESID : GM_SWIGLU;
   g.y = y;

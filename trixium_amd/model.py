@@ -25,7 +25,8 @@ f32 = np.float32
 
 (READ_LOGITS, READ_HIDDEN, READ_POSITION, READ_TOKEN, READ_OUT, READ_SLOT, READ_QKV, READ_ATTN, READ_ACT,
  READ_RESIDUAL) = range(10)
-INFO_ARENA_BYTES, INFO_DEVICE_BYTES, INFO_STREAM, INFO_WEIGHT_BYTES, INFO_PERSISTENT, INFO_PACKED_OPS = range(6)
+(INFO_ARENA_BYTES, INFO_DEVICE_BYTES, INFO_STREAM, INFO_WEIGHT_BYTES, _INFO_UNUSED, INFO_PACKED_OPS, INFO_ATTN_SPLITS,
+ INFO_ATTN_PASS) = range(8)
 
 # Projections run by the packed GEMV (TRX_PACK_* bits; PACK_AUTO lets the library choose).
 PACK_QKV, PACK_O, PACK_GATE_UP, PACK_DOWN, PACK_HEAD, PACK_DN = 1, 2, 4, 8, 16, 32
@@ -54,7 +55,7 @@ def layer_type_bits(layer_types, n_layer):
 
 
 def make_config(mc, weight_kind, head_kind, head_tied, emb_mode, emb_kind, max_ctx=None, max_new=256,
-                persistent=False, packed_ops=PACK_AUTO, prefill_chunk=0):
+                packed_ops=PACK_AUTO, prefill_chunk=0):
     """trx_model_config from a ModelConfig (or a BONS header turned into one)."""
     c = _lib.ModelConfig()
     for name in ("n_layer", "n_embd", "n_head", "n_kv_head", "head_dim", "ffn_dim", "vocab",
@@ -68,7 +69,6 @@ def make_config(mc, weight_kind, head_kind, head_tied, emb_mode, emb_kind, max_c
     c.layer_types[0], c.layer_types[1] = lo, hi
     c.weight_kind, c.head_kind, c.head_tied = weight_kind, head_kind, int(bool(head_tied))
     c.emb_mode, c.emb_kind, c.max_new = emb_mode, emb_kind, int(max_new)
-    c.persistent = int(persistent)
     c.packed_ops = int(packed_ops)
     c.prefill_chunk = int(prefill_chunk)
     return c
@@ -102,8 +102,7 @@ class Decoder:
 
     # Construction ------------------------------------------------------------------------------
     @classmethod
-    def from_image(cls, img, max_ctx=None, max_new=256, use_graph=True, persistent=False,
-                   packed_ops=PACK_AUTO, prefill_chunk=0):
+    def from_image(cls, img, max_ctx=None, max_new=256, use_graph=True, packed_ops=PACK_AUTO, prefill_chunk=0):
         """Load a BONS image (path or BONSReader) into HBM. prefill_chunk > 0: forward() and
         generate() run all but the last fed token through the batched prefill, that many
         positions per weight pass (0: one position per forward, as the firmware's loop)."""
@@ -137,13 +136,8 @@ class Decoder:
         else:
             head_kind = L.KIND_F16 if head["kind"] == L.KIND_F32 else head["kind"]
             emb_kind = emb["kind"] if emb is not None and L.is_ternary(emb["kind"]) else weight_kind
-        if rot is not None:
-            # A rotated model: one kernel per operation, every projection's input rotated first
-            # (no partial-sum handoffs between packed GEMVs, no persistent kernel).
-            if persistent:
-                raise ValueError("a rotated (Hadamard) image runs one kernel per operation")
-        cfg = make_config(mc, weight_kind, head_kind, head_tied, emb_mode, emb_kind, max_ctx, max_new, persistent,
-                          packed_ops, prefill_chunk)
+        cfg = make_config(mc, weight_kind, head_kind, head_tied, emb_mode, emb_kind, max_ctx, max_new, packed_ops,
+                          prefill_chunk)
         if rot is not None:
             block, scale, signs = rot
             cfg.hadamard_block, cfg.hadamard_scale = block, scale
@@ -168,13 +162,13 @@ class Decoder:
 
     @classmethod
     def synthetic(cls, mc, seed=0, weight_kind=L.KIND_TERNARY5, max_ctx=None, max_new=256,
-                  use_graph=True, persistent=False, packed_ops=PACK_AUTO, prefill_chunk=0):
+                  use_graph=True, packed_ops=PACK_AUTO, prefill_chunk=0):
         """Fill every tensor on the device from the counter-based generator (same values as
         trixium_amd.synth.hashed_*): ternary token_embd rows (embedded by decoding the row), an
         untied ternary LM head unless the config ties them. A hybrid's DeltaNet beta|alpha Q8
         rows come from the host (seeded int8 values, fp16 scales U(0.01, 0.05))."""
         cfg = make_config(mc, weight_kind, weight_kind, mc.tie_embeddings, 1, weight_kind, max_ctx, max_new,
-                          persistent, packed_ops, prefill_chunk)
+                          packed_ops, prefill_chunk)
         d = cls(mc, cfg, use_graph)
         try:
             ranges = np.array([SYNTH_SCALE[0], SYNTH_SCALE[1] - SYNTH_SCALE[0],
@@ -403,9 +397,10 @@ class Decoder:
         return v.value
 
     @property
-    def persistent(self):
-        """True when each position runs as one persistent kernel."""
-        return bool(self.info(INFO_PERSISTENT))
+    def attention_splits(self):
+        """(position splits per kv head, positions per pass of a split block) of the decode
+        attention: a split of c positions takes ceil(c / positions per pass) passes."""
+        return self.info(INFO_ATTN_SPLITS), self.info(INFO_ATTN_PASS)
 
     @property
     def stream(self):
