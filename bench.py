@@ -89,6 +89,9 @@ def parse_args():
     ap.add_argument("--trace-decode", type=int, default=0, metavar="N",
                     help="prefill the prompt, then run N decode positions and exit (for kernel traces "
                          "and hardware counters; with --no-graph every kernel launches eagerly)")
+    ap.add_argument("--probes", action="store_true",
+                    help="run only the streaming-read ceiling and the empty-kernel (graph node and "
+                         "stream launch) probes and print their record")
     ap.add_argument("--exact-rows", type=int, default=0, metavar="N",
                     help="time the engine matvec at the 8B gate|up shape on N int8 rows in one "
                          "weight pass (trx_gemv_ternary_exact_rows) against N single-row calls, "
@@ -244,27 +247,81 @@ def matvec_microbench(reps=1000, rotate_bytes=512 << 20):
                 _lib.call("trx_gemv_packed_f32", packed.ptr + i * stride, kind, M, K, xb.ptr, None,
                           ctypes.c_float(1e-6), ys.ptr, 0, None, work.ptr, None)
             us1 = timed(single, reps) / reps
-            # The engine's exact group sums on int8 x (the integer path), bit for bit.
+            del packed, part
+            # The engine's integer matvec on int8 x (the row-packet kernel reading BONS rows as
+            # stored), timed the same way: one launch over n2 copies of the rows laid back to
+            # back (at least rotate_bytes, each row read once per launch), as group sums
+            # gs[m][g] (the adder trees' output, G int32 per row) and as the engine-exact int32
+            # result (model/bitexact.py:101-119, with the tensor's B and R). The first and last
+            # copies' group sums are checked bit for bit against integer numpy, and their exact
+            # results against one launch over a single copy.
+            G = K // 128
+            row_b = L.row_bytes(K, kind)
+            mat_b = M * row_b
+            n2 = max(1, -(-rotate_bytes // mat_b))
+            rot = _lib.DeviceBuffer(mat_b * n2)
+            for i in range(n2):
+                _lib.call("trx_memcpy_d2d", rot.ptr + i * mat_b, rows.ptr, mat_b, None)
             xq = _lib.DeviceBuffer.from_array(x8)
-            gsb = _lib.DeviceBuffer(4 * M * (K // 128))
-            _lib.call("trx_gemv_ternary_groupsums", rows.ptr, kind, M, K, xq.ptr, gsb.ptr, None)
+            gsb = _lib.DeviceBuffer(4 * n2 * M * G)
+            n_int = max(2, -(-reps // n2))
+            us_gs = timed(lambda: _lib.call("trx_gemv_ternary_groupsums", rot.ptr, kind, n2 * M, K, xq.ptr, gsb.ptr,
+                                            None), n_int, lead=True)
+            gs = gsb.download(np.int32, n2 * M * G).reshape(n2, M, G)
+            gs_ok = bool(np.array_equal(gs[0], gs_want) and np.array_equal(gs[-1], gs_want))
+            del gsb
+            B_, R_ = exact_scale_bias(scales)
+            yb_ex = _lib.DeviceBuffer(4 * n2 * M)
+            st = _lib.DeviceBuffer(4)
+            st.zero()
+            us_ex = timed(lambda: _lib.call("trx_gemv_ternary_exact", rot.ptr, kind, n2 * M, K, xq.ptr, B_, R_,
+                                            yb_ex.ptr, st.ptr, None), n_int, lead=True)
+            y1 = _lib.DeviceBuffer(4 * M)
+            _lib.call("trx_gemv_ternary_exact", rows.ptr, kind, M, K, xq.ptr, B_, R_, y1.ptr, st.ptr, None)
             _lib.synchronize()
-            gs_ok = bool(np.array_equal(gsb.download(np.int32, M * (K // 128)).reshape(M, -1), gs_want))
+            ex = yb_ex.download(np.int32, n2 * M).reshape(n2, M)
+            one = y1.download(np.int32, M)
+            ex_ok = bool(np.array_equal(ex[0], one) and np.array_equal(ex[-1], one)
+                         and st.download(np.int32, 1)[0] == 0)
+            gs_bytes = mat_b + K + 4 * M * G            # rows, int8 x, int32 group sums
+            ex_bytes = mat_b + K + 4 * M
+            gs_gbs = gs_bytes * n2 * n_int / (us_gs * 1e-6) / 1e9
+            ex_gbs = ex_bytes * n2 * n_int / (us_ex * 1e-6) / 1e9
+            del rot, yb_ex
             out[f"{M}x{K}/{kname}"] = {
                 "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "us_per_matvec": round(us / count, 3),
                 "bytes_per_matvec": algo, "matvecs": count, "copies": n, "rotated_MB": round(n * stride / 2**20, 1),
                 "single_launch_us": round(us1, 3), "single_launch_GBs": round(algo / (us1 * 1e-6) / 1e9, 1),
-                "max_rel_err": float(f"{err:.2e}"), "groupsums_bitexact": gs_ok}
-            del packed, xb, yb, part, rows
+                "max_rel_err": float(f"{err:.2e}"),
+                "exact_int8": {"groupsums_GBs": round(gs_gbs, 1), "groupsums_frac": round(gs_gbs / HBM_PEAK_GBS, 4),
+                               "groupsums_bytes_per_matvec": gs_bytes, "groupsums_bitexact": gs_ok,
+                               "engine_exact_GBs": round(ex_gbs, 1), "engine_exact_frac": round(ex_gbs / HBM_PEAK_GBS, 4),
+                               "engine_exact_bytes_per_matvec": ex_bytes, "engine_exact_equal": ex_ok,
+                               "matvecs": n2 * n_int}}
+            del xb, yb, rows
     _lib.call("trx_event_destroy", e0)
     _lib.call("trx_event_destroy", e1)
     tot_bytes = sum(v["bytes_per_matvec"] * v["matvecs"] for v in out.values())
     tot_us = sum(v["us_per_matvec"] * v["matvecs"] for v in out.values())
     agg = tot_bytes / (tot_us * 1e-6) / 1e9
+    gs_b = sum(v["exact_int8"]["groupsums_bytes_per_matvec"] * v["exact_int8"]["matvecs"] for v in out.values())
+    gs_t = sum(v["exact_int8"]["groupsums_bytes_per_matvec"] * v["exact_int8"]["matvecs"] / v["exact_int8"]["groupsums_GBs"]
+               for v in out.values())
     return {"kernel": "packed table-lookup GEMV, many matvecs y = W x per dispatch over rotating copies of W "
                       "(trx_gemv_packed_batched_f32, one x: each block reuses its slice's table over several "
                       "matrices), fp32 x and y", "aggregate_GBs": round(agg, 1), "aggregate_frac": round(agg / HBM_PEAK_GBS, 4),
+            "exact_int8_kernel": "row-packet engine kernel on int8 x over BONS rows as stored "
+                                 "(trx_gemv_ternary_groupsums / trx_gemv_ternary_exact), one launch over the copies",
+            "exact_int8_groupsums_aggregate_GBs": round(gs_b / gs_t, 1),
             "peak_GBs": HBM_PEAK_GBS, "shapes": out}
+
+
+def exact_scale_bias(scales):
+    """The engine's per-tensor B and R for fp16 scales (model/bitexact.py:56-97):
+    B = 12 - max exponent, R the smallest shift that keeps every result within int32."""
+    from trixium_amd.fixedpoint import scale_bias, result_shift
+    B = scale_bias(scales)
+    return B, result_shift(scales, B)
 
 
 def copy_calibration(nbytes):
@@ -278,10 +335,12 @@ def copy_calibration(nbytes):
     print(json.dumps({"copy_bytes": nbytes, "launches": 10}), flush=True)
 
 
-def time_dominant_kernel(dec, mc, reps):
+def time_dominant_kernel(dec, mc, reps, graph=True):
     """Average duration of the gate|up GEMV over the resident layer matrices (HIP events on the
     model stream), launched as the decode launches it: with the packed gate|up and down, the
-    partial sums and slice sums of x^2 that down's prologue reduces."""
+    partial sums and slice sums of x^2 that down's prologue reduces. graph: the 36 launches are
+    captured into one hipGraph and replayed `reps` times, as the decode's graph replays its
+    kernels back to back (otherwise eager launches, for kernel traces)."""
     import ctypes
     from trixium_amd import _lib, layout as L
     from trixium_amd.model import PACK_GATE_UP, PACK_DOWN
@@ -321,14 +380,28 @@ def time_dominant_kernel(dec, mc, reps):
 
     launch()
     _lib.call("trx_stream_sync", s)
+    run = launch
+    exe = None
+    if graph:
+        exe = ctypes.c_void_p()
+        _lib.call("trx_graph_begin", s)
+        launch()
+        _lib.call("trx_graph_end", s, ctypes.byref(exe))
+
+        def run():
+            _lib.call("trx_graph_launch", exe, s)
+        run()
+        _lib.call("trx_stream_sync", s)
     e0, e1 = ctypes.c_void_p(), ctypes.c_void_p()
     _lib.call("trx_event_create", ctypes.byref(e0))
     _lib.call("trx_event_create", ctypes.byref(e1))
     _lib.call("trx_event_record", e0, s)
     for _ in range(reps):
-        launch()
+        run()
     _lib.call("trx_event_record", e1, s)
     _lib.call("trx_stream_sync", s)
+    if exe is not None:
+        _lib.call("trx_graph_destroy", exe)
     ms = ctypes.c_float()
     _lib.call("trx_event_elapsed_ms", e0, e1, ctypes.byref(ms))
     _lib.call("trx_event_destroy", e0)
@@ -337,6 +410,57 @@ def time_dominant_kernel(dec, mc, reps):
     rb = L.row_bytes(E, kind)
     algo = 2 * F * rb + E * 4 + E * 4 + F * 4
     return ms.value * 1e3 / n, algo, n, mode
+
+
+def probes(read_bytes=1 << 30, nodes=400, reps=10):
+    """Two references the kernels are held to, measured on this GPU: a plain streaming read of
+    device memory (trx_probe_stream_read over read_bytes, the best of a few launch shapes: the
+    practical read ceiling, against the 8 TB/s peak), and the fixed cost of an empty kernel as a
+    dependent node of a replayed hipGraph and as a stream launch (trx_probe_empty)."""
+    import ctypes
+    from trixium_amd import _lib
+    s = ctypes.c_void_p()
+    _lib.call("trx_stream_create", ctypes.byref(s))
+    e0, e1 = ctypes.c_void_p(), ctypes.c_void_p()
+    _lib.call("trx_event_create", ctypes.byref(e0))
+    _lib.call("trx_event_create", ctypes.byref(e1))
+
+    def timed(fn, n):
+        fn()
+        _lib.call("trx_stream_sync", s)
+        _lib.call("trx_event_record", e0, s)
+        for _ in range(n):
+            fn()
+        _lib.call("trx_event_record", e1, s)
+        _lib.call("trx_stream_sync", s)
+        ms = ctypes.c_float()
+        _lib.call("trx_event_elapsed_ms", e0, e1, ctypes.byref(ms))
+        return ms.value * 1e3 / n
+
+    buf = _lib.DeviceBuffer(read_bytes)
+    buf.zero()
+    out = _lib.DeviceBuffer(4 * 4096)
+    shapes = {}
+    for blocks, threads in ((256, 1024), (512, 1024), (1024, 512), (2048, 256), (4096, 256)):
+        us = timed(lambda: _lib.call("trx_probe_stream_read", buf.ptr, read_bytes, out.ptr, blocks, threads, s), 10)
+        shapes[f"{blocks}x{threads}"] = round(read_bytes / (us * 1e-6) / 1e9, 1)
+    best = max(shapes.values())
+    del buf
+    stream_us = timed(lambda: _lib.call("trx_probe_empty", s), 2000)
+    exe = ctypes.c_void_p()
+    _lib.call("trx_graph_begin", s)
+    for _ in range(nodes):
+        _lib.call("trx_probe_empty", s)
+    _lib.call("trx_graph_end", s, ctypes.byref(exe))
+    node_us = timed(lambda: _lib.call("trx_graph_launch", exe, s), reps) / nodes
+    _lib.call("trx_graph_destroy", exe)
+    _lib.call("trx_event_destroy", e0)
+    _lib.call("trx_event_destroy", e1)
+    _lib.call("trx_stream_destroy", s)
+    return {"stream_read": {"GBs": best, "frac_of_peak": round(best / HBM_PEAK_GBS, 4), "bytes": read_bytes,
+                            "by_blocks_x_threads": shapes},
+            "empty_kernel_us": {"graph_node": round(node_us, 3), "stream_launch": round(stream_us, 3),
+                                "graph_nodes": nodes}}
 
 
 def traffic_from_profile(kind, mode):
@@ -432,6 +556,9 @@ def main():
     if a.only_microbench:
         print(json.dumps({"matvec_microbench": matvec_microbench()}), flush=True)
         return
+    if a.probes:
+        print(json.dumps({"probes": probes()}), flush=True)
+        return
     mc = {"8b": C.QWEN3_8B, "1.7b": C.QWEN3_1P7B, "27b": C.QWEN35_27B}[a.model]
     if a.prompt is None:
         a.prompt = {"8b": 2048, "1.7b": 512, "27b": 1024}[a.model]
@@ -439,8 +566,9 @@ def main():
     if a.only_kernel:
         dec = Decoder.synthetic(mc, a.seed, weight_kind=kind, max_ctx=mc.max_ctx, max_new=8,
                                 packed_ops=a.packed_ops)
-        us, algo, n_launch, _ = time_dominant_kernel(dec, mc, a.kernel_reps)
+        us, algo, n_launch, _ = time_dominant_kernel(dec, mc, a.kernel_reps, graph=not a.no_graph)
         print(json.dumps({"kernel_us": round(us, 3), "bytes_per_launch": algo, "launches": n_launch,
+                          "timing": "eager launches" if a.no_graph else "graph replay",
                           "achieved_GBs": round(algo / (us * 1e-6) / 1e9, 1)}), flush=True)
         dec.close()
         return
@@ -562,7 +690,7 @@ def main():
         dec.close()
         return
 
-    us, algo, n_launch, gu_mode = time_dominant_kernel(dec, mc, a.kernel_reps)
+    us, algo, n_launch, gu_mode = time_dominant_kernel(dec, mc, a.kernel_reps, graph=graph)
     achieved = algo / (us * 1e-6) / 1e9
     from trixium_amd.model import PACK_QKV, PACK_O, PACK_GATE_UP, PACK_DOWN
     layer_ops = PACK_QKV | PACK_O | PACK_GATE_UP | PACK_DOWN
@@ -597,13 +725,16 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profile(a.kind, gu_mode),
                      "kernel": f"ternary GEMV gate|up {2 * mc.ffn_dim}x{mc.n_embd} {a.kind}, {kdesc}",
-                     "us_per_launch": round(us, 3), "bytes_per_launch": algo, "launches": n_launch},
+                     "us_per_launch": round(us, 3), "bytes_per_launch": algo, "launches": n_launch,
+                     "timing": ("HIP events over replays of a hipGraph of the 36 layers' launches (the decode's "
+                                "form)" if graph else "HIP events over eager launches")},
         "token_roofline": {"bytes_per_token": int(tok_bytes), "tok_s": round(roof_tok_s, 1),
                            "frac": round(tok_s / roof_tok_s, 4)},
         "cpu_baseline": None,
         "prefill": prefill,
     }
     dec.close()
+    rec["probes"] = probes()
     if not a.no_microbench:
         rec["matvec_microbench"] = matvec_microbench()
     if not a.no_cpu_baseline:

@@ -370,6 +370,22 @@ int trx_model_tensor_ptr(trx_model* m, int role, int layer, void** ptr, int64_t*
  * do not overlap with the model's own work). */
 int trx_model_packed_ptr(trx_model* m, int op, int layer, void** packed, void** workspace);
 
+/* Measurement (no counterpart in the reference; for benchmarks and tests) -------------------------
+ * trx_graph_begin / trx_graph_end: capture the work a caller enqueues on stream s (a created
+ *   stream) into a hipGraph and instantiate it (*exec); trx_graph_launch replays it on a stream;
+ *   trx_graph_destroy frees it. Library calls made between begin and end are captured, not run.
+ * trx_probe_stream_read: a plain streaming read of `bytes` (a multiple of 16) of device memory by
+ *   `blocks` blocks of `threads` threads (16-byte non-temporal loads, grid-stride), one float per
+ *   block to out: the read rate any HBM-bound kernel here can reach.
+ * trx_probe_empty: an empty kernel (one block of 64 threads): the fixed cost of a launch or of a
+ *   dependent graph node. */
+int trx_graph_begin(trx_stream_t s);
+int trx_graph_end(trx_stream_t s, void** exec);
+int trx_graph_launch(void* exec, trx_stream_t s);
+int trx_graph_destroy(void* exec);
+int trx_probe_stream_read(const void* buf, size_t bytes, float* out, int blocks, int threads, trx_stream_t s);
+int trx_probe_empty(trx_stream_t s);
+
 /* Tuning: force the GEMV rows per item (0 = automatic; 1: 4 rows, 2: 2 rows, 3: 1 row, 2 for
  * SwiGLU). Process-wide; for benchmarks and tests. No counterpart in the reference. */
 int trx_gemv_set_variant(int variant);

@@ -192,6 +192,42 @@ def test_packed_projections_match_oracle(tiny_images, golden, name, packed):
     assert got == golden[f"fastref_tokens/{name}"][:N_NEW[name]]
 
 
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-hybrid"])
+def test_taps_of_the_last_forward(tiny_images, golden, name):
+    """The intermediate vectors (q|k|v of the last attention layer, its attention output, the
+    last layer's SwiGLU activation) after a forward, with the packed GEMVs handing their partial
+    sums on (the attention sums the q|k|v partials and keeps the rows) and with the row-packet
+    kernel (which stores each projection): the same vectors within the int16 activations'
+    rounding, and the q|k|v rows equal to the oracle's projection of the last attention layer."""
+    from trixium_amd.model import Decoder
+    prompt = golden[f"prompt/{name}"]
+    taps = []
+    for packed in (63, 0):
+        dec = Decoder.from_image(tiny_images[(name, True)], max_new=4, packed_ops=packed)
+        dec.forward(prompt)
+        taps.append(dec.taps())
+        dec.close()
+    for k in ("qkv", "attn", "act"):
+        assert np.abs(taps[0][k]).max() > 0, k
+        assert _rel_err(taps[0][k], taps[1][k]) <= 2e-3, k
+    # The oracle's q|k|v of the last attention layer at the last prompt position.
+    img = bons.BONSReader(tiny_images[(name, True)])
+    ref = FloatRef(img, kv_fp16=True)
+    ref.forward(prompt[:-1])
+    la = max(l for l in range(ref.n_layer) if not ref.dn[l])
+    seen = {}
+    orig = ref.attention
+
+    def spy(l, hn, pos):
+        if l == la:
+            seen["qkv"] = np.concatenate([ref.proj(r, l, hn) for r in (L.ROLE_ATTN_Q, L.ROLE_ATTN_K, L.ROLE_ATTN_V)])
+        return orig(l, hn, pos)
+
+    ref.attention = spy
+    ref.step(prompt[-1])
+    assert _rel_err(taps[0]["qkv"], seen["qkv"]) <= 2e-3
+
+
 def test_packed_graph_replay_equals_eager(tiny_images, golden):
     from trixium_amd.model import Decoder
     name = "tiny-hybrid"

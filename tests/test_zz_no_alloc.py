@@ -63,3 +63,53 @@ def test_noalloc_gemv_refuses_an_oversized_workspace():
     with pytest.raises(_lib.TrxError):
         _lib.call("trx_gemv_packed_f32_noalloc", x.ptr, L.KIND_TERNARY5, 151936, 12288, x.ptr, None,
                   ctypes.c_float(1e-6), y.ptr, 0, None, None)
+
+
+_CAPTURE_SCRIPT = r"""
+import ctypes, sys
+import numpy as np
+sys.path.insert(0, sys.argv[1])
+from trixium_amd import _lib, layout as L
+from trixium_amd.bitexact import PackedMatrix
+r = np.random.default_rng(5)
+u = r.random((1024, 2048))
+codes = np.where(u < 0.3, 0, np.where(u < 0.7, 1, 2)).astype(np.uint8)
+pm = PackedMatrix(r.uniform(0.01, 0.05, (1024, 16)).astype(np.float16), codes, L.KIND_TERNARY5)
+x = r.standard_normal(2048).astype(np.float32)
+want = pm.matvec(x)
+s = ctypes.c_void_p()
+_lib.call("trx_stream_create", ctypes.byref(s))
+xb = _lib.DeviceBuffer.from_array(x)
+yb = _lib.DeviceBuffer(4 * 1024)
+exe = ctypes.c_void_p()
+# The process's first no-alloc call, inside the capture: the array's address lookup happens then
+# and its counter clearing is recorded into the graph.
+_lib.call("trx_graph_begin", s)
+_lib.call("trx_gemv_packed_f32_noalloc", pm.packed.ptr, pm.kind, 1024, 2048, xb.ptr, None, ctypes.c_float(1e-6),
+          yb.ptr, 0, None, s)
+_lib.call("trx_graph_end", s, ctypes.byref(exe))
+ok = True
+for rep in range(3):
+    yb.zero(s)
+    _lib.call("trx_graph_launch", exe, s)
+    _lib.call("trx_stream_sync", s)
+    ok = ok and np.array_equal(yb.download(np.float32, 1024), want)
+_lib.call("trx_graph_destroy", exe)
+_lib.call("trx_stream_destroy", s)
+print("replays equal:", ok, flush=True)
+sys.exit(0 if ok else 1)
+"""
+
+
+def test_noalloc_gemv_first_call_under_graph_capture():
+    """The no-alloc GEMV's first call in a process made while a stream is being captured (as a
+    caller under hipGraph capture makes it): the graph replays three times, each equal to the
+    GEMV with a caller workspace."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    print("no-alloc GEMV: first call under capture, in a fresh process", flush=True)
+    p = subprocess.run([sys.executable, "-c", _CAPTURE_SCRIPT, root], capture_output=True, text=True, timeout=120)
+    print(p.stdout, p.stderr[-2000:], flush=True)
+    assert p.returncode == 0

@@ -101,6 +101,12 @@ SIGNATURES = {
     "trx_model_info": [_vp, _i, _i64p],
     "trx_model_tensor_ptr": [_vp, _i, _i, ctypes.POINTER(_vp), _i64p],
     "trx_model_packed_ptr": [_vp, _i, _i, ctypes.POINTER(_vp), ctypes.POINTER(_vp)],
+    "trx_graph_begin": [_vp],
+    "trx_graph_end": [_vp, ctypes.POINTER(_vp)],
+    "trx_graph_launch": [_vp, _vp],
+    "trx_graph_destroy": [_vp],
+    "trx_probe_stream_read": [_vp, _sz, _vp, _i, _i, _vp],
+    "trx_probe_empty": [_vp],
 }
 _RESTYPES = {"trx_last_error": ctypes.c_char_p}
 

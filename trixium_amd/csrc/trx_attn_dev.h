@@ -21,6 +21,7 @@
 namespace trx {
 
 constexpr int kAttnThreads = 256;
+constexpr int kFdThreads = 256;            // threads of the one-launch kernel's blocks
 constexpr int kMaxRep = 8;
 constexpr int kMaxPass = 8;                 // register-held positions per thread
 constexpr int kMaxChunk = 128;

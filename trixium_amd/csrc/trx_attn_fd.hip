@@ -8,10 +8,9 @@
 //
 // Lanes: a position is handled by LPP = hd/8 lanes (8 dims each), a "group"; a block of 256
 // threads has 256/LPP groups. The split's K and V rows are loaded into registers first. q (and
-// the new k, v) are normalised and rotated in registers: sums over a group's lanes by DPP, the
-// rotation partner (dim d +- rope_n/2) from lane li ^ (rope_n/16). Each group computes the
-// scores of its positions, then their max, sum of exponentials and weighted V; the groups are
-// combined through LDS once.
+// the new k, v) are normalised and rotated once per block in LDS, then every group reads q.
+// Each group computes the scores of its positions, then their max, sum of exponentials and
+// weighted V; the groups are combined through LDS once.
 
 #include "trx_internal.h"
 #include "trx_ops.h"
@@ -21,7 +20,6 @@ namespace trx {
 
 constexpr int kFdMaxSplits = 64;
 constexpr int kCpolSc1 = 16;           // buffer cache policy: device (agent) scope
-constexpr int kDppRowRor8 = 0x128;     // lane l reads lane l ^ 8 within its 16-lane row
 
 // Sum over the LPP lanes of a position group (every lane gets the sum).
 template <int LPP>
@@ -34,18 +32,17 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
-// ROR8: the RoPE partner lane is li ^ 8 (rope_n = 128), a DPP row_ror:8; otherwise a shuffle. A
-// template parameter, so the choice is not a branch around every element.
 // QP: q, k and v arrive as the q|k|v GEMV's K-slice partial sums (p.qkv_part, [S][rows_p], with
-// its RMSNorm's slice sums of x^2 in p.qkv_ss), summed here: y = r * sum_s part[s], r =
-// 1/sqrt(sum(ss) / K + eps), the slices added in order as the GEMV's own tile reduction does.
-template <int REP, int HD, bool ROR8, bool QP>
-__global__ __launch_bounds__(kAttnThreads) void attn_fd_kernel(AttnParams p) {
+// its RMSNorm's slice sums of x^2 in p.qkv_ss), summed here in slice order: y = r * sum_s
+// part[s], r = 1/sqrt(sum(ss) / K + eps).
+// The q heads and the new k are normalised and rotated once per block (a wave per vector, then
+// every thread a few elements), not by every position group.
+template <int REP, int HD, bool QP>
+__global__ __launch_bounds__(kFdThreads) void attn_fd_kernel(AttnParams p) {
   constexpr int LPP = HD / 8;                         // lanes per position
   constexpr int PPW = 64 / LPP;                       // groups per wave
-  constexpr int NG = kAttnThreads / LPP;              // groups per block
+  constexpr int NG = kFdThreads / LPP;              // groups per block
   constexpr int PPP = NG;                             // positions per pass
-  __shared__ float cs_s[HD / 2], sn_s[HD / 2];
   __shared__ float gm[NG][REP], gl[NG][REP];
   __shared__ __align__(16) float go[NG][REP][HD];
   __shared__ float wgt[REP][kFdMaxSplits > NG ? kFdMaxSplits : NG];
@@ -64,31 +61,37 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fd_kernel(AttnParams p) {
   //    block (every position group uses the same values), the q heads, the new k and v and the
   //    two norm gains. None depends on the position, so they are in flight while the position
   //    is read, and a later wait for them does not cover the K/V stream.
-  const float fr = tid < half ? p.rope_freq[tid] : 0.f;
   const float* kraw = p.qkv + (size_t)p.n_head * qstride + (size_t)g * HD;
   constexpr int NST = REP + 4, STV = NST * HD / 4;                 // rows, float4s staged
-  constexpr int SPT = (STV + kAttnThreads - 1) / kAttnThreads;     // float4s per thread
+  constexpr int SPT = (STV + kFdThreads - 1) / kFdThreads;     // float4s per thread
   __shared__ __align__(16) float stg[NST][HD];
+  __shared__ float nrm[REP + 1][HD];               // the normalised q heads and k
   // With QP the position is read first: a scalar load, which the memory barrier below would
   // otherwise turn into a vector load queued behind the partial sums.
   const int pos_qp = QP ? *p.pos : 0;
   float4 sv[SPT];
   constexpr int NPS = QP ? kQkvPartMax : 1;
+  constexpr uint32_t kOutQ = 0x40000000u;          // a buffer offset past every buffer
+  const __amdgpu_buffer_rsrc_t rqp =
+      make_rsrc(p.qkv_part, QP ? (uint32_t)((size_t)p.qkv_S * p.qkv_rows_p * 4) : 0u);
   float4 pv[SPT][NPS];
-  float ssv[NPS];
 #pragma unroll
   for (int k = 0; k < SPT; ++k) {
-    const int e = min(tid + k * kAttnThreads, STV - 1);            // past the end: a repeat
+    const int e = min(tid + k * kFdThreads, STV - 1);            // past the end: a repeat
     const int row = 4 * e / HD, d = 4 * e - row * HD;
     if (QP) {
-      // Every partial of the q/k/v rows (a norm-gain row reads row 0's and drops them); past S a
-      // repeat of the last slice that gets no weight.
-      const size_t qi = row < REP ? (size_t)(g * REP + row) * qstride + d
-                        : row == REP ? (size_t)p.n_head * qstride + (size_t)g * HD + d
-                        : row == REP + 1 ? (size_t)p.n_head * qstride + (size_t)(p.n_kv + g) * HD + d : (size_t)d;
+      // Every partial of the q, k and v rows; the norm-gain rows' partial loads get an offset past
+      // the buffer (zeros, no memory access); past S a repeat of the last slice that gets no weight.
+      const uint32_t qi = row < REP ? (uint32_t)((g * REP + row) * HD + d)
+                          : row == REP ? (uint32_t)(p.n_head * HD + g * HD + d)
+                          : (uint32_t)(p.n_head * HD + (p.n_kv + g) * HD + d);
+      const uint32_t off0 = row < REP + 2 ? qi * 4u : kOutQ;
 #pragma unroll
-      for (int q = 0; q < NPS; ++q)
-        pv[k][q] = *(const float4*)(p.qkv_part + (size_t)min(q, p.qkv_S - 1) * p.qkv_rows_p + qi);
+      for (int q = 0; q < NPS; ++q) {
+        const auto a = __builtin_amdgcn_raw_buffer_load_b128(
+            rqp, off0 + (uint32_t)min(q, p.qkv_S - 1) * (uint32_t)p.qkv_rows_p * 4u, 0, 0);
+        pv[k][q] = make_float4(__uint_as_float(a[0]), __uint_as_float(a[1]), __uint_as_float(a[2]), __uint_as_float(a[3]));
+      }
       sv[k] = *(const float4*)(row == REP + 3 ? p.k_norm + d : p.q_norm + (row == REP + 2 ? d : 0));
     } else {
       const float* src = row < REP ? p.qkv + (size_t)(g * REP + row) * qstride + d
@@ -98,11 +101,12 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fd_kernel(AttnParams p) {
       sv[k] = *(const float4*)src;
     }
   }
+  float ssl = 0.f;
   if (QP) {
-#pragma unroll
-    for (int q = 0; q < NPS; ++q)     // vector loads: counted with the partials, not the position
-      ssv[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                   make_rsrc(p.qkv_ss, (uint32_t)p.qkv_S * 4u), (uint32_t)min(q, p.qkv_S - 1) * 4u, 0, 0));
+    // Lane i holds slice i's sum of squares (a vector load: counted with the partials, not the
+    // position; past S the buffer's range check gives 0).
+    ssl = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+              make_rsrc(p.qkv_ss, (uint32_t)p.qkv_S * 4u), (uint32_t)lane * 4u, 0, 0));
     // Keeps these loads ahead of the position's and the K/V rows' (the scheduler would otherwise
     // issue them after the K/V stream, and the scalar ones after its waits).
     asm volatile("" ::: "memory");
@@ -113,6 +117,26 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fd_kernel(AttnParams p) {
   const int p0 = sp * chunk, p1 = min(T, p0 + chunk), n = max(0, p1 - p0);
   const bool owner = n > 0 && pos >= p0 && pos < p1;
   const int npass = (n + PPP - 1) / PPP;
+
+  // The RoPE cos/sin of this lane's elements (d = lane + 64 i < 2 half) at pos, from the model's
+  // table (fp32, or the image's Q14 rows), loaded before the K/V rows.
+  constexpr int EPL = HD / 64;                        // elements per lane when a wave holds a vector
+  float rc[EPL], rsn[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int d = lane + 64 * i, ri = d < half ? d : d - half;
+    rc[i] = 1.f;
+    rsn[i] = 0.f;
+    if (d < 2 * half) {
+      if (p.rope_tab) {
+        rc[i] = (float)p.rope_tab[(size_t)pos * p.rope_n + ri] * (1.0f / 16384.0f);
+        rsn[i] = (float)p.rope_tab[(size_t)pos * p.rope_n + half + ri] * (1.0f / 16384.0f);
+      } else {
+        rc[i] = p.rope_cs[(size_t)pos * p.rope_n + ri];
+        rsn[i] = p.rope_cs[(size_t)pos * p.rope_n + half + ri];
+      }
+    }
+  }
 
   // 2. The split's K and V rows (the new position's come from the projection above).
   //    Every pass issues its loads: a position outside the split (or the new one) gets an offset
@@ -137,37 +161,71 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fd_kernel(AttnParams p) {
 
   // The staged inputs into LDS (the loads are waited for here, after the K/V loads went out).
   float rs = 1.f;
-  if (QP) {
-    float t = 0.f;
-#pragma unroll
-    for (int q = 0; q < NPS; ++q) t += q < p.qkv_S ? ssv[q] : 0.f;
-    rs = rsqrtf(t / (float)p.qkv_K + p.eps);
-  }
+  if (QP) rs = 1.0f / sqrtf(wave_sum_dpp(ssl) / (float)p.qkv_K + p.eps);
 #pragma unroll
   for (int k = 0; k < SPT; ++k) {
-    const int e = min(tid + k * kAttnThreads, STV - 1);
+    const int e = min(tid + k * kFdThreads, STV - 1);
     float4 v = sv[k];
     if (QP && 4 * e / HD < REP + 2) {
+      // The slices added in slice order, then the q|k|v GEMV's RMSNorm scale.
       float4 a = pv[k][0];
 #pragma unroll
       for (int q = 1; q < NPS; ++q)
         if (q < p.qkv_S) { a.x += pv[k][q].x; a.y += pv[k][q].y; a.z += pv[k][q].z; a.w += pv[k][q].w; }
       v = make_float4(a.x * rs, a.y * rs, a.z * rs, a.w * rs);
+      // The first split block of each kv head keeps its q, k and v rows in p.qkv, as the GEMV
+      // would have stored them (the q|k|v tap of the last attention layer).
+      if (sp == 0 && tid + k * kFdThreads < STV) {
+        const int row = 4 * e / HD, d = 4 * e - row * HD;
+        const size_t qi = row < REP ? (size_t)(g * REP + row) * HD + d
+                          : (size_t)p.n_head * HD + (size_t)((row - REP) * p.n_kv + g) * HD + d;
+        *(float4*)(p.qkv + qi) = v;
+      }
     }
     *(float4*)(&stg[0][0] + 4 * e) = v;
   }
-  float q[REP][8], kn[8], vn[8], qw[8], kw[8];
+  float q[REP][8], kn[8], vn[8];
   if (n > 0) {
-    if (tid < half) {
-      float sn, cs;
-      if (p.rope_tab) {
-        cs = (float)p.rope_tab[(size_t)pos * p.rope_n + tid] * (1.0f / 16384.0f);
-        sn = (float)p.rope_tab[(size_t)pos * p.rope_n + half + tid] * (1.0f / 16384.0f);
-      } else {
-        sincosf((float)pos * fr, &sn, &cs);
+    __syncthreads();
+    // The q heads and the new k normalised and rotated once per block: wave w takes vectors w,
+    // w + 4, ... (lane l holds elements l + 64 i). The rotation partner (d +- half) is read back
+    // from nrm, which only this wave writes for its vector. q is scaled by 1/sqrt(hd); k and v
+    // are rounded to fp16 (the cache's values, which the score of this position uses too) and
+    // stored to the cache by the block that holds the position.
+    const float qpost = 1.0f / sqrtf((float)HD);
+    for (int v = wave; v <= REP; v += kFdThreads / 64) {
+      const float* gw = stg[v < REP ? REP + 2 : REP + 3];
+      float x[EPL], ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) {
+        x[i] = stg[v][lane + 64 * i];
+        ss += x[i] * x[i];
       }
-      cs_s[tid] = cs;
-      sn_s[tid] = sn;
+      const float r = rsqrtf(wave_sum_dpp(ss) / (float)HD + p.eps);
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) {
+        x[i] = x[i] * r * gw[lane + 64 * i];
+        nrm[v][lane + 64 * i] = x[i];
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // this wave's stores before its reads
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) {
+        const int d = lane + 64 * i;
+        float y = x[i];
+        if (d < half) y = x[i] * rc[i] - nrm[v][d + half] * rsn[i];
+        else if (d < 2 * half) y = nrm[v][d - half] * rsn[i] + x[i] * rc[i];
+        if (v < REP) {
+          stg[v][d] = y * qpost;
+        } else {
+          const __half kh = __float2half(y), vh = __float2half(stg[REP + 1][d]);
+          stg[REP][d] = __half2float(kh);
+          stg[REP + 1][d] = __half2float(vh);
+          if (owner) {
+            p.kcache[cache0 + (size_t)pos * HD + d] = kh;
+            p.vcache[cache0 + (size_t)pos * HD + d] = vh;
+          }
+        }
+      }
     }
     __syncthreads();
 #pragma unroll
@@ -176,48 +234,6 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fd_kernel(AttnParams p) {
       for (int j = 0; j < REP; ++j) q[j][k] = stg[j][li * 8 + k];
       kn[k] = stg[REP][li * 8 + k];
       vn[k] = stg[REP + 1][li * 8 + k];
-      qw[k] = stg[REP + 2][li * 8 + k];
-      kw[k] = stg[REP + 3][li * 8 + k];
-    }
-    // Normalise (gain w), rotate, scale; `post` multiplies the result.
-    auto norm_rope = [&](float* v, const float* w, float post) {
-      float ss = 0.f;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) ss += v[k] * v[k];
-      ss = group_sum<LPP>(ss);
-      const float r = rsqrtf(ss / (float)HD + p.eps);
-#pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = v[k] * r * w[k];
-      const int pxor = half >> 3;                       // partner lane of dim d +- half
-      const int d0 = li * 8;
-      const bool lo = d0 < half, rot = d0 < 2 * half;   // the 8 dims of a lane share the case
-      const int ci = lo ? d0 : (rot ? d0 - half : 0);
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const float other = ROR8 ? dpp_f<kDppRowRor8>(v[k]) : __shfl_xor(v[k], pxor, 64);
-        const float c = cs_s[ci + k], sn = sn_s[ci + k];
-        const float rv = lo ? v[k] * c - other * sn : other * sn + v[k] * c;
-        v[k] = (rot ? rv : v[k]) * post;
-      }
-    };
-    const float qpost = 1.0f / sqrtf((float)HD);
-#pragma unroll
-    for (int j = 0; j < REP; ++j) norm_rope(q[j], qw, qpost);
-    if (owner) {
-      norm_rope(kn, kw, 1.0f);
-      // The cache holds fp16; the score of this position uses the rounded values too.
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        kn[k] = __half2float(__float2half(kn[k]));
-        vn[k] = __half2float(__float2half(vn[k]));
-      }
-      if (grp == 0) {
-        __half kh[8], vh[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) { kh[k] = __float2half(kn[k]); vh[k] = __float2half(vn[k]); }
-        *(uint4*)(p.kcache + cache0 + (size_t)pos * HD + li * 8) = *(const uint4*)kh;
-        *(uint4*)(p.vcache + cache0 + (size_t)pos * HD + li * 8) = *(const uint4*)vh;
-      }
     }
 
     // 3. This group's positions: every score, then the softmax pieces (max, sum, weighted V).
@@ -285,7 +301,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fd_kernel(AttnParams p) {
     __syncthreads();
     // Wave w combines q heads w, w + 4, ...: lane i holds group i's (max, sum) of the head.
     static_assert(NG <= 64, "one lane per group");
-    for (int j = wave; j < REP; j += kAttnThreads / 64) {
+    for (int j = wave; j < REP; j += kFdThreads / 64) {
       const float gmv = lane < NG ? gm[lane][j] : -INFINITY;
       const float glv = lane < NG ? gl[lane][j] : 0.f;
       const float M = wave_max(gmv);
@@ -298,7 +314,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fd_kernel(AttnParams p) {
       }
     }
     __syncthreads();
-    for (int i = tid; i < REP * HD; i += kAttnThreads) {
+    for (int i = tid; i < REP * HD; i += kFdThreads) {
       const int j = i / HD, d = i - j * HD;
       float o = 0.f;
 #pragma unroll
@@ -328,7 +344,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fd_kernel(AttnParams p) {
   const uint32_t nb = (uint32_t)((size_t)p.n_head * S * 4);
   const __amdgpu_buffer_rsrc_t rm = make_rsrc(p.part_m, nb), rl = make_rsrc(p.part_l, nb);
   const __amdgpu_buffer_rsrc_t ro = make_rsrc(p.part_o, nb * (uint32_t)HD);
-  for (int i = tid; i < REP * ns; i += kAttnThreads) {
+  for (int i = tid; i < REP * ns; i += kFdThreads) {
     const int j = i / ns, k = i - j * ns;
     const uint32_t off = (uint32_t)(((g * REP + j) * S + k) * 4);
     wgt[j][k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rm, off, 0, kCpolSc1));
@@ -347,7 +363,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fd_kernel(AttnParams p) {
     tot[tid] = L;
   }
   __syncthreads();
-  for (int i = tid; i < REP * HD; i += kAttnThreads) {
+  for (int i = tid; i < REP * HD; i += kFdThreads) {
     const int j = i / HD, d = i - j * HD, qh = g * REP + j;
     const uint32_t base = (uint32_t)(((size_t)qh * S * HD + d) * 4), step = (uint32_t)HD * 4u;
     float o = 0.f;
@@ -367,25 +383,18 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fd_kernel(AttnParams p) {
 
 bool attention_fd_supported(int rep, int hd, int rope_n, int n_split) {
   const int half = rope_n / 2;
-  const bool rope_ok = half >= 8 && half % 8 == 0 && ((half / 8) & (half / 8 - 1)) == 0 && 2 * half <= hd;
+  const bool rope_ok = half >= 1 && 2 * half <= hd;
   const bool rep_ok = rep == 1 || rep == 2 || rep == 4 || rep == 6 || rep == 8;
   return rope_ok && rep_ok && (hd == 64 || hd == 128 || hd == 256) && n_split <= kFdMaxSplits;
 }
 
 template <int REP, bool QP>
 static int launch_fd_qp(const AttnParams& p, hipStream_t s) {
-  const dim3 grid(p.n_kv * p.n_split), block(kAttnThreads);
-  const bool ror8 = p.rope_n == 128;       // partner lane li ^ (rope_n / 16) = li ^ 8
+  const dim3 grid(p.n_kv * p.n_split), block(kFdThreads);
   switch (p.hd) {
-    case 64: hipLaunchKernelGGL((attn_fd_kernel<REP, 64, false, QP>), grid, block, 0, s, p); break;
-    case 128:
-      if (ror8) hipLaunchKernelGGL((attn_fd_kernel<REP, 128, true, QP>), grid, block, 0, s, p);
-      else hipLaunchKernelGGL((attn_fd_kernel<REP, 128, false, QP>), grid, block, 0, s, p);
-      break;
-    case 256:
-      if (ror8) hipLaunchKernelGGL((attn_fd_kernel<REP, 256, true, QP>), grid, block, 0, s, p);
-      else hipLaunchKernelGGL((attn_fd_kernel<REP, 256, false, QP>), grid, block, 0, s, p);
-      break;
+    case 64: hipLaunchKernelGGL((attn_fd_kernel<REP, 64, QP>), grid, block, 0, s, p); break;
+    case 128: hipLaunchKernelGGL((attn_fd_kernel<REP, 128, QP>), grid, block, 0, s, p); break;
+    case 256: hipLaunchKernelGGL((attn_fd_kernel<REP, 256, QP>), grid, block, 0, s, p); break;
     default: TRX_CHECK(false, TRX_E_INVALID, "attention: head_dim %d unsupported", p.hd);
   }
   TRX_LAUNCHED();

@@ -7,6 +7,7 @@
 
 #include <stdio.h>
 #include <string.h>
+#include <math.h>
 #include <map>
 #include <vector>
 #include <functional>
@@ -52,6 +53,7 @@ struct Model {
   float *part_m = nullptr, *part_l = nullptr, *part_o = nullptr;
   unsigned* attn_done = nullptr;                   // [n_kv] split counters (one-launch attention)
   float *dn_io = nullptr, *dn_ba = nullptr, *dn_out = nullptr, *rope_dev = nullptr;
+  float* rope_cs = nullptr;                        // [max_ctx][rope_n]: cos(pos f_i), then sin
   int* ctl = nullptr;  // [0] pos, [1] n_fed, [2] cur_tok, [3] head_from, [4] error, [8..] fed tokens by
                        // absolute position (max_ctx), then the generated tokens (max_new)
   int host_pos = -1;   // host mirror of the device position after the enqueued steps
@@ -551,6 +553,7 @@ static int run_step(Model& m, hipStream_t s) {
       ap.q_norm = PF(m, TRX_ROLE_ATTN_Q_NORM, l);
       ap.k_norm = PF(m, TRX_ROLE_ATTN_K_NORM, l);
       ap.rope_freq = m.rope_dev;
+      ap.rope_cs = m.rope_cs;
       ap.rope_tab = m.cfg.rope_table ? (const int16_t*)P(m, TRX_ROLE_ROPE_TAB, 0) : nullptr;
       ap.pos = m.pos();
       const size_t per = (size_t)c.n_kv_head * c.max_ctx * hd;
@@ -896,6 +899,7 @@ static int run_prefill(Model& m, int p0, int R, hipStream_t s) {
       rp.q_norm = PF(m, TRX_ROLE_ATTN_Q_NORM, l);
       rp.k_norm = PF(m, TRX_ROLE_ATTN_K_NORM, l);
       rp.rope_freq = m.rope_dev;
+      rp.rope_cs = m.rope_cs;
       rp.rope_tab = c.rope_table ? (const int16_t*)P(m, TRX_ROLE_ROPE_TAB, 0) : nullptr;
       rp.p0 = p0;
       rp.R = R;
@@ -1033,6 +1037,7 @@ TRX_API int trx_model_create(const trx_model_config* cfg, const float* rope_freq
   if ((rc = dalloc(m, (void**)&m.part_o, (size_t)c.n_head * splits * hd * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.attn_done, (size_t)std::max(c.n_kv_head, 1) * kDoneStride * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.rope_dev, (size_t)rope_n * 4))) return fail(rc);
+  if ((rc = dalloc(m, (void**)&m.rope_cs, (size_t)c.max_ctx * rope_n * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.ctl, (size_t)(8 + c.max_ctx + c.max_new) * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.slot, 8))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.smp, 16))) return fail(rc);
@@ -1045,6 +1050,19 @@ TRX_API int trx_model_create(const trx_model_config* cfg, const float* rope_freq
     TRX_HIP(hipMemcpy(m.smp + 3, &rng0, 4, hipMemcpyHostToDevice));
   }
   TRX_HIP(hipMemcpy(m.rope_dev, m.rope_freq.data(), m.rope_freq.size() * 4, hipMemcpyHostToDevice));
+  {
+    // cos and sin of the float32 angle pos * f_i (the product rounded as fastref's float32
+    // angles are, model/fastref.py:62-63,229-235), each evaluated in double and rounded once.
+    const int half = rope_n / 2;
+    std::vector<float> tab((size_t)c.max_ctx * rope_n);
+    for (int pos = 0; pos < c.max_ctx; ++pos)
+      for (int i = 0; i < half; ++i) {
+        const float ang = (float)pos * m.rope_freq[i];
+        tab[(size_t)pos * rope_n + i] = (float)cos((double)ang);
+        tab[(size_t)pos * rope_n + half + i] = (float)sin((double)ang);
+      }
+    TRX_HIP(hipMemcpy(m.rope_cs, tab.data(), tab.size() * 4, hipMemcpyHostToDevice));
+  }
   {
     hipError_t e = hipStreamCreateWithFlags(&m.stream, hipStreamNonBlocking);
     if (e != hipSuccess) { set_error("stream: %s", hipGetErrorString(e)); return fail(TRX_E_HIP); }

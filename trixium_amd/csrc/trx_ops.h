@@ -32,6 +32,7 @@ struct AttnParams {
   const float* k_norm;
   const float* rope_freq;  // [rope_n/2]
   const int16_t* rope_tab; // or [max_ctx][rope_n] Q14: cos half, then sin half (null: rope_freq)
+  const float* rope_cs;    // [max_ctx][rope_n] fp32 cos half, then sin half (the one-launch kernel)
   const int* pos;
   __half* kcache;          // [n_kv][max_ctx][hd]
   __half* vcache;

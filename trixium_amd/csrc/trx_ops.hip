@@ -671,7 +671,7 @@ int attention_max_chunk(int head_dim) {
   return head_dim == 64 ? attn_max_chunk<64>() : head_dim == 128 ? attn_max_chunk<128>() : attn_max_chunk<256>();
 }
 
-int attention_pass_positions(int head_dim) { return kAttnThreads / (head_dim / 8); }
+int attention_pass_positions(int head_dim) { return kFdThreads / (head_dim / 8); }
 
 int attention_splits(int n_kv, int head_dim, int max_ctx) {
   // Enough blocks to cover the CUs, but at most 32 (the splits the o projection's prologue

@@ -59,6 +59,7 @@ struct RopeKvParams {
   const float* q_norm;
   const float* k_norm;
   const float* rope_freq;
+  const float* rope_cs;    // [max_ctx][rope_n] fp32 cos half, then sin half (or null)
   const int16_t* rope_tab;
   int p0, R;
   __half* kcache;          // [n_kv][max_ctx][hd]

@@ -517,6 +517,9 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(RopeKvParams p) {
       if (p.rope_tab) {
         cs = (float)p.rope_tab[(size_t)pos * p.rope_n + i] * (1.0f / 16384.0f);
         sn = (float)p.rope_tab[(size_t)pos * p.rope_n + half + i] * (1.0f / 16384.0f);
+      } else if (p.rope_cs) {
+        cs = p.rope_cs[(size_t)pos * p.rope_n + i];
+        sn = p.rope_cs[(size_t)pos * p.rope_n + half + i];
       } else {
         sincosf((float)pos * p.rope_freq[i], &sn, &cs);
       }
