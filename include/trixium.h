@@ -278,6 +278,12 @@ typedef struct {
   int prefill_chunk;           /* trx_model_generate runs the prompt (all but its last token)
                                   through trx_model_prefill in chunks of this many positions;
                                   0: one position per forward, as the firmware's loop */
+  int table_free_ops;          /* packed projections (TRX_PACK_* bits, among packed_ops) whose
+                                  GEMV looks each code byte's weights up in a 256-entry table and
+                                  multiplies them into x held as fp16 high and low planes (v_dot2),
+                                  instead of building the per-block table of partial dot products:
+                                  the same results to float32 rounding, faster where a block
+                                  streams few rows. TRX_PACK_AUTO: the library's choice. */
 } trx_model_config;
 
 #define TRX_PACK_QKV 1         /* attention q|k|v */
@@ -362,6 +368,7 @@ int trx_model_project_head(trx_model* m, const float* hidden, int n, float* logi
 #define TRX_INFO_ATTN_SPLITS 6    /* decode attention: blocks (position splits) per kv head */
 #define TRX_INFO_ATTN_PASS 7      /* decode attention: positions one pass of a split block covers
                                      (a split of c positions takes ceil(c / this) passes) */
+#define TRX_INFO_TABLE_FREE_OPS 8 /* TRX_PACK_* bits on the table-free lookups */
 int trx_model_info(trx_model* m, int what, int64_t* value);
 /* Device address and size of one resident tensor (for benchmarks and tests). */
 int trx_model_tensor_ptr(trx_model* m, int role, int layer, void** ptr, int64_t* bytes);

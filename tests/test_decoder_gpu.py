@@ -172,21 +172,23 @@ def test_device_generator_matches_host_hash(tmp_path):
 
 
 @pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-ternemb", "tiny-hybrid"])
-@pytest.mark.parametrize("packed", [0, 63])
-def test_packed_projections_match_oracle(tiny_images, golden, name, packed):
-    """Every projection on the packed GEMV (63 = TRX_PACK_ALL), or none of them: logits at every
+@pytest.mark.parametrize("packed,tf", [(0, 0), (63, 0), (63, 63)])
+@pytest.mark.parametrize("t5", [True, False])
+def test_packed_projections_match_oracle(tiny_images, golden, name, packed, tf, t5):
+    """Every projection on the packed GEMV (63 = TRX_PACK_ALL), with the per-block table or with
+    the table-free lookups (tf 63), or none of them, on trit5 and 2-bit images: logits at every
     position against the float oracle and the greedy tokens against the fixture."""
     from trixium_amd.model import Decoder
     prompt = golden[f"prompt/{name}"]
     seq = prompt + golden[f"fastref_tokens/{name}"][:12]
-    img = bons.BONSReader(tiny_images[(name, True)])
-    dec = Decoder.from_image(tiny_images[(name, True)], max_new=N_NEW[name], packed_ops=packed)
-    assert dec.packed_ops == packed
+    img = bons.BONSReader(tiny_images[(name, t5)])
+    dec = Decoder.from_image(tiny_images[(name, t5)], max_new=N_NEW[name], packed_ops=packed, table_free_ops=tf)
+    assert dec.packed_ops == packed and dec.table_free_ops == tf
     lg = _teacher_forced_logits(dec, seq, len(prompt))
     ref = FloatRef(img, kv_fp16=True)
     want = [ref.forward(prompt)] + [ref.step(t) for t in seq[len(prompt):]]
     errs = [_rel_err(g, w) for g, w in zip(lg, want)]
-    print(name, packed, "max rel err", max(errs))
+    print(name, packed, tf, t5, "max rel err", max(errs))
     assert max(errs) <= 2e-3
     got = dec.generate_fresh(prompt, N_NEW[name])
     assert got == golden[f"fastref_tokens/{name}"][:N_NEW[name]]

@@ -33,7 +33,8 @@ class ModelConfig(ctypes.Structure):
         (n, ctypes.c_int) for n in ("weight_kind", "head_kind", "head_tied", "emb_mode", "emb_kind",
                                     "max_new", "packed_ops")] + [
         ("hadamard_block", ctypes.c_int), ("hadamard_scale", ctypes.c_float),
-        ("hadamard_widths", ctypes.c_int * 4), ("rope_table", ctypes.c_int), ("prefill_chunk", ctypes.c_int)]
+        ("hadamard_widths", ctypes.c_int * 4), ("rope_table", ctypes.c_int), ("prefill_chunk", ctypes.c_int),
+        ("table_free_ops", ctypes.c_int)]
 
 
 _mcp = ctypes.POINTER(ModelConfig)

@@ -65,6 +65,7 @@ struct Model {
   // change), and the workspace their GEMVs share.
   std::map<std::pair<int, int>, PackedMat> packed;
   int packed_ops = 0;
+  int tf_ops = 0;                                  // packed projections on the table-free lookups
   bool pack_dirty = true;
   void* pack_work = nullptr;
   // Split-K partial sums handed from a packed GEMV to the next one, which reduces them in its
@@ -199,6 +200,9 @@ static uint8_t* P(Model& m, int role, int layer);
 // Packed copies: the projections selected by packed_ops (TRX_PACK_AUTO: the packed GEMV where it
 // is the faster kernel for the weight kind), one device allocation for all of them, and the
 // largest workspace any of them needs.
+// The library's default table_free_ops.
+constexpr int kTableFreeAuto = 0;
+
 static int plan_packed(Model& m) {
   const trx_model_config& c = m.cfg;
   int ops = c.packed_ops;
@@ -248,6 +252,14 @@ static int plan_packed(Model& m) {
     work = std::max(work, g.work_bytes);
   }
   m.packed_ops = ops;
+  {
+    // Measured choice: the table-free lookups where a block streams little (see the measurement
+    // notes); every bit must be a packed projection.
+    int tf = c.table_free_ops == TRX_PACK_AUTO ? kTableFreeAuto : c.table_free_ops;
+    TRX_CHECK(tf >= 0 && (tf & ~TRX_PACK_ALL) == 0, TRX_E_INVALID, "table_free_ops %d has unknown bits",
+              c.table_free_ops);
+    m.tf_ops = tf & ops;
+  }
   if (list.empty()) return TRX_OK;
   uint8_t* buf = nullptr;
   int rc;
@@ -321,6 +333,13 @@ static float* PF(Model& m, int role, int layer) { return (float*)P(m, role, laye
 // One ternary projection: the packed GEMV when the model holds a packed copy of it, otherwise the
 // row-packet kernel. In a rotated model the input (normalised first, with a norm) goes through
 // the width's rotation into xrot, and the GEMV takes that.
+// Whether projection `op` runs the packed GEMV's table-free lookups (config table_free_ops).
+static bool tf_op(const Model& m, int op) {
+  static const int bit[] = {TRX_PACK_QKV, TRX_PACK_O, TRX_PACK_GATE_UP, TRX_PACK_DOWN, TRX_PACK_HEAD, TRX_PACK_DN,
+                            TRX_PACK_DN};
+  return (m.tf_ops & bit[op]) != 0;
+}
+
 static int projection(Model& m, int op, int l, const uint8_t* rows, int kind, int M, int K, const float* x,
                       const float* norm_w, float* y, int epi, const float* resid, hipStream_t s,
                       unsigned long long* amax = nullptr, const int* gate_pos = nullptr,
@@ -336,7 +355,7 @@ static int projection(Model& m, int op, int l, const uint8_t* rows, int kind, in
       // The packed GEMV rotates its own slice of x in its prologue.
       const RotSrc rs = {signs, B, m.cfg.hadamard_scale};
       return tgemv_f32(it->second.buf, kind, M, K, x, norm_w, m.cfg.rms_eps, y, epi, resid, amax, m.pack_work, s,
-                       gate_pos, gate_from, nullptr, nullptr, &rs);
+                       gate_pos, gate_from, nullptr, nullptr, &rs, tf_op(m, op));
     }
     RotParams rp = {x, norm_w, m.cfg.rms_eps, K, B, signs, m.cfg.hadamard_scale, m.xrot};
     int rc;
@@ -346,7 +365,7 @@ static int projection(Model& m, int op, int l, const uint8_t* rows, int kind, in
   }
   if (it != m.packed.end())
     return tgemv_f32(it->second.buf, kind, M, K, x, norm_w, m.cfg.rms_eps, y, epi, resid, amax, m.pack_work, s,
-                     gate_pos, gate_from);
+                     gate_pos, gate_from, nullptr, nullptr, nullptr, tf_op(m, op));
   return gemv_f32(rows, kind, M, K, x, norm_w, m.cfg.rms_eps, y, epi, resid, epi == TRX_EPI_SWIGLU ? M / 2 : 0,
                   amax, s, gate_pos, gate_from);
 }
@@ -370,7 +389,8 @@ int dn_layer_launch(Model& m, int l, hipStream_t s, const PackedMat* pz = nullpt
   const float* x = pz ? xres : m.x;
   if (pz) {
     if ((rc = tgemv_f32(pz->buf, c.weight_kind, C + nvh, E, xin, PF(m, TRX_ROLE_ATTN_NORM, l), c.rms_eps, io,
-                        TRX_EPI_STORE, nullptr, nullptr, m.pack_work, s, nullptr, nullptr, nullptr, pp))) return rc;
+                        TRX_EPI_STORE, nullptr, nullptr, m.pack_work, s, nullptr, nullptr, nullptr, pp, nullptr,
+                        tf_op(m, OP_DN_QKVZ)))) return rc;
   } else if ((rc = projection(m, OP_DN_QKVZ, l, P(m, TRX_ROLE_ATTN_QKV, l), c.weight_kind, C + nvh, E, m.x,
                                PF(m, TRX_ROLE_ATTN_NORM, l), io, TRX_EPI_STORE, nullptr, s))) {
     return rc;
@@ -423,11 +443,11 @@ int dn_layer_launch(Model& m, int l, hipStream_t s, const PackedMat* pz = nullpt
     PartialSums out = {};
     out.out = m.dn_out_part;
     return tgemv_f32(pdo->buf, c.weight_kind, E, nvh, m.dn_out, nullptr, c.rms_eps, nullptr, TRX_EPI_STORE, nullptr,
-                     nullptr, m.pack_work, s, nullptr, nullptr, nullptr, &out);
+                     nullptr, m.pack_work, s, nullptr, nullptr, nullptr, &out, nullptr, tf_op(m, OP_DN_OUT));
   }
   if (pdo)
     return tgemv_f32(pdo->buf, c.weight_kind, E, nvh, m.dn_out, nullptr, c.rms_eps, m.x, TRX_EPI_RESID, xres, nullptr,
-                     m.pack_work, s);
+                     m.pack_work, s, nullptr, nullptr, nullptr, nullptr, nullptr, tf_op(m, OP_DN_OUT));
   return projection(m, OP_DN_OUT, l, P(m, TRX_ROLE_SSM_OUT, l), c.weight_kind, E, nvh, m.dn_out, nullptr,
                     m.x, TRX_EPI_RESID, m.x, s);
 }
@@ -542,7 +562,7 @@ static int run_step(Model& m, hipStream_t s) {
         }
         if ((rc = tgemv_f32(pq->buf, wk, qrows + 2 * kvrows, E, xin, PF(m, TRX_ROLE_ATTN_NORM, l), c.rms_eps,
                             qkv_hand ? nullptr : m.qkv, TRX_EPI_STORE, nullptr, nullptr, m.pack_work, s, nullptr,
-                            nullptr, nullptr, pp || qkv_hand ? &qp : nullptr)))
+                            nullptr, nullptr, pp || qkv_hand ? &qp : nullptr, nullptr, tf_op(m, OP_QKV))))
           return rc;
       } else if ((rc = projection(m, OP_QKV, l, P(m, TRX_ROLE_ATTN_Q, l), wk, qrows + 2 * kvrows, E, xc,
                                    PF(m, TRX_ROLE_ATTN_NORM, l), m.qkv, TRX_EPI_STORE, nullptr, s))) {
@@ -601,13 +621,15 @@ static int run_step(Model& m, hipStream_t s) {
           PartialSums out = {};
           out.out = m.o_part;
           if ((rc = tgemv_f32(po->buf, wk, E, c.n_head * hd, nullptr, nullptr, c.rms_eps, nullptr, TRX_EPI_STORE,
-                              nullptr, nullptr, m.pack_work, s, nullptr, nullptr, &ms, &out))) return rc;
+                              nullptr, nullptr, m.pack_work, s, nullptr, nullptr, &ms, &out, nullptr,
+                              tf_op(m, OP_O)))) return rc;
           pend.in = m.o_part;
           pend.S = m.o_S;
           pend.rows_p = m.o_rows_p;
         } else {
           if ((rc = tgemv_f32(po->buf, wk, E, c.n_head * hd, nullptr, nullptr, c.rms_eps, m.x, TRX_EPI_RESID, xc,
-                              nullptr, m.pack_work, s, nullptr, nullptr, &ms))) return rc;
+                              nullptr, m.pack_work, s, nullptr, nullptr, &ms, nullptr, nullptr, tf_op(m, OP_O))))
+            return rc;
           xc = m.x;
         }
       } else {
@@ -628,7 +650,8 @@ static int run_step(Model& m, hipStream_t s) {
       gu.out = m.ffn_part;
       gu.out_ss = m.ffn_ss;
       if ((rc = tgemv_f32(pg->buf, wk, 2 * F, E, xin, PF(m, TRX_ROLE_FFN_NORM, l), c.rms_eps, nullptr, TRX_EPI_SWIGLU,
-                          nullptr, nullptr, m.pack_work, s, nullptr, nullptr, nullptr, &gu))) return rc;
+                          nullptr, nullptr, m.pack_work, s, nullptr, nullptr, nullptr, &gu, nullptr,
+                          tf_op(m, OP_GATE_UP)))) return rc;
       PartialSums dn = {};
       dn.in = m.ffn_part;
       dn.in_ss = m.ffn_ss;
@@ -640,13 +663,13 @@ static int run_step(Model& m, hipStream_t s) {
       if (m.down_part && next_packed(l, m.down_S)) {
         dn.out = m.down_part;
         if ((rc = tgemv_f32(pd->buf, wk, E, F, nullptr, nullptr, c.rms_eps, nullptr, TRX_EPI_STORE, nullptr, nullptr,
-                            m.pack_work, s, nullptr, nullptr, nullptr, &dn))) return rc;
+                            m.pack_work, s, nullptr, nullptr, nullptr, &dn, nullptr, tf_op(m, OP_DOWN)))) return rc;
         pend.in = m.down_part;
         pend.S = m.down_S;
         pend.rows_p = m.down_rows_p;
       } else {
         if ((rc = tgemv_f32(pd->buf, wk, E, F, nullptr, nullptr, c.rms_eps, m.x, TRX_EPI_RESID, xc, nullptr,
-                            m.pack_work, s, nullptr, nullptr, nullptr, &dn))) return rc;
+                            m.pack_work, s, nullptr, nullptr, nullptr, &dn, nullptr, tf_op(m, OP_DOWN)))) return rc;
         xc = m.x;
       }
       continue;
@@ -655,7 +678,8 @@ static int run_step(Model& m, hipStream_t s) {
       const float* xin;
       const PartialSums* pp = take(xin);
       if ((rc = tgemv_f32(pg->buf, wk, 2 * F, E, xin, PF(m, TRX_ROLE_FFN_NORM, l), c.rms_eps, m.act, TRX_EPI_SWIGLU,
-                          nullptr, nullptr, m.pack_work, s, nullptr, nullptr, nullptr, pp))) return rc;
+                          nullptr, nullptr, m.pack_work, s, nullptr, nullptr, nullptr, pp, nullptr,
+                          tf_op(m, OP_GATE_UP)))) return rc;
     } else if ((rc = projection(m, OP_GATE_UP, l, P(m, TRX_ROLE_FFN_GATE, l), wk, 2 * F, E, xc,
                                  PF(m, TRX_ROLE_FFN_NORM, l), m.act, TRX_EPI_SWIGLU, nullptr, s))) {
       return rc;
@@ -664,7 +688,7 @@ static int run_step(Model& m, hipStream_t s) {
       PartialSums out = {};
       out.out = m.down_part;
       if ((rc = tgemv_f32(pd->buf, wk, E, F, m.act, nullptr, c.rms_eps, nullptr, TRX_EPI_STORE, nullptr, nullptr,
-                          m.pack_work, s, nullptr, nullptr, nullptr, &out))) return rc;
+                          m.pack_work, s, nullptr, nullptr, nullptr, &out, nullptr, tf_op(m, OP_DOWN)))) return rc;
       pend.in = m.down_part;
       pend.S = m.down_S;
       pend.rows_p = m.down_rows_p;
@@ -687,7 +711,8 @@ static int run_step(Model& m, hipStream_t s) {
     hp.out = m.head_part;
     hp.out_ss = m.head_ss;
     if ((rc = tgemv_f32(ph->buf, head_kind, c.vocab, E, xin, PF(m, TRX_ROLE_OUT_NORM, 0), c.rms_eps, nullptr,
-                        TRX_EPI_STORE, nullptr, nullptr, m.pack_work, s, m.pos(), m.head_from(), nullptr, &hp)))
+                        TRX_EPI_STORE, nullptr, nullptr, m.pack_work, s, m.pos(), m.head_from(), nullptr, &hp, nullptr,
+                        tf_op(m, OP_HEAD))))
       return rc;
     if ((rc = tgemv_reduce_f32(m.head_part, m.head_ss, m.head_S, m.head_rows_p, c.vocab, E, c.rms_eps, m.logits,
                                m.slot, s, m.pos(), m.head_from())))
@@ -1420,6 +1445,7 @@ TRX_API int trx_model_info(trx_model* h, int what, int64_t* value) {
     case TRX_INFO_STREAM: *value = (int64_t)(intptr_t)m.stream; break;
     case TRX_INFO_ATTN_SPLITS: *value = m.n_split; break;
     case TRX_INFO_ATTN_PASS: *value = attention_pass_positions(m.cfg.head_dim); break;
+    case TRX_INFO_TABLE_FREE_OPS: *value = m.tf_ops; break;
     case TRX_INFO_PACKED_OPS: *value = m.packed_ops; break;
     case TRX_INFO_WEIGHT_BYTES: {
       int64_t s = 0;

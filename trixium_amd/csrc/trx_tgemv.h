@@ -130,10 +130,13 @@ int tgemv_batched_geom(int kind, int M, int K, int n_mat, PackGeom& g, size_t* p
 int tgemv_f32_batched(const uint8_t* packed, size_t mat_stride, int n_mat, int n_copies, int kind, int M, int K,
                       const float* x, int x_stride, float* y, int y_stride, float* part, hipStream_t s);
 
+// tf: the table-free lookups (a code byte's weights from a 256-entry table, v_dot2 against x
+// split into fp16 high and low planes) instead of the per-block table of partial dot products;
+// the same results to float32 rounding, cheaper where a block streams few rows.
 int tgemv_f32(const uint8_t* packed, int kind, int M, int K, const float* x, const float* norm_w,
               float eps, float* y, int epi, const float* resid, unsigned long long* amax_slot,
               void* work, hipStream_t s, const int* gate_pos = nullptr, const int* gate_from = nullptr,
               const AttnMergeSrc* merge = nullptr, const PartialSums* parts = nullptr,
-              const RotSrc* rot = nullptr);
+              const RotSrc* rot = nullptr, bool tf = false);
 
 }  // namespace trx

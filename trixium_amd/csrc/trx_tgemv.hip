@@ -343,7 +343,94 @@ __device__ __forceinline__ float tg_item_sum(const uint4 c, uint32_t scales, uin
   return a[0] * __half2float(__ushort_as_half((unsigned short)(scales >> sshift)));
 }
 
-template <bool T5, int NB>
+// Table-free lookups (TF): a 256-entry table of each code byte's weights (digit - 1) as fp16
+// pairs, [w0 w1 | w2 w3 | w4 0 | 0] (trit5) or [w0 w1 | w2 w3 | 0 | 0] (2-bit), built in 4 KB
+// of LDS by the first 256 threads; the lane's 4 code positions' x values held in registers as
+// fp16 high and low planes (x = hi + lo to ~22 bits), so a code byte costs one LDS read and
+// v_dot2 products against both planes, with no per-block table of partial dot products.
+typedef _Float16 tf_h2 __attribute__((ext_vector_type(2)));
+
+template <bool T5>
+__device__ __forceinline__ void tf_build_lut(uint4* lut, int tid) {
+  if (tid >= 256) return;
+  int w[6] = {0, 0, 0, 0, 0, 0};
+  if (T5) {
+    int b = tid;
+    for (int k = 0; k < 5; ++k) {
+      w[k] = b % 3 - 1;
+      b /= 3;
+    }
+  } else {
+    for (int k = 0; k < 4; ++k) w[k] = ((tid >> (2 * k)) & 3) - 1;
+  }
+  uint32_t d[4];
+  for (int k = 0; k < 3; ++k) {
+    const tf_h2 v = {(_Float16)w[2 * k], (_Float16)w[2 * k + 1]};
+    d[k] = __builtin_bit_cast(uint32_t, v);
+  }
+  d[3] = 0u;
+  lut[tid] = make_uint4(d[0], d[1], d[2], d[3]);
+}
+
+// The x values of the lane's four code positions (4 * l16 + jj), digit by digit, split into fp16
+// planes: xh[jj][k] = (x of digits 2k, 2k + 1), xl the remainder.
+template <bool T5>
+__device__ __forceinline__ void tf_lane_x(const float* xs, int l16, tf_h2 (&xh)[4][3], tf_h2 (&xl)[4][3]) {
+  constexpr int DPB = T5 ? 5 : 4;                  // digits per code byte
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+    int g, byte;
+    tg_position(T5, 4 * l16 + jj, g, byte);
+    float x[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < DPB; ++k) {
+      const int cc = DPB * byte + k;
+      if (g >= 0 && cc < kGroup) x[k] = xs[kGroup * g + cc];
+    }
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      const _Float16 h0 = (_Float16)x[2 * k], h1 = (_Float16)x[2 * k + 1];
+      xh[jj][k] = tf_h2{h0, h1};
+      xl[jj][k] = tf_h2{(_Float16)(x[2 * k] - (float)h0), (_Float16)(x[2 * k + 1] - (float)h1)};
+    }
+  }
+}
+
+// tg_item_sum with the table-free lookups.
+template <bool T5>
+__device__ __forceinline__ float tf_item_sum(const uint4 c, uint32_t scales, uint32_t sshift, const uint4* lut,
+                                             const tf_h2 (&xh)[4][3], const tf_h2 (&xl)[4][3]) {
+  const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+  // Byte position outer, rows inner: the four rows' lookups are in flight together and their
+  // products go to eight independent sums (rows x planes).
+  float ah[4] = {0.f, 0.f, 0.f, 0.f}, al[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+    uint4 e[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) e[k] = lut[(cw[k] >> (8 * jj)) & 255u];
+#pragma unroll
+    for (int q = 0; q < (T5 ? 3 : 2); ++q) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t ed = q == 0 ? e[k].x : q == 1 ? e[k].y : e[k].z;
+        const tf_h2 wv = __builtin_bit_cast(tf_h2, ed);
+        ah[k] = __builtin_amdgcn_fdot2(wv, xh[jj][q], ah[k], false);
+        al[k] = __builtin_amdgcn_fdot2(wv, xl[jj][q], al[k], false);
+      }
+    }
+  }
+  float a[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) a[k] = ah[k] + al[k];
+  a[0] += dpp_f<kDppRowHalfMirror>(a[2]);
+  a[1] += dpp_f<kDppRowHalfMirror>(a[3]);
+  a[0] += dpp_f<kDppQuadXor2>(a[1]);
+  a[0] += dpp_f<kDppQuadXor1>(a[0]);
+  return a[0] * __half2float(__ushort_as_half((unsigned short)(scales >> sshift)));
+}
+
+template <bool T5, int NB, bool TF>
 __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgParams p) {
   __shared__ __align__(16) float tab[256 * kTabCols];
   __shared__ float xs[kSliceCols];
@@ -614,7 +701,8 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   if (p.norm_w && tid == 0)
     __hip_atomic_store(p.ss_out + j * p.S + s, (red[0] + red[1]) + (red[2] + red[3]), __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
-  tg_build_table<T5>(tab, xs, tid);
+  if constexpr (TF) tf_build_lut<T5>((uint4*)tab, tid);
+  else tg_build_table<T5>(tab, xs, tid);
   __syncthreads();
 
   // 4. The items: four rows x one dword per lane; sixteen lanes per row group.
@@ -629,8 +717,12 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   }
   const char* tb = (const char*)tab;
   const uint32_t sshift = 16u * (uint32_t)half;       // this lane's group scale in the dword
+  tf_h2 xh[4][3], xl[4][3];
+  if constexpr (TF) tf_lane_x<T5>(xs, l16, xh, xl);
   auto compute = [&](const TgItem<T5>& it, int pso) {
-    float v = tg_item_sum(it.c, it.sc, sshift, lw, sel, tb);
+    float v;
+    if constexpr (TF) v = tf_item_sum<T5>(it.c, it.sc, sshift, (const uint4*)tab, xh, xl);
+    else v = tg_item_sum(it.c, it.sc, sshift, lw, sel, tb);
     v += dpp_f<kDppRowRor8>(v);                      // the other group (lane l16 ^ 8)
     // Agent-scope store (sc1): the tile's reducing block may run on another XCD. (One kind of
     // store: a branch between two kinds would leave the compiler's vmcnt counts short, and every
@@ -1010,14 +1102,14 @@ int tgemv_partial_slices_max() { return kSwiPartMax; }
 int tgemv_resid_slices_max() { return kResPartMax; }
 
 template <bool T5>
-static const void* tg_fn() {
-  return (const void*)tgemv_kernel<T5, 4>;
+static const void* tg_fn(bool tf) {
+  return tf ? (const void*)tgemv_kernel<T5, 4, true> : (const void*)tgemv_kernel<T5, 4, false>;
 }
 
 int tgemv_f32(const uint8_t* packed, int kind, int M, int K, const float* x, const float* norm_w,
               float eps, float* y, int epi, const float* resid, unsigned long long* amax_slot,
               void* work, hipStream_t s, const int* gate_pos, const int* gate_from,
-              const AttnMergeSrc* merge, const PartialSums* parts, const RotSrc* rot) {
+              const AttnMergeSrc* merge, const PartialSums* parts, const RotSrc* rot, bool tf) {
   PackGeom g;
   int rc = pack_geom(g, kind, M, K);
   if (rc) return rc;
@@ -1078,7 +1170,7 @@ int tgemv_f32(const uint8_t* packed, int kind, int M, int K, const float* x, con
   TRX_CHECK(!rot || (x && !merge && !p_in && rot->signs && rot->B >= 1 && rot->B <= kTgThreads &&
                      (rot->B & (rot->B - 1)) == 0 && K % std::max(rot->B, kSliceCols) == 0),
             TRX_E_INVALID, "packed GEMV: rotation of block %d over %d columns unsupported", rot ? rot->B : 0, K);
-  const void* fn = kind == TRX_KIND_TERNARY5 ? tg_fn<true>() : tg_fn<false>();
+  const void* fn = kind == TRX_KIND_TERNARY5 ? tg_fn<true>(tf) : tg_fn<false>(tf);
   void* args[] = {(void*)&p};
   TRX_HIP(hipLaunchKernel(fn, dim3(g.S * g.bps), dim3(kTgThreads), args, 0, s));
   return TRX_OK;
@@ -1144,7 +1236,7 @@ int tgemv_f32_batched(const uint8_t* packed, size_t mat_stride, int n_mat, int n
   p.mat_copies = n_copies;
   p.n_mat = n_mat;
   int nx = g.S, ny = n_mat;
-  const void* fn = kind == TRX_KIND_TERNARY5 ? tg_fn<true>() : tg_fn<false>();
+  const void* fn = kind == TRX_KIND_TERNARY5 ? tg_fn<true>(false) : tg_fn<false>(false);
   if (multi) {
     // Blocks of slice pairs; the (matrix, tile) items spread evenly over ny groups, ny =
     // cus / gcd(S2, cus) so the grid's S2 * ny blocks fill whole rounds of the GPU (one round

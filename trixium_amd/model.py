@@ -26,7 +26,7 @@ f32 = np.float32
 (READ_LOGITS, READ_HIDDEN, READ_POSITION, READ_TOKEN, READ_OUT, READ_SLOT, READ_QKV, READ_ATTN, READ_ACT,
  READ_RESIDUAL) = range(10)
 (INFO_ARENA_BYTES, INFO_DEVICE_BYTES, INFO_STREAM, INFO_WEIGHT_BYTES, _INFO_UNUSED, INFO_PACKED_OPS, INFO_ATTN_SPLITS,
- INFO_ATTN_PASS) = range(8)
+ INFO_ATTN_PASS, INFO_TABLE_FREE_OPS) = range(9)
 
 # Projections run by the packed GEMV (TRX_PACK_* bits; PACK_AUTO lets the library choose).
 PACK_QKV, PACK_O, PACK_GATE_UP, PACK_DOWN, PACK_HEAD, PACK_DN = 1, 2, 4, 8, 16, 32
@@ -55,7 +55,7 @@ def layer_type_bits(layer_types, n_layer):
 
 
 def make_config(mc, weight_kind, head_kind, head_tied, emb_mode, emb_kind, max_ctx=None, max_new=256,
-                packed_ops=PACK_AUTO, prefill_chunk=0):
+                packed_ops=PACK_AUTO, prefill_chunk=0, table_free_ops=PACK_AUTO):
     """trx_model_config from a ModelConfig (or a BONS header turned into one)."""
     c = _lib.ModelConfig()
     for name in ("n_layer", "n_embd", "n_head", "n_kv_head", "head_dim", "ffn_dim", "vocab",
@@ -71,6 +71,7 @@ def make_config(mc, weight_kind, head_kind, head_tied, emb_mode, emb_kind, max_c
     c.emb_mode, c.emb_kind, c.max_new = emb_mode, emb_kind, int(max_new)
     c.packed_ops = int(packed_ops)
     c.prefill_chunk = int(prefill_chunk)
+    c.table_free_ops = int(table_free_ops)
     return c
 
 
@@ -102,7 +103,8 @@ class Decoder:
 
     # Construction ------------------------------------------------------------------------------
     @classmethod
-    def from_image(cls, img, max_ctx=None, max_new=256, use_graph=True, packed_ops=PACK_AUTO, prefill_chunk=0):
+    def from_image(cls, img, max_ctx=None, max_new=256, use_graph=True, packed_ops=PACK_AUTO, prefill_chunk=0,
+                   table_free_ops=PACK_AUTO):
         """Load a BONS image (path or BONSReader) into HBM. prefill_chunk > 0: forward() and
         generate() run all but the last fed token through the batched prefill, that many
         positions per weight pass (0: one position per forward, as the firmware's loop)."""
@@ -137,7 +139,7 @@ class Decoder:
             head_kind = L.KIND_F16 if head["kind"] == L.KIND_F32 else head["kind"]
             emb_kind = emb["kind"] if emb is not None and L.is_ternary(emb["kind"]) else weight_kind
         cfg = make_config(mc, weight_kind, head_kind, head_tied, emb_mode, emb_kind, max_ctx, max_new, packed_ops,
-                          prefill_chunk)
+                          prefill_chunk, table_free_ops)
         if rot is not None:
             block, scale, signs = rot
             cfg.hadamard_block, cfg.hadamard_scale = block, scale
@@ -162,13 +164,13 @@ class Decoder:
 
     @classmethod
     def synthetic(cls, mc, seed=0, weight_kind=L.KIND_TERNARY5, max_ctx=None, max_new=256,
-                  use_graph=True, packed_ops=PACK_AUTO, prefill_chunk=0):
+                  use_graph=True, packed_ops=PACK_AUTO, prefill_chunk=0, table_free_ops=PACK_AUTO):
         """Fill every tensor on the device from the counter-based generator (same values as
         trixium_amd.synth.hashed_*): ternary token_embd rows (embedded by decoding the row), an
         untied ternary LM head unless the config ties them. A hybrid's DeltaNet beta|alpha Q8
         rows come from the host (seeded int8 values, fp16 scales U(0.01, 0.05))."""
         cfg = make_config(mc, weight_kind, weight_kind, mc.tie_embeddings, 1, weight_kind, max_ctx, max_new,
-                          packed_ops, prefill_chunk)
+                          packed_ops, prefill_chunk, table_free_ops)
         d = cls(mc, cfg, use_graph)
         try:
             ranges = np.array([SYNTH_SCALE[0], SYNTH_SCALE[1] - SYNTH_SCALE[0],
@@ -410,6 +412,11 @@ class Decoder:
     def packed_ops(self):
         """TRX_PACK_* bits of the projections that run on the packed GEMV."""
         return self.info(INFO_PACKED_OPS)
+
+    @property
+    def table_free_ops(self):
+        """TRX_PACK_* bits of the packed projections on the table-free lookups."""
+        return self.info(INFO_TABLE_FREE_OPS)
 
     def packed_ptr(self, op, layer=0):
         """(packed copy, shared workspace) device addresses of one packed projection."""
