@@ -89,6 +89,9 @@ def parse_args():
     ap.add_argument("--trace-decode", type=int, default=0, metavar="N",
                     help="prefill the prompt, then run N decode positions and exit (for kernel traces "
                          "and hardware counters; with --no-graph every kernel launches eagerly)")
+    ap.add_argument("--rotated", type=int, default=0, metavar="B",
+                    help="a PrismML-rotated model: every projection input rotated in blocks of B columns "
+                         "(the basis real Bonsai weights are stored in; 0: plain)")
     ap.add_argument("--table-free-ops", type=int, default=-1,
                     help="packed projections on the table-free lookups, as TRX_PACK_* bits (-1: the library's "
                          "choice)")
@@ -568,7 +571,8 @@ def main():
     kind = L.KIND_TERNARY5 if a.kind == "trit5" else L.KIND_TERNARY
     if a.only_kernel:
         dec = Decoder.synthetic(mc, a.seed, weight_kind=kind, max_ctx=mc.max_ctx, max_new=8,
-                                packed_ops=a.packed_ops, table_free_ops=a.table_free_ops)
+                                packed_ops=a.packed_ops, table_free_ops=a.table_free_ops,
+                                hadamard_block=a.rotated)
         us, algo, n_launch, _ = time_dominant_kernel(dec, mc, a.kernel_reps, graph=not a.no_graph)
         print(json.dumps({"kernel_us": round(us, 3), "bytes_per_launch": algo, "launches": n_launch,
                           "timing": "eager launches" if a.no_graph else "graph replay",
@@ -577,7 +581,8 @@ def main():
         return
     if a.only_prefill or a.trace_decode:
         dec = Decoder.synthetic(mc, a.seed, weight_kind=kind, max_ctx=mc.max_ctx, max_new=a.trace_decode + 8,
-                                use_graph=not a.no_graph, packed_ops=a.packed_ops, table_free_ops=a.table_free_ops)
+                                use_graph=not a.no_graph, packed_ops=a.packed_ops, table_free_ops=a.table_free_ops,
+                                hadamard_block=a.rotated)
         prompt = np.random.default_rng(a.seed).integers(0, mc.vocab, a.prompt).astype(np.int32)
         chunk = a.prefill_chunk or 2048
         for rep in range(2 if a.only_prefill else 1):
@@ -601,7 +606,8 @@ def main():
         sys.exit(f"prompt {a.prompt} + {n_dec} decode tokens exceed the context {mc.max_ctx}")
     graph = not a.no_graph
     dec = Decoder.synthetic(mc, a.seed, weight_kind=kind, max_ctx=mc.max_ctx, max_new=n_dec + 8,
-                            use_graph=graph, packed_ops=a.packed_ops, table_free_ops=a.table_free_ops)
+                            use_graph=graph, packed_ops=a.packed_ops, table_free_ops=a.table_free_ops,
+                                hadamard_block=a.rotated)
     prompt = np.random.default_rng(a.seed).integers(0, mc.vocab, a.prompt).astype(np.int32)
     if a.sampling:
         t, p_, r = (float(v) for v in a.sampling.split(","))
@@ -686,7 +692,8 @@ def main():
                                    f"{a.prompt}-token prompt", "n_layer": mc.n_layer, "n_embd": mc.n_embd,
                        "ffn_dim": mc.ffn_dim, "vocab": mc.vocab, "prompt_tokens": a.prompt,
                        "decode_tokens": n_dec, "weights": a.kind, "hipgraph": graph,
-                       "packed_ops": dec.packed_ops, "table_free_ops": dec.table_free_ops},
+                       "packed_ops": dec.packed_ops, "table_free_ops": dec.table_free_ops,
+                   "rotation_block": a.rotated},
             "token_roofline": {"bytes_per_token": int(tok_bytes), "tok_s": round(HBM_PEAK_GBS * 1e9 / tok_bytes, 1),
                                "frac": round(tok_s / (HBM_PEAK_GBS * 1e9 / tok_bytes), 4)},
             "roofline": None, "cpu_baseline": None, "prefill": prefill}), flush=True)
@@ -723,7 +730,8 @@ def main():
                    "n_kv_head": mc.n_kv_head, "head_dim": mc.head_dim, "ffn_dim": mc.ffn_dim,
                    "vocab": mc.vocab, "max_ctx": mc.max_ctx, "prompt_tokens": a.prompt,
                    "decode_tokens": n_dec, "weights": a.kind, "hipgraph": graph,
-                   "packed_ops": dec.packed_ops, "table_free_ops": dec.table_free_ops},
+                   "packed_ops": dec.packed_ops, "table_free_ops": dec.table_free_ops,
+                   "rotation_block": a.rotated},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profile(a.kind, gu_mode),

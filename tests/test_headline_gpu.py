@@ -238,3 +238,32 @@ def test_full_depth_properties(shape):
     errs = [_rel_err(x, y) for x, y in zip(la, lr)]
     print(f"{shape} full depth: packed vs row-packet rel err {errs}", flush=True)
     assert max(errs) <= 2e-3
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("shape,block", [("8b", 128), ("27b", 256)])
+def test_rotated_full_width_handoffs_match_separate_launches(shape, block):
+    """A PrismML-rotated model at the full width (two layers; the 27B shape one Gated DeltaNet and
+    one gated attention layer): the packed GEMVs handing partial sums on, each rotating its input
+    in the prologue (blocks inside the K-slice), against every projection on the row-packet kernel
+    after a separate rotation launch (the path without handoffs): logits at 8 positions within
+    2e-3 (the row-packet kernel rounds its input to int16 per 128-group) and the same greedy
+    tokens."""
+    from trixium_amd.model import Decoder
+    if shape == "8b":
+        mc = C.QWEN3_8B.replace(name="qwen3-8b-shape-2l", n_layer=2, max_ctx=64)
+    else:
+        mc = C.QWEN35_27B.replace(name="qwen3.5-27b-shape-2l", n_layer=2, layer_types=("deltanet", "attn"),
+                                  max_ctx=64)
+    seed = 51
+    prompt = synth.random_prompt(mc, 8, seed)
+    a = Decoder.synthetic(mc, seed, weight_kind=TRIT5, max_new=8, hadamard_block=block)
+    b = Decoder.synthetic(mc, seed, weight_kind=TRIT5, max_new=8, hadamard_block=block, packed_ops=0)
+    la = [a.forward(prompt[:4])] + [a.forward([t]) for t in prompt[4:]]
+    lb = [b.forward(prompt[:4])] + [b.forward([t]) for t in prompt[4:]]
+    errs = [_rel_err(x, y) for x, y in zip(la, lb)]
+    print(f"{shape} rotated ({block}): handoffs vs separate launches rel err {max(errs):.2e}", flush=True)
+    assert max(errs) <= 2e-3
+    assert a.generate_fresh(prompt, 8) == b.generate_fresh(prompt, 8)
+    a.close()
+    b.close()

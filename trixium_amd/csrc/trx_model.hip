@@ -370,6 +370,18 @@ static int projection(Model& m, int op, int l, const uint8_t* rows, int kind, in
                   amax, s, gate_pos, gate_from);
 }
 
+// The rotation of a projection input of width K (null for a plain model), held in rots.
+static const RotSrc* rotation_of(Model& m, int K, RotSrc* rots) {
+  const trx_model_config& c = m.cfg;
+  if (!c.hadamard_block) return nullptr;
+  for (int wi = 0; wi < 4; ++wi)
+    if (c.hadamard_widths[wi] == K) {
+      rots[wi] = {PF(m, TRX_ROLE_HADAMARD, wi), c.hadamard_block, c.hadamard_scale};
+      return &rots[wi];
+    }
+  return nullptr;
+}
+
 // Gated DeltaNet layer: [qkv|z] GEMV and the beta/alpha Q8 GEMV (both with the attention
 // RMSNorm), conv, recurrence with the gated norm, then the out projection with the residual.
 // With the packed [qkv|z] and out GEMVs (pz, pdo): [qkv|z] reads x = xin, or xres + the partial
@@ -383,14 +395,15 @@ int dn_layer_launch(Model& m, int l, hipStream_t s, const PackedMat* pz = nullpt
   const int nq = c.dn_num_k_heads * c.dn_k_head_dim, nvh = c.dn_num_v_heads * c.dn_v_head_dim;
   const int C = 2 * nq + nvh;
   const int di = m.dn_index[l];
+  RotSrc rots[4];
   int rc;
   float* io = m.dn_io;                  // [C + nvh] projections
   float* conv_out = m.dn_io + C + nvh;  // [C]
   const float* x = pz ? xres : m.x;
   if (pz) {
     if ((rc = tgemv_f32(pz->buf, c.weight_kind, C + nvh, E, xin, PF(m, TRX_ROLE_ATTN_NORM, l), c.rms_eps, io,
-                        TRX_EPI_STORE, nullptr, nullptr, m.pack_work, s, nullptr, nullptr, nullptr, pp, nullptr,
-                        tf_op(m, OP_DN_QKVZ)))) return rc;
+                        TRX_EPI_STORE, nullptr, nullptr, m.pack_work, s, nullptr, nullptr, nullptr, pp,
+                        rotation_of(m, E, rots), tf_op(m, OP_DN_QKVZ)))) return rc;
   } else if ((rc = projection(m, OP_DN_QKVZ, l, P(m, TRX_ROLE_ATTN_QKV, l), c.weight_kind, C + nvh, E, m.x,
                                PF(m, TRX_ROLE_ATTN_NORM, l), io, TRX_EPI_STORE, nullptr, s))) {
     return rc;
@@ -443,11 +456,12 @@ int dn_layer_launch(Model& m, int l, hipStream_t s, const PackedMat* pz = nullpt
     PartialSums out = {};
     out.out = m.dn_out_part;
     return tgemv_f32(pdo->buf, c.weight_kind, E, nvh, m.dn_out, nullptr, c.rms_eps, nullptr, TRX_EPI_STORE, nullptr,
-                     nullptr, m.pack_work, s, nullptr, nullptr, nullptr, &out, nullptr, tf_op(m, OP_DN_OUT));
+                     nullptr, m.pack_work, s, nullptr, nullptr, nullptr, &out, rotation_of(m, nvh, rots),
+                     tf_op(m, OP_DN_OUT));
   }
   if (pdo)
     return tgemv_f32(pdo->buf, c.weight_kind, E, nvh, m.dn_out, nullptr, c.rms_eps, m.x, TRX_EPI_RESID, xres, nullptr,
-                     m.pack_work, s, nullptr, nullptr, nullptr, nullptr, nullptr, tf_op(m, OP_DN_OUT));
+                     m.pack_work, s, nullptr, nullptr, nullptr, nullptr, rotation_of(m, nvh, rots), tf_op(m, OP_DN_OUT));
   return projection(m, OP_DN_OUT, l, P(m, TRX_ROLE_SSM_OUT, l), c.weight_kind, E, nvh, m.dn_out, nullptr,
                     m.x, TRX_EPI_RESID, m.x, s);
 }
@@ -514,12 +528,16 @@ static int run_step(Model& m, hipStream_t s) {
     return &pin;
   };
   // The packed GEMV's own launches below (partial-sum handoffs, the attention merge in o's
-  // prologue) take no rotation: a rotated model runs every projection through projection().
+  // prologue) rotate their input in the prologue when the model is rotated with blocks of at most
+  // 256 columns (each block inside a GEMV's K-slice); a model with wider rotation blocks runs
+  // every projection through projection().
   auto packed = [&](int op, int l) -> const PackedMat* {
-    if (c.hadamard_block) return nullptr;
+    if (c.hadamard_block > kSliceCols) return nullptr;
     auto it = m.packed.find({op, l});
     return it == m.packed.end() ? nullptr : &it->second;
   };
+  RotSrc rots[4];
+  auto rot_for = [&](int K) { return rotation_of(m, K, rots); };
   // Whether the residual after layer l goes to a packed GEMV that takes the producer's S slices.
   auto next_packed = [&](int l, int S) {
     if (S > tgemv_resid_slices_max()) return false;
@@ -562,7 +580,7 @@ static int run_step(Model& m, hipStream_t s) {
         }
         if ((rc = tgemv_f32(pq->buf, wk, qrows + 2 * kvrows, E, xin, PF(m, TRX_ROLE_ATTN_NORM, l), c.rms_eps,
                             qkv_hand ? nullptr : m.qkv, TRX_EPI_STORE, nullptr, nullptr, m.pack_work, s, nullptr,
-                            nullptr, nullptr, pp || qkv_hand ? &qp : nullptr, nullptr, tf_op(m, OP_QKV))))
+                            nullptr, nullptr, pp || qkv_hand ? &qp : nullptr, rot_for(E), tf_op(m, OP_QKV))))
           return rc;
       } else if ((rc = projection(m, OP_QKV, l, P(m, TRX_ROLE_ATTN_Q, l), wk, qrows + 2 * kvrows, E, xc,
                                    PF(m, TRX_ROLE_ATTN_NORM, l), m.qkv, TRX_EPI_STORE, nullptr, s))) {
@@ -621,14 +639,15 @@ static int run_step(Model& m, hipStream_t s) {
           PartialSums out = {};
           out.out = m.o_part;
           if ((rc = tgemv_f32(po->buf, wk, E, c.n_head * hd, nullptr, nullptr, c.rms_eps, nullptr, TRX_EPI_STORE,
-                              nullptr, nullptr, m.pack_work, s, nullptr, nullptr, &ms, &out, nullptr,
-                              tf_op(m, OP_O)))) return rc;
+                              nullptr, nullptr, m.pack_work, s, nullptr, nullptr, &ms, &out,
+                              rot_for(c.n_head * hd), tf_op(m, OP_O)))) return rc;
           pend.in = m.o_part;
           pend.S = m.o_S;
           pend.rows_p = m.o_rows_p;
         } else {
           if ((rc = tgemv_f32(po->buf, wk, E, c.n_head * hd, nullptr, nullptr, c.rms_eps, m.x, TRX_EPI_RESID, xc,
-                              nullptr, m.pack_work, s, nullptr, nullptr, &ms, nullptr, nullptr, tf_op(m, OP_O))))
+                              nullptr, m.pack_work, s, nullptr, nullptr, &ms, nullptr, rot_for(c.n_head * hd),
+                              tf_op(m, OP_O))))
             return rc;
           xc = m.x;
         }
@@ -650,7 +669,7 @@ static int run_step(Model& m, hipStream_t s) {
       gu.out = m.ffn_part;
       gu.out_ss = m.ffn_ss;
       if ((rc = tgemv_f32(pg->buf, wk, 2 * F, E, xin, PF(m, TRX_ROLE_FFN_NORM, l), c.rms_eps, nullptr, TRX_EPI_SWIGLU,
-                          nullptr, nullptr, m.pack_work, s, nullptr, nullptr, nullptr, &gu, nullptr,
+                          nullptr, nullptr, m.pack_work, s, nullptr, nullptr, nullptr, &gu, rot_for(E),
                           tf_op(m, OP_GATE_UP)))) return rc;
       PartialSums dn = {};
       dn.in = m.ffn_part;
@@ -663,13 +682,13 @@ static int run_step(Model& m, hipStream_t s) {
       if (m.down_part && next_packed(l, m.down_S)) {
         dn.out = m.down_part;
         if ((rc = tgemv_f32(pd->buf, wk, E, F, nullptr, nullptr, c.rms_eps, nullptr, TRX_EPI_STORE, nullptr, nullptr,
-                            m.pack_work, s, nullptr, nullptr, nullptr, &dn, nullptr, tf_op(m, OP_DOWN)))) return rc;
+                            m.pack_work, s, nullptr, nullptr, nullptr, &dn, rot_for(F), tf_op(m, OP_DOWN)))) return rc;
         pend.in = m.down_part;
         pend.S = m.down_S;
         pend.rows_p = m.down_rows_p;
       } else {
         if ((rc = tgemv_f32(pd->buf, wk, E, F, nullptr, nullptr, c.rms_eps, m.x, TRX_EPI_RESID, xc, nullptr,
-                            m.pack_work, s, nullptr, nullptr, nullptr, &dn, nullptr, tf_op(m, OP_DOWN)))) return rc;
+                            m.pack_work, s, nullptr, nullptr, nullptr, &dn, rot_for(F), tf_op(m, OP_DOWN)))) return rc;
         xc = m.x;
       }
       continue;
@@ -678,7 +697,7 @@ static int run_step(Model& m, hipStream_t s) {
       const float* xin;
       const PartialSums* pp = take(xin);
       if ((rc = tgemv_f32(pg->buf, wk, 2 * F, E, xin, PF(m, TRX_ROLE_FFN_NORM, l), c.rms_eps, m.act, TRX_EPI_SWIGLU,
-                          nullptr, nullptr, m.pack_work, s, nullptr, nullptr, nullptr, pp, nullptr,
+                          nullptr, nullptr, m.pack_work, s, nullptr, nullptr, nullptr, pp, rot_for(E),
                           tf_op(m, OP_GATE_UP)))) return rc;
     } else if ((rc = projection(m, OP_GATE_UP, l, P(m, TRX_ROLE_FFN_GATE, l), wk, 2 * F, E, xc,
                                  PF(m, TRX_ROLE_FFN_NORM, l), m.act, TRX_EPI_SWIGLU, nullptr, s))) {
@@ -688,7 +707,7 @@ static int run_step(Model& m, hipStream_t s) {
       PartialSums out = {};
       out.out = m.down_part;
       if ((rc = tgemv_f32(pd->buf, wk, E, F, m.act, nullptr, c.rms_eps, nullptr, TRX_EPI_STORE, nullptr, nullptr,
-                          m.pack_work, s, nullptr, nullptr, nullptr, &out, nullptr, tf_op(m, OP_DOWN)))) return rc;
+                          m.pack_work, s, nullptr, nullptr, nullptr, &out, rot_for(F), tf_op(m, OP_DOWN)))) return rc;
       pend.in = m.down_part;
       pend.S = m.down_S;
       pend.rows_p = m.down_rows_p;
@@ -711,8 +730,8 @@ static int run_step(Model& m, hipStream_t s) {
     hp.out = m.head_part;
     hp.out_ss = m.head_ss;
     if ((rc = tgemv_f32(ph->buf, head_kind, c.vocab, E, xin, PF(m, TRX_ROLE_OUT_NORM, 0), c.rms_eps, nullptr,
-                        TRX_EPI_STORE, nullptr, nullptr, m.pack_work, s, m.pos(), m.head_from(), nullptr, &hp, nullptr,
-                        tf_op(m, OP_HEAD))))
+                        TRX_EPI_STORE, nullptr, nullptr, m.pack_work, s, m.pos(), m.head_from(), nullptr, &hp,
+                        rot_for(E), tf_op(m, OP_HEAD))))
       return rc;
     if ((rc = tgemv_reduce_f32(m.head_part, m.head_ss, m.head_S, m.head_rows_p, c.vocab, E, c.rms_eps, m.logits,
                                m.slot, s, m.pos(), m.head_from())))

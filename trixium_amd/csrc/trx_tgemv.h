@@ -115,7 +115,9 @@ int tgemv_resid_slices_max();
 
 // A PrismML rotation of the GEMV's input, applied in its prologue: x' = scale * H (signs * xhat)
 // per block of B columns (H the +-1 Sylvester matrix; B a power of two <= 1024 with K a multiple
-// of max(B, 256)). Each GEMV block transforms the rotation block(s) holding its 256 columns.
+// of max(B, 256)). Each GEMV block transforms the rotation block(s) holding its 256 columns; an x
+// taken from a producer's partial sums or the attention merge is rotated for B <= 256 (the
+// blocks then lie inside the slice).
 struct RotSrc {
   const float* signs;
   int B;

@@ -529,6 +529,10 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   // itself for blocks of <= 256 columns, else the rotation block containing it), times the gain
   // and its sign.
   const bool rot = p.rot_signs && xmode == kXPlain;
+  // A rotation of x taken from partial sums or the attention merge (blocks of <= 256 columns,
+  // inside the slice): the slice's signs, loaded with the prologue's other inputs.
+  const bool rot_in = p.rot_signs && xmode != kXPlain;
+  const float sgn = rot_in && tid < kSliceCols && cs < p.K ? p.rot_signs[cs] : 0.f;
   const int rL = p.rot_B > kSliceCols ? p.rot_B : kSliceCols;
   const int rbase = s * kSliceCols - (s * kSliceCols) % rL;
   float rv = 0.f;
@@ -689,6 +693,28 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
     tab[tid] = rv * p.rot_scale;
     __syncthreads();
     if (tid < kSliceCols) xs[tid] = tab[s * kSliceCols - rbase + tid];
+  } else if (rot_in) {
+    // The slice's x (times the gain), times the signs, through the butterflies of each rotation
+    // block (all inside the slice), scaled.
+    float r;
+    if (xmode == kXSwiglu) {
+      __syncthreads();                              // xs complete, the table's memory free
+      r = tid < kSliceCols ? xs[tid] * sgn : 0.f;
+    } else {
+      r = tid < kSliceCols && cs < p.K ? (p.norm_w ? xv * wv : xv) * sgn : 0.f;
+    }
+    for (int h = 1; h < 64 && h < p.rot_B; h <<= 1) {
+      const float o = __shfl_xor(r, h, 64);
+      r = (lane & h) ? o - r : r + o;
+    }
+    for (int h = 64; h < p.rot_B; h <<= 1) {
+      tab[tid] = r;
+      __syncthreads();
+      const float o = tab[tid ^ h];
+      __syncthreads();
+      r = (tid & h) ? o - r : r + o;
+    }
+    if (tid < kSliceCols) xs[tid] = r * p.rot_scale;
   } else if (xmode != kXSwiglu && tid < kSliceCols) {
     xs[tid] = p.norm_w ? xv * wv : xv;
   }
@@ -1167,8 +1193,8 @@ int tgemv_f32(const uint8_t* packed, int kind, int M, int K, const float* x, con
   p.x_stride = 0;
   p.part_sstride = g.rows_p;
   p.part_mstride = 0;
-  TRX_CHECK(!rot || (x && !merge && !p_in && rot->signs && rot->B >= 1 && rot->B <= kTgThreads &&
-                     (rot->B & (rot->B - 1)) == 0 && K % std::max(rot->B, kSliceCols) == 0),
+  TRX_CHECK(!rot || (rot->signs && rot->B >= 1 && rot->B <= kTgThreads && (rot->B & (rot->B - 1)) == 0 &&
+                     K % std::max(rot->B, kSliceCols) == 0 && (x || rot->B <= kSliceCols)),
             TRX_E_INVALID, "packed GEMV: rotation of block %d over %d columns unsupported", rot ? rot->B : 0, K);
   const void* fn = kind == TRX_KIND_TERNARY5 ? tg_fn<true>(tf) : tg_fn<false>(tf);
   void* args[] = {(void*)&p};

@@ -164,13 +164,23 @@ class Decoder:
 
     @classmethod
     def synthetic(cls, mc, seed=0, weight_kind=L.KIND_TERNARY5, max_ctx=None, max_new=256,
-                  use_graph=True, packed_ops=PACK_AUTO, prefill_chunk=0, table_free_ops=PACK_AUTO):
+                  use_graph=True, packed_ops=PACK_AUTO, prefill_chunk=0, table_free_ops=PACK_AUTO, hadamard_block=0):
         """Fill every tensor on the device from the counter-based generator (same values as
         trixium_amd.synth.hashed_*): ternary token_embd rows (embedded by decoding the row), an
         untied ternary LM head unless the config ties them. A hybrid's DeltaNet beta|alpha Q8
-        rows come from the host (seeded int8 values, fp16 scales U(0.01, 0.05))."""
+        rows come from the host (seeded int8 values, fp16 scales U(0.01, 0.05)).
+        hadamard_block > 0: a PrismML-rotated model (model/golden.py:250-289): every projection
+        input but the DeltaNet beta/alpha rotated blockwise, scale 1/sqrt(block), random +-1 signs
+        per input width (the synthetic weights stand in for weights in the rotated basis)."""
         cfg = make_config(mc, weight_kind, weight_kind, mc.tie_embeddings, 1, weight_kind, max_ctx, max_new,
                           packed_ops, prefill_chunk, table_free_ops)
+        widths = []
+        if hadamard_block:
+            widths = sorted({mc.n_embd, mc.ffn_dim, mc.n_head * mc.head_dim}
+                            | ({mc.dn_num_v_heads * mc.dn_v_head_dim} if mc.n_dn_layers else set()))
+            cfg.hadamard_block, cfg.hadamard_scale = int(hadamard_block), float(1.0 / np.sqrt(hadamard_block))
+            for i, w in enumerate(widths):
+                cfg.hadamard_widths[i] = w
         d = cls(mc, cfg, use_graph)
         try:
             ranges = np.array([SYNTH_SCALE[0], SYNTH_SCALE[1] - SYNTH_SCALE[0],
@@ -188,6 +198,9 @@ class Decoder:
                         q = rng.integers(-127, 128, (nv, mc.n_embd), dtype=np.int8)
                         sc = rng.uniform(0.01, 0.05, (nv, mc.n_embd // L.GROUP_Q8)).astype(np.float16)
                         d.set_tensor(r, l, encode_rows(L.KIND_Q8, mc.n_embd, sc, q))
+            rng = np.random.default_rng(seed + 1)
+            for i, w in enumerate(widths):
+                d.set_tensor(L.ROLE_HADAMARD, i, rng.choice(np.array([-1.0, 1.0], dtype=f32), w))
         except Exception:
             d.close()
             raise
