@@ -309,8 +309,17 @@ __global__ __launch_bounds__(kFdThreads) void attn_fd_kernel(AttnParams p) {
       if (lane < NG) wgt[j][lane] = w;
       const float L = wave_sum(glv * w);
       if (lane == 0) {
-        st_vec<true>(p.part_m + (size_t)(g * REP + j) * S + sp, M);
-        st_vec<true>(p.part_l + (size_t)(g * REP + j) * S + sp, L);
+        // Agent-scope stores when the last split block of this launch merges them; plain stores
+        // when the next kernel does (the launch's end makes them visible).
+        float* pm = p.part_m + (size_t)(g * REP + j) * S + sp;
+        float* pl = p.part_l + (size_t)(g * REP + j) * S + sp;
+        if (p.done) {
+          st_vec<true>(pm, M);
+          st_vec<true>(pl, L);
+        } else {
+          *pm = M;
+          *pl = L;
+        }
       }
     }
     __syncthreads();
@@ -319,7 +328,9 @@ __global__ __launch_bounds__(kFdThreads) void attn_fd_kernel(AttnParams p) {
       float o = 0.f;
 #pragma unroll
       for (int k = 0; k < NG; ++k) o += go[k][j][d] * wgt[j][k];
-      st_vec<true>(p.part_o + ((size_t)(g * REP + j) * S + sp) * HD + d, o);
+      float* po = p.part_o + ((size_t)(g * REP + j) * S + sp) * HD + d;
+      if (p.done) st_vec<true>(po, o);
+      else *po = o;
     }
   }
 

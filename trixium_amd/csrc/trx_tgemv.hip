@@ -430,7 +430,9 @@ __device__ __forceinline__ float tf_item_sum(const uint4 c, uint32_t scales, uin
   return a[0] * __half2float(__ushort_as_half((unsigned short)(scales >> sshift)));
 }
 
-template <bool T5, int NB, bool TF>
+// HAND: the partial sums go to the next GEMV (parts.out): plain stores, which the kernel's end
+// makes visible to the next launch; otherwise agent-scope stores for the tile's reducing block.
+template <bool T5, int NB, bool TF, bool HAND>
 __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgParams p) {
   __shared__ __align__(16) float tab[256 * kTabCols];
   __shared__ float xs[kSliceCols];
@@ -750,10 +752,10 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
     if constexpr (TF) v = tf_item_sum<T5>(it.c, it.sc, sshift, (const uint4*)tab, xh, xl);
     else v = tg_item_sum(it.c, it.sc, sshift, lw, sel, tb);
     v += dpp_f<kDppRowRor8>(v);                      // the other group (lane l16 ^ 8)
-    // Agent-scope store (sc1): the tile's reducing block may run on another XCD. (One kind of
-    // store: a branch between two kinds would leave the compiler's vmcnt counts short, and every
-    // item would also wait for the next item's loads.)
-    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), rpart, po0, pso, kCpolSc1);
+    // Agent-scope store (sc1) when the tile's reducing block (possibly on another XCD) reads it.
+    // (One kind of store per kernel: a branch between two kinds would leave the compiler's vmcnt
+    // counts short, and every item would also wait for the next item's loads.)
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), rpart, po0, pso, HAND ? 0 : kCpolSc1);
   };
   // Whole groups of NB items (a loop with one exit keeps the compiler's vmcnt waits exact: item
   // n waits only for itself), then the remaining < NB items, already in flight.
@@ -1128,8 +1130,9 @@ int tgemv_partial_slices_max() { return kSwiPartMax; }
 int tgemv_resid_slices_max() { return kResPartMax; }
 
 template <bool T5>
-static const void* tg_fn(bool tf) {
-  return tf ? (const void*)tgemv_kernel<T5, 4, true> : (const void*)tgemv_kernel<T5, 4, false>;
+static const void* tg_fn(bool tf, bool hand) {
+  if (hand) return tf ? (const void*)tgemv_kernel<T5, 4, true, true> : (const void*)tgemv_kernel<T5, 4, false, true>;
+  return tf ? (const void*)tgemv_kernel<T5, 4, true, false> : (const void*)tgemv_kernel<T5, 4, false, false>;
 }
 
 int tgemv_f32(const uint8_t* packed, int kind, int M, int K, const float* x, const float* norm_w,
@@ -1196,7 +1199,7 @@ int tgemv_f32(const uint8_t* packed, int kind, int M, int K, const float* x, con
   TRX_CHECK(!rot || (rot->signs && rot->B >= 1 && rot->B <= kTgThreads && (rot->B & (rot->B - 1)) == 0 &&
                      K % std::max(rot->B, kSliceCols) == 0 && (x || rot->B <= kSliceCols)),
             TRX_E_INVALID, "packed GEMV: rotation of block %d over %d columns unsupported", rot ? rot->B : 0, K);
-  const void* fn = kind == TRX_KIND_TERNARY5 ? tg_fn<true>(tf) : tg_fn<false>(tf);
+  const void* fn = kind == TRX_KIND_TERNARY5 ? tg_fn<true>(tf, p_out) : tg_fn<false>(tf, p_out);
   void* args[] = {(void*)&p};
   TRX_HIP(hipLaunchKernel(fn, dim3(g.S * g.bps), dim3(kTgThreads), args, 0, s));
   return TRX_OK;
@@ -1262,7 +1265,7 @@ int tgemv_f32_batched(const uint8_t* packed, size_t mat_stride, int n_mat, int n
   p.mat_copies = n_copies;
   p.n_mat = n_mat;
   int nx = g.S, ny = n_mat;
-  const void* fn = kind == TRX_KIND_TERNARY5 ? tg_fn<true>(false) : tg_fn<false>(false);
+  const void* fn = kind == TRX_KIND_TERNARY5 ? tg_fn<true>(false, true) : tg_fn<false>(false, true);
   if (multi) {
     // Blocks of slice pairs; the (matrix, tile) items spread evenly over ny groups, ny =
     // cus / gcd(S2, cus) so the grid's S2 * ny blocks fill whole rounds of the GPU (one round
