@@ -106,6 +106,7 @@ struct Model {
   float *pf_ba = nullptr, *pf_conv = nullptr, *pf_oraw = nullptr;
   _Float16 *pf_h = nullptr, *pf_l = nullptr;
   float* pf_xs = nullptr;                          // [pf_rows] row scales of the input planes
+  float* pf_rs = nullptr;                          // [pf_rows] a rotated input's 1/rms per row
   int host_n_fed = 0, host_head_from = 0;          // host copies of the control words
   hipGraph_t graph = nullptr;
   hipGraphExec_t graph_exec = nullptr;
@@ -786,6 +787,7 @@ static int pf_prep(Model& m, const float* x, int ldx, int K, int R, const float*
   pp.xh = m.pf_h;
   pp.xl = m.pf_l;
   pp.xs = m.pf_xs;
+  pp.rs = m.pf_rs;
   if (m.cfg.hadamard_block && !plain) {
     int wi = 0;
     while (wi < 4 && m.cfg.hadamard_widths[wi] != K) ++wi;
@@ -848,6 +850,7 @@ static int pf_alloc(Model& m, int R) {
       {(void**)&m.pf_h, (size_t)kmax * 2},
       {(void**)&m.pf_l, (size_t)kmax * 2},
       {(void**)&m.pf_xs, 4},
+      {(void**)&m.pf_rs, 4},
       {(void**)&m.pf_qkv, (size_t)io * 4},
       {(void**)&m.pf_att, (size_t)att * 4},
       {(void**)&m.pf_act, (size_t)F * 4},

@@ -47,6 +47,7 @@ struct PrepParams {
   _Float16* xh;            // [R][K]
   _Float16* xl;
   float* xs;               // [R]
+  float* rs;               // [R] a rotated input's 1/rms per row (null without a rotation)
 };
 int launch_prep(const PrepParams& p, hipStream_t s);
 

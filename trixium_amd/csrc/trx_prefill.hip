@@ -414,42 +414,40 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepParams p) {
 
 // Rotated input: one block of B threads per (rotation block, position), as rotate_kernel does for
 // one vector (the whole row's sum of squares, the butterflies by shuffles then LDS).
-__global__ __launch_bounds__(1024) void prep_rot_kernel(PrepParams p) {
-  __shared__ float v[1024];
+// The rotated input's row statistics, one block of 256 threads per position: the RMSNorm scale
+// 1/rms(x) (1 without a norm) and the power of two that keeps the row's planes finite. Every
+// output of a rotation block is bounded by scale * B times the row's largest |x * gain| (times
+// 1/rms), which sets one scale for all of the row's blocks.
+__global__ __launch_bounds__(256) void prep_rot_stats_kernel(PrepParams p) {
   __shared__ float red[16];
-  const int t = threadIdx.x, B = blockDim.x, c = blockIdx.x * B + t, r = blockIdx.y;
-  const int lane = t & 63, w = t >> 6;
-  __shared__ float mred[16];
+  const int r = blockIdx.x, t = threadIdx.x;
   const float* x = p.x + (size_t)r * p.ldx;
-  float a = x[c] * p.signs[c];
-  // The whole row's sum of squares (RMSNorm) and maximum of |x * gain|: every output of a
-  // rotation block is bounded by scale * B times that maximum (times 1/rms), which sets the row's
-  // scale for every block alike.
   float ss = 0.f, am = 0.f;
-  for (int i = t; i < p.K; i += B) {
+  for (int i = t; i < p.K; i += 256) {
     ss += x[i] * x[i];
     am = fmaxf(am, fabsf(p.norm_w ? x[i] * p.norm_w[i] : x[i]));
   }
-  ss = wave_sum(ss);
-  am = wave_max(am);
-  if (lane == 0) {
-    red[w] = ss;
-    mred[w] = am;
-  }
-  __syncthreads();
-  float tot = 0.f, amax = 0.f;
-  for (int k = 0; k < B / 64; ++k) {
-    tot += red[k];
-    amax = fmaxf(amax, mred[k]);
-  }
-  float rsn = 1.f;
-  if (p.norm_w) {
-    rsn = 1.0f / sqrtf(tot / (float)p.K + p.eps);
-    a *= p.norm_w[c] * rsn;
-  }
+  const float tot = block_sum(ss, red);
+  const float amax = block_max(am, red);
+  const float rsn = p.norm_w ? 1.0f / sqrtf(tot / (float)p.K + p.eps) : 1.f;
   float down, up;
-  row_scale(fabsf(p.scale) * (float)B * amax * rsn, down, up);
-  if (blockIdx.x == 0 && t == 0) p.xs[r] = up;
+  row_scale(fabsf(p.scale) * (float)p.B * amax * rsn, down, up);
+  if (t == 0) {
+    p.xs[r] = up;
+    p.rs[r] = rsn;
+  }
+}
+
+// Rotated input: one block of B threads per (rotation block, position), as rotate_kernel does for
+// one vector (the butterflies by shuffles then LDS), with the row's statistics from above.
+__global__ __launch_bounds__(1024) void prep_rot_kernel(PrepParams p) {
+  __shared__ float v[1024];
+  const int t = threadIdx.x, B = blockDim.x, c = blockIdx.x * B + t, r = blockIdx.y;
+  const int lane = t & 63;
+  const float* x = p.x + (size_t)r * p.ldx;
+  float a = x[c] * p.signs[c];
+  if (p.norm_w) a *= p.norm_w[c] * p.rs[r];
+  const float down = 1.0f / p.xs[r];               // a power of two: exact
   for (int h = 1; h < 64; h <<= 1) {
     const float o = __shfl_xor(a, h, 64);
     a = (lane & h) ? o - a : a + o;
@@ -469,6 +467,8 @@ int launch_prep(const PrepParams& p, hipStream_t s) {
   if (p.signs) {
     TRX_CHECK(p.B >= 64 && p.B <= 1024 && (p.B & (p.B - 1)) == 0 && p.K % p.B == 0, TRX_E_INVALID,
               "prefill input: rotation block %d over %d columns unsupported", p.B, p.K);
+    TRX_CHECK(p.rs, TRX_E_INVALID, "prefill input: a rotation needs the row-scale buffer");
+    hipLaunchKernelGGL(prep_rot_stats_kernel, dim3(p.R), dim3(256), 0, s, p);
     hipLaunchKernelGGL(prep_rot_kernel, dim3(p.K / p.B, p.R), dim3(p.B), 0, s, p);
   } else {
     hipLaunchKernelGGL(prep_kernel, dim3(p.R), dim3(256), 0, s, p);
