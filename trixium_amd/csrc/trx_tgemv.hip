@@ -286,16 +286,19 @@ template <bool T5>
 __device__ __forceinline__ void tg_build_table(float* tab, const float* xs, int tid) {
   constexpr int NLO = T5 ? 9 : 16;     // values of the low digits (trit5: 2 digits; 2-bit: 2 codes)
   constexpr int NHI = T5 ? 29 : 16;    // values of the rest (b / 9 <= 28; b >> 4)
+  // Column c's group and byte as tg_position gives them, without branches: every lane loads
+  // its digits' x (a clamped index), and a position without a byte or a digit past the group
+  // takes 0 by a select.
   const int c = tid & (kTabCols - 1);
-  int g, byte;
-  tg_position(T5, c, g, byte);
+  const int l = c >> 2, jj = c & 3, g = l >> 3, ll = l & 7;
+  const bool has = !T5 || ll < 6 || (ll == 6 && (g ? jj >= 2 : jj < 2));
+  const int byte = !T5 || ll < 6 ? 4 * ll + jj : (g ? 22 + jj : 24 + jj);
   float u[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
-  if (g >= 0) {
 #pragma unroll
-    for (int k = 0; k < (T5 ? 5 : 4); ++k) {
-      const int cc = (T5 ? 5 : 4) * byte + k;
-      if (cc < kGroup) u[k] = xs[kGroup * g + cc];
-    }
+  for (int k = 0; k < (T5 ? 5 : 4); ++k) {
+    const int cc = (T5 ? 5 : 4) * byte + k;
+    const float v = xs[min(kGroup * g + cc, kSliceCols - 1)];
+    u[k] = has && cc < kGroup ? v : 0.f;
   }
   float lo[NLO];
 #pragma unroll
@@ -435,6 +438,9 @@ __device__ __forceinline__ float tf_item_sum(const uint4 c, uint32_t scales, uin
 template <bool T5, int NB, bool TF, bool HAND>
 __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgParams p) {
   __shared__ __align__(16) float tab[256 * kTabCols];
+  // The prologue's partial-sum groups (their own memory, so the table can be built while the
+  // last of them are read).
+  __shared__ __align__(16) float scr[16 * kSliceCols];
   __shared__ float xs[kSliceCols];
   __shared__ float red[16];
   __shared__ int todo[kMaxTilesPerBlock];
@@ -456,35 +462,29 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   const int cs = s * kSliceCols + tid;
   float xv = 0.f, wv = 1.f, ssin = 0.f;
   float4 pv[kSwiVec > kResVec ? (kSwiVec > kMergeVec ? kSwiVec : kMergeVec) : (kResVec > kMergeVec ? kResVec : kMergeVec)];
-  int ns = 0, h0 = 0, nh = 0;
+  int h0 = 0, nh = 0, mpos = 0;
+  float mv = -INFINITY, lv = 0.f;
   if (xmode == kXMerge) {
-    // The slice's attention output from the split partials: the splits' o values in flight,
-    // then (m, l) of the slice's heads.
+    // The slice's attention output from the split partials: every split's o values and the
+    // (m, l) of the slice's heads, none of which waits for the position (the splits holding
+    // positions are known once it arrives, after the weight loads are issued).
     const AttnMergeSrc& a = p.merge;
-    const int T = *a.pos + 1, chunk = (T + a.n_split - 1) / a.n_split;
-    ns = min(a.n_split, (T + chunk - 1) / chunk);
+    mpos = *a.pos;
     h0 = (s * kSliceCols) / a.hd;
     nh = kSliceCols / a.hd;
     // Thread t loads columns 4 (t % 64) .. + 3 of splits t / 64 and t / 64 + 16 (16 bytes each;
-    // splits past ns re-read the last one, their weight is 0: unconditional loads measured faster
-    // here, at long contexts every split holds positions).
+    // past n_split a repeat of the last split). A split without positions keeps what an earlier
+    // position left, and is dropped by a select, not a zero weight.
     const int c0 = s * kSliceCols + 4 * (tid % (kSliceCols / 4)), sl = tid / (kSliceCols / 4);
     const int h = c0 / a.hd, d = c0 - h * a.hd;
 #pragma unroll
     for (int k = 0; k < kMergeVec; ++k)
-      pv[k] = c0 < p.K ? *(const float4*)(a.o + ((size_t)h * a.n_split + min(sl + kMergeSlicesPerPass * k, ns - 1)) * a.hd + d)
+      pv[k] = c0 < p.K ? *(const float4*)(a.o + ((size_t)h * a.n_split + min(sl + kMergeSlicesPerPass * k, a.n_split - 1)) * a.hd + d)
                        : make_float4(0.f, 0.f, 0.f, 0.f);
-    // Split weights of the slice's heads: wave w takes head h0 + w, lane k split k.
-    if (w < nh) {
-      const int hh = h0 + w;
-      const bool ok = lane < ns && hh * a.hd < p.K;
-      const float mv = ok ? a.m[(size_t)hh * a.n_split + lane] : -INFINITY;
-      const float lv = ok ? a.l[(size_t)hh * a.n_split + lane] : 0.f;
-      const float M = wave_max(mv);
-      const float wv = ok ? __expf(mv - M) : 0.f;
-      const float L = wave_sum(lv * wv);
-      if (lane < kMergeMax) amw[w][lane] = wv;
-      if (lane == 0) atot[w] = L;
+    // Split statistics of the slice's heads: wave w takes head h0 + w, lane k split k.
+    if (w < nh && lane < a.n_split && (h0 + w) * a.hd < p.K) {
+      mv = a.m[(size_t)(h0 + w) * a.n_split + lane];
+      lv = a.l[(size_t)(h0 + w) * a.n_split + lane];
     }
   } else if (xmode == kXSwiglu) {
     // The gate|up partial sums of this slice's 128 packed row quads ([g 2q, g 2q+1, u 2q,
@@ -595,8 +595,20 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
 
   // 3. The slice's x (times the RMSNorm gain; 1/rms(x) scales the sums), then the table.
   if (xmode == kXMerge) {
-    // Each thread's two splits weighted, the 16 split groups summed through the table's memory
-    // (in group order), then scaled by the heads' 1 / L.
+    // The splits holding positions (of pos + 1), their softmax weights per head, then each
+    // thread's two splits weighted, the 16 split groups summed through scr (in
+    // group order), then scaled by the heads' 1 / L.
+    const int T = mpos + 1, chunk = (T + p.merge.n_split - 1) / p.merge.n_split;
+    const int ns = min(p.merge.n_split, (T + chunk - 1) / chunk);
+    if (w < nh) {
+      const bool ok = lane < ns && (h0 + w) * p.merge.hd < p.K;
+      const float mk = ok ? mv : -INFINITY;
+      const float M = wave_max(mk);
+      const float wv = ok ? __expf(mk - M) : 0.f;
+      const float L = wave_sum(ok ? lv * wv : 0.f);
+      if (lane < kMergeMax) amw[w][lane] = wv;
+      if (lane == 0) atot[w] = L;
+    }
     __syncthreads();
     {
       constexpr int NQ = kSliceCols / 4;
@@ -605,25 +617,26 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
 #pragma unroll
       for (int k = 0; k < kMergeVec; ++k) {
         const int sp = sl + kMergeSlicesPerPass * k;
-        const float wk = sp < ns ? amw[hl][sp] : 0.f;
-        v = make_float4(v.x + pv[k].x * wk, v.y + pv[k].y * wk, v.z + pv[k].z * wk, v.w + pv[k].w * wk);
+        if (sp < ns) {
+          const float wk = amw[hl][sp];
+          v = make_float4(v.x + pv[k].x * wk, v.y + pv[k].y * wk, v.z + pv[k].z * wk, v.w + pv[k].w * wk);
+        }
       }
-      *(float4*)(tab + sl * kSliceCols + 4 * (tid % NQ)) = v;
+      *(float4*)(scr + sl * kSliceCols + 4 * (tid % NQ)) = v;
     }
     __syncthreads();
     if (tid < kSliceCols && cs < p.K) {
       const int hl = tid / p.merge.hd, h = h0 + hl;
       float o = 0.f;
 #pragma unroll
-      for (int i = 0; i < kMergeSlicesPerPass; ++i) o += tab[i * kSliceCols + tid];
+      for (int i = 0; i < kMergeSlicesPerPass; ++i) o += scr[i * kSliceCols + tid];
       o /= atot[hl];
       if (p.merge.gated) o *= sigmoidf_(p.merge.qkv[(size_t)h * 2 * p.merge.hd + p.merge.hd + (cs - h * p.merge.hd)]);
       xv = o;
       if (j == 0) p.merge.out[cs] = o;
     }
-    __syncthreads();                                // the table's memory is rewritten below
   } else if (xmode == kXSwiglu) {
-    // Each thread's slices summed, the 8 slice groups through the table's memory (in group
+    // Each thread's slices summed, the 8 slice groups through scr (in group
     // order), then per quad x[2q] = silu(r g0) * (r u0), x[2q + 1] = silu(r g1) * (r u1).
     constexpr int NQ = 2 * kSliceCols / 4;
     const int sl = tid / NQ;
@@ -632,7 +645,7 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
     for (int k = 0; k < kSwiVec; ++k)
       if (sl + kSwiSlicesPerPass * k < p.parts.S)
         v = make_float4(v.x + pv[k].x, v.y + pv[k].y, v.z + pv[k].z, v.w + pv[k].w);
-    *(float4*)(tab + sl * 2 * kSliceCols + 4 * (tid % NQ)) = v;
+    *(float4*)(scr + sl * 2 * kSliceCols + 4 * (tid % NQ)) = v;
     if (w == 0) {
       const float t = wave_sum_dpp(ssin);
       if (lane == 0) red[0] = t;
@@ -640,10 +653,10 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
     __syncthreads();
     if (tid < NQ) {
       const float r = p.parts.in_ss ? 1.0f / sqrtf(red[0] / (float)p.parts.in_K + p.eps) : 1.f;
-      float4 a = *(const float4*)(tab + 4 * tid);
+      float4 a = *(const float4*)(scr + 4 * tid);
 #pragma unroll
       for (int i = 1; i < kSwiSlicesPerPass; ++i) {
-        const float4 b = *(const float4*)(tab + i * 2 * kSliceCols + 4 * tid);
+        const float4 b = *(const float4*)(scr + i * 2 * kSliceCols + 4 * tid);
         a = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
       }
       const int fl = 2 * tid, f = s * kSliceCols + fl;
@@ -657,7 +670,7 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
       }
     }
   } else if (xmode == kXResid) {
-    // Each thread's slices summed, then the 16 slice groups through the table's memory (in
+    // Each thread's slices summed, then the 16 slice groups through scr (in
     // group order).
     constexpr int NQ = kSliceCols / 4;
     const int sl = tid / NQ;
@@ -666,17 +679,16 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
     for (int k = 0; k < kResVec; ++k)
       if (sl + kResSlicesPerPass * k < p.parts.S)
         v = make_float4(v.x + pv[k].x, v.y + pv[k].y, v.z + pv[k].z, v.w + pv[k].w);
-    *(float4*)(tab + sl * kSliceCols + 4 * (tid % NQ)) = v;
+    *(float4*)(scr + sl * kSliceCols + 4 * (tid % NQ)) = v;
     __syncthreads();
     if (tid < kSliceCols && cs < p.K) {
       float a = 0.f;
 #pragma unroll
-      for (int i = 0; i < kResSlicesPerPass; ++i) a += tab[i * kSliceCols + tid];
+      for (int i = 0; i < kResSlicesPerPass; ++i) a += scr[i * kSliceCols + tid];
       xv += a;
       if (j == 0 && p.parts.act) p.parts.act[cs] = xv;
     }
     if (gated_off) return;
-    __syncthreads();                                // the table's memory is rewritten below
   }
   if (rot) {
     // H over each rotation block of the span: butterflies of span < 64 by wave shuffles, the
@@ -700,7 +712,7 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
     // block (all inside the slice), scaled.
     float r;
     if (xmode == kXSwiglu) {
-      __syncthreads();                              // xs complete, the table's memory free
+      __syncthreads();                              // xs complete
       r = tid < kSliceCols ? xs[tid] * sgn : 0.f;
     } else {
       r = tid < kSliceCols && cs < p.K ? (p.norm_w ? xv * wv : xv) * sgn : 0.f;
