@@ -280,12 +280,16 @@ struct TgItem {
 // The slice's lookup table from its 256 x values: T[b][c] = sum over the digits (codes) k of
 // byte b of (digit - 1) * x at table position c's k-th column, at tab[b * kTabCols + c]. T = hi(b)
 // + lo(b): lo from the low digits (trit5: b % 9; 2-bit: b & 15), hi from the rest (b / 9; b >> 4).
-// A thread owns one column: its x values and its lo sums in registers, then whole runs of entries
-// sharing one hi (waves take different hi values).
-template <bool T5>
-__device__ __forceinline__ void tg_build_table(float* tab, const float* xs, int tid) {
+// Waves w0 .. w0 + NW - 1 of the block build it (the others return at once). A thread owns one
+// column: its x values and its lo sums in registers, then whole runs of entries sharing one hi
+// (a wave-uniform hi value per run). The per-column set-up is repeated by every building wave,
+// so NW = 8 of the 16 waves measured faster than all 16.
+template <bool T5, int NW>
+__device__ __forceinline__ void tg_build_table(float* tab, const float* xs, int tid, int w0) {
   constexpr int NLO = T5 ? 9 : 16;     // values of the low digits (trit5: 2 digits; 2-bit: 2 codes)
   constexpr int NHI = T5 ? 29 : 16;    // values of the rest (b / 9 <= 28; b >> 4)
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6) - w0;
+  if (wv < 0 || wv >= NW) return;
   // Column c's group and byte as tg_position gives them, without branches: every lane loads
   // its digits' x (a clamped index), and a position without a byte or a digit past the group
   // takes 0 by a select.
@@ -300,24 +304,29 @@ __device__ __forceinline__ void tg_build_table(float* tab, const float* xs, int 
     const float v = xs[min(kGroup * g + cc, kSliceCols - 1)];
     u[k] = has && cc < kGroup ? v : 0.f;
   }
-  float lo[NLO];
-#pragma unroll
-  for (int e = 0; e < NLO; ++e) {
-    const int d0 = T5 ? e % 3 : (e & 3), d1 = T5 ? e / 3 : (e >> 2);
-    lo[e] = (float)(d0 - 1) * u[0] + (float)(d1 - 1) * u[1];
-  }
-  for (int h = tid >> 6; h < NHI; h += kTgThreads / kTabCols) {
-    float hv;
-    if (T5) {
+  if constexpr (T5) {
+    // lo(e) = (e % 3 - 1) u0 + (e / 3 - 1) u1 is one of 0, +-u0, +-u1, +-(u0 + u1), +-(u0 - u1)
+    // (every product is exact, and rounding is symmetric in sign).
+    const float s01 = u[0] + u[1], d01 = u[0] - u[1];
+    for (int h = wv; h < NHI; h += NW) {
       const int h1 = h / 3, h2 = h1 / 3;
-      hv = (float)(h - 3 * h1 - 1) * u[2] + (float)(h1 - 3 * h2 - 1) * u[3] + (float)(h2 % 3 - 1) * u[4];
-    } else {
-      hv = (float)((h & 3) - 1) * u[2] + (float)((h >> 2) - 1) * u[3];
-    }
-    float* col = tab + h * NLO * kTabCols + c;
+      const float hv = (float)(h - 3 * h1 - 1) * u[2] + (float)(h1 - 3 * h2 - 1) * u[3] + (float)(h2 % 3 - 1) * u[4];
+      const float t[NLO] = {hv - s01, hv - u[1], hv + d01, hv - u[0], hv, hv + u[0], hv - d01, hv + u[1], hv + s01};
+      float* col = tab + h * NLO * kTabCols + c;
 #pragma unroll
-    for (int e = 0; e < NLO; ++e)
-      if (h * NLO + e < 256) col[e * kTabCols] = lo[e] + hv;
+      for (int e = 0; e < NLO; ++e)
+        if (h * NLO + e < 256) col[e * kTabCols] = t[e];
+    }
+  } else {
+    float lo[NLO];
+#pragma unroll
+    for (int e = 0; e < NLO; ++e) lo[e] = (float)((e & 3) - 1) * u[0] + (float)((e >> 2) - 1) * u[1];
+    for (int h = wv; h < NHI; h += NW) {
+      const float hv = (float)((h & 3) - 1) * u[2] + (float)((h >> 2) - 1) * u[3];
+      float* col = tab + h * NLO * kTabCols + c;
+#pragma unroll
+      for (int e = 0; e < NLO; ++e) col[e * kTabCols] = lo[e] + hv;
+    }
   }
 }
 
@@ -433,6 +442,8 @@ __device__ __forceinline__ float tf_item_sum(const uint4 c, uint32_t scales, uin
   return a[0] * __half2float(__ushort_as_half((unsigned short)(scales >> sshift)));
 }
 
+constexpr int kBuildWaves = 8;           // waves that build the single-slice kernel's table
+
 // HAND: the partial sums go to the next GEMV (parts.out): plain stores, which the kernel's end
 // makes visible to the next launch; otherwise agent-scope stores for the tile's reducing block.
 template <bool T5, int NB, bool TF, bool HAND>
@@ -463,7 +474,7 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   float xv = 0.f, wv = 1.f, ssin = 0.f;
   float4 pv[kSwiVec > kResVec ? (kSwiVec > kMergeVec ? kSwiVec : kMergeVec) : (kResVec > kMergeVec ? kResVec : kMergeVec)];
   int h0 = 0, nh = 0, mpos = 0;
-  float mv = -INFINITY, lv = 0.f;
+  float mv = -INFINITY, lv = 0.f, sw0 = 0.f, sw1 = 0.f;
   if (xmode == kXMerge) {
     // The slice's attention output from the split partials: every split's o values and the
     // (m, l) of the slice's heads, none of which waits for the position (the splits holding
@@ -596,8 +607,8 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   // 3. The slice's x (times the RMSNorm gain; 1/rms(x) scales the sums), then the table.
   if (xmode == kXMerge) {
     // The splits holding positions (of pos + 1), their softmax weights per head, then each
-    // thread's two splits weighted, the 16 split groups summed through scr (in
-    // group order), then scaled by the heads' 1 / L.
+    // thread's two splits weighted, the 16 split groups summed through scr (in group order),
+    // then scaled by the heads' 1 / L.
     const int T = mpos + 1, chunk = (T + p.merge.n_split - 1) / p.merge.n_split;
     const int ns = min(p.merge.n_split, (T + chunk - 1) / chunk);
     if (w < nh) {
@@ -633,7 +644,6 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
       o /= atot[hl];
       if (p.merge.gated) o *= sigmoidf_(p.merge.qkv[(size_t)h * 2 * p.merge.hd + p.merge.hd + (cs - h * p.merge.hd)]);
       xv = o;
-      if (j == 0) p.merge.out[cs] = o;
     }
   } else if (xmode == kXSwiglu) {
     // Each thread's slices summed, the 8 slice groups through scr (in group
@@ -664,10 +674,8 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
       const float x1 = f + 1 < p.K ? silu(r * a.y) * (r * a.w) : 0.f;
       xs[fl] = x0;
       xs[fl + 1] = x1;
-      if (j == 0 && p.parts.act) {
-        if (f < p.K) p.parts.act[f] = x0;
-        if (f + 1 < p.K) p.parts.act[f + 1] = x1;
-      }
+      sw0 = x0;
+      sw1 = x1;
     }
   } else if (xmode == kXResid) {
     // Each thread's slices summed, then the 16 slice groups through scr (in
@@ -686,7 +694,7 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
 #pragma unroll
       for (int i = 0; i < kResSlicesPerPass; ++i) a += scr[i * kSliceCols + tid];
       xv += a;
-      if (j == 0 && p.parts.act) p.parts.act[cs] = xv;
+      if (gated_off && j == 0 && p.parts.act) p.parts.act[cs] = xv;
     }
     if (gated_off) return;
   }
@@ -738,11 +746,8 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
     if (lane == 0) red[w] = q;
   }
   __syncthreads();
-  if (p.norm_w && tid == 0)
-    __hip_atomic_store(p.ss_out + j * p.S + s, (red[0] + red[1]) + (red[2] + red[3]), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
   if constexpr (TF) tf_build_lut<T5>((uint4*)tab, tid);
-  else tg_build_table<T5>(tab, xs, tid);
+  else tg_build_table<T5, kBuildWaves>(tab, xs, tid, 0);
   __syncthreads();
 
   // 4. The items: four rows x one dword per lane; sixteen lanes per row group.
@@ -794,6 +799,24 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   for (int ph = 0; ph < NB - 1; ++ph) {
     if (ph < rem) compute(buf[ph], rp[ph]);
   }
+
+  // The prologue's own outputs, stored after the weight stream: a store issued before the table
+  // would make its wave's first lookups wait for it (vmcnt completes in order). Block j = 0
+  // keeps x (the residual handed on, or the attention output), every block its slice sum of x^2.
+  if (j == 0 && tid < kSliceCols) {
+    if (xmode == kXMerge && cs < p.K) {
+      p.merge.out[cs] = xv;
+    } else if (xmode == kXResid && p.parts.act && cs < p.K) {
+      p.parts.act[cs] = xv;
+    } else if (xmode == kXSwiglu && p.parts.act && tid < kSliceCols / 2) {
+      const int f = s * kSliceCols + 2 * tid;
+      if (f < p.K) p.parts.act[f] = sw0;
+      if (f + 1 < p.K) p.parts.act[f + 1] = sw1;
+    }
+  }
+  if (p.norm_w && tid == 0)
+    __hip_atomic_store(p.ss_out + j * p.S + s, (red[0] + red[1]) + (red[2] + red[3]), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
 
   // The next GEMV reduces the partial sums (their stores complete before the launch ends).
   if (p.parts.out) return;
@@ -998,8 +1021,8 @@ __global__ __launch_bounds__(kTgThreads, 1) void tgemv_pair_kernel(TgParams p) {
   // 3. The two tables.
   if (tid < 2 * kSliceCols) xs[tid] = xv;
   __syncthreads();
-  tg_build_table<T5>(tab, xs, tid);
-  tg_build_table<T5>(tab + kTab, xs + kSliceCols, tid);
+  tg_build_table<T5, kTgThreads / 128>(tab, xs, tid, 0);
+  tg_build_table<T5, kTgThreads / 128>(tab + kTab, xs + kSliceCols, tid, kTgThreads / 128);
   __syncthreads();
 
   // 4. The items (as in the single-slice kernel, once per slice).
@@ -1051,27 +1074,26 @@ __global__ __launch_bounds__(kRdThreads) void tgemv_reduce_kernel(RdParams p) {
   const int gpos = p.gate_pos ? *p.gate_pos : 0, gfrom = p.gate_pos ? *p.gate_from : 0;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int r0 = blockIdx.x * p.rpb;
-  // Rows r0 + tid + i * 256 (i < kRdRowsMax): every partial of every row in flight per chunk of
-  // slices; a row past the block's range or M re-reads row r0 and is not stored.
-  int row[kRdRowsMax];
-  bool live[kRdRowsMax];
-#pragma unroll
-  for (int i = 0; i < kRdRowsMax; ++i) {
-    const int r = r0 + tid + i * kRdThreads;
-    live[i] = tid + i * kRdThreads < p.rpb && r < p.M;
-    row[i] = live[i] ? r : min(r0, p.M - 1);
-  }
+  // Rows q .. q + 3, q = r0 + 4 tid (rpb and rows_p are multiples of 4): one 16-byte load per
+  // slice, the slice's offset scalar, every slice of a chunk in flight. A thread past the block's
+  // range or M loads zeros (an offset past the buffer) and stores nothing.
+  const int q = r0 + kRdRowsMax * tid;
+  const bool live = kRdRowsMax * tid < p.rpb && q < p.M;
+  const __amdgpu_buffer_rsrc_t rp = make_rsrc(p.part, (uint32_t)((size_t)p.S * p.rows_p * 4));
+  const uint32_t vo = live ? (uint32_t)q * 4u : 0x40000000u;
   float acc[kRdRowsMax] = {};
   for (int q0 = 0; q0 < p.S; q0 += kRdChunk) {
-    float v[kRdRowsMax][kRdChunk];
+    float v[kRdChunk][kRdRowsMax];
 #pragma unroll
-    for (int i = 0; i < kRdRowsMax; ++i)
+    for (int k = 0; k < kRdChunk; ++k) {
+      const auto a = __builtin_amdgcn_raw_buffer_load_b128(rp, vo, (uint32_t)min(q0 + k, p.S - 1) * (uint32_t)p.rows_p * 4u, 0);
 #pragma unroll
-      for (int k = 0; k < kRdChunk; ++k) v[i][k] = p.part[(size_t)min(q0 + k, p.S - 1) * p.rows_p + row[i]];
+      for (int i = 0; i < kRdRowsMax; ++i) v[k][i] = __uint_as_float(a[i]);
+    }
 #pragma unroll
-    for (int i = 0; i < kRdRowsMax; ++i)
+    for (int k = 0; k < kRdChunk; ++k)
 #pragma unroll
-      for (int k = 0; k < kRdChunk; ++k) acc[i] += q0 + k < p.S ? v[i][k] : 0.f;
+      for (int i = 0; i < kRdRowsMax; ++i) acc[i] += q0 + k < p.S ? v[k][i] : 0.f;
   }
   float rs = 1.f;
   if (p.ss) {
@@ -1083,16 +1105,17 @@ __global__ __launch_bounds__(kRdThreads) void tgemv_reduce_kernel(RdParams p) {
   unsigned long long key = 0;
 #pragma unroll
   for (int i = 0; i < kRdRowsMax; ++i) {
-    if (!live[i]) continue;
+    const int row = q + i;
+    if (!live || row >= p.M) continue;
     const float out = acc[i] * rs;
     if (p.mat_rows_p) {
-      const int mt = row[i] / p.mat_rows_p, r = row[i] - mt * p.mat_rows_p;
+      const int mt = row / p.mat_rows_p, r = row - mt * p.mat_rows_p;
       if (r < p.mat_M) p.y[(size_t)mt * p.y_stride + r] = out;
       continue;
     }
-    p.y[row[i]] = out;
+    p.y[row] = out;
     const unsigned long long kr =
-        ((unsigned long long)ordered_bits(out) << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)row[i]);
+        ((unsigned long long)ordered_bits(out) << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)row);
     key = kr > key ? kr : key;
   }
   if (!p.amax_slot) return;
@@ -1130,8 +1153,8 @@ int tgemv_reduce_f32(const float* part, const float* ss, int S, int rows_p, int 
   p.gate_from = gate_from;
   p.mat_rows_p = p.mat_M = p.y_stride = 0;
   const int blocks = std::min(kRdBlocks, cdiv(M, kRdThreads));
-  p.rpb = cdiv(M, blocks);
-  TRX_CHECK(p.rpb <= kRdRowsMax * kRdThreads, TRX_E_INVALID, "partial-sum reduction: %d rows (at most %d)", M,
+  p.rpb = cdiv(cdiv(M, blocks), kRdRowsMax) * kRdRowsMax;
+  TRX_CHECK(rows_p % kRdRowsMax == 0 && p.rpb <= kRdRowsMax * kRdThreads, TRX_E_INVALID, "partial-sum reduction: %d rows (at most %d)", M,
             kRdBlocks * kRdRowsMax * kRdThreads);
   hipLaunchKernelGGL(tgemv_reduce_kernel, dim3(cdiv(M, p.rpb)), dim3(kRdThreads), 0, s, p);
   TRX_LAUNCHED();
@@ -1304,7 +1327,7 @@ int tgemv_f32_batched(const uint8_t* packed, size_t mat_stride, int n_mat, int n
   r.mat_M = M;
   r.y_stride = y_stride;
   const int blocks = std::min(kRdBlocks, cdiv(r.M, kRdThreads));
-  r.rpb = cdiv(r.M, blocks);
+  r.rpb = cdiv(cdiv(r.M, blocks), kRdRowsMax) * kRdRowsMax;
   if (r.rpb > kRdRowsMax * kRdThreads) {
     // More rows than one pass of the grid holds: more blocks.
     r.rpb = kRdRowsMax * kRdThreads;
