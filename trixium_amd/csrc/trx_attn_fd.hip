@@ -57,52 +57,42 @@ __global__ __launch_bounds__(kFdThreads) void attn_fd_kernel(AttnParams p) {
   const int qstride = p.gated ? 2 * HD : HD;
   const int half = p.rope_n / 2;
 
-  // 1. The prologue's inputs first: the RoPE frequency of this thread, then, loaded once by the
-  //    block (every position group uses the same values), the q heads, the new k and v and the
-  //    two norm gains. None depends on the position, so they are in flight while the position
-  //    is read, and a later wait for them does not cover the K/V stream.
+  // 1. The prologue's inputs first, none of which depends on the position, so they are in flight
+  //    while the position is read, and a later wait for them does not cover the K/V stream.
   const float* kraw = p.qkv + (size_t)p.n_head * qstride + (size_t)g * HD;
   constexpr int NST = REP + 4, STV = NST * HD / 4;                 // rows, float4s staged
   constexpr int SPT = (STV + kFdThreads - 1) / kFdThreads;     // float4s per thread
   __shared__ __align__(16) float stg[NST][HD];
-  __shared__ float nrm[REP + 1][HD];               // the normalised q heads and k
+  // QP: thread t holds float4 e = t + 256 k of the REP + 2 rows (q heads, k, v), RW threads a row
+  // (a row never straddles a wave): every slice's partial of it and its norm gain.
+  constexpr int RW = HD / 4, NQE = (REP + 2) * RW;
+  constexpr int SPQ = (NQE + kFdThreads - 1) / kFdThreads;
+  constexpr int NPS = QP ? kQkvPartMax : 1;
   // With QP the position is read first: a scalar load, which the memory barrier below would
   // otherwise turn into a vector load queued behind the partial sums.
   const int pos_qp = QP ? *p.pos : 0;
-  float4 sv[SPT];
-  constexpr int NPS = QP ? kQkvPartMax : 1;
-  constexpr uint32_t kOutQ = 0x40000000u;          // a buffer offset past every buffer
-  const __amdgpu_buffer_rsrc_t rqp =
-      make_rsrc(p.qkv_part, QP ? (uint32_t)((size_t)p.qkv_S * p.qkv_rows_p * 4) : 0u);
-  float4 pv[SPT][NPS];
+  float4 sv[QP ? SPQ : SPT];
+  float4 pv[QP ? SPQ : 1][NPS];
+  float ssl = 0.f;
+  if constexpr (QP) {
+    constexpr uint32_t kOutQ = 0x40000000u;        // a buffer offset past every buffer
+    const __amdgpu_buffer_rsrc_t rqp = make_rsrc(p.qkv_part, (uint32_t)((size_t)p.qkv_S * p.qkv_rows_p * 4));
 #pragma unroll
-  for (int k = 0; k < SPT; ++k) {
-    const int e = min(tid + k * kFdThreads, STV - 1);            // past the end: a repeat
-    const int row = 4 * e / HD, d = 4 * e - row * HD;
-    if (QP) {
-      // Every partial of the q, k and v rows; the norm-gain rows' partial loads get an offset past
-      // the buffer (zeros, no memory access); past S a repeat of the last slice that gets no weight.
+    for (int k = 0; k < SPQ; ++k) {
+      const int e = tid + k * kFdThreads, row = e / RW, d = 4 * (e - row * RW);
       const uint32_t qi = row < REP ? (uint32_t)((g * REP + row) * HD + d)
-                          : row == REP ? (uint32_t)(p.n_head * HD + g * HD + d)
-                          : (uint32_t)(p.n_head * HD + (p.n_kv + g) * HD + d);
-      const uint32_t off0 = row < REP + 2 ? qi * 4u : kOutQ;
+                          : (uint32_t)(p.n_head * HD + ((row - REP) * p.n_kv + g) * HD + d);
+      // Past the rows: an offset past the buffer (zeros, no memory access); past S a repeat of
+      // the last slice that gets no weight.
+      const uint32_t off0 = e < NQE ? qi * 4u : kOutQ;
 #pragma unroll
       for (int q = 0; q < NPS; ++q) {
         const auto a = __builtin_amdgcn_raw_buffer_load_b128(
             rqp, off0 + (uint32_t)min(q, p.qkv_S - 1) * (uint32_t)p.qkv_rows_p * 4u, 0, 0);
         pv[k][q] = make_float4(__uint_as_float(a[0]), __uint_as_float(a[1]), __uint_as_float(a[2]), __uint_as_float(a[3]));
       }
-      sv[k] = *(const float4*)(row == REP + 3 ? p.k_norm + d : p.q_norm + (row == REP + 2 ? d : 0));
-    } else {
-      const float* src = row < REP ? p.qkv + (size_t)(g * REP + row) * qstride + d
-                         : row == REP ? kraw + d
-                         : row == REP + 1 ? kraw + (size_t)p.n_kv * HD + d
-                         : row == REP + 2 ? p.q_norm + d : p.k_norm + d;
-      sv[k] = *(const float4*)src;
+      sv[k] = *(const float4*)((row == REP ? p.k_norm : p.q_norm) + (e < NQE ? d : 0));
     }
-  }
-  float ssl = 0.f;
-  if (QP) {
     // Lane i holds slice i's sum of squares (a vector load: counted with the partials, not the
     // position; past S the buffer's range check gives 0).
     ssl = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
@@ -110,6 +100,19 @@ __global__ __launch_bounds__(kFdThreads) void attn_fd_kernel(AttnParams p) {
     // Keeps these loads ahead of the position's and the K/V rows' (the scheduler would otherwise
     // issue them after the K/V stream, and the scalar ones after its waits).
     asm volatile("" ::: "memory");
+  } else {
+    // The q heads, the new k and v and the two norm gains, loaded once by the block (every
+    // position group uses the same values).
+#pragma unroll
+    for (int k = 0; k < SPT; ++k) {
+      const int e = min(tid + k * kFdThreads, STV - 1);            // past the end: a repeat
+      const int row = 4 * e / HD, d = 4 * e - row * HD;
+      const float* src = row < REP ? p.qkv + (size_t)(g * REP + row) * qstride + d
+                         : row == REP ? kraw + d
+                         : row == REP + 1 ? kraw + (size_t)p.n_kv * HD + d
+                         : row == REP + 2 ? p.q_norm + d : p.k_norm + d;
+      sv[k] = *(const float4*)src;
+    }
   }
 
   const int pos = QP ? pos_qp : *p.pos, T = pos + 1;
@@ -118,13 +121,16 @@ __global__ __launch_bounds__(kFdThreads) void attn_fd_kernel(AttnParams p) {
   const bool owner = n > 0 && pos >= p0 && pos < p1;
   const int npass = (n + PPP - 1) / PPP;
 
-  // The RoPE cos/sin of this lane's elements (d = lane + 64 i < 2 half) at pos, from the model's
-  // table (fp32, or the image's Q14 rows), loaded before the K/V rows.
-  constexpr int EPL = HD / 64;                        // elements per lane when a wave holds a vector
-  float rc[EPL], rsn[EPL];
+  // The RoPE cos/sin at pos, from the model's table (fp32, or the image's Q14 rows), loaded
+  // before the K/V rows: QP, of this thread's four elements (d .. d + 3, one side of the
+  // rotation); otherwise of this lane's elements (d = lane + 64 i) when a wave holds a vector.
+  constexpr int EPL = HD / 64;
+  constexpr int NRC = QP ? 4 * SPQ : EPL;
+  float rc[NRC], rsn[NRC];
 #pragma unroll
-  for (int i = 0; i < EPL; ++i) {
-    const int d = lane + 64 * i, ri = d < half ? d : d - half;
+  for (int i = 0; i < NRC; ++i) {
+    const int d = QP ? 4 * ((tid + (i / 4) * kFdThreads) % RW) + (i % 4) : lane + 64 * i;
+    const int ri = d < half ? d : d - half;
     rc[i] = 1.f;
     rsn[i] = 0.f;
     if (d < 2 * half) {
@@ -159,75 +165,118 @@ __global__ __launch_bounds__(kFdThreads) void attn_fd_kernel(AttnParams p) {
     vr[ps] = make_uint4(b[0], b[1], b[2], b[3]);
   }
 
-  // The staged inputs into LDS (the loads are waited for here, after the K/V loads went out).
-  float rs = 1.f;
-  if (QP) rs = 1.0f / sqrtf(wave_sum_dpp(ssl) / (float)p.qkv_K + p.eps);
+  const float qpost = 1.0f / sqrtf((float)HD);
+  if constexpr (QP) {
+    // The slices added in slice order, times the q|k|v GEMV's RMSNorm scale; then each q head
+    // and k RMS-normalised over its row's RW threads (DPP and lane swaps), times its gain, and
+    // rotated with the partner element d +- half from the thread half / 4 lanes away; q scaled by
+    // 1/sqrt(hd); k and v rounded to fp16 (the cache's values, which the score of this position
+    // uses too) and stored to the cache by the block that holds the position. No LDS round trip
+    // and no barrier before the rows go to stg.
+    const float rs = 1.0f / sqrtf(wave_sum_dpp(ssl) / (float)p.qkv_K + p.eps);
 #pragma unroll
-  for (int k = 0; k < SPT; ++k) {
-    const int e = min(tid + k * kFdThreads, STV - 1);
-    float4 v = sv[k];
-    if (QP && 4 * e / HD < REP + 2) {
-      // The slices added in slice order, then the q|k|v GEMV's RMSNorm scale.
+    for (int k = 0; k < SPQ; ++k) {
+      const int e = tid + k * kFdThreads, row = e / RW, d = 4 * (e - row * RW);
       float4 a = pv[k][0];
 #pragma unroll
       for (int q = 1; q < NPS; ++q)
         if (q < p.qkv_S) { a.x += pv[k][q].x; a.y += pv[k][q].y; a.z += pv[k][q].z; a.w += pv[k][q].w; }
-      v = make_float4(a.x * rs, a.y * rs, a.z * rs, a.w * rs);
+      const float x[4] = {a.x * rs, a.y * rs, a.z * rs, a.w * rs};
       // The first split block of each kv head keeps its q, k and v rows in p.qkv, as the GEMV
       // would have stored them (the q|k|v tap of the last attention layer).
-      if (sp == 0 && tid + k * kFdThreads < STV) {
-        const int row = 4 * e / HD, d = 4 * e - row * HD;
+      if (sp == 0 && e < NQE) {
         const size_t qi = row < REP ? (size_t)(g * REP + row) * HD + d
                           : (size_t)p.n_head * HD + (size_t)((row - REP) * p.n_kv + g) * HD + d;
-        *(float4*)(p.qkv + qi) = v;
+        *(float4*)(p.qkv + qi) = make_float4(x[0], x[1], x[2], x[3]);
       }
-    }
-    *(float4*)(&stg[0][0] + 4 * e) = v;
-  }
-  float q[REP][8], kn[8], vn[8];
-  if (n > 0) {
-    __syncthreads();
-    // The q heads and the new k normalised and rotated once per block: wave w takes vectors w,
-    // w + 4, ... (lane l holds elements l + 64 i). The rotation partner (d +- half) is read back
-    // from nrm, which only this wave writes for its vector. q is scaled by 1/sqrt(hd); k and v
-    // are rounded to fp16 (the cache's values, which the score of this position uses too) and
-    // stored to the cache by the block that holds the position.
-    const float qpost = 1.0f / sqrtf((float)HD);
-    for (int v = wave; v <= REP; v += kFdThreads / 64) {
-      const float* gw = stg[v < REP ? REP + 2 : REP + 3];
-      float x[EPL], ss = 0.f;
+      float ss = (x[0] * x[0] + x[1] * x[1]) + (x[2] * x[2] + x[3] * x[3]);
+      ss = row16_sum(ss);
+      if (RW >= 32) ss += __shfl_xor(ss, 16, 64);
+      if (RW >= 64) ss += __shfl_xor(ss, 32, 64);
+      const float r = rsqrtf(ss / (float)HD + p.eps);
+      const float gw[4] = {sv[k].x, sv[k].y, sv[k].z, sv[k].w};
+      float xn[4], pr[4];
 #pragma unroll
-      for (int i = 0; i < EPL; ++i) {
-        x[i] = stg[v][lane + 64 * i];
-        ss += x[i] * x[i];
-      }
-      const float r = rsqrtf(wave_sum_dpp(ss) / (float)HD + p.eps);
+      for (int i = 0; i < 4; ++i) xn[i] = x[i] * r * gw[i];
 #pragma unroll
-      for (int i = 0; i < EPL; ++i) {
-        x[i] = x[i] * r * gw[lane + 64 * i];
-        nrm[v][lane + 64 * i] = x[i];
-      }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // this wave's stores before its reads
+      for (int i = 0; i < 4; ++i) pr[i] = __shfl_xor(xn[i], half / 4, 64);
+      if (e < NQE) {
+        float y[4];
 #pragma unroll
-      for (int i = 0; i < EPL; ++i) {
-        const int d = lane + 64 * i;
-        float y = x[i];
-        if (d < half) y = x[i] * rc[i] - nrm[v][d + half] * rsn[i];
-        else if (d < 2 * half) y = nrm[v][d - half] * rsn[i] + x[i] * rc[i];
-        if (v < REP) {
-          stg[v][d] = y * qpost;
+        for (int i = 0; i < 4; ++i) {
+          const float c = rc[4 * k + i], sn = rsn[4 * k + i];
+          y[i] = d < half ? xn[i] * c - pr[i] * sn : d < 2 * half ? pr[i] * sn + xn[i] * c : xn[i];
+        }
+        if (row < REP) {
+          *(float4*)&stg[row][d] = make_float4(y[0] * qpost, y[1] * qpost, y[2] * qpost, y[3] * qpost);
         } else {
-          const __half kh = __float2half(y), vh = __float2half(stg[REP + 1][d]);
-          stg[REP][d] = __half2float(kh);
-          stg[REP + 1][d] = __half2float(vh);
+          // k (normalised, rotated) or v (as it came).
+          const float* src = row == REP ? y : x;
+          __half h[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) h[i] = __float2half(src[i]);
+          *(float4*)&stg[row][d] = make_float4(__half2float(h[0]), __half2float(h[1]), __half2float(h[2]), __half2float(h[3]));
           if (owner) {
-            p.kcache[cache0 + (size_t)pos * HD + d] = kh;
-            p.vcache[cache0 + (size_t)pos * HD + d] = vh;
+            __half* dst = (row == REP ? p.kcache : p.vcache) + cache0 + (size_t)pos * HD + d;
+            *(uint2*)dst = make_uint2(__builtin_bit_cast(uint32_t, __halves2half2(h[0], h[1])),
+                                      __builtin_bit_cast(uint32_t, __halves2half2(h[2], h[3])));
           }
         }
       }
     }
+  } else {
+#pragma unroll
+    for (int k = 0; k < SPT; ++k) {
+      const int e = min(tid + k * kFdThreads, STV - 1);
+      *(float4*)(&stg[0][0] + 4 * e) = sv[k];
+    }
+  }
+  float q[REP][8], kn[8], vn[8];
+  if (n > 0) {
     __syncthreads();
+    if constexpr (!QP) {
+      // The q heads and the new k normalised and rotated once per block: wave w takes vectors w,
+      // w + 4, ... (lane l holds elements l + 64 i). The rotation partner (d +- half) is read back
+      // from nrm, which only this wave writes for its vector. q is scaled by 1/sqrt(hd); k and v
+      // are rounded to fp16 (the cache's values, which the score of this position uses too) and
+      // stored to the cache by the block that holds the position.
+      __shared__ float nrm[REP + 1][HD];
+      for (int v = wave; v <= REP; v += kFdThreads / 64) {
+        const float* gw = stg[v < REP ? REP + 2 : REP + 3];
+        float x[EPL], ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) {
+          x[i] = stg[v][lane + 64 * i];
+          ss += x[i] * x[i];
+        }
+        const float r = rsqrtf(wave_sum_dpp(ss) / (float)HD + p.eps);
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) {
+          x[i] = x[i] * r * gw[lane + 64 * i];
+          nrm[v][lane + 64 * i] = x[i];
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // this wave's stores before its reads
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) {
+          const int d = lane + 64 * i;
+          float y = x[i];
+          if (d < half) y = x[i] * rc[i] - nrm[v][d + half] * rsn[i];
+          else if (d < 2 * half) y = nrm[v][d - half] * rsn[i] + x[i] * rc[i];
+          if (v < REP) {
+            stg[v][d] = y * qpost;
+          } else {
+            const __half kh = __float2half(y), vh = __float2half(stg[REP + 1][d]);
+            stg[REP][d] = __half2float(kh);
+            stg[REP + 1][d] = __half2float(vh);
+            if (owner) {
+              p.kcache[cache0 + (size_t)pos * HD + d] = kh;
+              p.vcache[cache0 + (size_t)pos * HD + d] = vh;
+            }
+          }
+        }
+      }
+      __syncthreads();
+    }
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
 #pragma unroll
@@ -392,6 +441,12 @@ __global__ __launch_bounds__(kFdThreads) void attn_fd_kernel(AttnParams p) {
   }
 }
 
+bool attention_qp_supported(int hd, int rope_n) {
+  // The partial-sum prologue swaps a thread's four elements with the thread half / 4 lanes away.
+  const int half = rope_n / 2, q = half / 4;
+  return half >= 4 && half % 4 == 0 && (q & (q - 1)) == 0 && 2 * half <= hd;
+}
+
 bool attention_fd_supported(int rep, int hd, int rope_n, int n_split) {
   const int half = rope_n / 2;
   const bool rope_ok = half >= 1 && 2 * half <= hd;
@@ -420,7 +475,7 @@ static int launch_fd_rep(const AttnParams& p, hipStream_t s) {
 int launch_attention_fd(const AttnParams& p, hipStream_t s) {
   TRX_CHECK(attention_fd_supported(p.n_rep, p.hd, p.rope_n, p.n_split), TRX_E_INVALID,
             "attention: rep %d hd %d rope %d splits %d unsupported", p.n_rep, p.hd, p.rope_n, p.n_split);
-  TRX_CHECK(!p.qkv_part || (p.qkv_ss && !p.gated && p.qkv_S >= 1 && p.qkv_S <= kQkvPartMax &&
+  TRX_CHECK(!p.qkv_part || (p.qkv_ss && !p.gated && attention_qp_supported(p.hd, p.rope_n) && p.qkv_S >= 1 && p.qkv_S <= kQkvPartMax &&
                             p.qkv_rows_p % 4 == 0 && p.qkv_K > 0 &&
                             p.qkv_rows_p >= (p.n_head + 2 * p.n_kv) * p.hd),
             TRX_E_INVALID, "attention: unsupported q|k|v partial sums (S %d, rows %d)", p.qkv_S, p.qkv_rows_p);

@@ -570,7 +570,8 @@ static int run_step(Model& m, hipStream_t s) {
       // one-launch attention when that kernel takes them (non-gated), else it reduces them.
       const int rope_n = c.rope_dims ? c.rope_dims : hd;
       const bool fd_ok = attention_fd_supported(c.n_head / c.n_kv_head, hd, rope_n, m.n_split);
-      const bool qkv_hand = fd_ok && m.qkv_part && m.qkv_rows_p % 4 == 0 && packed(OP_QKV, l);
+      const bool qkv_hand = fd_ok && attention_qp_supported(hd, rope_n) && m.qkv_part && m.qkv_rows_p % 4 == 0 &&
+                            packed(OP_QKV, l);
       if (const PackedMat* pq = packed(OP_QKV, l)) {
         const float* xin;
         const PartialSums* pp = take(xin);

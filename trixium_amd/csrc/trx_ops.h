@@ -167,6 +167,9 @@ int launch_attention(const AttnParams& p, hipStream_t s);
 // One-launch attention (trx_attn_fd.hip) for the geometries attention_fd_supported accepts: the
 // split partials, merged by the last split block of each kv head when `done` is set (the output
 // in `out`), left for the consumer to merge otherwise (attn_merge_into_x, the packed o GEMV).
+// The one-launch attention takes the q|k|v GEMV's partial sums (its rotation partner a power-of-two
+// number of float4s away).
+bool attention_qp_supported(int hd, int rope_n);
 bool attention_fd_supported(int rep, int hd, int rope_n, int n_split);
 int launch_attention_fd(const AttnParams& p, hipStream_t s);
 // The split partials of attention_fd merged by one block per q head (into `out`).

@@ -51,7 +51,8 @@ TRX_API int trx_graph_end(trx_stream_t s, void** exec) {
   TRX_HIP(hipStreamEndCapture((hipStream_t)s, &g));
   hipGraphExec_t e = nullptr;
   const hipError_t err = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
-  hipGraphDestroy(g);
+  const hipError_t derr = hipGraphDestroy(g);
+  TRX_CHECK(derr == hipSuccess || err != hipSuccess, TRX_E_HIP, "trx_graph_end: destroy: %s", hipGetErrorString(derr));
   TRX_CHECK(err == hipSuccess, TRX_E_HIP, "trx_graph_end: instantiate: %s", hipGetErrorString(err));
   *exec = (void*)e;
   return TRX_OK;
