@@ -32,13 +32,15 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
-// QP: q, k and v arrive as the q|k|v GEMV's K-slice partial sums (p.qkv_part, [S][rows_p], with
-// its RMSNorm's slice sums of x^2 in p.qkv_ss), summed here in slice order: y = r * sum_s
-// part[s], r = 1/sqrt(sum(ss) / K + eps).
-// The q heads and the new k are normalised and rotated once per block (a wave per vector, then
-// every thread a few elements), not by every position group.
-template <int REP, int HD, bool QP>
+// QPS > 0 (QP): q, k and v arrive as the q|k|v GEMV's K-slice partial sums (p.qkv_part,
+// [S][rows_p], S <= QPS, with its RMSNorm's slice sums of x^2 in p.qkv_ss), summed here in slice
+// order: y = r * sum_s part[s], r = 1/sqrt(sum(ss) / K + eps). QPS is 8 or 16, the smallest that
+// holds S, so a GEMV of 8 slices does not load each partial twice.
+// The q heads and the new k are normalised and rotated once per block, not by every position
+// group.
+template <int REP, int HD, int QPS>
 __global__ __launch_bounds__(kFdThreads) void attn_fd_kernel(AttnParams p) {
+  constexpr bool QP = QPS > 0;
   constexpr int LPP = HD / 8;                         // lanes per position
   constexpr int PPW = 64 / LPP;                       // groups per wave
   constexpr int NG = kFdThreads / LPP;              // groups per block
@@ -67,7 +69,7 @@ __global__ __launch_bounds__(kFdThreads) void attn_fd_kernel(AttnParams p) {
   // (a row never straddles a wave): every slice's partial of it and its norm gain.
   constexpr int RW = HD / 4, NQE = (REP + 2) * RW;
   constexpr int SPQ = (NQE + kFdThreads - 1) / kFdThreads;
-  constexpr int NPS = QP ? kQkvPartMax : 1;
+  constexpr int NPS = QP ? QPS : 1;
   // With QP the position is read first: a scalar load, which the memory barrier below would
   // otherwise turn into a vector load queued behind the partial sums.
   const int pos_qp = QP ? *p.pos : 0;
@@ -454,13 +456,13 @@ bool attention_fd_supported(int rep, int hd, int rope_n, int n_split) {
   return rope_ok && rep_ok && (hd == 64 || hd == 128 || hd == 256) && n_split <= kFdMaxSplits;
 }
 
-template <int REP, bool QP>
+template <int REP, int QPS>
 static int launch_fd_qp(const AttnParams& p, hipStream_t s) {
   const dim3 grid(p.n_kv * p.n_split), block(kFdThreads);
   switch (p.hd) {
-    case 64: hipLaunchKernelGGL((attn_fd_kernel<REP, 64, QP>), grid, block, 0, s, p); break;
-    case 128: hipLaunchKernelGGL((attn_fd_kernel<REP, 128, QP>), grid, block, 0, s, p); break;
-    case 256: hipLaunchKernelGGL((attn_fd_kernel<REP, 256, QP>), grid, block, 0, s, p); break;
+    case 64: hipLaunchKernelGGL((attn_fd_kernel<REP, 64, QPS>), grid, block, 0, s, p); break;
+    case 128: hipLaunchKernelGGL((attn_fd_kernel<REP, 128, QPS>), grid, block, 0, s, p); break;
+    case 256: hipLaunchKernelGGL((attn_fd_kernel<REP, 256, QPS>), grid, block, 0, s, p); break;
     default: TRX_CHECK(false, TRX_E_INVALID, "attention: head_dim %d unsupported", p.hd);
   }
   TRX_LAUNCHED();
@@ -469,7 +471,9 @@ static int launch_fd_qp(const AttnParams& p, hipStream_t s) {
 
 template <int REP>
 static int launch_fd_rep(const AttnParams& p, hipStream_t s) {
-  return p.qkv_part ? launch_fd_qp<REP, true>(p, s) : launch_fd_qp<REP, false>(p, s);
+  if (!p.qkv_part) return launch_fd_qp<REP, 0>(p, s);
+  static_assert(kQkvPartMax == 16, "the partial-sum prologue takes 8 or 16 slices");
+  return p.qkv_S <= 8 ? launch_fd_qp<REP, 8>(p, s) : launch_fd_qp<REP, 16>(p, s);
 }
 
 int launch_attention_fd(const AttnParams& p, hipStream_t s) {
