@@ -319,6 +319,20 @@ int trx_model_set_tensor(trx_model* m, int role, int layer, const void* data, si
 int trx_model_synthesize(trx_model* m, uint32_t seed, const float* ranges);
 /* Clear the position, the argmax slot and the DeltaNet state (golden.py:304-320). */
 int trx_model_reset(trx_model* m);
+/* Checkpoint of the decode state, so that forwards can be run again from it: the firmware's
+ * forward_checked (firmware/infer.c:1926-1960), which re-runs a forward from the state that
+ * hybrid_ckpt_save kept (firmware/hybrid.c:2904-2930). TRX_CKPT_SAVE copies the state after the
+ * work enqueued so far (position, fed and generated tokens, argmax slot, sampler stream, every
+ * DeltaNet layer's conv window and recurrent matrix) into a buffer of the model (allocated on the
+ * first save: the DeltaNet state's size, 151 MB at the 27B hybrid's shape); TRX_CKPT_RESTORE
+ * enqueues the copy back, and the next forwards give the results they gave after the save. The KV
+ * rows are not copied: a forward writes its own position's row, so rows past the restored
+ * position are rewritten before they are read. Outputs of the last forward (logits, taps) are not
+ * state and are not restored. Asynchronous on the model's stream; TRX_E_STATE restores with no
+ * checkpoint saved. */
+#define TRX_CKPT_SAVE 0
+#define TRX_CKPT_RESTORE 1
+int trx_model_checkpoint(trx_model* m, int op);
 /* Feed tokens at the next n positions (after the forwards already enqueued); logits are computed
  * from absolute position head_from on (-1: the last fed token). */
 int trx_model_set_prompt(trx_model* m, const int32_t* tokens, int n, int head_from);

@@ -89,6 +89,7 @@ SIGNATURES = {
     "trx_model_set_sampling": [_vp, ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_uint32, _i],
     "trx_model_synthesize": [_vp, ctypes.c_uint32, _fp],
     "trx_model_reset": [_vp],
+    "trx_model_checkpoint": [_vp, _i],
     "trx_model_set_prompt": [_vp, _ip, _i, _i],
     "trx_model_step": [_vp, _i, _i],
     "trx_model_prefill": [_vp, _i, _i],

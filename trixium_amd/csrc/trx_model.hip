@@ -110,6 +110,12 @@ struct Model {
   int host_n_fed = 0, host_head_from = 0;          // host copies of the control words
   hipGraph_t graph = nullptr;
   hipGraphExec_t graph_exec = nullptr;
+  // Decode-state checkpoint (trx_model_checkpoint): device copy of the control words, the argmax
+  // slot, the sampler and the DeltaNet state; host copies of the host mirrors.
+  uint8_t* ckpt = nullptr;
+  size_t ckpt_bytes = 0;
+  bool ckpt_valid = false;
+  int ck_pos = -1, ck_n_fed = 0, ck_head_from = 0;
   size_t dev_bytes = 0;
   std::vector<void*> allocs;
 
@@ -1230,6 +1236,69 @@ TRX_API int trx_model_reset(trx_model* h) {
     TRX_HIP(hipMemsetAsync(m.dn_state, 0, (size_t)m.n_dn * nvh * c.dn_k_head_dim * 4, m.stream));
   }
   TRX_HIP(hipStreamSynchronize(m.stream));
+  return TRX_OK;
+}
+
+// The device regions a forward reads and rewrites from one position to the next: the control words
+// with the fed and generated tokens, the argmax slot, the sampler's settings, stream and candidates,
+// and every DeltaNet layer's conv window and recurrent matrix. The KV rows are not among them: a
+// forward appends the row of its own position, so rows past a restored position are written again
+// before any forward reads them.
+struct StateRegion {
+  void* p;
+  size_t bytes;
+};
+static std::vector<StateRegion> state_regions(Model& m) {
+  const trx_model_config& c = m.cfg;
+  std::vector<StateRegion> r = {{m.ctl, (size_t)(8 + c.max_ctx + c.max_new) * 4},
+                                {m.slot, 8},
+                                {m.smp, 16},
+                                {m.smp_cand, 33 * 8}};
+  if (m.n_dn) {
+    const int nq = c.dn_num_k_heads * c.dn_k_head_dim, nvh = c.dn_num_v_heads * c.dn_v_head_dim;
+    r.push_back({m.conv_state, (size_t)m.n_dn * (c.dn_conv_kernel - 1) * (2 * nq + nvh) * 4});
+    r.push_back({m.dn_state, (size_t)m.n_dn * nvh * c.dn_k_head_dim * 4});
+  }
+  return r;
+}
+
+TRX_API int trx_model_checkpoint(trx_model* h, int op) {
+  // firmware/infer.c:1926-1960 forward_checked with hybrid.c:2904-2930 hybrid_ckpt_save/restore:
+  // save the state after the forwards enqueued so far; restore puts it back, so the next forwards
+  // run again from there and give the same results.
+  TRX_CHECK(h && (op == TRX_CKPT_SAVE || op == TRX_CKPT_RESTORE), TRX_E_INVALID,
+            "trx_model_checkpoint: bad arguments");
+  Model& m = h->m;
+  const std::vector<StateRegion> regs = state_regions(m);
+  size_t total = 0;
+  for (const StateRegion& s : regs) total += (s.bytes + 255) / 256 * 256;
+  if (op == TRX_CKPT_SAVE) {
+    if (!m.ckpt) {
+      int rc;
+      if ((rc = dalloc(m, (void**)&m.ckpt, total))) return rc;
+      m.ckpt_bytes = total;
+    }
+    TRX_CHECK(m.ckpt_bytes == total, TRX_E_STATE, "trx_model_checkpoint: state size changed");
+    size_t off = 0;
+    for (const StateRegion& s : regs) {
+      TRX_HIP(hipMemcpyAsync(m.ckpt + off, s.p, s.bytes, hipMemcpyDeviceToDevice, m.stream));
+      off += (s.bytes + 255) / 256 * 256;
+    }
+    m.ck_pos = m.host_pos;
+    m.ck_n_fed = m.host_n_fed;
+    m.ck_head_from = m.host_head_from;
+    m.ckpt_valid = true;
+    return TRX_OK;
+  }
+  TRX_CHECK(m.ckpt_valid, TRX_E_STATE, "trx_model_checkpoint: no checkpoint saved");
+  size_t off = 0;
+  for (const StateRegion& s : regs) {
+    TRX_HIP(hipMemcpyAsync(s.p, m.ckpt + off, s.bytes, hipMemcpyDeviceToDevice, m.stream));
+    off += (s.bytes + 255) / 256 * 256;
+  }
+  m.host_pos = m.ck_pos;
+  m.host_n_fed = m.ck_n_fed;
+  m.host_head_from = m.ck_head_from;
   return TRX_OK;
 }
 

@@ -31,6 +31,7 @@ f32 = np.float32
 # Projections run by the packed GEMV (TRX_PACK_* bits; PACK_AUTO lets the library choose).
 PACK_QKV, PACK_O, PACK_GATE_UP, PACK_DOWN, PACK_HEAD, PACK_DN = 1, 2, 4, 8, 16, 32
 PACK_ALL, PACK_AUTO = 63, -1
+CKPT_SAVE, CKPT_RESTORE = 0, 1
 
 # Ranges of the counter-based synthetic weights (the ternary group scales and the RMSNorm gains).
 SYNTH_SCALE = (0.01, 0.05)
@@ -283,6 +284,18 @@ class Decoder:
     # State and decoding ------------------------------------------------------------------------
     def reset(self):
         _lib.call("trx_model_reset", self._h)
+
+    def checkpoint(self):
+        """Save the decode state after the work enqueued so far (position, fed and generated
+        tokens, argmax slot, sampler stream, DeltaNet conv windows and recurrent state), as the
+        firmware's hybrid_ckpt_save does before a forward it may run again
+        (firmware/hybrid.c:2904-2930, infer.c:1926-1960 forward_checked)."""
+        _lib.call("trx_model_checkpoint", self._h, CKPT_SAVE)
+
+    def restore(self):
+        """Put the last checkpoint's state back: the next forwards give the results they gave
+        after checkpoint() (KV rows past the position are rewritten before they are read)."""
+        _lib.call("trx_model_checkpoint", self._h, CKPT_RESTORE)
 
     def feed(self, tokens, head_from=-1):
         """Queue tokens for the next len(tokens) positions; the forwards run on step()."""
