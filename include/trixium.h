@@ -333,6 +333,17 @@ int trx_model_reset(trx_model* m);
 #define TRX_CKPT_SAVE 0
 #define TRX_CKPT_RESTORE 1
 int trx_model_checkpoint(trx_model* m, int op);
+/* KV ring past the window (firmware/hybrid.c:156-181, the console's `kvring` and hybrid_set_pin):
+ * with the ring on, forwards go on past max_ctx. Position p < max_ctx keeps KV slot p; past it the
+ * first `pin` positions stay (at least 4 sinks, at most max_ctx / 4) and position p takes slot
+ * pin + (p - pin) % (max_ctx - pin), so the attention reads every slot: the pinned positions and
+ * the most recent max_ctx - pin, K rotated at their own positions. enable: 1 on, 0 off, -1 the
+ * default (on for a model with DeltaNet layers, as the firmware's hybrid; off otherwise, which
+ * stops at max_ctx as the firmware's Qwen3 loop does). Both take effect at the next reset, and the
+ * pin lasts one reset (then 4 again); the ring stays off where max_ctx <= 2 pin. A model whose
+ * image carries a RoPE table (no rows past max_ctx) cannot turn it on: TRX_E_INVALID. Positions
+ * past the window run one position per forward (trx_model_prefill steps them). */
+int trx_model_set_kv_ring(trx_model* m, int enable, int pin);
 /* Feed tokens at the next n positions (after the forwards already enqueued); logits are computed
  * from absolute position head_from on (-1: the last fed token). */
 int trx_model_set_prompt(trx_model* m, const int32_t* tokens, int n, int head_from);
@@ -383,6 +394,8 @@ int trx_model_project_head(trx_model* m, const float* hidden, int n, float* logi
 #define TRX_INFO_ATTN_PASS 7      /* decode attention: positions one pass of a split block covers
                                      (a split of c positions takes ceil(c / this) passes) */
 #define TRX_INFO_TABLE_FREE_OPS 8 /* TRX_PACK_* bits on the table-free lookups */
+#define TRX_INFO_KV_PIN 9         /* positions the KV ring keeps past the window since the last
+                                     reset (0: no ring, forwards stop at max_ctx) */
 int trx_model_info(trx_model* m, int what, int64_t* value);
 /* Device address and size of one resident tensor (for benchmarks and tests). */
 int trx_model_tensor_ptr(trx_model* m, int role, int layer, void** ptr, int64_t* bytes);

@@ -20,6 +20,9 @@ f32 = np.float32
 
 
 class FloatRef:
+    # KV ring past the window (set_kv_ring): off unless asked for.
+    ring_cap, ring_pin_next, ring_window, kv_pin = None, 4, False, 0
+
     def __init__(self, img, kv_fp16=False):
         self.img = img
         h = self.h = img.header
@@ -138,7 +141,20 @@ class FloatRef:
         return np.where(x > 20, x, np.log1p(np.exp(np.minimum(x, 20)))).astype(f32)
 
     # State (golden.py:304-320) ---------------------------------------------------------------
+    def set_kv_ring(self, ctx_cap, pin=4, window=False):
+        """From the next reset: keep ctx_cap KV slots per layer, past them the first `pin`
+        positions (4 to ctx_cap // 4, firmware/hybrid.c:1148-1149) and a ring of the most recent
+        ones in the rest (kv_slot, hybrid.c:176-181), every slot attended (hybrid.c:2483); the ring
+        only where ctx_cap > 2 pin (kv_ring_on, hybrid.c:170-173). ctx_cap None: no ring.
+        window=True keeps every row instead and attends the positions the ring keeps, [0, pin) and
+        the last ctx_cap - pin (the ring's specification, for checking it)."""
+        self.ring_cap, self.ring_pin_next, self.ring_window = ctx_cap, pin, window
+
     def reset(self):
+        self.kv_pin = 0
+        if self.ring_cap is not None:
+            pin = max(4, min(self.ring_pin_next, self.ring_cap // 4))
+            self.kv_pin = pin if self.ring_cap > 2 * pin else 0
         self.pos = 0
         self.k_cache = {l: [] for l in range(self.n_layer) if not self.dn[l]}
         self.v_cache = {l: [] for l in range(self.n_layer) if not self.dn[l]}
@@ -185,10 +201,19 @@ class FloatRef:
         q = (q * f32(1.0 / np.sqrt(hd))).astype(f32)
         if self.kv_fp16:
             k, v = k.astype(np.float16).astype(f32), v.astype(np.float16).astype(f32)
-        self.k_cache[l].append(k)
-        self.v_cache[l].append(v)
+        cap, pin = self.ring_cap, self.kv_pin
+        if pin and pos >= cap and not self.ring_window:
+            slot = pin + (pos - pin) % (cap - pin)  # firmware/hybrid.c:176-181 kv_slot
+            self.k_cache[l][slot] = k
+            self.v_cache[l][slot] = v
+        else:
+            self.k_cache[l].append(k)
+            self.v_cache[l].append(v)
         Kc = np.stack(self.k_cache[l])             # [T, nkv, hd]
         Vc = np.stack(self.v_cache[l])
+        if pin and pos >= cap and self.ring_window:
+            keep = np.r_[0:pin, pos - (cap - pin) + 1:pos + 1]
+            Kc, Vc = Kc[keep], Vc[keep]
         rep = nh // nkv
         out = np.empty((nh, hd), f32)
         for h in range(nh):
@@ -392,8 +417,9 @@ class FloatRef:
         """Run `tokens` at the next len(tokens) positions as one teacher-forced sequence
         (fastref.py:244-258's whole-sequence form; the caches, conv windows and recurrent states
         end as after that many step() calls). Returns the last position's logits when asked."""
-        X = np.stack([self.embed(int(t)) for t in tokens]).astype(f32)
         pos0 = self.pos
+        assert not (self.kv_pin and pos0 + len(tokens) > self.ring_cap), "past the KV window: step()"
+        X = np.stack([self.embed(int(t)) for t in tokens]).astype(f32)
         for l in range(self.n_layer):
             hn = self.rmsnorm(X, self.norm_attn[l])
             y = self.deltanet_many(l, hn) if self.dn[l] else self.attention_many(l, hn, pos0)

@@ -354,3 +354,45 @@ def test_restored_row_exact_pinned():
             assert np.all(np.abs(gf - got) <= 2.0 ** max(e, int(ef[0])) * 1.0001), (hb, t)
     m, e = ob.restored_row_exact(np.full(2, 0.5, np.float16), np.ones(256, np.uint8), np.ones(256, np.int64), 64)
     assert e == 0 and not m.any()
+
+
+def test_kv_ring_keeps_the_sinks_and_the_most_recent_positions(tiny_images, golden):
+    """The oracle's KV ring (firmware/hybrid.c:170-181 kv_slot, every slot attended) against its
+    specification: attention over the positions it keeps, [0, pin) and the last ctx_cap - pin, from
+    a full cache (the same set in another order: equal to float rounding); and, with a window the
+    sequence never leaves, the plain path exactly. A slot off by one keeps another position and
+    fails the first comparison."""
+    img = bons.BONSReader(tiny_images[("tiny-hybrid", True)])
+    toks = golden["prompt/tiny-hybrid"] + golden["fastref_tokens/tiny-hybrid"]
+    toks = (toks * 3)[:58]
+    cap, pin = 20, 5
+
+    def run(ring=None, window=False):
+        r = FloatRef(img, kv_fp16=True)
+        if ring:
+            r.set_kv_ring(*ring, window=window)
+        r.reset()
+        return r, np.stack([r.step(t) for t in toks])
+
+    r, ringed = run((cap, pin))
+    assert r.kv_pin == pin
+    assert all(len(r.k_cache[l]) == cap for l in r.k_cache)
+    _, windowed = run((cap, pin), window=True)
+    for i in range(len(toks)):
+        err = np.abs(ringed[i] - windowed[i]).max() / np.abs(windowed[i]).max()
+        assert err <= 1e-5, (i, err)
+    _, plain = run()
+    assert np.array_equal(ringed[:cap], plain[:cap])
+    assert np.abs(ringed[cap + 8:] - plain[cap + 8:]).max() > 1e-3   # the ring forgets positions
+    _, wide = run((len(toks), pin))
+    assert np.array_equal(wide, plain)
+
+
+def test_kv_ring_pin_is_clamped_as_the_firmware_clamps_it(tiny_images):
+    """hybrid.c:1148-1149: at least the 4 sinks, at most a quarter of the window; no ring where the
+    window holds at most twice the pin (kv_ring_on)."""
+    r = FloatRef(bons.BONSReader(tiny_images[("tiny-hybrid", True)]))
+    for cap, want_pin, got in ((64, 100, 16), (64, 0, 4), (64, 9, 9), (8, 4, 0), (9, 4, 4)):
+        r.set_kv_ring(cap, want_pin)
+        r.reset()
+        assert r.kv_pin == got, (cap, want_pin, r.kv_pin)

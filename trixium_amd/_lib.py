@@ -90,6 +90,7 @@ SIGNATURES = {
     "trx_model_synthesize": [_vp, ctypes.c_uint32, _fp],
     "trx_model_reset": [_vp],
     "trx_model_checkpoint": [_vp, _i],
+    "trx_model_set_kv_ring": [_vp, _i, _i],
     "trx_model_set_prompt": [_vp, _ip, _i, _i],
     "trx_model_step": [_vp, _i, _i],
     "trx_model_prefill": [_vp, _i, _i],

@@ -53,12 +53,14 @@ __device__ __forceinline__ void attn_split_body(const AttnParams& p, int bid, Wa
   const int S = p.n_split;
   const int g = bid / S, sp = bid - g * S;
   const bool active = g < p.n_kv;
-  const int pos = *p.pos, T = pos + 1;
+  // The position (RoPE), the KV slot its k and v go to, and the T slots attended (the position
+  // and pos + 1 inside the window, the KV ring's slot and every slot past it).
+  const int pos = p.pos[0], slot = p.pos[5], T = p.pos[6];
   const int chunk = (T + S - 1) / S;
   const int p0 = sp * chunk, p1 = min(T, p0 + chunk), n = active ? max(0, p1 - p0) : 0;
   const int qstride = p.gated ? 2 * HD : HD;
   const size_t cache0 = (size_t)g * p.max_ctx * HD;
-  const bool owner = n > 0 && pos >= p0 && pos < p1;
+  const bool owner = n > 0 && slot >= p0 && slot < p1;
   const int li = lane % LPP, sub = lane / LPP;
   const int npass = (n + PPP - 1) / PPP;
 
@@ -68,7 +70,7 @@ __device__ __forceinline__ void attn_split_body(const AttnParams& p, int bid, Wa
 #pragma unroll
   for (int ps = 0; ps < kMaxPass; ++ps) {
     const int t = ps * PPP + wave * PPW + sub;
-    if (worker && ps < npass && t < n && p0 + t != pos) {
+    if (worker && ps < npass && t < n && p0 + t != slot) {
       const size_t off = cache0 + (size_t)(p0 + t) * HD + li * 8;
       kr[ps] = *(const uint4*)(p.kcache + off);
       vr[ps] = *(const uint4*)(p.vcache + off);
@@ -146,8 +148,8 @@ __device__ __forceinline__ void attn_split_body(const AttnParams& p, int bid, Wa
     __syncthreads();
     if (owner && tid < HD) {
       const __half kh = __float2half(hv[REP][tid]), vh = __float2half(hv[REP + 1][tid]);
-      p.kcache[cache0 + (size_t)pos * HD + tid] = kh;
-      p.vcache[cache0 + (size_t)pos * HD + tid] = vh;
+      p.kcache[cache0 + (size_t)slot * HD + tid] = kh;
+      p.vcache[cache0 + (size_t)slot * HD + tid] = vh;
       hv[REP][tid] = __half2float(kh);
       hv[REP + 1][tid] = __half2float(vh);
     }
@@ -164,7 +166,7 @@ __device__ __forceinline__ void attn_split_body(const AttnParams& p, int bid, Wa
         if (ps >= npass) break;
         const int t = ps * PPP + wave * PPW + sub;
         float kv[8];
-        if (owner && p0 + t == pos) {
+        if (owner && p0 + t == slot) {
 #pragma unroll
           for (int k = 0; k < 8; ++k) kv[k] = hv[REP][li * 8 + k];
         } else {
@@ -216,7 +218,7 @@ __device__ __forceinline__ void attn_split_body(const AttnParams& p, int bid, Wa
         const int t = ps * PPP + wave * PPW + sub;
         if (t >= n) continue;
         float v[8];
-        if (owner && p0 + t == pos) {
+        if (owner && p0 + t == slot) {
 #pragma unroll
           for (int k = 0; k < 8; ++k) v[k] = hv[REP + 1][li * 8 + k];
         } else {
@@ -272,7 +274,7 @@ __device__ __forceinline__ void attn_merge_body(const AttnParams& p, int qh) {
   __shared__ float wsp[kMaxSplits];
   const int tid = threadIdx.x;
   const int S = p.n_split, hd = p.hd;
-  const int T = *p.pos + 1;
+  const int T = p.pos[6];                               // KV slots attended
   const int chunk = (T + S - 1) / S;
   const int ns = min(S, (T + chunk - 1) / chunk);      // splits holding positions
   const float* pm = p.part_m + (size_t)qh * S;

@@ -70,9 +70,9 @@ __global__ __launch_bounds__(kFdThreads) void attn_fd_kernel(AttnParams p) {
   constexpr int RW = HD / 4, NQE = (REP + 2) * RW;
   constexpr int SPQ = (NQE + kFdThreads - 1) / kFdThreads;
   constexpr int NPS = QP ? QPS : 1;
-  // With QP the position is read first: a scalar load, which the memory barrier below would
-  // otherwise turn into a vector load queued behind the partial sums.
-  const int pos_qp = QP ? *p.pos : 0;
+  // With QP the control words are read first: scalar loads, which the memory barrier below would
+  // otherwise turn into vector loads queued behind the partial sums.
+  const int pos_qp = QP ? p.pos[0] : 0, slot_qp = QP ? p.pos[5] : 0, T_qp = QP ? p.pos[6] : 0;
   float4 sv[QP ? SPQ : SPT];
   float4 pv[QP ? SPQ : 1][NPS];
   float ssl = 0.f;
@@ -117,10 +117,13 @@ __global__ __launch_bounds__(kFdThreads) void attn_fd_kernel(AttnParams p) {
     }
   }
 
-  const int pos = QP ? pos_qp : *p.pos, T = pos + 1;
+  // The position (for RoPE), the KV slot its k and v go to and the T slots attended: the slot is
+  // the position and T = pos + 1 inside the window, the KV ring's past it.
+  const int pos = QP ? pos_qp : p.pos[0], slot = QP ? slot_qp : p.pos[5], T = QP ? T_qp : p.pos[6];
+  const int rrow = min(pos, p.max_ctx);               // the fp32 table's row of the position
   const int chunk = (T + S - 1) / S;
   const int p0 = sp * chunk, p1 = min(T, p0 + chunk), n = max(0, p1 - p0);
-  const bool owner = n > 0 && pos >= p0 && pos < p1;
+  const bool owner = n > 0 && slot >= p0 && slot < p1;
   const int npass = (n + PPP - 1) / PPP;
 
   // The RoPE cos/sin at pos, from the model's table (fp32, or the image's Q14 rows), loaded
@@ -140,8 +143,8 @@ __global__ __launch_bounds__(kFdThreads) void attn_fd_kernel(AttnParams p) {
         rc[i] = (float)p.rope_tab[(size_t)pos * p.rope_n + ri] * (1.0f / 16384.0f);
         rsn[i] = (float)p.rope_tab[(size_t)pos * p.rope_n + half + ri] * (1.0f / 16384.0f);
       } else {
-        rc[i] = p.rope_cs[(size_t)pos * p.rope_n + ri];
-        rsn[i] = p.rope_cs[(size_t)pos * p.rope_n + half + ri];
+        rc[i] = p.rope_cs[(size_t)rrow * p.rope_n + ri];
+        rsn[i] = p.rope_cs[(size_t)rrow * p.rope_n + half + ri];
       }
     }
   }
@@ -159,7 +162,7 @@ __global__ __launch_bounds__(kFdThreads) void attn_fd_kernel(AttnParams p) {
 #pragma unroll
   for (int ps = 0; ps < kMaxPass; ++ps) {
     const int t = ps * PPP + grp;
-    const bool ok = ps < npass && t < n && p0 + t != pos;
+    const bool ok = ps < npass && t < n && p0 + t != slot;
     const uint32_t off = ok ? ((uint32_t)(p0 + t) * HD + li * 8) * 2u : kOut;
     const auto a = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0);
     const auto b = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0);
@@ -219,7 +222,7 @@ __global__ __launch_bounds__(kFdThreads) void attn_fd_kernel(AttnParams p) {
           for (int i = 0; i < 4; ++i) h[i] = __float2half(src[i]);
           *(float4*)&stg[row][d] = make_float4(__half2float(h[0]), __half2float(h[1]), __half2float(h[2]), __half2float(h[3]));
           if (owner) {
-            __half* dst = (row == REP ? p.kcache : p.vcache) + cache0 + (size_t)pos * HD + d;
+            __half* dst = (row == REP ? p.kcache : p.vcache) + cache0 + (size_t)slot * HD + d;
             *(uint2*)dst = make_uint2(__builtin_bit_cast(uint32_t, __halves2half2(h[0], h[1])),
                                       __builtin_bit_cast(uint32_t, __halves2half2(h[2], h[3])));
           }
@@ -271,8 +274,8 @@ __global__ __launch_bounds__(kFdThreads) void attn_fd_kernel(AttnParams p) {
             stg[REP][d] = __half2float(kh);
             stg[REP + 1][d] = __half2float(vh);
             if (owner) {
-              p.kcache[cache0 + (size_t)pos * HD + d] = kh;
-              p.vcache[cache0 + (size_t)pos * HD + d] = vh;
+              p.kcache[cache0 + (size_t)slot * HD + d] = kh;
+              p.vcache[cache0 + (size_t)slot * HD + d] = vh;
             }
           }
         }
@@ -296,7 +299,7 @@ __global__ __launch_bounds__(kFdThreads) void attn_fd_kernel(AttnParams p) {
       if (ps >= npass) continue;
       const int t = ps * PPP + grp;
       float kv[8];
-      if (owner && p0 + t == pos) {
+      if (owner && p0 + t == slot) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) kv[k] = kn[k];
       } else {
@@ -327,7 +330,7 @@ __global__ __launch_bounds__(kFdThreads) void attn_fd_kernel(AttnParams p) {
       const int t = ps * PPP + grp;
       if (t >= n) continue;
       float vv[8];
-      if (owner && p0 + t == pos) {
+      if (owner && p0 + t == slot) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) vv[k] = vn[k];
       } else {

@@ -28,6 +28,11 @@ struct Tensor {
   bool loaded = false;
 };
 
+// Positions every KV ring keeps past the window at least (firmware/hybrid.c:161 KV_SINKS), and the
+// sampler's repetition window (the last 64 tokens, firmware/infer.c:385-488).
+constexpr int kKvSinks = 4;
+constexpr int kSmpWindow = 64;
+
 // Projections that can run on the packed GEMV (trx_tgemv.h), keyed with their layer.
 enum PackedOp { OP_QKV, OP_O, OP_GATE_UP, OP_DOWN, OP_HEAD, OP_DN_QKVZ, OP_DN_OUT };
 
@@ -53,9 +58,11 @@ struct Model {
   float *part_m = nullptr, *part_l = nullptr, *part_o = nullptr;
   unsigned* attn_done = nullptr;                   // [n_kv] split counters (one-launch attention)
   float *dn_io = nullptr, *dn_ba = nullptr, *dn_out = nullptr, *rope_dev = nullptr;
-  float* rope_cs = nullptr;                        // [max_ctx][rope_n]: cos(pos f_i), then sin
-  int* ctl = nullptr;  // [0] pos, [1] n_fed, [2] cur_tok, [3] head_from, [4] error, [8..] fed tokens by
-                       // absolute position (max_ctx), then the generated tokens (max_new)
+  float* rope_cs = nullptr;                        // [max_ctx + 1][rope_n]: cos(pos f_i), then sin
+                                                   // (row max_ctx: the position past the window)
+  int* ctl = nullptr;  // [0] pos, [1] n_fed, [2] cur_tok, [3] head_from, [4] error, [5] the position's
+                       // KV slot, [6] KV slots attended, [7] KV ring pin (0: no ring), [8..] a ring
+                       // of fed tokens (prompt_ring), then the generated tokens (max_new)
   int host_pos = -1;   // host mirror of the device position after the enqueued steps
   unsigned long long* slot = nullptr;
   int n_attn = 0, n_dn = 0;
@@ -110,12 +117,19 @@ struct Model {
   int host_n_fed = 0, host_head_from = 0;          // host copies of the control words
   hipGraph_t graph = nullptr;
   hipGraphExec_t graph_exec = nullptr;
+  // KV ring past the window (trx_model_set_kv_ring; firmware/hybrid.c:156-181): enabled (1), off
+  // (0) or the default (-1: on for a model with DeltaNet layers), the pinned positions the next
+  // reset applies, and the pinned positions in effect since the last reset (0: no ring).
+  int kv_ring = -1;
+  int kv_pin_next = kKvSinks;
+  int kv_pin = 0;
+  int prompt_ring = 0;                             // fed tokens kept: position p at p % prompt_ring
   // Decode-state checkpoint (trx_model_checkpoint): device copy of the control words, the argmax
   // slot, the sampler and the DeltaNet state; host copies of the host mirrors.
   uint8_t* ckpt = nullptr;
   size_t ckpt_bytes = 0;
   bool ckpt_valid = false;
-  int ck_pos = -1, ck_n_fed = 0, ck_head_from = 0;
+  int ck_pos = -1, ck_n_fed = 0, ck_head_from = 0, ck_kv_pin = 0;
   size_t dev_bytes = 0;
   std::vector<void*> allocs;
 
@@ -125,7 +139,7 @@ struct Model {
   int* cur_tok() { return ctl + 2; }
   int* head_from() { return ctl + 3; }
   int* prompt() { return ctl + 8; }
-  int* out() { return ctl + 8 + cfg.max_ctx; }
+  int* out() { return ctl + 8 + prompt_ring; }
   int* err() { return ctl + 4; }                   // set by a kernel whose bounded wait timed out
 };
 
@@ -502,6 +516,11 @@ static int run_step(Model& m, hipStream_t s) {
   ep.pos = m.pos();
   ep.n_prompt = m.n_prompt();
   ep.prompt = m.prompt();
+  ep.prompt_ring = m.prompt_ring;
+  ep.max_ctx = c.max_ctx;
+  ep.rope_cs = m.rope_cs;
+  ep.rope_freq = m.rope_dev;
+  ep.rope_n = c.rope_dims ? c.rope_dims : c.head_dim;
   ep.slot = m.slot;
   ep.out = m.out();
   ep.max_out = c.max_new;
@@ -765,9 +784,9 @@ static int run_step(Model& m, hipStream_t s) {
                           m.head_from()))) return rc;
   }
   if (m.sampling) {
-    SampleParams sp = {m.logits, c.vocab, m.smp_channels, 64, m.pos(), m.head_from(), m.n_prompt(), m.prompt(),
-                       m.out(), c.max_new, m.smp, (uint32_t*)(m.smp + 3), m.slot, m.smp_cand,
-                       (unsigned*)(m.smp_cand + 32)};
+    SampleParams sp = {m.logits, c.vocab, m.smp_channels, kSmpWindow, m.pos(), m.head_from(), m.n_prompt(),
+                       m.prompt(), m.out(), c.max_new, m.smp, (uint32_t*)(m.smp + 3), m.slot, m.smp_cand,
+                       (unsigned*)(m.smp_cand + 32), m.prompt_ring};
     if ((rc = launch_sample(sp, s))) return rc;
   }
   m.hidden = xc;
@@ -1091,8 +1110,9 @@ TRX_API int trx_model_create(const trx_model_config* cfg, const float* rope_freq
   if ((rc = dalloc(m, (void**)&m.part_o, (size_t)c.n_head * splits * hd * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.attn_done, (size_t)std::max(c.n_kv_head, 1) * kDoneStride * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.rope_dev, (size_t)rope_n * 4))) return fail(rc);
-  if ((rc = dalloc(m, (void**)&m.rope_cs, (size_t)c.max_ctx * rope_n * 4))) return fail(rc);
-  if ((rc = dalloc(m, (void**)&m.ctl, (size_t)(8 + c.max_ctx + c.max_new) * 4))) return fail(rc);
+  if ((rc = dalloc(m, (void**)&m.rope_cs, (size_t)(c.max_ctx + 1) * rope_n * 4))) return fail(rc);
+  m.prompt_ring = c.max_ctx + kSmpWindow;
+  if ((rc = dalloc(m, (void**)&m.ctl, (size_t)(8 + m.prompt_ring + c.max_new) * 4))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.slot, 8))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.smp, 16))) return fail(rc);
   if ((rc = dalloc(m, (void**)&m.smp_cand, 33 * 8))) return fail(rc);
@@ -1224,7 +1244,14 @@ TRX_API int trx_model_reset(trx_model* h) {
   TRX_CHECK(h, TRX_E_INVALID, "trx_model_reset: null");
   Model& m = h->m;
   const trx_model_config& c = m.cfg;
-  int init[8] = {-1, 0, 0, 0, 0, 0, 0, 0};
+  // The KV ring of this generation (firmware/hybrid.c:1148-1150): the pinned positions asked for,
+  // at least the sinks and at most a quarter of the window, and the ring only where the window holds
+  // more than twice them (kv_ring_on, hybrid.c:170-173). The request lasts one reset.
+  const bool ring = m.kv_ring > 0 || (m.kv_ring < 0 && m.n_dn > 0);
+  const int pin = std::max(kKvSinks, std::min(m.kv_pin_next, c.max_ctx / 4));
+  m.kv_pin = ring && !c.rope_table && c.max_ctx > 2 * pin ? pin : 0;
+  m.kv_pin_next = kKvSinks;
+  int init[8] = {-1, 0, 0, 0, 0, -1, 0, m.kv_pin};
   m.host_pos = -1;
   m.host_n_fed = 0;
   m.host_head_from = 0;
@@ -1250,7 +1277,7 @@ struct StateRegion {
 };
 static std::vector<StateRegion> state_regions(Model& m) {
   const trx_model_config& c = m.cfg;
-  std::vector<StateRegion> r = {{m.ctl, (size_t)(8 + c.max_ctx + c.max_new) * 4},
+  std::vector<StateRegion> r = {{m.ctl, (size_t)(8 + m.prompt_ring + c.max_new) * 4},
                                 {m.slot, 8},
                                 {m.smp, 16},
                                 {m.smp_cand, 33 * 8}};
@@ -1287,6 +1314,7 @@ TRX_API int trx_model_checkpoint(trx_model* h, int op) {
     m.ck_pos = m.host_pos;
     m.ck_n_fed = m.host_n_fed;
     m.ck_head_from = m.host_head_from;
+    m.ck_kv_pin = m.kv_pin;
     m.ckpt_valid = true;
     return TRX_OK;
   }
@@ -1299,6 +1327,19 @@ TRX_API int trx_model_checkpoint(trx_model* h, int op) {
   m.host_pos = m.ck_pos;
   m.host_n_fed = m.ck_n_fed;
   m.host_head_from = m.ck_head_from;
+  m.kv_pin = m.ck_kv_pin;
+  return TRX_OK;
+}
+
+TRX_API int trx_model_set_kv_ring(trx_model* h, int enable, int pin) {
+  // The console's `kvring on|off` and hybrid_set_pin (firmware/hybrid.c:156-168): both take effect
+  // at the next reset.
+  TRX_CHECK(h && enable >= -1 && enable <= 1 && pin >= 0, TRX_E_INVALID, "trx_model_set_kv_ring: bad arguments");
+  Model& m = h->m;
+  TRX_CHECK(enable <= 0 || !m.cfg.rope_table, TRX_E_INVALID,
+            "trx_model_set_kv_ring: the image's RoPE table has no rows past max_ctx");
+  m.kv_ring = enable;
+  m.kv_pin_next = pin;
   return TRX_OK;
 }
 
@@ -1314,12 +1355,18 @@ TRX_API int trx_model_set_prompt(trx_model* h, const int32_t* tokens, int n, int
   TRX_CHECK(h && tokens && n > 0, TRX_E_INVALID, "trx_model_set_prompt: bad arguments");
   Model& m = h->m;
   const int first = m.host_pos + 1;
-  TRX_CHECK(first + n <= m.cfg.max_ctx, TRX_E_STATE, "%d tokens after position %d exceed max_ctx %d", n,
-            m.host_pos, m.cfg.max_ctx);
+  // With the KV ring the positions go on past the window; a call feeds at most a window's worth.
+  TRX_CHECK(m.kv_pin > 0 ? n <= m.cfg.max_ctx : first + n <= m.cfg.max_ctx, TRX_E_STATE,
+            "%d tokens after position %d exceed max_ctx %d", n, m.host_pos, m.cfg.max_ctx);
   for (int i = 0; i < n; ++i)
     TRX_CHECK(tokens[i] >= 0 && tokens[i] < m.cfg.vocab, TRX_E_INVALID, "token %d out of range", tokens[i]);
   const int n_fed = first + n, hf = head_from < 0 ? first + n - 1 : head_from;
-  TRX_HIP(hipMemcpyAsync(m.prompt() + first, tokens, (size_t)n * 4, hipMemcpyHostToDevice, m.stream));
+  // The fed tokens' ring holds max_ctx + 64 positions: n <= max_ctx new ones leave the 64 before
+  // them, which the sampler's repetition window reads, in place.
+  const int i0 = first % m.prompt_ring, n1 = std::min(n, m.prompt_ring - i0);
+  TRX_HIP(hipMemcpyAsync(m.prompt() + i0, tokens, (size_t)n1 * 4, hipMemcpyHostToDevice, m.stream));
+  if (n1 < n)
+    TRX_HIP(hipMemcpyAsync(m.prompt(), tokens + n1, (size_t)(n - n1) * 4, hipMemcpyHostToDevice, m.stream));
   TRX_HIP(hipMemcpyAsync(m.ctl + 1, &n_fed, 4, hipMemcpyHostToDevice, m.stream));
   TRX_HIP(hipMemcpyAsync(m.ctl + 3, &hf, 4, hipMemcpyHostToDevice, m.stream));
   TRX_HIP(hipStreamSynchronize(m.stream));
@@ -1344,8 +1391,8 @@ TRX_API int trx_model_step(trx_model* h, int n_steps, int use_graph) {
     m.graph = g;
     TRX_HIP(hipGraphInstantiate(&m.graph_exec, m.graph, nullptr, nullptr, 0));
   }
-  TRX_CHECK(m.host_pos + n_steps < m.cfg.max_ctx, TRX_E_STATE, "%d steps after position %d exceed max_ctx %d",
-            n_steps, m.host_pos, m.cfg.max_ctx);
+  TRX_CHECK(m.kv_pin > 0 || m.host_pos + n_steps < m.cfg.max_ctx, TRX_E_STATE,
+            "%d steps after position %d exceed max_ctx %d", n_steps, m.host_pos, m.cfg.max_ctx);
   for (int i = 0; i < n_steps; ++i) {
     ++m.host_pos;
     if (use_graph) {
@@ -1369,14 +1416,19 @@ TRX_API int trx_model_prefill(trx_model* h, int n, int chunk) {
             "trx_model_prefill: position %d computes logits (head_from %d); step it instead", first + n - 1,
             m.host_head_from);
   if (n == 0) return TRX_OK;
-  if (chunk <= 0) chunk = 1024;
-  chunk = std::min(chunk, n);
-  if ((rc = pf_alloc(m, chunk))) return rc;
-  for (int p0 = first; p0 < first + n; p0 += chunk) {
-    const int R = std::min(chunk, first + n - p0);
-    if ((rc = run_prefill(m, p0, R, m.stream))) return rc;
+  // Positions past the window (the KV ring) run one forward each.
+  const int n_in = std::max(0, std::min(n, m.cfg.max_ctx - first));
+  if (n_in > 0) {
+    if (chunk <= 0) chunk = 1024;
+    chunk = std::min(chunk, n_in);
+    if ((rc = pf_alloc(m, chunk))) return rc;
+    for (int p0 = first; p0 < first + n_in; p0 += chunk) {
+      const int R = std::min(chunk, first + n_in - p0);
+      if ((rc = run_prefill(m, p0, R, m.stream))) return rc;
+    }
+    m.host_pos = first + n_in - 1;
   }
-  m.host_pos = first + n - 1;
+  if (n_in < n) return trx_model_step(h, n - n_in, m.graph_exec != nullptr);
   return TRX_OK;
 }
 
@@ -1410,10 +1462,10 @@ TRX_API int trx_model_generate(trx_model* h, const int32_t* prompt, int n_prompt
   Model& m = h->m;
   TRX_CHECK(n_new <= m.cfg.max_new, TRX_E_INVALID, "n_new %d exceeds max_new %d", n_new, m.cfg.max_new);
   TRX_CHECK(n_prompt <= m.cfg.max_ctx, TRX_E_INVALID, "prompt of %d tokens exceeds max_ctx", n_prompt);
-  TRX_CHECK(n_prompt + n_new - 1 <= m.cfg.max_ctx, TRX_E_STATE, "context of %d positions exceeds max_ctx %d",
-            n_prompt + n_new - 1, m.cfg.max_ctx);
   int rc;
   if ((rc = trx_model_reset(h))) return rc;
+  TRX_CHECK(m.kv_pin > 0 || n_prompt + n_new - 1 <= m.cfg.max_ctx, TRX_E_STATE,
+            "context of %d positions exceeds max_ctx %d", n_prompt + n_new - 1, m.cfg.max_ctx);
   if ((rc = trx_model_set_prompt(h, prompt, n_prompt, -1))) return rc;
   const int pre = m.cfg.prefill_chunk > 0 ? n_prompt - 1 : 0;
   if (pre && (rc = trx_model_prefill(h, pre, m.cfg.prefill_chunk))) return rc;
@@ -1538,6 +1590,7 @@ TRX_API int trx_model_info(trx_model* h, int what, int64_t* value) {
     case TRX_INFO_ATTN_SPLITS: *value = m.n_split; break;
     case TRX_INFO_ATTN_PASS: *value = attention_pass_positions(m.cfg.head_dim); break;
     case TRX_INFO_TABLE_FREE_OPS: *value = m.tf_ops; break;
+    case TRX_INFO_KV_PIN: *value = m.kv_pin; break;
     case TRX_INFO_PACKED_OPS: *value = m.packed_ops; break;
     case TRX_INFO_WEIGHT_BYTES: {
       int64_t s = 0;

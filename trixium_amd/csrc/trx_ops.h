@@ -14,9 +14,16 @@ struct EmbedParams {
   const int32_t* exps;     // table mode: [vocab]
   const uint8_t* rows;     // ternary mode: row packets of token_embd
   int kind, row_bytes, code_off;
-  int* pos;                // device: position of the current token (incremented here)
+  int* pos;                // device control words: [0] position of the current token
+                           // (incremented here), [5] its KV slot, [6] KV slots attended, [7] the
+                           // KV ring's pinned positions (0: no ring)
   const int* n_prompt;     // device
-  const int* prompt;       // device [n_prompt]
+  const int* prompt;       // device ring of prompt_ring fed tokens (position p at p % prompt_ring)
+  int prompt_ring;
+  int max_ctx;             // KV slots; past them (the ring) the position's RoPE row is computed
+  float* rope_cs;          // into row max_ctx of this fp32 cos|sin table (may be null)
+  const float* rope_freq;  // [rope_n / 2]
+  int rope_n;
   unsigned long long* slot;  // argmax of the previous step (cleared here)
   int* out;                // generated tokens [max_out]
   int max_out;
@@ -32,8 +39,9 @@ struct AttnParams {
   const float* k_norm;
   const float* rope_freq;  // [rope_n/2]
   const int16_t* rope_tab; // or [max_ctx][rope_n] Q14: cos half, then sin half (null: rope_freq)
-  const float* rope_cs;    // [max_ctx][rope_n] fp32 cos half, then sin half (the one-launch kernel)
-  const int* pos;
+  const float* rope_cs;    // [max_ctx + 1][rope_n] fp32 cos half, then sin half (the one-launch
+                           // kernel; row max_ctx: the current position's, past the KV slots)
+  const int* pos;          // control words: [0] position, [5] its KV slot, [6] KV slots attended
   __half* kcache;          // [n_kv][max_ctx][hd]
   __half* vcache;
   float* part_m;           // [n_head][n_split]
@@ -124,7 +132,7 @@ struct SampleParams {
   const int* pos;
   const int* head_from;
   const int* n_prompt;
-  const int* prompt;
+  const int* prompt;       // ring of prompt_ring fed tokens
   const int* out;
   int max_out;
   const float* cfg;        // temperature, top_p, repetition
@@ -132,6 +140,7 @@ struct SampleParams {
   unsigned long long* slot;
   unsigned long long* cand;  // [32] the slices' (value bits, token) between the blocks
   unsigned* done;            // blocks finished (zero between launches)
+  int prompt_ring;           // the fed tokens' ring: position p at prompt[p % prompt_ring]
 };
 
 // The final normed hidden state and the sequence score of one position (model/fastref.py:244-273:

@@ -198,17 +198,29 @@ __device__ void embed_token(const EmbedParams& p, int tok, float* x) {
 }
 
 __global__ __launch_bounds__(kEmbedThreads) void embed_kernel(EmbedParams p) {
-  __shared__ int s_tok;
+  __shared__ int s_tok, s_pos;
   const int tid = threadIdx.x;
   if (tid == 0) {
     // The control words are read together (one round trip), before the position is written.
-    const int pos0 = *p.pos, np = *p.n_prompt;
+    const int pos0 = *p.pos, np = *p.n_prompt, pin = p.pos[7];
     const unsigned long long key = *p.slot;
     const int pos = pos0 + 1;
     *p.pos = pos;
+    // The position's KV slot and the slots the attention reads (firmware/hybrid.c:170-181,2483):
+    // inside the window the position itself and pos + 1 slots; past it, with the ring on (pin > 0),
+    // the first pin positions stay and the others share the rest of the window as a ring, all
+    // max_ctx slots attended.
+    int slot = pos, nslots = pos + 1;
+    if (pos >= p.max_ctx && pin > 0) {
+      slot = pin + (pos - pin) % (p.max_ctx - pin);
+      nslots = p.max_ctx;
+    }
+    p.pos[5] = slot;
+    p.pos[6] = nslots;
+    s_pos = pos;
     int tok;
     if (pos < np) {
-      tok = p.prompt[pos];
+      tok = p.prompt[pos % p.prompt_ring];
     } else {
       tok = slot_token(key);
       const int k = pos - np;
@@ -220,6 +232,15 @@ __global__ __launch_bounds__(kEmbedThreads) void embed_kernel(EmbedParams p) {
     s_tok = tok;
   }
   __syncthreads();
+  // Past the window the RoPE table has no row for the position: row max_ctx gets its cos and sin
+  // of the float32 angle pos * f_i, evaluated in double and rounded once (as the table's rows).
+  const int pos = s_pos, half = p.rope_n / 2;
+  if (pos >= p.max_ctx && p.rope_cs && tid < half) {
+    const double ang = (double)((float)pos * p.rope_freq[tid]);
+    float* row = p.rope_cs + (size_t)p.max_ctx * p.rope_n;
+    row[tid] = (float)cos(ang);
+    row[half + tid] = (float)sin(ang);
+  }
   embed_token(p, s_tok, p.x);
 }
 
@@ -457,7 +478,7 @@ __global__ __launch_bounds__(1024) void sample_kernel(SampleParams p) {
     seen[t] = 0;
   } else if (t >= 64 && t - 64 < nwin) {
     const int j = j0 + t - 64, g = j - np;   // position j: a prompt token or generated token g
-    win[t - 64] = j < np ? p.prompt[j] : (g < p.max_out ? p.out[g] : -1);
+    win[t - 64] = j < np ? p.prompt[j % p.prompt_ring] : (g < p.max_out ? p.out[g] : -1);
   }
   __syncthreads();
   const float temp = p.cfg[0], top_p = p.cfg[1], rep = p.cfg[2];

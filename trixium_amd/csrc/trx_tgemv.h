@@ -70,7 +70,7 @@ struct AttnMergeSrc {
   const float* m;          // [n_head][n_split]
   const float* l;
   const float* o;          // [n_head][n_split][hd]
-  const int* pos;          // the position attended (splits of pos + 1 positions)
+  const int* pos;          // control words: [6] the KV slots attended (the splits' positions)
   int n_split, hd, gated;
   const float* qkv;        // gated: the gate after each q head
   float* out;              // [n_head * hd]

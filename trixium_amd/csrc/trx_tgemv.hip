@@ -473,14 +473,14 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
   const int cs = s * kSliceCols + tid;
   float xv = 0.f, wv = 1.f, ssin = 0.f;
   float4 pv[kSwiVec > kResVec ? (kSwiVec > kMergeVec ? kSwiVec : kMergeVec) : (kResVec > kMergeVec ? kResVec : kMergeVec)];
-  int h0 = 0, nh = 0, mpos = 0;
+  int h0 = 0, nh = 0, mT = 0;
   float mv = -INFINITY, lv = 0.f, sw0 = 0.f, sw1 = 0.f;
   if (xmode == kXMerge) {
     // The slice's attention output from the split partials: every split's o values and the
     // (m, l) of the slice's heads, none of which waits for the position (the splits holding
     // positions are known once it arrives, after the weight loads are issued).
     const AttnMergeSrc& a = p.merge;
-    mpos = *a.pos;
+    mT = a.pos[6];                                   // KV slots attended
     h0 = (s * kSliceCols) / a.hd;
     nh = kSliceCols / a.hd;
     // Thread t loads columns 4 (t % 64) .. + 3 of splits t / 64 and t / 64 + 16 (16 bytes each;
@@ -606,10 +606,10 @@ __global__ __launch_bounds__(kTgThreads, kTgBlocksPerCU) void tgemv_kernel(TgPar
 
   // 3. The slice's x (times the RMSNorm gain; 1/rms(x) scales the sums), then the table.
   if (xmode == kXMerge) {
-    // The splits holding positions (of pos + 1), their softmax weights per head, then each
+    // The splits holding positions (of the T slots attended), their softmax weights per head, then each
     // thread's two splits weighted, the 16 split groups summed through scr (in group order),
     // then scaled by the heads' 1 / L.
-    const int T = mpos + 1, chunk = (T + p.merge.n_split - 1) / p.merge.n_split;
+    const int T = mT, chunk = (T + p.merge.n_split - 1) / p.merge.n_split;
     const int ns = min(p.merge.n_split, (T + chunk - 1) / chunk);
     if (w < nh) {
       const bool ok = lane < ns && (h0 + w) * p.merge.hd < p.K;

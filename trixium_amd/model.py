@@ -26,7 +26,7 @@ f32 = np.float32
 (READ_LOGITS, READ_HIDDEN, READ_POSITION, READ_TOKEN, READ_OUT, READ_SLOT, READ_QKV, READ_ATTN, READ_ACT,
  READ_RESIDUAL) = range(10)
 (INFO_ARENA_BYTES, INFO_DEVICE_BYTES, INFO_STREAM, INFO_WEIGHT_BYTES, _INFO_UNUSED, INFO_PACKED_OPS, INFO_ATTN_SPLITS,
- INFO_ATTN_PASS, INFO_TABLE_FREE_OPS) = range(9)
+ INFO_ATTN_PASS, INFO_TABLE_FREE_OPS, INFO_KV_PIN) = range(10)
 
 # Projections run by the packed GEMV (TRX_PACK_* bits; PACK_AUTO lets the library choose).
 PACK_QKV, PACK_O, PACK_GATE_UP, PACK_DOWN, PACK_HEAD, PACK_DN = 1, 2, 4, 8, 16, 32
@@ -291,6 +291,18 @@ class Decoder:
         firmware's hybrid_ckpt_save does before a forward it may run again
         (firmware/hybrid.c:2904-2930, infer.c:1926-1960 forward_checked)."""
         _lib.call("trx_model_checkpoint", self._h, CKPT_SAVE)
+
+    def set_kv_ring(self, enable=-1, pin=4):
+        """The KV ring past max_ctx (firmware/hybrid.c:156-181, the console's `kvring` and
+        hybrid_set_pin), from the next reset on: the first `pin` positions stay (4 to max_ctx/4)
+        and the rest of the window is a ring of the most recent positions, so forwards go on past
+        max_ctx. enable: 1 on, 0 off, -1 the default (on for a model with DeltaNet layers)."""
+        _lib.call("trx_model_set_kv_ring", self._h, int(enable), int(pin))
+
+    @property
+    def kv_pin(self):
+        """Positions the KV ring keeps past the window since the last reset (0: no ring)."""
+        return self.info(INFO_KV_PIN)
 
     def restore(self):
         """Put the last checkpoint's state back: the next forwards give the results they gave
