@@ -28,7 +28,12 @@ Besides the JSON contract fields the line carries
                 same first token;
   matvec_microbench  the isolated ternary matvec at the Qwen3-1.7B layer shapes, trit5 and 2-bit,
                 over more than 512 MB of distinct matrix copies, at least 1000 matvecs per
-                shape: GB/s against 8 TB/s, with the exact integer group sums checked.
+                shape: GB/s against 8 TB/s, with the exact integer group sums checked;
+  other_shapes  the same decode loop at the Qwen3-1.7B shape (256 tokens after a 512-token
+                prompt) and the Qwen3.5-27B hybrid shape (128 tokens after a 1024-token prompt):
+                tok/s, the bytes-per-token roofline, time to first token, and the float oracle
+                timed on a sample of each shape (one layer of each kind, the LM head on a row
+                sample, scaled).
 """
 
 import argparse
@@ -63,6 +68,8 @@ def parse_args():
     ap.add_argument("--kernel-reps", type=int, default=10,
                     help="passes over the 36 layers when timing the dominant kernel")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-other-shapes", action="store_true",
+                    help="skip the Qwen3-1.7B and Qwen3.5-27B decode lines of the default run")
     ap.add_argument("--sampling", default=None, metavar="T,P,R",
                     help="sample with temperature T, top-p P and repetition penalty R instead of the "
                          "greedy argmax (the firmware's sampler; not the headline workload)")
@@ -544,6 +551,112 @@ def cpu_baseline(mc, ctx):
                        f"= {per_tok:.1f} s")}
 
 
+def cpu_shape_sample(mc, ctx, head_rows=16384):
+    """The float oracle's decode step at a shape, timed on a sample: one layer of each kind the
+    model has (full size, context ctx) and the LM head over head_rows of its rows, scaled to the
+    model's layer counts and vocabulary (a matvec's time is linear in its rows)."""
+    import dataclasses
+    from oracle.floatref import ShapeSample
+    small = dataclasses.replace(mc, vocab=head_rows)
+    kinds = ["attn"] + (["deltanet"] if mc.n_dn_layers else [])
+    per_kind, t_head = {}, []
+    for k in kinds:
+        s = ShapeSample(small, 1, ctx, seed=0, kinds=[k])
+        s.step(1)                               # first touch of every buffer
+        t0 = time.perf_counter()
+        s.step(2, want_logits=False)
+        per_kind[k] = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        s.step(3, want_logits=True)
+        t_head.append(max(time.perf_counter() - t0 - per_kind[k], 0.0))
+        del s
+    head = min(t_head) * mc.vocab / head_rows
+    n_dn = mc.n_dn_layers
+    per_tok = (mc.n_layer - n_dn) * per_kind["attn"] + n_dn * per_kind.get("deltanet", 0.0) + head
+    layers = " + ".join(f"{n} x {k} layer {per_kind[k]:.2f} s" for k, n in
+                        (("attn", mc.n_layer - n_dn), ("deltanet", n_dn)) if n)
+    cores = len(os.sched_getaffinity(0))
+    threads = int(os.environ.get("OMP_NUM_THREADS", cores))
+    return {"value": round(1.0 / per_tok, 6), "unit": "tok/s", "cores": min(cores, threads), "kind": "port",
+            "sample": (f"float oracle decode step (numpy, fp16 weight cache) at context {ctx}: one layer of "
+                       f"each kind and the LM head over {head_rows} of its {mc.vocab} rows, scaled: "
+                       f"{layers} + head {head:.2f} s = {per_tok:.1f} s per token")}
+
+
+def decode_at_shape(mc, prompt_len, n_dec, warmup, seed, kind, graph=True, packed_ops=-1, table_free_ops=-1,
+                    rotated=0, sampling=None, prefill_chunk=2048):
+    """Batch-1 decode of a synthetic model of shape mc: time to first token of a random prompt
+    through the batched prefill, then `warmup` untimed and n_dec - warmup timed decode tokens
+    (hipGraph replay). Returns (tok/s, seconds timed, record, decoder)."""
+    from trixium_amd import layout as L
+    from trixium_amd.model import Decoder, INFO_WEIGHT_BYTES
+    dec = Decoder.synthetic(mc, seed, weight_kind=kind, max_ctx=mc.max_ctx, max_new=n_dec + 8,
+                            use_graph=graph, packed_ops=packed_ops, table_free_ops=table_free_ops,
+                            hadamard_block=rotated)
+    prompt = np.random.default_rng(seed).integers(0, mc.vocab, prompt_len).astype(np.int32)
+    if sampling:
+        t, p_, r = (float(v) for v in sampling.split(","))
+        dec.set_sampling(t, p_, r, seed=seed + 1)
+    ttft = []
+    for _ in range(2):
+        dec.reset()
+        dec.feed(prompt)
+        dec.synchronize()
+        t0 = time.perf_counter()
+        dec.prefill(prompt_len - 1, prefill_chunk)
+        dec.step(1)
+        dec.synchronize()
+        ttft.append(time.perf_counter() - t0)
+    dec.step(warmup)
+    dec.synchronize()
+    steps = n_dec - 1 - warmup
+    t0 = time.perf_counter()
+    dec.step(steps)
+    dec.synchronize()
+    dt = time.perf_counter() - t0
+    dec.finalize()
+    toks = dec.outputs()[:n_dec]
+    assert np.all((toks >= 0) & (toks < mc.vocab)), "decoded ids out of range"
+    tok_s = steps / dt
+    # Bytes per token: the weights (a tied head reads the whole embedding table, an untied model
+    # one embedding row), K/V of the attention layers up to the mean timed position, every
+    # DeltaNet layer's recurrent state read and written.
+    wbytes = dec.info(INFO_WEIGHT_BYTES)
+    emb_rows = dec.tensor_ptr(L.ROLE_TOK_EMB, 0)[1]
+    emb_row = L.row_bytes(mc.n_embd, kind)
+    mean_pos = prompt_len + warmup + (steps - 1) / 2.0
+    n_attn = mc.n_layer - mc.n_dn_layers
+    kv = 2 * n_attn * mc.n_kv_head * mc.head_dim * 2 * (mean_pos + 1)
+    dn = 2 * mc.n_dn_layers * mc.dn_num_v_heads * mc.dn_v_head_dim * mc.dn_k_head_dim * 4
+    tok_bytes = wbytes + (0 if mc.tie_embeddings else emb_row - emb_rows) + kv + dn
+    roof = HBM_PEAK_GBS * 1e9 / tok_bytes
+    rec = {"prompt_tokens": prompt_len, "decode_tokens": n_dec, "timed_tokens": steps,
+           "tok_s": round(tok_s, 2), "ms_per_token": round(1e3 / tok_s, 4),
+           "token_roofline": {"bytes_per_token": int(tok_bytes), "tok_s": round(roof, 1),
+                              "frac": round(tok_s / roof, 4)},
+           "ttft_ms": round(min(ttft) * 1e3, 2), "prefill_chunk": prefill_chunk,
+           "packed_ops": dec.packed_ops}
+    return tok_s, dt, rec, dec
+
+
+# The other decode workloads: the Qwen3-1.7B shape (256 tokens after a 512-token prompt) and the
+# Qwen3.5-27B hybrid shape (128 tokens after a 1024-token prompt).
+OTHER_SHAPES = (("1.7b", 512, 256), ("27b", 1024, 128))
+
+
+def other_shapes(kind, seed, cpu=True):
+    from trixium_amd import configs as C
+    out = {}
+    for key, prompt_len, n_dec in OTHER_SHAPES:
+        mc = {"1.7b": C.QWEN3_1P7B, "27b": C.QWEN35_27B}[key]
+        _, _, rec, dec = decode_at_shape(mc, prompt_len, n_dec, 16, seed, kind)
+        dec.close()
+        if cpu:
+            rec["cpu_baseline"] = cpu_shape_sample(mc, prompt_len)
+        out[mc.name] = rec
+    return out
+
+
 def main():
     a = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -605,6 +718,28 @@ def main():
     if a.prompt + n_dec > mc.max_ctx:
         sys.exit(f"prompt {a.prompt} + {n_dec} decode tokens exceed the context {mc.max_ctx}")
     graph = not a.no_graph
+    if a.model != "8b":
+        tok_s, dt, rec, dec = decode_at_shape(mc, a.prompt, 1 + n_dec, a.warmup, a.seed, kind, graph, a.packed_ops,
+                                              a.table_free_ops, a.rotated, a.sampling, a.prefill_chunk or 2048)
+        print(json.dumps({
+            "metric": f"batch-1 decode tok/s ({mc.name})", "value": rec["tok_s"], "unit": "tok/s",
+            "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": rec["ms_per_token"],
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "ternary weights (fp16 group scales), fp32 activations, fp32 accumulate, fp16 KV"
+                     + (", fp32 DeltaNet state" if mc.n_dn_layers else ""),
+            "data": "synthetic: random ternary weights from a counter-based hash, random prompt",
+            "config": {"workload": f"{mc.name} ternary decoder, batch-1 greedy decode after a "
+                                   f"{a.prompt}-token prompt", "n_layer": mc.n_layer, "n_embd": mc.n_embd,
+                       "ffn_dim": mc.ffn_dim, "vocab": mc.vocab, "prompt_tokens": a.prompt,
+                       "decode_tokens": 1 + n_dec, "weights": a.kind, "hipgraph": graph,
+                       "packed_ops": dec.packed_ops, "table_free_ops": dec.table_free_ops,
+                       "rotation_block": a.rotated},
+            "token_roofline": rec["token_roofline"], "roofline": None,
+            "cpu_baseline": None if a.no_cpu_baseline else cpu_shape_sample(mc, a.prompt),
+            "prefill": {"prompt_tokens": a.prompt, "chunk": rec["prefill_chunk"], "ttft_ms": rec["ttft_ms"]}}),
+            flush=True)
+        dec.close()
+        return
     dec = Decoder.synthetic(mc, a.seed, weight_kind=kind, max_ctx=mc.max_ctx, max_new=n_dec + 8,
                             use_graph=graph, packed_ops=a.packed_ops, table_free_ops=a.table_free_ops,
                                 hadamard_block=a.rotated)
@@ -673,32 +808,6 @@ def main():
     tok_bytes = wbytes - emb_rows + emb_row + kv
     roof_tok_s = HBM_PEAK_GBS * 1e9 / tok_bytes
 
-    if a.model != "8b":
-        # Bytes per token: the weights, one embedding row, K/V of the attention layers up to the
-        # mean position, every DeltaNet layer's recurrent state read and written.
-        n_attn = mc.n_layer - mc.n_dn_layers
-        kv = 2 * n_attn * mc.n_kv_head * mc.head_dim * 2 * (mean_pos + 1)
-        dn = 2 * mc.n_dn_layers * mc.dn_num_v_heads * mc.dn_v_head_dim * mc.dn_k_head_dim * 4
-        # A tied head reads the whole embedding table every token.
-        tok_bytes = wbytes + (0 if mc.tie_embeddings else emb_row - emb_rows) + kv + dn
-        print(json.dumps({
-            "metric": f"batch-1 decode tok/s ({mc.name})", "value": round(tok_s, 2), "unit": "tok/s",
-            "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(1e3 / tok_s, 4),
-            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-            "dtype": "ternary weights (fp16 group scales), fp32 activations, fp32 accumulate, fp16 KV"
-                     + (", fp32 DeltaNet state" if mc.n_dn_layers else ""),
-            "data": "synthetic: random ternary weights from a counter-based hash, random prompt",
-            "config": {"workload": f"{mc.name} ternary decoder, batch-1 greedy decode after a "
-                                   f"{a.prompt}-token prompt", "n_layer": mc.n_layer, "n_embd": mc.n_embd,
-                       "ffn_dim": mc.ffn_dim, "vocab": mc.vocab, "prompt_tokens": a.prompt,
-                       "decode_tokens": n_dec, "weights": a.kind, "hipgraph": graph,
-                       "packed_ops": dec.packed_ops, "table_free_ops": dec.table_free_ops,
-                   "rotation_block": a.rotated},
-            "token_roofline": {"bytes_per_token": int(tok_bytes), "tok_s": round(HBM_PEAK_GBS * 1e9 / tok_bytes, 1),
-                               "frac": round(tok_s / (HBM_PEAK_GBS * 1e9 / tok_bytes), 4)},
-            "roofline": None, "cpu_baseline": None, "prefill": prefill}), flush=True)
-        dec.close()
-        return
 
     us, algo, n_launch, gu_mode = time_dominant_kernel(dec, mc, a.kernel_reps, graph=graph)
     achieved = algo / (us * 1e-6) / 1e9
@@ -750,6 +859,8 @@ def main():
         rec["matvec_microbench"] = matvec_microbench()
     if not a.no_cpu_baseline:
         rec["cpu_baseline"] = cpu_baseline(mc, a.prompt)
+    if not a.no_other_shapes:
+        rec["other_shapes"] = other_shapes(kind, a.seed, cpu=not a.no_cpu_baseline)
     print(json.dumps(rec), flush=True)
 
 

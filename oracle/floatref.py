@@ -112,11 +112,15 @@ class FloatRef:
         return out
 
     def proj(self, role, l, x):
+        """W x in fp32 from the fp16 weight cache, 8192 rows at a time (fastref.py:119-125)."""
         W = self.weight(role, l)
         x = np.asarray(x, dtype=f32)
         if self.hb and role not in (L.ROLE_SSM_BETA, L.ROLE_SSM_ALPHA):
             x = self.rotate(x, W.shape[1])
-        return (W.astype(f32) @ x).astype(f32)
+        out = np.empty(W.shape[0], f32)
+        for r0 in range(0, W.shape[0], 8192):
+            out[r0:r0 + 8192] = W[r0:r0 + 8192].astype(f32) @ x
+        return out
 
     # Elementwise ops (fastref.py:143-156) ----------------------------------------------------
     def rmsnorm(self, x, w):
@@ -437,26 +441,30 @@ class FloatRef:
 
 
 class ShapeSample(FloatRef):
-    """FloatRef's decode step on random weights of a full-attention shape, built without an
-    image (the CPU baseline of a large model is timed on a sample of its layers).
+    """FloatRef's decode step on random weights of a model shape, built without an image (the CPU
+    baseline of a large model is timed on a sample of its layers).
 
     Weights are ternary-valued fp16 matrices ((code - 1) * scale, scales U(0.01, 0.05)), the
     embedding table random int16 mantissas, the KV caches filled with `ctx` random positions, so
     the next step() runs at position `ctx` with the per-token work of the full shape restricted to
-    `n_layer` layers."""
+    `n_layer` layers. `kinds` gives the sample layers' kinds ("attn" or "deltanet"; default all
+    attention): a DeltaNet layer gets the shape's conv, gates and a random recurrent state."""
 
-    def __init__(self, mc, n_layer, ctx, seed=0):
+    def __init__(self, mc, n_layer, ctx, seed=0, kinds=None):
         rng = np.random.default_rng(seed)
+        kinds = list(kinds or ["attn"] * n_layer)
+        assert len(kinds) == n_layer
         self.n_layer, self.n_embd = n_layer, mc.n_embd
         self.n_head, self.n_kv, self.hd = mc.n_head, mc.n_kv_head, mc.head_dim
         self.rope_n = mc.rope_dims or mc.head_dim
         self.eps = f32(mc.rms_eps)
-        self.gated = False
+        self.gated = bool(mc.attn_gated)
         self.hb, self.hwidths = 0, []          # plain basis
         self.vocab = mc.vocab
-        self.dn = [False] * n_layer
-        self.nk = self.hk = self.nv = self.hv = 0
-        self.K = 1
+        self.dn = [k == "deltanet" for k in kinds]
+        self.nk, self.hk = mc.dn_num_k_heads, mc.dn_k_head_dim
+        self.nv, self.hv = mc.dn_num_v_heads, mc.dn_v_head_dim
+        self.K = mc.dn_conv_kernel if any(self.dn) else 1
         self.kv_fp16 = True
         self.rope_freq = np.array([f32(f32(mc.rope_theta) ** f32(-2.0 * i / self.rope_n))
                                    for i in range(self.rope_n // 2)], dtype=f32)
@@ -471,25 +479,39 @@ class ShapeSample(FloatRef):
             return np.tile(blk, (-(-rows // b), 1))[:rows]
 
         E, q, kv, F = mc.n_embd, mc.n_head * mc.head_dim, mc.n_kv_head * mc.head_dim, mc.ffn_dim
+        nq, nvh = self.nk * self.hk, self.nv * self.hv
         self.wcache = {}
         for l in range(n_layer):
-            for role, r, c in ((L.ROLE_ATTN_Q, q, E), (L.ROLE_ATTN_K, kv, E), (L.ROLE_ATTN_V, kv, E),
-                               (L.ROLE_ATTN_OUT, E, q), (L.ROLE_FFN_GATE, F, E), (L.ROLE_FFN_UP, F, E),
-                               (L.ROLE_FFN_DOWN, E, F)):
+            if self.dn[l]:
+                mats = ((L.ROLE_ATTN_QKV, 2 * nq + nvh, E), (L.ROLE_ATTN_ZGATE, nvh, E),
+                        (L.ROLE_SSM_BETA, self.nv, E), (L.ROLE_SSM_ALPHA, self.nv, E), (L.ROLE_SSM_OUT, E, nvh))
+            else:
+                mats = ((L.ROLE_ATTN_Q, q * (2 if self.gated else 1), E), (L.ROLE_ATTN_K, kv, E),
+                        (L.ROLE_ATTN_V, kv, E), (L.ROLE_ATTN_OUT, E, q))
+            for role, r, c in mats + ((L.ROLE_FFN_GATE, F, E), (L.ROLE_FFN_UP, F, E), (L.ROLE_FFN_DOWN, E, F)):
                 self.wcache[(role, l)] = tern(r, c)
         self.head_role = L.ROLE_LM_HEAD
         self.wcache[(L.ROLE_LM_HEAD, 0)] = tern(mc.vocab, E)
         gain = lambda n: rng.uniform(0.8, 1.2, n).astype(f32)
         self.norm_attn = [gain(E) for _ in range(n_layer)]
         self.norm_ffn = [gain(E) for _ in range(n_layer)]
-        self.norm_q = {l: gain(mc.head_dim) for l in range(n_layer)}
-        self.norm_k = {l: gain(mc.head_dim) for l in range(n_layer)}
+        self.norm_q = {l: gain(mc.head_dim) for l in range(n_layer) if not self.dn[l]}
+        self.norm_k = {l: gain(mc.head_dim) for l in range(n_layer) if not self.dn[l]}
+        dls = [l for l in range(n_layer) if self.dn[l]]
+        self.norm_ssm = {l: gain(self.hv) for l in dls}
+        self.ssm_a = {l: -np.exp(rng.uniform(-1.5, 0.5, self.nv)).astype(f32) for l in dls}
+        self.ssm_dt = {l: rng.uniform(-2.0, 0.5, self.nv).astype(f32) for l in dls}
+        self.conv_w = {l: rng.uniform(-0.5, 0.5, (2 * nq + nvh, self.K)).astype(f32) for l in dls}
         self.out_norm = gain(E)
         self.emb_mant = np.tile(rng.integers(-32767, 32768, size=(256, E), dtype=np.int16),
                                 (-(-mc.vocab // 256), 1))[:mc.vocab]
         self.emb_exp = np.full(mc.vocab, -20, np.int32)
         self.reset()
+        for l in dls:
+            self.dn_state[l] = (0.1 * rng.standard_normal((self.nv, self.hv, self.hk))).astype(f32)
         for l in range(n_layer):
+            if self.dn[l]:
+                continue
             kc = rng.standard_normal((ctx, self.n_kv, self.hd)).astype(np.float16).astype(f32)
             vc = rng.standard_normal((ctx, self.n_kv, self.hd)).astype(np.float16).astype(f32)
             self.k_cache[l] = list(kc)
