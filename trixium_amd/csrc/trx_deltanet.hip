@@ -15,12 +15,27 @@ namespace trx {
 // Conv of one head-sized segment of the qkv channels (q heads, then k heads, then v heads): thread
 // t < hk takes channel seg * hk + t; every thread of the block (blockDim >= hk, a multiple of 64)
 // calls this, the ones past hk only for the L2 norm's barrier.
+// [qkv | z] value i from the GEMV's K-slice partial sums: r * the slices' sum in slice order.
+__device__ __forceinline__ float dn_part_value(const DnConvParams& p, int i) {
+  float ss = 0.f;
+  for (int k = 0; k < p.S; ++k) ss += p.part_ss[k];
+  const float r = 1.0f / sqrtf(ss / (float)p.K + p.rms_eps);
+  float v[kDnPartMax];
+#pragma unroll
+  for (int k = 0; k < kDnPartMax; ++k) v[k] = k < p.S ? p.part[(size_t)k * p.rows_p + i] : 0.f;
+  float a = v[0];
+#pragma unroll
+  for (int k = 1; k < kDnPartMax; ++k)
+    if (k < p.S) a += v[k];
+  return a * r;
+}
+
 __device__ __forceinline__ void dn_conv_seg(const DnConvParams& p, int seg, int t, float* red) {
   const bool on = t < p.hk;
   const int c = seg * p.hk + (on ? t : 0);
   float y = 0.f;
   if (on) {
-    const float x = p.qkv[c];
+    const float x = p.part ? dn_part_value(p, c) : p.qkv[c];
     float acc = 0.f;
     for (int i = 0; i < p.Kc - 1; ++i) acc += p.taps[c * p.Kc + i] * p.state[(size_t)i * p.C + c];
     acc += p.taps[c * p.Kc + p.Kc - 1] * x;
@@ -47,11 +62,19 @@ __global__ void dn_conv_kernel(DnConvParams p) {
 }
 
 // The conv segments and the beta/alpha rows in one launch (both read only the [qkv|z] GEMV's
-// output and the residual): blocks below n_seg take a conv segment, the rest a Q8 row each.
+// output and the residual): blocks below n_seg take a conv segment, the next dp.M a Q8 row each;
+// with partial sums (cp.part) the last blocks reduce the z rows, 256 values each.
 __global__ __launch_bounds__(256) void dn_conv_q8_kernel(DnConvParams cp, DenseParams dp, int n_seg) {
   __shared__ float red[2][4];
-  if ((int)blockIdx.x < n_seg) dn_conv_seg(cp, blockIdx.x, threadIdx.x, red[0]);
-  else q8_row_dot(dp, blockIdx.x - n_seg, threadIdx.x, red);
+  const int b = blockIdx.x;
+  if (b < n_seg) {
+    dn_conv_seg(cp, b, threadIdx.x, red[0]);
+  } else if (b < n_seg + dp.M) {
+    q8_row_dot(dp, b - n_seg, threadIdx.x, red);
+  } else {
+    const int i = (b - n_seg - dp.M) * 256 + (int)threadIdx.x;
+    if (i < cp.nz) cp.qkv[cp.C + i] = dn_part_value(cp, cp.C + i);
+  }
 }
 
 // One block per value head; threads split the head's rows (hv) and columns (hk).
@@ -180,8 +203,10 @@ int launch_dn_conv_q8(const DnConvParams& cp, const DenseParams& dp, hipStream_t
             dp.K % 32 == 0 && dp.code_off % 16 == 0 && dp.row_bytes % 16 == 0 &&
             ((uintptr_t)dp.W | (uintptr_t)dp.x | (uintptr_t)dp.norm_w) % 16 == 0,
             TRX_E_INVALID, "deltanet conv + beta/alpha: unsupported geometry");
-  const int n_seg = cp.C / cp.hk;
-  hipLaunchKernelGGL(dn_conv_q8_kernel, dim3(n_seg + dp.M), dim3(256), 0, s, cp, dp, n_seg);
+  TRX_CHECK(!cp.part || (cp.part_ss && cp.S >= 1 && cp.S <= kDnPartMax && cp.rows_p >= cp.C + cp.nz && cp.K > 0),
+            TRX_E_INVALID, "deltanet conv: partial sums of %d slices unsupported", cp.S);
+  const int n_seg = cp.C / cp.hk, n_z = cp.part ? cdiv(cp.nz, 256) : 0;
+  hipLaunchKernelGGL(dn_conv_q8_kernel, dim3(n_seg + dp.M + n_z), dim3(256), 0, s, cp, dp, n_seg);
   TRX_LAUNCHED();
   return TRX_OK;
 }

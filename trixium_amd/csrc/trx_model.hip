@@ -89,6 +89,8 @@ struct Model {
   int down_S = 0, down_rows_p = 0;
   float* dn_out_part = nullptr;                    // DeltaNet out projection -> the FFN's gate|up
   int dn_out_S = 0, dn_out_rows_p = 0;
+  float *dnz_part = nullptr, *dnz_ss = nullptr;    // DeltaNet [qkv|z] -> the conv kernel, which sums them
+  int dnz_S = 0, dnz_rows_p = 0;
   float* head_part = nullptr;                      // LM head: partial sums reduced by many blocks
   float* head_ss = nullptr;
   int head_S = 0, head_rows_p = 0;
@@ -309,6 +311,8 @@ static int plan_packed(Model& m) {
     if ((rc = part_buf(E, F, &m.down_part, &m.down_S, &m.down_rows_p, nullptr, wk))) return rc;
   if ((ops & TRX_PACK_DN) && (ops & TRX_PACK_GATE_UP) && m.n_dn > 0 && cdiv(nvh, kSliceCols) <= tgemv_resid_slices_max())
     if ((rc = part_buf(E, nvh, &m.dn_out_part, &m.dn_out_S, &m.dn_out_rows_p, nullptr, wk))) return rc;
+  if ((ops & TRX_PACK_DN) && m.n_dn > 0 && cdiv(E, kSliceCols) <= kDnPartMax)
+    if ((rc = part_buf(2 * nq + 2 * nvh, E, &m.dnz_part, &m.dnz_S, &m.dnz_rows_p, &m.dnz_ss, wk))) return rc;
   for (auto& e : list)
     if (e.first.first == OP_HEAD &&
         (rc = part_buf(c.vocab, E, &m.head_part, &m.head_S, &m.head_rows_p, &m.head_ss, e.second.kind)))
@@ -421,14 +425,6 @@ int dn_layer_launch(Model& m, int l, hipStream_t s, const PackedMat* pz = nullpt
   float* io = m.dn_io;                  // [C + nvh] projections
   float* conv_out = m.dn_io + C + nvh;  // [C]
   const float* x = pz ? xres : m.x;
-  if (pz) {
-    if ((rc = tgemv_f32(pz->buf, c.weight_kind, C + nvh, E, xin, PF(m, TRX_ROLE_ATTN_NORM, l), c.rms_eps, io,
-                        TRX_EPI_STORE, nullptr, nullptr, m.pack_work, s, nullptr, nullptr, nullptr, pp,
-                        rotation_of(m, E, rots), tf_op(m, OP_DN_QKVZ)))) return rc;
-  } else if ((rc = projection(m, OP_DN_QKVZ, l, P(m, TRX_ROLE_ATTN_QKV, l), c.weight_kind, C + nvh, E, m.x,
-                               PF(m, TRX_ROLE_ATTN_NORM, l), io, TRX_EPI_STORE, nullptr, s))) {
-    return rc;
-  }
   DenseParams dp = {};
   dp.W = P(m, TRX_ROLE_SSM_BETA, l);
   dp.kind = TRX_KIND_Q8;
@@ -453,6 +449,31 @@ int dn_layer_launch(Model& m, int l, hipStream_t s, const PackedMat* pz = nullpt
   // One launch for both when the combined kernel takes them (aligned Q8 rows), else two.
   const bool fused = c.dn_k_head_dim <= 256 && C % c.dn_k_head_dim == 0 && E % 32 == 0 && dp.code_off % 16 == 0 &&
                      dp.row_bytes % 16 == 0 && ((uintptr_t)dp.W | (uintptr_t)dp.x | (uintptr_t)dp.norm_w) % 16 == 0;
+  // The packed [qkv|z] GEMV hands its K-slice partial sums to the combined kernel, whose blocks
+  // sum the values they take (no tile reduction in the GEMV); otherwise it stores [qkv | z].
+  const bool qz_hand = pz && fused && m.dnz_part;
+  if (qz_hand) {
+    PartialSums qz = pp ? *pp : PartialSums{};
+    qz.out = m.dnz_part;
+    qz.out_ss = m.dnz_ss;
+    if ((rc = tgemv_f32(pz->buf, c.weight_kind, C + nvh, E, xin, PF(m, TRX_ROLE_ATTN_NORM, l), c.rms_eps, nullptr,
+                        TRX_EPI_STORE, nullptr, nullptr, m.pack_work, s, nullptr, nullptr, nullptr, &qz,
+                        rotation_of(m, E, rots), tf_op(m, OP_DN_QKVZ)))) return rc;
+    cp.part = m.dnz_part;
+    cp.part_ss = m.dnz_ss;
+    cp.S = m.dnz_S;
+    cp.rows_p = m.dnz_rows_p;
+    cp.K = E;
+    cp.nz = nvh;
+    cp.rms_eps = c.rms_eps;
+  } else if (pz) {
+    if ((rc = tgemv_f32(pz->buf, c.weight_kind, C + nvh, E, xin, PF(m, TRX_ROLE_ATTN_NORM, l), c.rms_eps, io,
+                        TRX_EPI_STORE, nullptr, nullptr, m.pack_work, s, nullptr, nullptr, nullptr, pp,
+                        rotation_of(m, E, rots), tf_op(m, OP_DN_QKVZ)))) return rc;
+  } else if ((rc = projection(m, OP_DN_QKVZ, l, P(m, TRX_ROLE_ATTN_QKV, l), c.weight_kind, C + nvh, E, m.x,
+                               PF(m, TRX_ROLE_ATTN_NORM, l), io, TRX_EPI_STORE, nullptr, s))) {
+    return rc;
+  }
   if (fused) {
     if ((rc = launch_dn_conv_q8(cp, dp, s))) return rc;
   } else if ((rc = launch_dense_gemv(dp, s)) || (rc = launch_dn_conv(cp, s))) {

@@ -83,13 +83,22 @@ struct SynthParams {
 };
 
 struct DnConvParams {
-  const float* qkv;        // raw projection [C]
+  float* qkv;              // raw projection [C] (with part: the reduced [qkv | z] is stored here)
   const float* taps;       // [C][Kc]
   float* state;            // [Kc-1][C], oldest row first
   float* out;              // [C]: conv + SiLU, q and k heads L2-normalised
   int C, Kc, nq, hk;
   float eps;
+  // When set, [qkv | z] arrives as the packed GEMV's K-slice partial sums ([S][rows_p], S <=
+  // kDnPartMax, with its RMSNorm's slice sums of x^2 in part_ss over K columns): each value is
+  // r * sum_s part[s] (slices in order, r = 1/sqrt(sum(ss) / K + eps)); the z rows (nz after the
+  // C conv channels) are reduced into qkv + C for the recurrence.
+  const float* part;
+  const float* part_ss;
+  int S, rows_p, K, nz;
+  float rms_eps;
 };
+constexpr int kDnPartMax = 32;     // [qkv | z] K-slices the conv kernel sums (8192 columns)
 
 struct DnRecurParams {
   const float* conv;       // [C]: q [nk*hk] | k [nk*hk] | v [nv*hv]
