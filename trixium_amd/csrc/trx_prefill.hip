@@ -887,67 +887,76 @@ __global__ void dn_conv_tail_kernel(DnRowsParams p) {
   for (int i = 0; i < p.Kc - 1; ++i) p.conv_state[(size_t)i * p.C + c] = keep[i];
 }
 
-// The recurrence of one value head over the chunk, kRB state rows per block: a row's HK columns
-// over HK/4 lanes (a float4 each), row sums by shuffles. The position's k, q, v, beta and alpha
-// are loaded one position ahead. The per-position arithmetic is dn_recur_fixed_kernel's.
-constexpr int kRB = 32;
+// The recurrence of one value head over the chunk, one pass of state rows per block (8 rows at
+// HK = 128, 16 at 64; 256 threads): a row's HK columns over HK/4 lanes (a float4 each), row sums by
+// DPP. First every block computes its head's decay and beta gates of all the chunk's positions at
+// once (into LDS), so the serial loop carries only the state's arithmetic; each position's k, q
+// and v are loaded kScanAhead positions ahead. The per-position arithmetic is
+// dn_recur_fixed_kernel's.
+constexpr int kScanAhead = 4;          // positions whose inputs are in flight ahead of the scan
+constexpr int kScanRMax = 8192;        // chunk positions whose gates fit the LDS (64 KB)
+template <int HK>
+constexpr int scan_rows() { return 4 * (64 / (HK / 4)); }
+// Sum over a row's LPR lanes (16 or 32, aligned), every lane getting it: DPP within each 16-lane
+// row, then one lane swap between the two rows of a 32-lane row.
+template <int LPR>
+__device__ __forceinline__ float row_sum(float v) {
+  static_assert(LPR == 16 || LPR == 32, "row width");
+  v = row16_sum(v);
+  if (LPR == 32) v += __shfl_xor(v, 16, 64);
+  return v;
+}
 template <int HK>
 __global__ __launch_bounds__(256) void dn_scan_kernel(DnRowsParams p) {
-  constexpr int LPR = HK / 4, RPW = 64 / LPR, RPP = 4 * RPW, NIT = kRB / RPP;
-  static_assert(NIT >= 1 && kRB % RPP == 0, "rows per block");
+  constexpr int LPR = HK / 4, RPW = 64 / LPR, RB = scan_rows<HK>();
+  extern __shared__ float gates[];      // [R] decay, then [R] beta
   const int h = blockIdx.x, rb = blockIdx.y, t = threadIdx.x, w = t >> 6, lane = t & 63;
   const int sub = lane / LPR, c4 = lane % LPR;
   const int nk = p.nk, kh = h % nk, hv = p.hv;
+  const int jr = rb * RB + w * RPW + sub;
   float4* S = (float4*)(p.S + (size_t)h * hv * HK);
-  float4 sv[NIT];
-  int jr[NIT];
-#pragma unroll
-  for (int it = 0; it < NIT; ++it) {
-    jr[it] = rb * kRB + (it * 4 + w) * RPW + sub;
-    sv[it] = S[jr[it] * LPR + c4];
-  }
+  float4 sv = S[jr * LPR + c4];
   const float Ah = p.A[h], dth = p.dt[h];
+  for (int r = t; r < p.R; r += 256) {
+    const float a = p.ba[(size_t)r * 2 * p.nv + p.nv + h] + dth;
+    const float sp = a > 20.f ? a : log1pf(expf(a));
+    gates[r] = expf(sp * Ah);
+    gates[p.R + r] = sigmoidf_(p.ba[(size_t)r * 2 * p.nv + h]);
+  }
   const float qs = 1.0f / sqrtf((float)HK);
-  auto ld = [&](int r, float4& k4, float4& q4, float* vj, float& bb, float& aa) {
+  auto ld = [&](int r, float4& k4, float4& q4, float& vj) {
     const float* cr = p.conv_out + (size_t)r * p.C;
     k4 = *(const float4*)(cr + p.nq + kh * HK + 4 * c4);
     q4 = *(const float4*)(cr + kh * HK + 4 * c4);
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) vj[it] = cr[2 * p.nq + h * hv + jr[it]];
-    bb = p.ba[(size_t)r * 2 * p.nv + h];
-    aa = p.ba[(size_t)r * 2 * p.nv + p.nv + h];
+    vj = cr[2 * p.nq + h * hv + jr];
   };
-  float4 k4, q4;
-  float vj[NIT], bb, aa;
-  ld(0, k4, q4, vj, bb, aa);
-  for (int r = 0; r < p.R; ++r) {
-    const float4 ck = k4, cq = q4;
-    float cv[NIT];
+  // A ring of the next kScanAhead positions' inputs in registers: a position's loads are issued
+  // kScanAhead positions before it is used, so their latency is covered by that many steps of the
+  // recurrence (one step is shorter than a memory round trip).
+  float4 k4[kScanAhead], q4[kScanAhead];
+  float vj[kScanAhead];
 #pragma unroll
-    for (int it = 0; it < NIT; ++it) cv[it] = vj[it];
-    const float cb = bb, ca = aa;
-    if (r + 1 < p.R) ld(r + 1, k4, q4, vj, bb, aa);
-    const float a = ca + dth;
-    const float sp = a > 20.f ? a : log1pf(expf(a));
-    const float decay = expf(sp * Ah);
-    const float beta = sigmoidf_(cb);
+  for (int u = 0; u < kScanAhead; ++u)
+    if (u < p.R) ld(u, k4[u], q4[u], vj[u]);
+  __syncthreads();
+  for (int r0 = 0; r0 < p.R; r0 += kScanAhead)
 #pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-      float4 s4 = make_float4(sv[it].x * decay, sv[it].y * decay, sv[it].z * decay, sv[it].w * decay);
-      float dot = (s4.x * ck.x + s4.y * ck.y) + (s4.z * ck.z + s4.w * ck.w);
-#pragma unroll
-      for (int o = LPR >> 1; o >= 1; o >>= 1) dot += __shfl_xor(dot, o, 64);
-      const float delta = (cv[it] - dot) * beta;
-      s4 = make_float4(s4.x + delta * ck.x, s4.y + delta * ck.y, s4.z + delta * ck.z, s4.w + delta * ck.w);
-      sv[it] = s4;
-      float oq = (s4.x * cq.x + s4.y * cq.y) + (s4.z * cq.z + s4.w * cq.w);
-#pragma unroll
-      for (int o = LPR >> 1; o >= 1; o >>= 1) oq += __shfl_xor(oq, o, 64);
-      if (c4 == 0) p.o_raw[(size_t)r * p.nv * hv + (size_t)h * hv + jr[it]] = oq * qs;
-    }
+  for (int u = 0; u < kScanAhead; ++u) {
+    const int r = r0 + u;
+    if (r >= p.R) break;
+    const float4 ck = k4[u], cq = q4[u];
+    const float cv = vj[u];
+    if (r + kScanAhead < p.R) ld(r + kScanAhead, k4[u], q4[u], vj[u]);
+    const float decay = gates[r], beta = gates[p.R + r];
+    float4 s4 = make_float4(sv.x * decay, sv.y * decay, sv.z * decay, sv.w * decay);
+    const float dot = row_sum<LPR>((s4.x * ck.x + s4.y * ck.y) + (s4.z * ck.z + s4.w * ck.w));
+    const float delta = (cv - dot) * beta;
+    s4 = make_float4(s4.x + delta * ck.x, s4.y + delta * ck.y, s4.z + delta * ck.z, s4.w + delta * ck.w);
+    sv = s4;
+    const float oq = row_sum<LPR>((s4.x * cq.x + s4.y * cq.y) + (s4.z * cq.z + s4.w * cq.w));
+    if (c4 == 0) p.o_raw[(size_t)r * p.nv * hv + (size_t)h * hv + jr] = oq * qs;
   }
-#pragma unroll
-  for (int it = 0; it < NIT; ++it) S[jr[it] * LPR + c4] = sv[it];
+  S[jr * LPR + c4] = sv;
 }
 
 // Gated RMSNorm of every (position, value head), into the grouped output order.
@@ -966,18 +975,20 @@ __global__ void dn_gnorm_rows_kernel(DnRowsParams p) {
 }
 
 int launch_dn_rows(const DnRowsParams& p, hipStream_t s) {
-  TRX_CHECK(p.R >= 1 && p.hk <= 256 && p.C % p.hk == 0 && p.Kc >= 1 && p.Kc <= 9 && p.nv % p.nk == 0 &&
-            (p.hk == 64 || p.hk == 128) && p.hv % kRB == 0 && p.hv <= 1024, TRX_E_INVALID,
-            "prefill DeltaNet: unsupported geometry hk=%d hv=%d Kc=%d", p.hk, p.hv, p.Kc);
+  const int rb = p.hk == 128 ? scan_rows<128>() : scan_rows<64>();
+  TRX_CHECK(p.R >= 1 && p.R <= kScanRMax && p.hk <= 256 && p.C % p.hk == 0 && p.Kc >= 1 && p.Kc <= 9 &&
+            p.nv % p.nk == 0 && (p.hk == 64 || p.hk == 128) && p.hv % rb == 0 && p.hv <= 1024, TRX_E_INVALID,
+            "prefill DeltaNet: unsupported geometry hk=%d hv=%d Kc=%d (chunk %d)", p.hk, p.hv, p.Kc, p.R);
   hipLaunchKernelGGL(dn_conv_rows_kernel, dim3(p.C / p.hk, p.R), dim3(p.hk), 0, s, p);
   TRX_LAUNCHED();
   if (p.Kc > 1) {
     hipLaunchKernelGGL(dn_conv_tail_kernel, dim3(cdiv(p.C, 256)), dim3(256), 0, s, p);
     TRX_LAUNCHED();
   }
-  const dim3 sg(p.nv, p.hv / kRB);
-  if (p.hk == 128) hipLaunchKernelGGL(dn_scan_kernel<128>, sg, dim3(256), 0, s, p);
-  else hipLaunchKernelGGL(dn_scan_kernel<64>, sg, dim3(256), 0, s, p);
+  const dim3 sg(p.nv, p.hv / rb);
+  const size_t lds = (size_t)2 * p.R * sizeof(float);
+  if (p.hk == 128) hipLaunchKernelGGL(dn_scan_kernel<128>, sg, dim3(256), lds, s, p);
+  else hipLaunchKernelGGL(dn_scan_kernel<64>, sg, dim3(256), lds, s, p);
   TRX_LAUNCHED();
   hipLaunchKernelGGL(dn_gnorm_rows_kernel, dim3(p.nv, p.R), dim3(std::min(256, p.hv)), 0, s, p);
   TRX_LAUNCHED();
