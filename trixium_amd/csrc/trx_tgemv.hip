@@ -66,7 +66,8 @@ __host__ __device__ inline void tg_record_byte(bool t5, int d, int bi, int& g, i
   }
 }
 
-constexpr int kMaxTilesPerBlock = 64;   // also bounds the tiles of a reduction pass
+constexpr int kMaxTilesPerBlock = 128;  // also bounds the tiles of a reduction pass
+constexpr int kMaxBatchedTiles = 64;     // row tiles of a batched launch's matrix (16384 rows)
 // Tile counters sit 128 bytes apart: the S blocks of a tile count themselves at about the same
 // time, and atomics to one line are serialised.
 constexpr int kCntStride = 32;
@@ -1244,8 +1245,8 @@ int tgemv_batched_geom(int kind, int M, int K, int n_mat, PackGeom& g, size_t* p
   int rc = pack_geom(g, kind, M, K);
   if (rc) return rc;
   TRX_CHECK(n_mat >= 1 && n_mat <= 65535, TRX_E_INVALID, "batched GEMV: %d matrices (1..65535)", n_mat);
-  TRX_CHECK(g.n_tiles <= kMaxTilesPerBlock, TRX_E_INVALID, "batched GEMV: %d rows (at most %d)", M,
-            kMaxTilesPerBlock * kTileRows);
+  TRX_CHECK(g.n_tiles <= kMaxBatchedTiles, TRX_E_INVALID, "batched GEMV: %d rows (at most %d)", M,
+            kMaxBatchedTiles * kTileRows);
   // One block per (slice, matrix) streams every row of its slice: one table per slice column.
   g.bps = 1;
   g.tpb = g.n_tiles;
