@@ -329,7 +329,9 @@ int trx_model_reset(trx_model* m);
  * rows are not copied: a forward writes its own position's row, so rows past the restored
  * position are rewritten before they are read. Outputs of the last forward (logits, taps) are not
  * state and are not restored. Asynchronous on the model's stream; TRX_E_STATE restores with no
- * checkpoint saved. */
+ * checkpoint saved. With the KV ring past the window (trx_model_set_kv_ring) a forward there
+ * overwrites the ring slot of the position that leaves the window, so a restore there undoes at
+ * most one forward, as the firmware's retry does (TRX_E_STATE after more). */
 #define TRX_CKPT_SAVE 0
 #define TRX_CKPT_RESTORE 1
 int trx_model_checkpoint(trx_model* m, int op);

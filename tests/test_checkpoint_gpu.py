@@ -71,3 +71,40 @@ def test_restore_without_a_checkpoint_is_an_error(tiny_images):
     dec = _decoder(tiny_images[("tiny-qwen3", True)])
     with pytest.raises(TrxError):
         dec.restore()
+
+
+def test_restore_after_a_reset_rewrote_the_rows_is_an_error(tiny_images, golden):
+    """The KV rows are not in the checkpoint: forwards after a reset rewrite the rows below the
+    checkpoint's position, so its restore is refused."""
+    name = "tiny-qwen3"
+    prompt = golden[f"prompt/{name}"]
+    dec = _decoder(tiny_images[(name, True)])
+    dec.reset()
+    dec.forward(prompt)
+    dec.checkpoint()
+    dec.reset()
+    dec.forward(prompt[:4])
+    with pytest.raises(TrxError):
+        dec.restore()
+
+
+def test_restore_past_the_kv_window_undoes_one_forward(tiny_images, golden):
+    """With the KV ring past the window a forward overwrites the ring slot of the position that
+    leaves the window: one forward can be run again exactly (the firmware's retry), more are
+    refused."""
+    name = "tiny-hybrid"
+    toks = ((golden[f"prompt/{name}"] + golden[f"fastref_tokens/{name}"]) * 2)[:30]
+    dec = _decoder(tiny_images[(name, True)], max_ctx=20)
+    dec.set_kv_ring(1, 5)
+    dec.reset()
+    for t in toks[:26]:
+        dec.forward([t])
+    dec.checkpoint()
+    first = dec.forward([toks[26]])
+    dec.restore()
+    assert np.array_equal(dec.forward([toks[26]]), first)
+    dec.restore()
+    dec.forward([toks[26]])
+    dec.forward([toks[27]])
+    with pytest.raises(TrxError):
+        dec.restore()

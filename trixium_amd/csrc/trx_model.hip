@@ -132,6 +132,7 @@ struct Model {
   size_t ckpt_bytes = 0;
   bool ckpt_valid = false;
   int ck_pos = -1, ck_n_fed = 0, ck_head_from = 0, ck_kv_pin = 0;
+  int ck_lowest = 0x7fffffff;                      // lowest position a forward ran at since then
   size_t dev_bytes = 0;
   std::vector<void*> allocs;
 
@@ -1336,10 +1337,23 @@ TRX_API int trx_model_checkpoint(trx_model* h, int op) {
     m.ck_n_fed = m.host_n_fed;
     m.ck_head_from = m.host_head_from;
     m.ck_kv_pin = m.kv_pin;
+    m.ck_lowest = 0x7fffffff;
     m.ckpt_valid = true;
     return TRX_OK;
   }
   TRX_CHECK(m.ckpt_valid, TRX_E_STATE, "trx_model_checkpoint: no checkpoint saved");
+  // The KV rows are not in the checkpoint: a forward since then at or below its position (after a
+  // reset) rewrote rows the restored state reads.
+  TRX_CHECK(m.ck_lowest > m.ck_pos, TRX_E_STATE,
+            "trx_model_checkpoint: a forward at position %d since the checkpoint at %d rewrote its KV rows",
+            m.ck_lowest, m.ck_pos);
+  // Past the window a forward at position q writes the KV ring slot of position q - (max_ctx -
+  // pin), which the forwards from the checkpoint on still read until they reach q: after one
+  // forward that slot's position has left the window anyway (the firmware re-runs one forward),
+  // after more the restored state would attend to rows written by the forwards it undoes.
+  TRX_CHECK(!m.ck_kv_pin || m.host_pos < std::max(m.cfg.max_ctx, m.ck_pos + 2), TRX_E_STATE,
+            "trx_model_checkpoint: %d forwards past the KV window since the checkpoint at position %d "
+            "(at most one can be undone there)", m.host_pos - m.ck_pos, m.ck_pos);
   size_t off = 0;
   for (const StateRegion& s : regs) {
     TRX_HIP(hipMemcpyAsync(s.p, m.ckpt + off, s.bytes, hipMemcpyDeviceToDevice, m.stream));
@@ -1349,6 +1363,7 @@ TRX_API int trx_model_checkpoint(trx_model* h, int op) {
   m.host_n_fed = m.ck_n_fed;
   m.host_head_from = m.ck_head_from;
   m.kv_pin = m.ck_kv_pin;
+  m.ck_lowest = 0x7fffffff;
   return TRX_OK;
 }
 
@@ -1414,6 +1429,7 @@ TRX_API int trx_model_step(trx_model* h, int n_steps, int use_graph) {
   }
   TRX_CHECK(m.kv_pin > 0 || m.host_pos + n_steps < m.cfg.max_ctx, TRX_E_STATE,
             "%d steps after position %d exceed max_ctx %d", n_steps, m.host_pos, m.cfg.max_ctx);
+  if (n_steps > 0) m.ck_lowest = std::min(m.ck_lowest, m.host_pos + 1);
   for (int i = 0; i < n_steps; ++i) {
     ++m.host_pos;
     if (use_graph) {
@@ -1437,6 +1453,7 @@ TRX_API int trx_model_prefill(trx_model* h, int n, int chunk) {
             "trx_model_prefill: position %d computes logits (head_from %d); step it instead", first + n - 1,
             m.host_head_from);
   if (n == 0) return TRX_OK;
+  m.ck_lowest = std::min(m.ck_lowest, first);
   // Positions past the window (the KV ring) run one forward each.
   const int n_in = std::max(0, std::min(n, m.cfg.max_ctx - first));
   if (n_in > 0) {
