@@ -52,6 +52,12 @@ def test_errors_are_reported_without_a_device_call():
     assert rc == _lib.TRX_E_INVALID and b"not ternary" in L.trx_last_error()
     rc = L.trx_pack_geometry(5, 4, 200, ctypes.byref(pb), ctypes.byref(wb))
     assert rc == _lib.TRX_E_INVALID and b"multiple of 128" in L.trx_last_error()
+    # The decode-state checkpoint and the KV ring refuse a missing model or an unknown request.
+    assert L.trx_model_checkpoint(None, 0) == _lib.TRX_E_INVALID
+    assert L.trx_model_checkpoint(fake, 2) == _lib.TRX_E_INVALID
+    assert L.trx_model_set_kv_ring(None, 1, 4) == _lib.TRX_E_INVALID
+    assert L.trx_model_set_kv_ring(fake, 2, 4) == _lib.TRX_E_INVALID
+    assert L.trx_model_set_kv_ring(fake, 1, -1) == _lib.TRX_E_INVALID
 
 
 def test_decoder_config_from_images(tiny_images):
