@@ -276,12 +276,13 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
   stage_step(0, 0);
   if (NS > 2) load_step(2, 0);
   __syncthreads();
+  // NS is even, so every pass of the loop takes both halves: no exit between them (with one the
+  // compiler gave the two halves' accumulators different registers and copied them every pass).
   for (int st = 0; st < NS; st += 2) {
     compute(0);
-    if (st + 1 < NS) stage_step(st + 1, 1);
+    stage_step(st + 1, 1);
     if (st + 3 < NS) load_step(st + 3, 1);
     __syncthreads();
-    if (st + 1 >= NS) break;
     compute(1);
     if (st + 2 < NS) stage_step(st + 2, 0);
     if (st + 4 < NS) load_step(st + 4, 0);
