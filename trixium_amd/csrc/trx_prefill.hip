@@ -1,9 +1,9 @@
 // Batched prefill kernels: R prompt positions per forward, one weight pass for all of them.
 //
-// The projections run on the matrix cores (v_mfma_f32_32x32x16_f16): a block decodes 256 stored
-// ternary rows into LDS as fp16 weights, 64 columns at a time, and multiplies 128 (or 64)
-// positions by them, x split into two fp16 planes (hi, lo) so the fp32 accumulation sees x to
-// ~22 bits.
+// The projections run on the matrix cores (v_mfma_f32_32x32x16_f16): four waves of a block decode
+// 256 stored ternary rows into LDS as fp16 weights, 64 columns at a time, while its other four
+// multiply 128 (or 64) positions by the previous 64 columns, x split into two fp16 planes (hi,
+// lo) so the fp32 accumulation sees x to ~22 bits.
 // Attention, the RoPE/KV append and the Gated DeltaNet recurrence are the one-position rules of
 // the decode kernels applied to every position of the chunk (the recurrence in order).
 
@@ -11,12 +11,14 @@
 #include "trx_prefill.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace trx {
 
 // GEMM ------------------------------------------------------------------------------------------
 
-constexpr int kGmThreads = 256;
+constexpr int kGmStage = 256;              // staging threads per block (waves 4-7)
+constexpr int kGmThreads = 512;            // waves 0-3 run the MFMAs
 constexpr int kGmBM = 256;                 // weight rows per block
 constexpr int kGmLd = kGroup / 2 + 8;      // LDS row stride in halves (144 bytes): half a group per step
 
@@ -57,14 +59,16 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
   __shared__ __align__(16) _Float16 xs[2][2][BR * kGmLd];
   __shared__ __align__(16) uint4 lut[2][256];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const bool cw = w < 4;                    // a wave that runs the MFMAs
+  const int stid = max(tid - kGmStage, 0);  // staging thread index
   const int r0 = blockIdx.y * BR;
   const int G = p.K / kGroup;
 
   // Code byte -> (digit - 1) as fp16, two per dword. trit5: the even table starts a byte's five
   // digits on a dword boundary (d0 d1 | d2 d3 | d4 0), the odd one a half later (0 d0 | d1 d2 | d3
   // d4): two consecutive bytes fill five dwords. 2-bit: (c0 c1 | c2 c3).
-  {
-    const int b = tid;
+  if (!cw) {
+    const int b = stid;
     if (KIND == TRX_KIND_TERNARY5) {
       uint32_t h[5];
       int v = b;
@@ -83,9 +87,9 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
     }
   }
 
-  // Staging roles: thread t decodes the 128 codes of LDS row t (two halves of 64), and copies
-  // eight 16-byte pieces of the two x planes.
-  const int srow = tid;
+  // Staging roles (waves 4-7): staging thread t decodes the 128 codes of LDS row t (two halves
+  // of 64), and copies eight 16-byte pieces of the two x planes.
+  const int srow = stid;
   const int wrow = gm_wrow(EPI, srow, p.M);
   const bool wvalid = wrow < p.M;
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.W, p.w_bytes);
@@ -115,12 +119,12 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
       raw.sc = __builtin_amdgcn_raw_buffer_load_b32(rw, rbase + 2u * (4u * (uint32_t)g + 2u * (uint32_t)shalf), 0, 0);
     }
   };
-  constexpr int XQ = BR * 8 / kGmThreads;          // 16-byte x pieces per thread, plane and step
+  constexpr int XQ = BR * 8 / kGmStage;            // 16-byte x pieces per thread, plane and step
   // x of step st (columns 64 st .. + 63): thread t moves pieces t + 256 q (row piece / 8, 8 columns).
   auto load_x = [&](uint4* xr, int st) {
 #pragma unroll
     for (int q = 0; q < XQ; ++q) {
-      const int piece = tid + kGmThreads * q, row = piece >> 3, c8 = piece & 7;
+      const int piece = stid + kGmStage * q, row = piece >> 3, c8 = piece & 7;
       const uint32_t off = ((uint32_t)(r0 + row) * (uint32_t)p.K + (uint32_t)(64 * st + 8 * c8)) * 2u;
       const auto a = __builtin_amdgcn_raw_buffer_load_b128(rxh, off, 0, 0);
       const auto b = __builtin_amdgcn_raw_buffer_load_b128(rxl, off, 0, 0);
@@ -128,13 +132,13 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
       xr[XQ + q] = make_uint4(b[0], b[1], b[2], b[3]);
     }
   };
-  // Decoded weights of this thread's 64 codes: 32 dwords of fp16 pairs, times the scale.
-  auto stage_w = [&](const GmRaw<KIND>& raw, int g, int shalf, int buf) {
+  // Decoded weights of this thread's 64 codes: 32 dwords of fp16 pairs, times the scale (0 for
+  // a row past M, whose codes were read from row 0). The half of the group (shc, a compile-time
+  // constant) is also the LDS buffer. No branch: one block of code per half.
+  auto stage_w = [&](const GmRaw<KIND>& raw, int g, auto shc) {
+    constexpr int shalf = decltype(shc)::value, buf = shalf;
     uint32_t D[32];
-    if (!wvalid) {
-#pragma unroll
-      for (int i = 0; i < 32; ++i) D[i] = 0u;
-    } else if (KIND == TRX_KIND_TERNARY5) {
+    if (KIND == TRX_KIND_TERNARY5) {
       const uint32_t o = (uint32_t)p.code_off + 26u * (uint32_t)g + (shalf ? 12u : 0u);
       const uint32_t sh = o & 3u;
       const uint32_t d0 = __builtin_amdgcn_alignbyte(raw.c[0].y, raw.c[0].x, sh);
@@ -143,7 +147,7 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
       const uint32_t d3 = __builtin_amdgcn_alignbyte(0u, raw.c[0].w, sh);
       const uint32_t dw[4] = {d0, d1, d2, d3};
       auto byte = [&](int j) { return (dw[j >> 2] >> (8 * (j & 3))) & 0xFFu; };
-      if (shalf == 0) {
+      if constexpr (shalf == 0) {
         // bytes 0..12: codes 0..64, of which 0..63 are this half's
 #pragma unroll
         for (int i = 0; i < 6; ++i) {
@@ -198,16 +202,15 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
         D[2 * j + 1] = q(2) | q(3) << 16;
       }
     }
-    if (wvalid) {
-      if (KIND == TRX_KIND_Q8) {
-        const uint32_t s0 = raw.sc & 0xFFFFu, s1 = raw.sc >> 16;
+    const uint32_t sc = wvalid ? raw.sc : 0u;
+    if (KIND == TRX_KIND_Q8) {
+      const uint32_t s0 = sc & 0xFFFFu, s1 = sc >> 16;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) D[i] = pk_mul_h2(D[i], i < 16 ? (s0 | s0 << 16) : (s1 | s1 << 16));
-      } else {
-        const uint32_t s2 = (raw.sc & 0xFFFFu) | (raw.sc << 16);
+      for (int i = 0; i < 32; ++i) D[i] = pk_mul_h2(D[i], i < 16 ? (s0 | s0 << 16) : (s1 | s1 << 16));
+    } else {
+      const uint32_t s2 = (sc & 0xFFFFu) | (sc << 16);
 #pragma unroll
-        for (int i = 0; i < 32; ++i) D[i] = pk_mul_h2(D[i], s2);
-      }
+      for (int i = 0; i < 32; ++i) D[i] = pk_mul_h2(D[i], s2);
     }
     uint4* dst = (uint4*)(ws[buf] + srow * kGmLd);
 #pragma unroll
@@ -216,7 +219,7 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
   auto stage_x = [&](const uint4* xr, int buf) {
 #pragma unroll
     for (int q = 0; q < XQ; ++q) {
-      const int piece = tid + kGmThreads * q, row = piece >> 3, c8 = piece & 7;
+      const int piece = stid + kGmStage * q, row = piece >> 3, c8 = piece & 7;
       *(uint4*)(xs[buf][0] + row * kGmLd + 8 * c8) = xr[q];
       *(uint4*)(xs[buf][1] + row * kGmLd + 8 * c8) = xr[XQ + q];
     }
@@ -244,10 +247,13 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
     load_w(raw[slot], st >> 1, st & 1);
     load_x(xr[slot], st);
   };
-  auto stage_step = [&](int st, int slot) {
-    stage_w(raw[slot], st >> 1, st & 1, slot);
-    stage_x(xr[slot], slot);
+  // A step's half is its register slot and LDS buffer: st & 1 == slot.
+  auto stage_step = [&](int st, auto slot) {
+    stage_w(raw[decltype(slot)::value], st >> 1, slot);
+    stage_x(xr[decltype(slot)::value], decltype(slot)::value);
   };
+  const std::integral_constant<int, 0> I0;
+  const std::integral_constant<int, 1> I1;
   auto compute = [&](int buf) {
 #pragma unroll
     for (int kk = 0; kk < kGroup / 32; ++kk) {
@@ -270,22 +276,36 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
         for (int t = 0; t < 4; ++t) acc[a][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[a], b[t], acc[a][t], 0, 0, 0);
     }
   };
-  load_step(0, 0);
-  load_step(1, 1);                        // NS >= 2: K is a multiple of 128
-  __syncthreads();                        // the code tables are written
-  stage_step(0, 0);
-  if (NS > 2) load_step(2, 0);
+  // Waves 0-3 run the MFMAs, waves 4-7 decode and stage the next step meanwhile (with both roles
+  // in every wave, all four waves decoded at once and the matrix cores sat idle meanwhile). Each
+  // role has a loop of its own, so neither role's registers are live in the other's (two waves
+  // per SIMD leave 256 registers a wave), and both pass the same 2 + NS barriers. The loops take
+  // two steps a pass with no exit between them: with one, the compiler gave the two halves'
+  // accumulators different registers and copied them every pass. A staging thread's loads past
+  // the last step repeat it, so its halves have no branch either.
+  if (!cw) {
+    load_step(0, 0);
+    load_step(1, 1);                      // NS >= 2: K is a multiple of 128
+    __syncthreads();                      // the code tables are written
+    stage_step(0, I0);
+    load_step(min(2, NS - 1), 0);
+    __syncthreads();
+    for (int st = 0; st < NS; st += 2) {
+      stage_step(st + 1, I1);
+      load_step(min(st + 3, NS - 1), 1);
+      __syncthreads();
+      stage_step(st + 2, I0);             // the last pass stages a step NS that nothing reads
+      load_step(min(st + 4, NS - 1), 0);
+      __syncthreads();
+    }
+    return;
+  }
   __syncthreads();
-  // NS is even, so every pass of the loop takes both halves: no exit between them (with one the
-  // compiler gave the two halves' accumulators different registers and copied them every pass).
+  __syncthreads();
   for (int st = 0; st < NS; st += 2) {
     compute(0);
-    stage_step(st + 1, 1);
-    if (st + 3 < NS) load_step(st + 3, 1);
     __syncthreads();
     compute(1);
-    if (st + 2 < NS) stage_step(st + 2, 0);
-    if (st + 4 < NS) load_step(st + 4, 0);
     __syncthreads();
   }
 
