@@ -57,33 +57,28 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
   // cores read the other.
   __shared__ __align__(16) _Float16 ws[2][kGmBM * kGmLd];
   __shared__ __align__(16) _Float16 xs[2][2][BR * kGmLd];
-  __shared__ __align__(16) uint4 lut[2][256];
+  __shared__ uint32_t tsel[16];
+  __shared__ uint2 tsel27[32];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const bool cw = w < 4;                    // a wave that runs the MFMAs
   const int stid = max(tid - kGmStage, 0);  // staging thread index
   const int r0 = blockIdx.y * BR;
   const int G = p.K / kGroup;
 
-  // Code byte -> (digit - 1) as fp16, two per dword. trit5: the even table starts a byte's five
-  // digits on a dword boundary (d0 d1 | d2 d3 | d4 0), the odd one a half later (0 d0 | d1 d2 | d3
-  // d4): two consecutive bytes fill five dwords. 2-bit: (c0 c1 | c2 c3).
-  if (!cw) {
-    const int b = stid;
+  // Weights are decoded by v_perm_b32 from a register pair holding -s, 0, s and 2s as fp16 (s the
+  // group's scale): selector half g(c) = 0x0100 + c * 0x0202 picks (c - 1) * s for code c. trit5:
+  // a code byte b = lo + 9 hi, tsel[lo] = g(d0) | g(d1) << 16 and tsel27[hi] = {g(d2) | g(d3) <<
+  // 16, g(d4)} (hi <= 28 for any byte). 2-bit: tsel[nibble] = g(c0) | g(c1) << 16. No table has
+  // more entries than the LDS has banks, so its reads never conflict (a 256-entry table of the
+  // decoded bytes stalled the LDS a third of the time).
+  if (!cw && stid < 32) {
+    auto gsel = [](int c) { return 0x0100u + 0x0202u * (uint32_t)c; };
+    const int t = stid;
     if (KIND == TRX_KIND_TERNARY5) {
-      uint32_t h[5];
-      int v = b;
-#pragma unroll
-      for (int k = 0; k < 5; ++k) {
-        h[k] = half_bits((float)(v % 3 - 1));
-        v /= 3;
-      }
-      lut[0][b] = make_uint4(h[0] | h[1] << 16, h[2] | h[3] << 16, h[4], 0u);
-      lut[1][b] = make_uint4(h[0] << 16, h[1] | h[2] << 16, h[3] | h[4] << 16, 0u);
+      if (t < 9) tsel[t] = gsel(t % 3) | gsel(t / 3) << 16;
+      tsel27[t] = make_uint2(gsel(t % 3) | gsel(t / 3 % 3) << 16, gsel(t / 9 % 3));
     } else if (KIND == TRX_KIND_TERNARY) {
-      uint32_t h[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) h[k] = half_bits((float)(((b >> (2 * k)) & 3) - 1));
-      lut[0][b] = make_uint4(h[0] | h[1] << 16, h[2] | h[3] << 16, 0u, 0u);
+      if (t < 16) tsel[t] = gsel(t & 3) | gsel(t >> 2) << 16;
     }
   }
 
@@ -138,79 +133,88 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
   auto stage_w = [&](const GmRaw<KIND>& raw, int g, auto shc) {
     constexpr int shalf = decltype(shc)::value, buf = shalf;
     uint32_t D[32];
-    if (KIND == TRX_KIND_TERNARY5) {
-      const uint32_t o = (uint32_t)p.code_off + 26u * (uint32_t)g + (shalf ? 12u : 0u);
-      const uint32_t sh = o & 3u;
-      const uint32_t d0 = __builtin_amdgcn_alignbyte(raw.c[0].y, raw.c[0].x, sh);
-      const uint32_t d1 = __builtin_amdgcn_alignbyte(raw.c[0].z, raw.c[0].y, sh);
-      const uint32_t d2 = __builtin_amdgcn_alignbyte(raw.c[0].w, raw.c[0].z, sh);
-      const uint32_t d3 = __builtin_amdgcn_alignbyte(0u, raw.c[0].w, sh);
-      const uint32_t dw[4] = {d0, d1, d2, d3};
-      auto byte = [&](int j) { return (dw[j >> 2] >> (8 * (j & 3))) & 0xFFu; };
-      if constexpr (shalf == 0) {
-        // bytes 0..12: codes 0..64, of which 0..63 are this half's
-#pragma unroll
-        for (int i = 0; i < 6; ++i) {
-          const uint4 e = lut[0][byte(2 * i)], od = lut[1][byte(2 * i + 1)];
-          D[5 * i] = e.x;
-          D[5 * i + 1] = e.y;
-          D[5 * i + 2] = e.z | od.x;
-          D[5 * i + 3] = od.y;
-          D[5 * i + 4] = od.z;
-        }
-        const uint4 e = lut[0][byte(12)];
-        D[30] = e.x;
-        D[31] = e.y;
-      } else {
-        // bytes 12..25: codes 60..129; this half takes 64..127
-        const uint4 e0 = lut[0][byte(0)], o1 = lut[1][byte(1)];
-        D[0] = e0.z | o1.x;
-        D[1] = o1.y;
-        D[2] = o1.z;
-#pragma unroll
-        for (int i = 1; i < 6; ++i) {
-          const uint4 e = lut[0][byte(2 * i)], od = lut[1][byte(2 * i + 1)];
-          D[5 * i - 2] = e.x;
-          D[5 * i - 1] = e.y;
-          D[5 * i] = e.z | od.x;
-          D[5 * i + 1] = od.y;
-          D[5 * i + 2] = od.z;
-        }
-        const uint4 e = lut[0][byte(12)], od = lut[1][byte(13)];
-        D[28] = e.x;
-        D[29] = e.y;
-        D[30] = e.z | od.x;
-        D[31] = od.y;
-      }
-    } else if (KIND == TRX_KIND_TERNARY) {
-      const uint32_t dw[4] = {raw.c[0].x, raw.c[0].y, raw.c[0].z, raw.c[0].w};
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const uint4 e = lut[0][(dw[j >> 2] >> (8 * (j & 3))) & 0xFFu];
-        D[2 * j] = e.x;
-        D[2 * j + 1] = e.y;
-      }
-    } else {
-      // Q8: int8 -> fp16 exactly, times the 32-column group's scale in fp16 (fp16(q * s)).
+    const uint32_t sc = wvalid ? raw.sc : 0u;
+    if (KIND == TRX_KIND_Q8) {
+      // int8 -> fp16 exactly, times the 32-column group's scale in fp16 (fp16(q * s)).
       const uint32_t dw[16] = {raw.c[0].x, raw.c[0].y, raw.c[0].z, raw.c[0].w, raw.c[1].x, raw.c[1].y,
                                raw.c[1].z, raw.c[1].w, raw.c[2].x, raw.c[2].y, raw.c[2].z, raw.c[2].w,
                                raw.c[3].x, raw.c[3].y, raw.c[3].z, raw.c[3].w};
+      const uint32_t s0 = sc & 0xFFFFu, s1 = sc >> 16;
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         auto q = [&](int b) { return half_bits((float)(int8_t)(uint8_t)(dw[j] >> (8 * b))); };
-        D[2 * j] = q(0) | q(1) << 16;
-        D[2 * j + 1] = q(2) | q(3) << 16;
+        const uint32_t s2 = j < 8 ? (s0 | s0 << 16) : (s1 | s1 << 16);
+        D[2 * j] = pk_mul_h2(q(0) | q(1) << 16, s2);
+        D[2 * j + 1] = pk_mul_h2(q(2) | q(3) << 16, s2);
       }
-    }
-    const uint32_t sc = wvalid ? raw.sc : 0u;
-    if (KIND == TRX_KIND_Q8) {
-      const uint32_t s0 = sc & 0xFFFFu, s1 = sc >> 16;
-#pragma unroll
-      for (int i = 0; i < 32; ++i) D[i] = pk_mul_h2(D[i], i < 16 ? (s0 | s0 << 16) : (s1 | s1 << 16));
     } else {
-      const uint32_t s2 = (sc & 0xFFFFu) | (sc << 16);
+      // The permute pair: bytes 0-3 {-s, 0}, bytes 4-7 {s, 2s} (fp16(1 * s), fp16(2 * s)).
+      const uint32_t s16 = sc & 0xFFFFu;
+      const uint32_t plo = s16 ^ 0x8000u, phi = pk_mul_h2(s16 | s16 << 16, 0x40003C00u);
+      auto wp = [&](uint32_t sel) { return __builtin_amdgcn_perm(phi, plo, sel); };
+      if (KIND == TRX_KIND_TERNARY5) {
+        const uint32_t o = (uint32_t)p.code_off + 26u * (uint32_t)g + (shalf ? 12u : 0u);
+        const uint32_t sh = o & 3u;
+        const uint32_t d0 = __builtin_amdgcn_alignbyte(raw.c[0].y, raw.c[0].x, sh);
+        const uint32_t d1 = __builtin_amdgcn_alignbyte(raw.c[0].z, raw.c[0].y, sh);
+        const uint32_t d2 = __builtin_amdgcn_alignbyte(raw.c[0].w, raw.c[0].z, sh);
+        const uint32_t d3 = __builtin_amdgcn_alignbyte(0u, raw.c[0].w, sh);
+        const uint32_t dw[4] = {d0, d1, d2, d3};
+        // Byte j's selectors: lo pair (d0, d1) and hi {(d2, d3), d4}.
+        auto sel = [&](int j, uint32_t& lo, uint2& hi) {
+          const uint32_t b = (dw[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+          const uint32_t h = (b * 57u) >> 9;          // b / 9 for every byte value
+          lo = tsel[b - 9u * h];
+          hi = tsel27[h];
+        };
+        // An even byte's five codes start a dword, the odd byte's five follow: five dwords.
+        auto pair5 = [&](int j, uint32_t* out) {
+          uint32_t e9, o9;
+          uint2 e27, o27;
+          sel(j, e9, e27);
+          sel(j + 1, o9, o27);
+          out[0] = wp(e9);
+          out[1] = wp(e27.x);
+          out[2] = wp(e27.y | o9 << 16);
+          out[3] = wp(__builtin_amdgcn_alignbit(o27.x, o9, 16));
+          out[4] = wp(__builtin_amdgcn_alignbit(o27.y, o27.x, 16));
+        };
+        if constexpr (shalf == 0) {
+          // bytes 0..12: codes 0..64, of which 0..63 are this half's
 #pragma unroll
-      for (int i = 0; i < 32; ++i) D[i] = pk_mul_h2(D[i], s2);
+          for (int i = 0; i < 6; ++i) pair5(2 * i, D + 5 * i);
+          uint32_t e9;
+          uint2 e27;
+          sel(12, e9, e27);
+          D[30] = wp(e9);
+          D[31] = wp(e27.x);
+        } else {
+          // bytes 12..25: codes 60..129; this half takes 64..127
+          uint32_t e9, o9;
+          uint2 e27, o27;
+          sel(0, e9, e27);
+          sel(1, o9, o27);
+          D[0] = wp(e27.y | o9 << 16);
+          D[1] = wp(__builtin_amdgcn_alignbit(o27.x, o9, 16));
+          D[2] = wp(__builtin_amdgcn_alignbit(o27.y, o27.x, 16));
+#pragma unroll
+          for (int i = 1; i < 6; ++i) pair5(2 * i, D + 5 * i - 2);
+          uint32_t t[5];
+          pair5(12, t);
+          D[28] = t[0];
+          D[29] = t[1];
+          D[30] = t[2];
+          D[31] = t[3];
+        }
+      } else {
+        const uint32_t dw[4] = {raw.c[0].x, raw.c[0].y, raw.c[0].z, raw.c[0].w};
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const uint32_t b = (dw[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+          D[2 * j] = wp(tsel[b & 15u]);
+          D[2 * j + 1] = wp(tsel[b >> 4]);
+        }
+      }
     }
     uint4* dst = (uint4*)(ws[buf] + srow * kGmLd);
 #pragma unroll
