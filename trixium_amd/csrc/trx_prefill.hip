@@ -717,11 +717,14 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnPrefillParams p) 
 //                 the score layout (lane half h holds keys 4h..4h+3 and 8+4h..8+4h+3 of each 16).
 // Numerics as attn_prefill_kernel's to fp32 rounding (softmax in fp32, __expf).
 template <int HD>
-__global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(AttnPrefillParams p) {
+__global__ __launch_bounds__(256, HD <= 128 ? 2 : 1) void attn_prefill_mfma_kernel(AttnPrefillParams p) {
   constexpr int NC = HD / 16, NDT = HD / 32;       // q chunks of 16 dims; 32-dim output tiles
-  constexpr int KS = HD + 8, VS = 32 + 8;           // LDS row strides (halfs)
-  __shared__ __align__(16) _Float16 ks[32 * KS];
-  __shared__ __align__(16) _Float16 vt[HD * VS];
+  // LDS row strides (halfs). V^T rows of 36 halves (18 dwords): the staging threads' 16-byte
+  // stores to rows 2dp and the MFMA lanes' 8-byte reads of rows j both spread over every bank.
+  constexpr int KS = HD + 8, VS = 32 + 4;
+  // Two buffers of each: the next key tile is stored into one while the waves read the other.
+  __shared__ __align__(16) _Float16 ks[2][32 * KS];
+  __shared__ __align__(16) _Float16 vt[2][HD * VS];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, j = lane & 31;
   const int rep = p.n_head / p.n_kv, PW = 32 / rep, g = blockIdx.y;
   const int q0 = blockIdx.x * 4 * PW;                              // chunk offset of the block
@@ -731,6 +734,7 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(AttnPrefillParam
   const int qpos = cvalid ? p.p0 + qrow : -1;                      // -1: every key masked
   const int head = g * rep + jh;
   const int wave_last = p.p0 + min(p.R, q0 + (w + 1) * PW) - 1;
+  const int wave_first = p.p0 + q0 + w * PW;
   const int block_last = p.p0 + min(p.R, q0 + 4 * PW) - 1;
 
   // This column's q as fp16 hi/lo planes in the B-operand layout (dims 16c + 8h .. + 7).
@@ -758,29 +762,53 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(AttnPrefillParam
   float m = -INFINITY, l = 0.f;
   const __half* kc = p.kcache + (size_t)g * p.max_ctx * HD;
   const __half* vc = p.vcache + (size_t)g * p.max_ctx * HD;
-  // Staging: thread t moves 16 bytes (8 dims) of key row t / (HD / 8) per pass; rows past the
-  // block's last query are zeros (their V would otherwise meet probability 0 as garbage).
+  // Staging, rows past the block's last query as zeros (their V would otherwise meet probability
+  // 0 as garbage). K: thread t moves 16 bytes (8 dims) of key row t / (HD / 8) per pass. V: thread
+  // t loads dims 2 dp, 2 dp + 1 (dp = t % (HD / 2)) of KPT consecutive keys, one dword each (a
+  // wave reads whole rows), and stores them as KPT keys of V^T rows 2 dp and 2 dp + 1 (one or two
+  // 16-byte stores each; storing V^T one half at a time put 16 lanes on one bank).
   constexpr int SEG = HD / 8, PASS = 256 / SEG, NPASS = 32 / PASS;
   const int srow = tid / SEG, sd = (tid % SEG) * 8;
+  constexpr int KPT = HD / 16;                       // keys per thread for V (4, 8, 16)
+  const int dp = tid % (HD / 2), kg = tid / (HD / 2);
 
-  for (int t0 = 0; t0 <= block_last; t0 += 32) {
-    uint4 kr[NPASS], vr[NPASS];
+  // The next tile's rows are loaded into registers while the waves work on this one, and stored
+  // to the other buffer at the top of the next pass: one barrier a tile, and the loads' latency
+  // behind the MFMAs. A wave that passed a barrier has finished reading the buffer that barrier's
+  // pass did not fill, so the store two passes later is safe.
+  uint4 kr[NPASS];
+  uint32_t vr[KPT];
+  auto load_tile = [&](int t0) {
 #pragma unroll
     for (int ps = 0; ps < NPASS; ++ps) {
       const int kp = t0 + ps * PASS + srow;
-      const bool ok = kp <= block_last;
-      kr[ps] = ok ? *(const uint4*)(kc + (size_t)kp * HD + sd) : make_uint4(0, 0, 0, 0);
-      vr[ps] = ok ? *(const uint4*)(vc + (size_t)kp * HD + sd) : make_uint4(0, 0, 0, 0);
+      kr[ps] = kp <= block_last ? *(const uint4*)(kc + (size_t)kp * HD + sd) : make_uint4(0, 0, 0, 0);
     }
-    __syncthreads();                                  // the previous tile's reads are done
 #pragma unroll
-    for (int ps = 0; ps < NPASS; ++ps) {
-      const int r = ps * PASS + srow;
-      *(uint4*)(ks + r * KS + sd) = kr[ps];
-      const _Float16* vh = (const _Float16*)&vr[ps];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) vt[(sd + k) * VS + r] = vh[k];
+    for (int i = 0; i < KPT; ++i) {
+      const int kp = t0 + kg * KPT + i;
+      vr[i] = kp <= block_last ? *(const uint32_t*)(vc + (size_t)kp * HD + 2 * dp) : 0u;
     }
+  };
+  load_tile(0);
+  for (int t0 = 0, buf = 0; t0 <= block_last; t0 += 32, buf ^= 1) {
+#pragma unroll
+    for (int ps = 0; ps < NPASS; ++ps) *(uint4*)(ks[buf] + (ps * PASS + srow) * KS + sd) = kr[ps];
+    {
+      uint32_t lo[KPT / 2], hi[KPT / 2];             // rows 2 dp and 2 dp + 1, two keys a dword
+#pragma unroll
+      for (int i = 0; i < KPT / 2; ++i) {
+        lo[i] = __builtin_amdgcn_perm(vr[2 * i + 1], vr[2 * i], 0x05040100u);
+        hi[i] = __builtin_amdgcn_perm(vr[2 * i + 1], vr[2 * i], 0x07060302u);
+      }
+      _Float16* v0 = vt[buf] + (2 * dp) * VS + kg * KPT;
+#pragma unroll
+      for (int i = 0; i < KPT / 2; i += 2) {
+        *(uint2*)(v0 + 2 * i) = make_uint2(lo[i], lo[i + 1]);
+        *(uint2*)(v0 + VS + 2 * i) = make_uint2(hi[i], hi[i + 1]);
+      }
+    }
+    load_tile(t0 + 32);                               // past the block's last key: zeros, no load
     __syncthreads();
     if (t0 > wave_last) continue;                     // every key past this wave's queries
 
@@ -789,18 +817,22 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(AttnPrefillParam
     for (int e = 0; e < 16; ++e) s[e] = 0.f;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const half8_t a = *(const half8_t*)(ks + j * KS + 16 * c + 8 * h);
+      const half8_t a = *(const half8_t*)(ks[buf] + j * KS + 16 * c + 8 * h);
       s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qh[c], s, 0, 0, 0);
       s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, ql[c], s, 0, 0, 0);
     }
-    // Causal mask and the column's running max over its keys.
+    // Causal mask (only a tile that reaches past the wave's first query needs it; the columns
+    // that hold no query are never stored) and the column's running max over its keys.
+    if (t0 + 31 > wave_first) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int kp = t0 + 8 * (e >> 2) + 4 * h + (e & 3);
+        if (kp > qpos) s[e] = -INFINITY;
+      }
+    }
     float mx = -INFINITY;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int kp = t0 + 8 * (e >> 2) + 4 * h + (e & 3);
-      if (kp > qpos) s[e] = -INFINITY;
-      mx = fmaxf(mx, s[e]);
-    }
+    for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[e]);
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float mn = fmaxf(m, mx);
     const float corr = mn == -INFINITY ? 1.f : __expf(m - mn);
@@ -816,15 +848,20 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(AttnPrefillParam
     }
     ps_ += __shfl_xor(ps_, 32, 64);
     l = l * corr + ps_;
+    // The output is rescaled only when some column's max rose (otherwise every corr is 1).
+    if (__any(mn != m)) {
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[dt][e] *= corr;
+    }
     m = mn;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) o[dt][e] *= corr;
-#pragma unroll
       for (int kh = 0; kh < 2; ++kh) {
         // V^T rows dt * 32 + j, keys 16 kh + 4h .. + 3 and 16 kh + 8 + 4h .. + 3.
-        const _Float16* vr0 = vt + (dt * 32 + j) * VS + 16 * kh + 4 * h;
+        const _Float16* vr0 = vt[buf] + (dt * 32 + j) * VS + 16 * kh + 4 * h;
         const uint2 lo4 = *(const uint2*)vr0, hi4 = *(const uint2*)(vr0 + 8);
         const uint4 av = make_uint4(lo4.x, lo4.y, hi4.x, hi4.y);
         const half8_t a = __builtin_bit_cast(half8_t, av);
