@@ -436,6 +436,54 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepParams p) {
   }
 }
 
+// The same with 16-byte loads and 8-byte plane stores (K and the row stride multiples of 4).
+__global__ __launch_bounds__(256) void prep_vec_kernel(PrepParams p) {
+  __shared__ float red[16];
+  const int r = blockIdx.x, t = threadIdx.x, K4 = p.K / 4;
+  const float4* x = (const float4*)(p.x + (size_t)r * p.ldx);
+  const float4* gw = (const float4*)p.norm_w;
+  float rs = 1.f;
+  if (gw) {
+    float ss = 0.f;
+    for (int c = t; c < K4; c += 256) {
+      const float4 v = x[c];
+      ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+    }
+    rs = 1.0f / sqrtf(block_sum(ss, red) / (float)p.K + p.eps);
+  }
+  auto val = [&](int c) {
+    float4 v = x[c];
+    if (gw) {
+      const float4 g = gw[c];
+      v = make_float4(v.x * rs * g.x, v.y * rs * g.y, v.z * rs * g.z, v.w * rs * g.w);
+    }
+    return v;
+  };
+  float am = 0.f;
+  for (int c = t; c < K4; c += 256) {
+    const float4 v = val(c);
+    am = fmaxf(am, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+  }
+  float down, up;
+  row_scale(block_max(am, red), down, up);
+  if (t == 0) p.xs[r] = up;
+  uint2* xh = (uint2*)(p.xh + (size_t)r * p.K);
+  uint2* xl = (uint2*)(p.xl + (size_t)r * p.K);
+  for (int c = t; c < K4; c += 256) {
+    const float4 v = val(c);
+    const float e[4] = {v.x * down, v.y * down, v.z * down, v.w * down};
+    uint32_t hb[4], lb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const _Float16 h = (_Float16)e[i];
+      hb[i] = __builtin_bit_cast(uint16_t, h);
+      lb[i] = half_bits(e[i] - (float)h);
+    }
+    xh[c] = make_uint2(hb[0] | hb[1] << 16, hb[2] | hb[3] << 16);
+    xl[c] = make_uint2(lb[0] | lb[1] << 16, lb[2] | lb[3] << 16);
+  }
+}
+
 // Rotated input: one block of B threads per (rotation block, position), as rotate_kernel does for
 // one vector (the whole row's sum of squares, the butterflies by shuffles then LDS).
 // The rotated input's row statistics, one block of 256 threads per position: the RMSNorm scale
@@ -494,6 +542,8 @@ int launch_prep(const PrepParams& p, hipStream_t s) {
     TRX_CHECK(p.rs, TRX_E_INVALID, "prefill input: a rotation needs the row-scale buffer");
     hipLaunchKernelGGL(prep_rot_stats_kernel, dim3(p.R), dim3(256), 0, s, p);
     hipLaunchKernelGGL(prep_rot_kernel, dim3(p.K / p.B, p.R), dim3(p.B), 0, s, p);
+  } else if (p.K % 4 == 0 && p.ldx % 4 == 0) {
+    hipLaunchKernelGGL(prep_vec_kernel, dim3(p.R), dim3(256), 0, s, p);
   } else {
     hipLaunchKernelGGL(prep_kernel, dim3(p.R), dim3(256), 0, s, p);
   }
