@@ -2,8 +2,9 @@
 1956-1977 forward_pair: several prompt positions per weight pass).
 
 - The multi-position GEMM (trx_gemm_ternary_f32) against float64 on trit5, 2-bit and Q8 rows:
-  ragged row counts, odd group counts, positions not a multiple of the block's 64, every
-  epilogue, with and without the RMSNorm prologue.
+  ragged row counts, odd group counts and a single group (the kernel's two 64-column steps),
+  positions not a multiple of the block's 64, every epilogue, with and without the RMSNorm
+  prologue.
 - The decoder after a prefill against the fastref fixtures (greedy tokens) and the float oracle
   (logits at the last prompt position and at later teacher-forced positions), on the tiny
   models, the YaRN and rotated images and the 27B hybrid geometry; chunks of 1, 2 (shorter than
@@ -63,7 +64,7 @@ def _gemm(rows, kind, M, K, x, norm_w, eps, epi, y0=None):
 @pytest.mark.parametrize("kname", ["trit5", "2bit", "q8"])
 @pytest.mark.parametrize("epi", [_lib.EPI_STORE, _lib.EPI_RESID, _lib.EPI_SWIGLU])
 @pytest.mark.parametrize("M,K,n,norm", [(384, 256, 70, True), (200, 384, 5, False), (1024, 2048, 130, True),
-                                        (6144, 2048, 64, False)])
+                                        (6144, 2048, 64, False), (130, 128, 33, True)])
 def test_gemm_matches_float64(kname, epi, M, K, n, norm):
     kind = KINDS[kname]
     rng = np.random.default_rng(M * 31 + K + n + epi)
