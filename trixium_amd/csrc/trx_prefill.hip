@@ -777,7 +777,11 @@ __global__ __launch_bounds__(256, HD <= 128 ? 2 : 1) void attn_prefill_mfma_kern
   __shared__ __align__(16) _Float16 vt[2][HD * VS];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, j = lane & 31;
   const int rep = p.n_head / p.n_kv, PW = 32 / rep, g = blockIdx.y;
-  const int q0 = blockIdx.x * 4 * PW;                              // chunk offset of the block
+  // The causal work of a block grows with its position tile. Blocks b and b + 256 share a CU
+  // (blocks go round-robin over the XCDs and their CUs), so the upper half of the kv heads takes
+  // the tiles in reverse: a CU holds tiles x and last - x, not two of the longest.
+  const int bx = blockIdx.y >= (gridDim.y + 1) / 2 ? gridDim.x - 1 - blockIdx.x : blockIdx.x;
+  const int q0 = bx * 4 * PW;                                      // chunk offset of the block
   const int pq = j / rep, jh = j - pq * rep;
   const int qrow = q0 + w * PW + pq;                               // chunk row of this column
   const bool cvalid = pq < PW && qrow < p.R;
@@ -862,15 +866,18 @@ __global__ __launch_bounds__(256, HD <= 128 ? 2 : 1) void attn_prefill_mfma_kern
     __syncthreads();
     if (t0 > wave_last) continue;                     // every key past this wave's queries
 
-    f32x16_t s;
+    // The hi and lo planes' products in two accumulators: two independent MFMA chains.
+    f32x16_t s, sl;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) s[e] = 0.f;
+    for (int e = 0; e < 16; ++e) s[e] = sl[e] = 0.f;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const half8_t a = *(const half8_t*)(ks[buf] + j * KS + 16 * c + 8 * h);
       s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qh[c], s, 0, 0, 0);
-      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, ql[c], s, 0, 0, 0);
+      sl = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, ql[c], sl, 0, 0, 0);
     }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s[e] += sl[e];
     // Causal mask (only a tile that reaches past the wave's first query needs it; the columns
     // that hold no query are never stored) and the column's running max over its keys.
     if (t0 + 31 > wave_first) {
