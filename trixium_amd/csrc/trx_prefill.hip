@@ -832,16 +832,22 @@ __global__ __launch_bounds__(256, HD <= 128 ? 2 : 1) void attn_prefill_mfma_kern
   // pass did not fill, so the store two passes later is safe.
   uint4 kr[NPASS];
   uint32_t vr[KPT];
+  // Buffer loads over the kv head's cache rows; a key past the block's last query gets an offset
+  // past the range (zeros, no memory access), so the loads carry no branches.
+  const uint32_t head_bytes = (uint32_t)p.max_ctx * HD * 2u, kOut = 0x40000000u;
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kc, head_bytes), rv = make_rsrc(vc, head_bytes);
   auto load_tile = [&](int t0) {
 #pragma unroll
     for (int ps = 0; ps < NPASS; ++ps) {
       const int kp = t0 + ps * PASS + srow;
-      kr[ps] = kp <= block_last ? *(const uint4*)(kc + (size_t)kp * HD + sd) : make_uint4(0, 0, 0, 0);
+      const auto a = __builtin_amdgcn_raw_buffer_load_b128(
+          rk, kp <= block_last ? ((uint32_t)kp * HD + sd) * 2u : kOut, 0, 0);
+      kr[ps] = make_uint4(a[0], a[1], a[2], a[3]);
     }
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
       const int kp = t0 + kg * KPT + i;
-      vr[i] = kp <= block_last ? *(const uint32_t*)(vc + (size_t)kp * HD + 2 * dp) : 0u;
+      vr[i] = __builtin_amdgcn_raw_buffer_load_b32(rv, kp <= block_last ? ((uint32_t)kp * HD + 2 * dp) * 2u : kOut, 0, 0);
     }
   };
   load_tile(0);
@@ -897,7 +903,10 @@ __global__ __launch_bounds__(256, HD <= 128 ? 2 : 1) void attn_prefill_mfma_kern
     half8_t ph[2], pl[2];
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const float pe = s[e] == -INFINITY ? 0.f : __expf(s[e] - mn);
+      // A masked score gives exp(-inf) = 0: the running max of a column that holds a query is
+      // finite from its first tile on (key 0 is never masked for it); a column that holds none
+      // may turn NaN, but it only reaches its own output column, which is never stored.
+      const float pe = __expf(s[e] - mn);
       ps_ += pe;
       const _Float16 hi = (_Float16)pe;
       ph[e >> 3][e & 7] = hi;
