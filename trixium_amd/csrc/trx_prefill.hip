@@ -897,8 +897,12 @@ __global__ __launch_bounds__(256, HD <= 128 ? 2 : 1) void attn_prefill_mfma_kern
 #pragma unroll
     for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[e]);
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mn = fmaxf(m, mx);
-    const float corr = mn == -INFINITY ? 1.f : __expf(m - mn);
+    // The running max moves only when this tile's exceeds it by more than 8, so a probability
+    // stays below e^8 (~2981: its fp16 hi plane finite, hi + lo still ~22 bits) and the output
+    // is rescaled in few tiles; o / l is the same whichever max they share.
+    const bool raise = mx > m + 8.f;
+    const float mn = raise ? mx : m;
+    const float corr = raise ? __expf(m - mn) : 1.f;
     float ps_ = 0.f;
     half8_t ph[2], pl[2];
 #pragma unroll
@@ -914,8 +918,7 @@ __global__ __launch_bounds__(256, HD <= 128 ? 2 : 1) void attn_prefill_mfma_kern
     }
     ps_ += __shfl_xor(ps_, 32, 64);
     l = l * corr + ps_;
-    // The output is rescaled only when some column's max rose (otherwise every corr is 1).
-    if (__any(mn != m)) {
+    if (__any(raise)) {
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
