@@ -92,6 +92,33 @@ def test_gemm_matches_float64(kname, epi, M, K, n, norm):
     assert np.all(err <= bound)
 
 
+@pytest.mark.parametrize("norm", [False, True])
+def test_gemm_input_not_16_byte_aligned(norm):
+    """x rows starting 4 bytes into a buffer take the input-plane kernel's 4-byte path; the result
+    is held to the same float64 bound as the aligned calls."""
+    kind, M, K, n = L.KIND_TERNARY5, 256, 512, 40
+    rng = np.random.default_rng(17 + norm)
+    rows, W = _matrix(kind, M, K, rng)
+    x = rng.standard_normal((n, K)).astype(np.float32)
+    g = rng.uniform(0.8, 1.2, K).astype(np.float32) if norm else None
+    eps = 1e-6
+    xd = x.astype(np.float64)
+    if norm:
+        xd = xd / np.sqrt(np.mean(xd * xd, axis=1, keepdims=True) + eps) * g.astype(np.float64)
+    ref, mag = xd @ W.T, np.abs(xd) @ np.abs(W).T
+    rb = _lib.DeviceBuffer.from_array(rows)
+    xb = _lib.DeviceBuffer(4 * (n * K + 1))
+    xb.upload(x, offset=4)
+    gb = _lib.DeviceBuffer.from_array(g) if norm else None
+    yb = _lib.DeviceBuffer(4 * n * M)
+    wb = _lib.DeviceBuffer(4 * n * (K + 1))
+    _lib.call("trx_gemm_ternary_f32", rb.ptr, kind, M, K, xb.ptr + 4, n, gb.ptr if gb else None,
+              ctypes.c_float(eps), yb.ptr, _lib.EPI_STORE, wb.ptr, None)
+    _lib.call("trx_stream_sync", None)
+    got = yb.download(np.float32, n * M).reshape(n, M).astype(np.float64)
+    assert np.all(np.abs(got - ref) <= 2e-5 * mag + 1e-7)
+
+
 @pytest.mark.parametrize("epi", [_lib.EPI_STORE, _lib.EPI_SWIGLU])
 @pytest.mark.parametrize("norm", [False, True])
 def test_gemm_large_inputs_stay_finite(epi, norm):

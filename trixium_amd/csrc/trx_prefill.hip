@@ -542,7 +542,7 @@ int launch_prep(const PrepParams& p, hipStream_t s) {
     TRX_CHECK(p.rs, TRX_E_INVALID, "prefill input: a rotation needs the row-scale buffer");
     hipLaunchKernelGGL(prep_rot_stats_kernel, dim3(p.R), dim3(256), 0, s, p);
     hipLaunchKernelGGL(prep_rot_kernel, dim3(p.K / p.B, p.R), dim3(p.B), 0, s, p);
-  } else if (p.K % 4 == 0 && p.ldx % 4 == 0) {
+  } else if (p.K % 4 == 0 && p.ldx % 4 == 0 && ((uintptr_t)p.x & 15) == 0 && ((uintptr_t)p.norm_w & 15) == 0) {
     hipLaunchKernelGGL(prep_vec_kernel, dim3(p.R), dim3(256), 0, s, p);
   } else {
     hipLaunchKernelGGL(prep_kernel, dim3(p.R), dim3(256), 0, s, p);
@@ -960,6 +960,9 @@ __global__ __launch_bounds__(256, HD <= 128 ? 2 : 1) void attn_prefill_mfma_kern
 int launch_attn_prefill(const AttnPrefillParams& p, hipStream_t s) {
   TRX_CHECK(p.n_kv >= 1 && p.n_head % p.n_kv == 0 && p.n_head / p.n_kv <= 64 && p.R >= 1 &&
             p.p0 + p.R <= p.max_ctx, TRX_E_INVALID, "prefill attention: bad geometry");
+  // A kv head's cache rows lie below the offset the loads use for keys past a block's queries.
+  TRX_CHECK((size_t)p.max_ctx * p.hd * 2 < 0x40000000u, TRX_E_INVALID, "prefill attention: context %d too long",
+            p.max_ctx);
   const int rep = p.n_head / p.n_kv, QT = 64 / rep;
   if ((p.hd == 64 || p.hd == 128 || p.hd == 256) && rep <= 32) {
     const dim3 mgrid(cdiv(p.R, 4 * (32 / rep)), p.n_kv);
