@@ -769,8 +769,9 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnPrefillParams p) 
 template <int HD>
 __global__ __launch_bounds__(256, HD <= 128 ? 2 : 1) void attn_prefill_mfma_kernel(AttnPrefillParams p) {
   constexpr int NC = HD / 16, NDT = HD / 32;       // q chunks of 16 dims; 32-dim output tiles
-  // LDS row strides (halfs). V^T rows of 36 halves (18 dwords): the staging threads' 16-byte
-  // stores to rows 2dp and the MFMA lanes' 8-byte reads of rows j both spread over every bank.
+  // LDS row strides (halfs). V^T rows of 36 halves (18 dwords, 8-byte aligned): the MFMA lanes'
+  // 8-byte reads of rows j spread over every bank, and the staging threads' 8-byte stores to
+  // rows 2 dp conflict at most two ways.
   constexpr int KS = HD + 8, VS = 32 + 4;
   // Two buffers of each: the next key tile is stored into one while the waves read the other.
   __shared__ __align__(16) _Float16 ks[2][32 * KS];
@@ -819,8 +820,8 @@ __global__ __launch_bounds__(256, HD <= 128 ? 2 : 1) void attn_prefill_mfma_kern
   // Staging, rows past the block's last query as zeros (their V would otherwise meet probability
   // 0 as garbage). K: thread t moves 16 bytes (8 dims) of key row t / (HD / 8) per pass. V: thread
   // t loads dims 2 dp, 2 dp + 1 (dp = t % (HD / 2)) of KPT consecutive keys, one dword each (a
-  // wave reads whole rows), and stores them as KPT keys of V^T rows 2 dp and 2 dp + 1 (one or two
-  // 16-byte stores each; storing V^T one half at a time put 16 lanes on one bank).
+  // wave reads whole rows), and stores them as KPT keys of V^T rows 2 dp and 2 dp + 1 (8-byte
+  // stores, KPT / 4 a row; storing V^T one half at a time put 16 lanes on one bank).
   constexpr int SEG = HD / 8, PASS = 256 / SEG, NPASS = 32 / PASS;
   const int srow = tid / SEG, sd = (tid % SEG) * 8;
   constexpr int KPT = HD / 16;                       // keys per thread for V (4, 8, 16)
