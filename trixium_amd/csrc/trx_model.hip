@@ -31,6 +31,7 @@ struct Tensor {
 // Positions every KV ring keeps past the window at least (firmware/hybrid.c:161 KV_SINKS), and the
 // sampler's repetition window (the last 64 tokens, firmware/infer.c:385-488).
 constexpr int kKvSinks = 4;
+constexpr int kPfPartRow = 16 * 128;   // floats of K-part sums per prefill row
 constexpr int kSmpWindow = 64;
 
 // Projections that can run on the packed GEMV (trx_tgemv.h), keyed with their layer.
@@ -113,6 +114,9 @@ struct Model {
   int pf_rows = 0;
   float *pf_x = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_att = nullptr, *pf_act = nullptr;
   float *pf_ba = nullptr, *pf_conv = nullptr, *pf_oraw = nullptr;
+  // [pf_rows][kPfPartRow] the sums of a small GEMM's K parts (launch_gemm splits the K of a grid
+  // that leaves most CUs idle, as the DeltaNet beta|alpha rows': up to 16 parts of 128 columns).
+  float* pf_part = nullptr;
   _Float16 *pf_h = nullptr, *pf_l = nullptr;
   float* pf_xs = nullptr;                          // [pf_rows] row scales of the input planes
   float* pf_rs = nullptr;                          // [pf_rows] a rotated input's 1/rms per row
@@ -866,6 +870,8 @@ static int pf_gemm(Model& m, int role, int l, int kind, int M, int K, int R, int
   g.epi = epi;
   g.y = y;
   g.ldy = ldy;
+  g.part = m.pf_part;
+  g.part_floats = (size_t)kPfPartRow * m.pf_rows;
   return launch_gemm(g, s);
 }
 
@@ -905,7 +911,8 @@ static int pf_alloc(Model& m, int R) {
       {(void**)&m.pf_q, m.n_attn ? (size_t)c.n_head * hd * 4 : 0},
       {(void**)&m.pf_ba, m.n_dn ? (size_t)2 * c.dn_num_v_heads * 4 : 0},
       {(void**)&m.pf_conv, m.n_dn ? (size_t)C * 4 : 0},
-      {(void**)&m.pf_oraw, m.n_dn ? (size_t)nvh * 4 : 0}};
+      {(void**)&m.pf_oraw, m.n_dn ? (size_t)nvh * 4 : 0},
+      {(void**)&m.pf_part, (size_t)kPfPartRow * 4}};
   int rc;
   if (m.pf_rows > 0) {
     TRX_HIP(hipStreamSynchronize(m.stream));

@@ -28,6 +28,10 @@ struct GemmParams {
   int epi;
   float* y;                // GM_STORE: y[r*ldy + m] = acc; GM_RESID: y[r*ldy + m] += acc;
   int ldy;                 // GM_SWIGLU (W = [gate; up], M = 2F): y[r*ldy + f] = silu(g[f]) * u[f]
+  // GM_STORE with few blocks (a small M): with part != null K may be split over up to 16 parts
+  // whose sums go to part[z][R][ldy] (part_floats of room) and are then added in part order.
+  float* part;
+  size_t part_floats;
 };
 int launch_gemm(const GemmParams& p, hipStream_t s);
 

@@ -63,7 +63,9 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
   const bool cw = w < 4;                    // a wave that runs the MFMAs
   const int stid = max(tid - kGmStage, 0);  // staging thread index
   const int r0 = blockIdx.y * BR;
-  const int G = p.K / kGroup;
+  // K in gridDim.z parts (more than one only for a plain store into p.part): this block's groups
+  // g0 .. g0 + G - 1.
+  const int G = p.K / kGroup / (int)gridDim.z, g0 = (int)blockIdx.z * G;
 
   // Weights are decoded by v_perm_b32 from a register pair holding -s, 0, s and 2s as fp16 (s the
   // group's scale): selector half g(c) = 0x0100 + c * 0x0202 picks (c - 1) * s for code c. trit5:
@@ -248,12 +250,12 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
   GmRaw<KIND> raw[2];
   uint4 xr[2][2 * XQ];
   auto load_step = [&](int st, int slot) {
-    load_w(raw[slot], st >> 1, st & 1);
-    load_x(xr[slot], st);
+    load_w(raw[slot], g0 + (st >> 1), st & 1);
+    load_x(xr[slot], 2 * g0 + st);
   };
   // A step's half is its register slot and LDS buffer: st & 1 == slot.
   auto stage_step = [&](int st, auto slot) {
-    stage_w(raw[decltype(slot)::value], st >> 1, slot);
+    stage_w(raw[decltype(slot)::value], g0 + (st >> 1), slot);
     stage_x(xr[decltype(slot)::value], decltype(slot)::value);
   };
   const std::integral_constant<int, 0> I0;
@@ -321,7 +323,7 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
     const int i = 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
     const int r = r0 + 32 * NA * wr + 32 * a + i;
     if (r >= p.R) continue;
-    float* yr = p.y + (size_t)r * p.ldy;
+    float* yr = (gridDim.z > 1 ? p.part + (size_t)blockIdx.z * p.R * p.ldy : p.y) + (size_t)r * p.ldy;
     const float up = p.xs[r];              // the row's plane scale (a power of two: exact)
     if (EPI == GM_SWIGLU) {
 #pragma unroll
@@ -339,6 +341,16 @@ __global__ __launch_bounds__(kGmThreads, 1) void gemm_kernel(GemmParams p) {
         }
       }
     }
+  }
+}
+
+// y[r][m] = sum over z of part[z][r][m], in part order: one block per row.
+__global__ __launch_bounds__(256) void gemm_parts_kernel(const float* part, int kp, int R, int M, int ldy, float* y) {
+  const int r = blockIdx.x;
+  for (int m = threadIdx.x; m < M; m += 256) {
+    float v = 0.f;
+    for (int z = 0; z < kp; ++z) v += part[((size_t)z * R + r) * ldy + m];
+    y[(size_t)r * ldy + m] = v;
   }
 }
 
@@ -368,7 +380,18 @@ int launch_gemm(const GemmParams& p, hipStream_t s) {
   TRX_HIP(hipGetDevice(&dev));
   TRX_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
   const bool small = 0.78 * cdiv(nx * cdiv(p.R, 64), cus) < (double)cdiv(nx * cdiv(p.R, 128), cus);
-  const dim3 grid(nx, cdiv(p.R, small ? 64 : 128));
+  // A grid that leaves most CUs idle (a few weight rows, as the DeltaNet beta|alpha rows) splits
+  // K into parts when the caller gives room for their sums: the largest divisor of the group
+  // count, at most 16, whose blocks still fit one round.
+  const int blocks = nx * cdiv(p.R, small ? 64 : 128), G = p.K / kGroup;
+  int kp = 1;
+  if (p.part && p.epi == GM_STORE && 2 * blocks <= cus)
+    for (int d = std::min(16, cus / blocks); d > 1; --d)
+      if (G % d == 0 && (size_t)d * p.R * p.ldy <= p.part_floats) {
+        kp = d;
+        break;
+      }
+  const dim3 grid(nx, cdiv(p.R, small ? 64 : 128), kp);
   if (p.kind == TRX_KIND_TERNARY5) {
     if (small) gemm_dispatch<TRX_KIND_TERNARY5, 1>(p, grid, s);
     else gemm_dispatch<TRX_KIND_TERNARY5, 2>(p, grid, s);
@@ -380,6 +403,10 @@ int launch_gemm(const GemmParams& p, hipStream_t s) {
     else gemm_dispatch<TRX_KIND_Q8, 2>(p, grid, s);
   }
   TRX_LAUNCHED();
+  if (kp > 1) {
+    hipLaunchKernelGGL(gemm_parts_kernel, dim3(p.R), dim3(256), 0, s, p.part, kp, p.R, p.M, p.ldy, p.y);
+    TRX_LAUNCHED();
+  }
   return TRX_OK;
 }
 
